@@ -1,0 +1,353 @@
+#!/usr/bin/env python3
+"""KV-copy throughput on one MI355X: BASELINE.json configs[1] (headline) plus configs 3 and 4.
+
+Headline workload: 32 layers of Llama-3-8B KV caches
+[8192 blocks, 16, 8 kv-heads, 128] bf16 (paged layout [NB, NH, HD, BS]),
+64 sequences with lengths uniform in [128, 4096] (redrawn with a fixed seed
+until they fit), int64 slot mappings from random block tables, N(0,1) data.
+One step = the multi-layer linear->paged scatter followed by the reverse
+paged->linear gather, each a single call of the library's C-ABI
+(musa_aiter_kv_linear_to_paged_multi_layer_bfloat16 /
+musa_aiter_kv_paged_to_linear_multi_layer_bfloat16) on torch's current
+stream.  Inputs are resident in HBM before timing; host-side validation runs
+once, outside the timed region.
+
+``value`` = algorithmic bytes (payload read + payload written + 8 B per slot)
+of K steps / device time of the K steps between HIP events, in GB/s.
+``roofline`` is reported for the dominant kernel (the direction with the
+larger total time) against the 8 TB/s HBM peak.  ``cpu_baseline`` times the
+numpy oracle (oracle/kv_oracle.py, a port of the reference algorithm) on a
+bounded sample of the same workload on this host and scales by bytes.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "musa-aiter_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "KV copy HBM GB/s & % of 8 TB/s peak, paged↔linear/FP8, 1 MI355X"
+NL, NB, BS, NH, HD = 32, 8192, 16, 8, 128
+ROW = NH * HD  # elements per K or V token row
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def make_slots(seed: int, num_seqs: int, lo: int, hi: int, num_blocks: int, block_size: int) -> np.ndarray:
+    from tests.kvgen import sequence_lengths, sequence_slots
+
+    rng = np.random.default_rng(seed)
+    lengths = sequence_lengths(rng, num_seqs, lo, hi, num_blocks=num_blocks, block_size=block_size)
+    return sequence_slots(rng, lengths, num_blocks=num_blocks, block_size=block_size)
+
+
+class EventTimer:
+    """Accumulates device time between HIP events recorded on torch's current stream."""
+
+    def __init__(self):
+        self.pairs: list[tuple[torch.cuda.Event, torch.cuda.Event]] = []
+
+    def start(self) -> torch.cuda.Event:
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        return ev
+
+    def stop(self, start: torch.cuda.Event) -> None:
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        self.pairs.append((start, ev))
+
+    def ms(self) -> list[float]:
+        return [a.elapsed_time(b) for a, b in self.pairs]
+
+
+def _bind(lib, name: str, nargs_ptr: int, nargs_i64: int):
+    fn = getattr(lib, name)
+    fn.argtypes = [ctypes.c_void_p] * nargs_ptr + [ctypes.c_int64] * nargs_i64 + [ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+    return fn
+
+
+def _check(rc: int, name: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{name} returned HIP error {rc}")
+
+
+def bench_config2(steps: int, warmup: int) -> dict:
+    """Multi-layer bf16 paged<->linear scatter + gather."""
+    import musa_aiter
+    from musa_aiter.ops import _hip
+
+    dev = torch.device("cuda", 0)
+    slots_np = make_slots(1002, 64, 128, 4096, NB, BS)
+    t = int(slots_np.shape[0])
+    log(f"config 2: T={t} tokens, {NL} layers, caches 2 x {NL * NB * ROW * BS * 2 / 2**30:.1f} GiB")
+    gen = torch.Generator(device=dev).manual_seed(2)
+    slots = torch.from_numpy(slots_np).to(dev)
+    kl = torch.randn((NL, t, NH, HD), generator=gen, device=dev, dtype=torch.bfloat16)
+    vl = torch.randn((NL, t, NH, HD), generator=gen, device=dev, dtype=torch.bfloat16)
+    kc = torch.randn((NL, NB, NH, HD, BS), generator=gen, device=dev, dtype=torch.bfloat16)
+    vc = torch.randn((NL, NB, NH, HD, BS), generator=gen, device=dev, dtype=torch.bfloat16)
+    ok = torch.empty_like(kl)
+    ov = torch.empty_like(vl)
+
+    # Validated public-API pass (not timed): scatter then gather must give the input back.
+    musa_aiter.kv_linear_to_paged_multi_layer(kl, vl, kc, vc, slots)
+    musa_aiter.kv_paged_to_linear_multi_layer(kc, vc, slots, out_k=ok, out_v=ov)
+    torch.cuda.synchronize()
+    parity = bool(torch.equal(ok, kl) and torch.equal(ov, vl))
+    log(f"config 2 round-trip parity: {parity}")
+
+    lib = _hip.library()
+    scatter = _bind(lib, "musa_aiter_kv_linear_to_paged_multi_layer_bfloat16", 5, 6)
+    gather = _bind(lib, "musa_aiter_kv_paged_to_linear_multi_layer_bfloat16", 5, 6)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    s_args = (kl.data_ptr(), vl.data_ptr(), slots.data_ptr(), kc.data_ptr(), vc.data_ptr(), NL, t, NB, NH, HD, BS,
+              stream)
+    g_args = (kc.data_ptr(), vc.data_ptr(), slots.data_ptr(), ok.data_ptr(), ov.data_ptr(), NL, t, NB, NH, HD, BS,
+              stream)
+    for _ in range(warmup):
+        _check(scatter(*s_args), "scatter")
+        _check(gather(*g_args), "gather")
+    torch.cuda.synchronize()
+    t_scatter, t_gather, t_total = EventTimer(), EventTimer(), EventTimer()
+    total0 = t_total.start()
+    for _ in range(steps):
+        e0 = t_scatter.start()
+        _check(scatter(*s_args), "scatter")
+        t_scatter.stop(e0)
+        e1 = t_gather.start()
+        _check(gather(*g_args), "gather")
+        t_gather.stop(e1)
+    t_total.stop(total0)
+    torch.cuda.synchronize()
+    parity = parity and bool(torch.equal(ok, kl) and torch.equal(ov, vl))
+
+    payload = 2 * NL * t * ROW * 2          # K and V rows of every layer, bf16
+    per_dir = 2 * payload + 8 * t           # read + write + slots
+    ms_s, ms_g = np.array(t_scatter.ms()), np.array(t_gather.ms())
+    total_ms = t_total.ms()[0]
+    dominant = ("gather", ms_g) if ms_g.sum() >= ms_s.sum() else ("scatter", ms_s)
+    avg_dom = float(dominant[1].mean())
+    return {
+        "tokens": t,
+        "bytes_per_direction": per_dir,
+        "total_ms": total_ms,
+        "ms_per_step": total_ms / steps,
+        "value_gbs": 2 * per_dir * steps / (total_ms * 1e-3) / 1e9,
+        "scatter": {"avg_ms": float(ms_s.mean()), "p50_ms": float(np.median(ms_s)),
+                    "p95_ms": float(np.percentile(ms_s, 95)), "gbs": per_dir / (ms_s.mean() * 1e-3) / 1e9,
+                    "tokens_per_ms": t / ms_s.mean()},
+        "gather": {"avg_ms": float(ms_g.mean()), "p50_ms": float(np.median(ms_g)),
+                   "p95_ms": float(np.percentile(ms_g, 95)), "gbs": per_dir / (ms_g.mean() * 1e-3) / 1e9,
+                   "tokens_per_ms": t / ms_g.mean()},
+        "dominant": dominant[0],
+        "dominant_avg_ms": avg_dom,
+        "parity_roundtrip": parity,
+        "_tensors": (slots_np, kc, vc),
+    }
+
+
+def bench_config3(steps: int, warmup: int) -> dict:
+    """FP8 E4M3 quant-store into a uint8 paged cache and dequant-gather to bf16, per-head scales."""
+    import musa_aiter
+
+    dev = torch.device("cuda", 0)
+    slots_np = make_slots(1003, 64, 128, 4096, NB, BS)
+    t = int(slots_np.shape[0])
+    gen = torch.Generator(device=dev).manual_seed(3)
+    slots = torch.from_numpy(slots_np).to(dev)
+    kl = torch.randn((t, NH, HD), generator=gen, device=dev) * 2.0
+    vl = torch.randn((t, NH, HD), generator=gen, device=dev) * 2.0
+    for x in (kl, vl):
+        x.mul_(torch.where(torch.rand(x.shape, generator=gen, device=dev) < 0.01, 50.0, 1.0))
+    kl, vl = kl.to(torch.bfloat16), vl.to(torch.bfloat16)
+    ks = (kl.float().abs().amax(dim=(0, 2)) / 448.0).contiguous()
+    vs = (vl.float().abs().amax(dim=(0, 2)) / 448.0).contiguous()
+    kc = torch.zeros((NB, NH, HD, BS), dtype=torch.uint8, device=dev)
+    vc = torch.zeros_like(kc)
+    ok = torch.empty_like(kl)
+    ov = torch.empty_like(vl)
+    for _ in range(warmup):
+        musa_aiter.kv_linear_to_paged_fp8(kl, vl, kc, vc, slots, ks, vs)
+        musa_aiter.kv_paged_fp8_to_linear(kc, vc, slots, ks, vs, out_k=ok, out_v=ov)
+    torch.cuda.synchronize()
+    # Time the device work only: bind the generic entry with validated arguments.
+    from musa_aiter.ops import _hip
+
+    tq, td = EventTimer(), EventTimer()
+    for _ in range(steps * 4):
+        e0 = tq.start()
+        _hip.paged_tiles(op="bench", scatter=True, codec=1, cache_elt=1, lin_elt=2, lin_dtype=2, key_cache=kc,
+                         value_cache=vc, key_linear=kl, value_linear=vl, slots=slots, num_layers=1, num_tokens=t,
+                         num_blocks=NB, num_heads=NH, head_dim=HD, block_size=BS, lin_token_stride=ROW,
+                         lin_layer_stride=t * ROW, k_scale=ks, v_scale=vs, scale_mode=1, fill_zeros=False)
+        tq.stop(e0)
+        e1 = td.start()
+        _hip.paged_tiles(op="bench", scatter=False, codec=1, cache_elt=1, lin_elt=2, lin_dtype=2, key_cache=kc,
+                         value_cache=vc, key_linear=ok, value_linear=ov, slots=slots, num_layers=1, num_tokens=t,
+                         num_blocks=NB, num_heads=NH, head_dim=HD, block_size=BS, lin_token_stride=ROW,
+                         lin_layer_stride=t * ROW, k_scale=ks, v_scale=vs, scale_mode=1, fill_zeros=True)
+        td.stop(e1)
+    torch.cuda.synchronize()
+    quant_bytes = 2 * t * ROW * (2 + 1) + 8 * t
+    mq, md = np.array(tq.ms()), np.array(td.ms())
+    err = float(((ok.float() - kl.float()).abs() / (kl.float().abs() + 1e-3)).median())
+    return {"tokens": t, "bytes_per_call": quant_bytes,
+            "quant_store": {"avg_ms": float(mq.mean()), "gbs": quant_bytes / (mq.mean() * 1e-3) / 1e9,
+                            "tokens_per_ms": t / mq.mean()},
+            "dequant_gather": {"avg_ms": float(md.mean()), "gbs": quant_bytes / (md.mean() * 1e-3) / 1e9,
+                               "tokens_per_ms": t / md.mean()},
+            "median_rel_err_roundtrip": err}
+
+
+def bench_config4(steps: int, warmup: int) -> dict:
+    """SGLang-MP [2, 32, 4096, 16, 8, 128] bf16 <-> LMCache [2, 32, 256, 1024], 16 chunks."""
+    import musa_aiter
+
+    dev = torch.device("cuda", 0)
+    nl, nb, chunk, nchunks = 32, 4096, 256, 16
+    gen = torch.Generator(device=dev).manual_seed(4)
+    cache = torch.randn((2, nl, nb, BS, NH, HD), generator=gen, device=dev, dtype=torch.bfloat16)
+    kvcaches = [list(cache[0].unbind(0)), list(cache[1].unbind(0))]
+    slots_np = make_slots(1004, 64, 128, 4096, nb, BS)[: chunk * nchunks]
+    slots = torch.from_numpy(slots_np).to(dev)
+    memory = torch.empty((2, nl, chunk * nchunks, ROW), dtype=torch.bfloat16, device=dev)
+    chunks = [(slots[i * chunk:(i + 1) * chunk].contiguous(), memory[:, :, i * chunk:(i + 1) * chunk])
+              for i in range(nchunks)]
+    for _ in range(warmup):
+        for s, m in chunks:
+            musa_aiter.lmcache_kv_paged_to_buffer_two_x_nl(kvcaches, m, s, BS, NH, HD)
+    torch.cuda.synchronize()
+    tg, tb, ts = EventTimer(), EventTimer(), EventTimer()
+    for _ in range(steps):
+        for s, m in chunks:
+            e = tg.start()
+            musa_aiter.lmcache_kv_paged_to_buffer_two_x_nl(kvcaches, m, s, BS, NH, HD)
+            tg.stop(e)
+        e = tb.start()
+        musa_aiter.lmcache_kv_paged_to_buffer_two_x_nl(kvcaches, memory, slots, BS, NH, HD)
+        tb.stop(e)
+        e = ts.start()
+        musa_aiter.lmcache_kv_buffer_to_paged_two_x_nl(memory, kvcaches, slots, 0, BS, NH, HD)
+        ts.stop(e)
+    torch.cuda.synchronize()
+    per_chunk = 2 * (2 * nl * chunk * ROW * 2) + 8 * chunk
+    mg, mb, ms = np.array(tg.ms()), np.array(tb.ms()), np.array(ts.ms())
+    return {"chunk_tokens": chunk, "chunks": nchunks, "bytes_per_chunk": per_chunk,
+            "gather_per_chunk": {"avg_ms": float(mg.mean()), "p50_ms": float(np.median(mg)),
+                                 "gbs": per_chunk / (np.median(mg) * 1e-3) / 1e9},
+            "gather_batched_16": {"avg_ms": float(mb.mean()), "gbs": per_chunk * nchunks / (mb.mean() * 1e-3) / 1e9},
+            "scatter_batched_16": {"avg_ms": float(ms.mean()), "gbs": per_chunk * nchunks / (ms.mean() * 1e-3) / 1e9},
+            "note": "per-chunk times include the host-side Python call overhead between events"}
+
+
+def cpu_baseline(slots_np: np.ndarray, kc: torch.Tensor, vc: torch.Tensor) -> dict:
+    """Time the numpy oracle on a bounded sample of configs[1]: all tokens, first 2 layers, both directions."""
+    from oracle import kv_oracle as ko
+
+    layers = 2
+    t = int(slots_np.shape[0])
+    k_np = kc[:layers].view(torch.int16).cpu().numpy().view(np.uint16)
+    v_np = vc[:layers].view(torch.int16).cpu().numpy().view(np.uint16)
+    start = time.perf_counter()
+    ks = [ko.paged_to_linear(k_np[layer], slots_np) for layer in range(layers)]
+    vs = [ko.paged_to_linear(v_np[layer], slots_np) for layer in range(layers)]
+    for layer in range(layers):
+        ko.linear_to_paged(ks[layer], k_np[layer], slots_np)
+        ko.linear_to_paged(vs[layer], v_np[layer], slots_np)
+    elapsed = time.perf_counter() - start
+    sample_bytes = 2 * (2 * (2 * layers * t * ROW * 2) + 8 * t)
+    return {"value": sample_bytes / elapsed / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"numpy oracle (oracle/kv_oracle.py) gather+scatter of {t} tokens x {layers} of {NL} layers "
+                      f"(K and V), {elapsed:.2f} s, scaled by algorithmic bytes; host has {os.cpu_count()} cpus",
+            "seconds": elapsed}
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--configs", default="2,3,4", help="comma list of BASELINE configs to run (2 is the headline)")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X only; --gpus {args.gpus} is not supported (the path does not shard "
+              "across GPUs in this build; see the sharding notes in the docs)", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    torch.cuda.set_device(0)
+    configs = {int(c) for c in args.configs.split(",") if c}
+    extra = {}
+    c2 = bench_config2(args.steps, args.warmup)
+    slots_np, kc, vc = c2.pop("_tensors")
+    log(f"config 2: scatter {c2['scatter']['gbs']:.0f} GB/s, gather {c2['gather']['gbs']:.0f} GB/s")
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(slots_np, kc, vc)
+        cpu.pop("seconds")
+        log(f"cpu baseline {cpu['value']:.2f} GB/s")
+    del kc, vc
+    torch.cuda.empty_cache()
+    if 3 in configs:
+        extra["config3_fp8_e4m3_per_head"] = bench_config3(max(1, args.steps // 2), max(1, args.warmup))
+        log(f"config 3: {json.dumps(extra['config3_fp8_e4m3_per_head'])}")
+        torch.cuda.empty_cache()
+    if 4 in configs:
+        extra["config4_lmcache_two_x_nl"] = bench_config4(max(1, args.steps // 4), max(1, args.warmup // 2))
+        log(f"config 4: {json.dumps(extra['config4_lmcache_two_x_nl'])}")
+        torch.cuda.empty_cache()
+    dom = c2[c2["dominant"]]
+    achieved = c2["bytes_per_direction"] / (c2["dominant_avg_ms"] * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(c2["value_gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(c2["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) KV rows, random block tables; no checkpoint)",
+        "config": {"workload": "configs[1]: 32-layer linear->paged scatter + paged->linear gather, bf16, caches "
+                               "[32,8192,8,128,16] (paged [NB,NH,HD,BS]), 64 seqs len U[128,4096]",
+                   "tokens": c2["tokens"], "layers": NL, "num_blocks": NB, "block_size": BS, "kv_heads": NH,
+                   "head_dim": HD, "step": "scatter + gather (2 launches of the C-ABI)"},
+        "pct_of_peak": round(100.0 * c2["value_gbs"] / HBM_PEAK_GBS, 2),
+        "tokens_per_ms": {"scatter": round(c2["scatter"]["tokens_per_ms"], 1),
+                          "gather": round(c2["gather"]["tokens_per_ms"], 1)},
+        "directions": {"scatter": c2["scatter"], "gather": c2["gather"]},
+        "parity_roundtrip": c2["parity_roundtrip"],
+        "roofline": {"bound": "hbm", "kernel": f"paged_tile_kernel ({c2['dominant']}, 64 planes)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": c2["bytes_per_direction"], "avg_launch_ms": round(c2["dominant_avg_ms"], 4)},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    _ = dom
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

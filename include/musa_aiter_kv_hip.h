@@ -1,0 +1,306 @@
+/*
+ * C-ABI of libmusa_aiter_kv_hip.so -- MI355X (gfx950) KV-cache movement kernels.
+ *
+ * Every function below is exported with C linkage, takes plain pointers
+ * (device addresses unless noted) and 64-bit sizes, launches asynchronously
+ * on `stream` (a hipStream_t passed as void*; NULL = the default stream) and
+ * returns the HIP status as an int (0 = success).  Names and argument orders
+ * are the ones the reference (musa_aiter 0.5.0) binds through ctypes, cited
+ * per entry as file:line of the reference's musa_aiter/ops Python modules (the
+ * binding) and of its csrc/kvcache .mu sources (the symbol it replaces).  A reference build that binds
+ * these names with restype=None keeps working; binding restype=c_int gives
+ * the launch status.
+ *
+ * Conventions shared by all entries:
+ *   slot = block * block_size + offset; slot < 0 skips the token (gathers
+ *   write zeros, scatters leave the destination untouched); slots outside
+ *   the cache are treated as skipped.  Scatters keep last-writer-wins for
+ *   duplicate destinations, like the reference's token loop: a claim pass
+ *   records the last token per destination in a per-(device, stream) scratch
+ *   array owned by the library (allocated on first use, grown on demand).
+ *   Element types: "_float" = fp32, "_half" = fp16, "_bfloat16" / "_u16" =
+ *   16-bit payloads (bf16 or fp16, copied bit-exactly).
+ */
+#ifndef MUSA_AITER_KV_HIP_H_
+#define MUSA_AITER_KV_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- ABI probes (kv_transfer_float.mu:3021-3027, :3277; fp8_kv_cache.mu:1529-1531) ---- */
+int musa_aiter_kv_transfer_abi_version(void);
+int native_lmcache_kv_transfer_abi_version(void);
+int musa_aiter_fp8_kv_cache_abi_version(void);
+int musa_aiter_dsv4_kv_copy_abi_version(void);
+/* No reference counterpart: backend label and HIP error text for diagnostics. */
+const char* musa_aiter_hip_backend_name(void);
+const char* musa_aiter_hip_error_string(int code);
+
+/* ---- Generic entries used by this package's Python host layer (no reference counterpart) ----
+ * Paged-A caches [NL, NB, NH, HD, BS] <-> linear rows with explicit strides.
+ * scatter: 0 gather, 1 scatter; codec: 0 copy, 1 FP8 E4M3, 2 FP8 E5M2;
+ * cache_elt / lin_elt: element bytes; lin_dtype (FP8 only): 0 f32, 1 f16, 2 bf16;
+ * lin_token_stride / lin_layer_stride in linear elements; scale_mode: 0 scalar,
+ * 1 [NH], 2 [NL, NH]; fill_zeros: gather writes zeros for skipped tokens;
+ * dedupe: scatter runs the last-writer claim pass. */
+int musa_aiter_hip_paged_tiles(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtype, void* key_cache,
+                               void* value_cache, void* key_linear, void* value_linear, const int64_t* slot_mapping,
+                               int64_t num_layers, int64_t num_tokens, int64_t num_blocks, int64_t num_heads,
+                               int64_t head_dim, int64_t block_size, int64_t lin_token_stride,
+                               int64_t lin_layer_stride, const float* k_scale, const float* v_scale, int scale_mode,
+                               int fill_zeros, int dedupe, void* stream);
+/* Row copies between plane sets: planes given as host arrays (src_planes/dst_planes)
+ * or device arrays (src_table/dst_table); a side is indexed through src_idx/dst_idx
+ * or addressed directly (row = token + offset).  zero_invalid zero-fills directly
+ * addressed destination rows whose source is skipped, and rows [num_tokens, num_rows_out). */
+int musa_aiter_hip_copy_rows(const uint64_t* src_planes, const uint64_t* dst_planes, const uint64_t* src_table,
+                             const uint64_t* dst_table, int64_t num_planes, const int64_t* src_idx,
+                             const int64_t* dst_idx, int64_t num_tokens, int64_t num_rows_out, int64_t src_offset,
+                             int64_t dst_offset, int64_t src_rows, int64_t dst_rows, int64_t row_bytes,
+                             int64_t src_stride, int64_t dst_stride, int zero_invalid, int dedupe, void* stream);
+
+/* ---- Paged-A [NB,NH,HD,BS] <-> linear [T,NH,HD] -------------------------------------------------
+ * binding kv_transfer.py:350-376 (gather), :410-436 (scatter), :480-508 / :542-570 (multi-layer),
+ * :615-639 / :671-695 / :741-767 / :799-825 (merged), :872-898 / :933-959 (MLA split);
+ * replaces kv_transfer_float.mu:58-86, :169-235, :237-385, :387-671, :673-825, :1523-1590 and
+ * lmcache_kv_transfer_extended.mu:577-628. */
+#define MUSA_AITER_KV_HIP_PAGED_DECLS(SUFFIX)                                                                       \
+  int musa_aiter_kv_paged_to_linear_##SUFFIX(const void* key_cache, const void* value_cache,                       \
+                                             const int64_t* slot_mapping, void* out_k, void* out_v,                \
+                                             int64_t num_tokens, int64_t num_blocks, int64_t num_heads,            \
+                                             int64_t head_dim, int64_t block_size, void* stream);                  \
+  int musa_aiter_kv_linear_to_paged_##SUFFIX(const void* key_linear, const void* value_linear,                     \
+                                             const int64_t* slot_mapping, void* key_cache, void* value_cache,      \
+                                             int64_t num_tokens, int64_t num_blocks, int64_t num_heads,            \
+                                             int64_t head_dim, int64_t block_size, void* stream);                  \
+  int musa_aiter_kv_paged_to_linear_multi_layer_##SUFFIX(                                                          \
+      const void* key_cache, const void* value_cache, const int64_t* slot_mapping, void* out_k, void* out_v,       \
+      int64_t num_layers, int64_t num_tokens, int64_t num_blocks, int64_t num_heads, int64_t head_dim,             \
+      int64_t block_size, void* stream);                                                                           \
+  int musa_aiter_kv_linear_to_paged_multi_layer_##SUFFIX(                                                          \
+      const void* key_linear, const void* value_linear, const int64_t* slot_mapping, void* key_cache,              \
+      void* value_cache, int64_t num_layers, int64_t num_tokens, int64_t num_blocks, int64_t num_heads,            \
+      int64_t head_dim, int64_t block_size, void* stream);                                                         \
+  int musa_aiter_kv_paged_to_merged_linear_##SUFFIX(const void* key_cache, const void* value_cache,                \
+                                                    const int64_t* slot_mapping, void* out, int64_t num_tokens,    \
+                                                    int64_t num_blocks, int64_t num_heads, int64_t head_dim,       \
+                                                    int64_t block_size, void* stream);                             \
+  int musa_aiter_kv_merged_linear_to_paged_##SUFFIX(const void* merged, const int64_t* slot_mapping,               \
+                                                    void* key_cache, void* value_cache, int64_t num_tokens,        \
+                                                    int64_t num_blocks, int64_t num_heads, int64_t head_dim,       \
+                                                    int64_t block_size, void* stream);                             \
+  int musa_aiter_kv_paged_to_merged_linear_multi_layer_##SUFFIX(                                                   \
+      const void* key_cache, const void* value_cache, const int64_t* slot_mapping, void* out, int64_t num_layers,  \
+      int64_t num_tokens, int64_t num_blocks, int64_t num_heads, int64_t head_dim, int64_t block_size,             \
+      void* stream);                                                                                               \
+  int musa_aiter_kv_merged_linear_to_paged_multi_layer_##SUFFIX(                                                   \
+      const void* merged, const int64_t* slot_mapping, void* key_cache, void* value_cache, int64_t num_layers,     \
+      int64_t num_tokens, int64_t num_blocks, int64_t num_heads, int64_t head_dim, int64_t block_size,             \
+      void* stream);                                                                                               \
+  int musa_aiter_kv_paged_to_mla_linear_##SUFFIX(const void* kv_cache, const void* pe_cache,                      \
+                                                 const int64_t* slot_mapping, void* out_kv, void* out_pe,          \
+                                                 int64_t num_tokens, int64_t num_blocks, int64_t block_size,       \
+                                                 int64_t kv_dim, int64_t pe_dim, void* stream);                    \
+  int musa_aiter_kv_mla_linear_to_paged_##SUFFIX(const void* kv_linear, const void* pe_linear,                    \
+                                                 const int64_t* slot_mapping, void* kv_cache, void* pe_cache,      \
+                                                 int64_t num_tokens, int64_t num_blocks, int64_t block_size,       \
+                                                 int64_t kv_dim, int64_t pe_dim, void* stream);
+
+MUSA_AITER_KV_HIP_PAGED_DECLS(float)
+MUSA_AITER_KV_HIP_PAGED_DECLS(half)
+MUSA_AITER_KV_HIP_PAGED_DECLS(bfloat16)
+
+/* ---- FP8 quant-store / dequant-gather (uint8 paged-A caches) ----------------------------------
+ * binding kv_transfer.py:2401-2480 (vec4 scatter), :2485-2555 (scalar scatter), :2560-2640 (hd/bs
+ * gathers), :2640-2800 (vec4 / scalar gathers), :2805-2980 (multi-layer); replaces
+ * fp8_kv_cache.mu:146-272, :326-452, :454-740, :742-882, :884-1302, :1304-1460.
+ * dtype_code: 1 float16, 2 bfloat16 (reference codes), 3 float32 (extension).
+ * Scales are device float32: scalar (scale_mode 0), [NH] (1) or [NL, NH] (2).
+ * Encoding follows the reference PyTorch encoder (kv_transfer.py:2161-2183) bit-exactly. */
+#define MUSA_AITER_KV_HIP_FP8_DECLS(FMT)                                                                            \
+  int musa_aiter_kv_linear_to_paged_fp8_##FMT(const void* key_linear, const void* value_linear,                    \
+                                              const int64_t* slot_mapping, void* key_cache, void* value_cache,     \
+                                              const float* k_scale, const float* v_scale, int64_t num_tokens,      \
+                                              int64_t num_blocks, int64_t num_heads, int64_t head_dim,             \
+                                              int64_t block_size, int dtype_code, void* stream);                   \
+  int musa_aiter_kv_linear_to_paged_fp8_vec4_##FMT(                                                                \
+      const void* key_linear, const void* value_linear, const int64_t* slot_mapping, void* key_cache,              \
+      void* value_cache, const float* k_scale, const float* v_scale, int64_t num_tokens, int64_t num_blocks,       \
+      int64_t num_heads, int64_t head_dim, int64_t block_size, int dtype_code, void* stream, int scale_mode);      \
+  int musa_aiter_kv_paged_fp8_to_linear_##FMT(const void* key_cache, const void* value_cache,                      \
+                                              const int64_t* slot_mapping, const float* k_scale,                   \
+                                              const float* v_scale, void* out_k, void* out_v, int64_t num_tokens,  \
+                                              int64_t num_blocks, int64_t num_heads, int64_t head_dim,             \
+                                              int64_t block_size, int dtype_code, void* stream);                   \
+  int musa_aiter_kv_paged_fp8_to_linear_vec4_##FMT(                                                                \
+      const void* key_cache, const void* value_cache, const int64_t* slot_mapping, const float* k_scale,           \
+      const float* v_scale, void* out_k, void* out_v, int64_t num_tokens, int64_t num_blocks, int64_t num_heads,   \
+      int64_t head_dim, int64_t block_size, int dtype_code, void* stream, int scale_mode);                         \
+  int musa_aiter_kv_linear_to_paged_fp8_multi_layer_##FMT(                                                         \
+      const void* key_linear, const void* value_linear, const int64_t* slot_mapping, void* key_cache,              \
+      void* value_cache, const float* k_scale, const float* v_scale, int64_t num_layers, int64_t num_tokens,       \
+      int64_t num_blocks, int64_t num_heads, int64_t head_dim, int64_t block_size, int dtype_code, void* stream,   \
+      int scale_mode);                                                                                             \
+  int musa_aiter_kv_paged_fp8_to_linear_multi_layer_##FMT(                                                         \
+      const void* key_cache, const void* value_cache, const int64_t* slot_mapping, const float* k_scale,           \
+      const float* v_scale, void* out_k, void* out_v, int64_t num_layers, int64_t num_tokens, int64_t num_blocks,  \
+      int64_t num_heads, int64_t head_dim, int64_t block_size, int dtype_code, void* stream, int scale_mode);      \
+  int musa_aiter_kv_paged_fp8_to_linear_hd64_bs16_##FMT(                                                           \
+      const void* key_cache, const void* value_cache, const int64_t* slot_mapping, const float* k_scale,           \
+      const float* v_scale, void* out_k, void* out_v, int64_t num_tokens, int64_t num_blocks, int64_t num_heads,   \
+      int dtype_code, void* stream);                                                                               \
+  int musa_aiter_kv_paged_fp8_to_linear_hd128_bs16_##FMT(                                                          \
+      const void* key_cache, const void* value_cache, const int64_t* slot_mapping, const float* k_scale,           \
+      const float* v_scale, void* out_k, void* out_v, int64_t num_tokens, int64_t num_blocks, int64_t num_heads,   \
+      int dtype_code, void* stream);                                                                               \
+  int musa_aiter_kv_paged_fp8_to_linear_hd128_bs32_##FMT(                                                          \
+      const void* key_cache, const void* value_cache, const int64_t* slot_mapping, const float* k_scale,           \
+      const float* v_scale, void* out_k, void* out_v, int64_t num_tokens, int64_t num_blocks, int64_t num_heads,   \
+      int dtype_code, void* stream);
+
+MUSA_AITER_KV_HIP_FP8_DECLS(e4m3)
+MUSA_AITER_KV_HIP_FP8_DECLS(e5m2)
+
+/* ---- LMCache legacy 6-D [NL,2,NB,BS,NH,HS] and MLA [NL,NB,BS,HS] <-> buffers -------------------
+ * binding lmcache_kv_transfer.py:628-696 (_call_non_mla_symbol / _call_mla_symbol);
+ * replaces kv_transfer_float.mu:1592-2030.  No-suffix = fp32, _u16 = 16-bit payloads. */
+int lmcache_kv_buffer_to_paged(const void* kv_buffer, void* paged_kv_cache, const int64_t* slot_mapping,
+                               int64_t num_layers, int64_t num_tokens, int64_t num_blocks, int64_t block_size,
+                               int64_t num_heads, int64_t head_size, void* stream);
+int lmcache_paged_to_kv_buffer(const void* paged_kv_cache, void* kv_buffer, const int64_t* slot_mapping,
+                               int64_t num_layers, int64_t num_tokens, int64_t num_blocks, int64_t block_size,
+                               int64_t num_heads, int64_t head_size, void* stream);
+int lmcache_kv_buffer_to_paged_u16(const void* kv_buffer, void* paged_kv_cache, const int64_t* slot_mapping,
+                                   int64_t num_layers, int64_t num_tokens, int64_t num_blocks, int64_t block_size,
+                                   int64_t num_heads, int64_t head_size, void* stream);
+int lmcache_paged_to_kv_buffer_u16(const void* paged_kv_cache, void* kv_buffer, const int64_t* slot_mapping,
+                                   int64_t num_layers, int64_t num_tokens, int64_t num_blocks, int64_t block_size,
+                                   int64_t num_heads, int64_t head_size, void* stream);
+int lmcache_kv_buffer_to_paged_mla(const void* kv_buffer, void* paged_kv_cache, const int64_t* slot_mapping,
+                                   int64_t num_layers, int64_t num_tokens, int64_t num_blocks, int64_t block_size,
+                                   int64_t hidden_size, void* stream);
+int lmcache_paged_to_kv_buffer_mla(const void* paged_kv_cache, void* kv_buffer, const int64_t* slot_mapping,
+                                   int64_t num_layers, int64_t num_tokens, int64_t num_blocks, int64_t block_size,
+                                   int64_t hidden_size, void* stream);
+int lmcache_kv_buffer_to_paged_mla_u16(const void* kv_buffer, void* paged_kv_cache, const int64_t* slot_mapping,
+                                       int64_t num_layers, int64_t num_tokens, int64_t num_blocks,
+                                       int64_t block_size, int64_t hidden_size, void* stream);
+int lmcache_paged_to_kv_buffer_mla_u16(const void* paged_kv_cache, void* kv_buffer, const int64_t* slot_mapping,
+                                       int64_t num_layers, int64_t num_tokens, int64_t num_blocks,
+                                       int64_t block_size, int64_t hidden_size, void* stream);
+
+/* ---- LMCache SGLang-MP 2 x NL x [NB,BS,NH,HS] <-> [2,NL,M,NH*HS] --------------------------------
+ * per-(axis, layer) plane: binding lmcache_kv_transfer.py:713-761 (_call_two_x_nl_symbol), replaces
+ * kv_transfer_float.mu:2158-2308 and lmcache_kv_transfer_extended.mu:517-539;
+ * all planes in one launch (cache_ptrs: host array of 2*NL device pointers, K layers then V
+ * layers): replaces kv_transfer_float.mu:2072-2156 (coalesced u16). */
+int lmcache_kv_buffer_to_paged_two_x_nl_float(const void* memory_tensor, void* cache, const int64_t* slot_mapping,
+                                              int64_t kv_axis, int64_t layer_index, int64_t num_layers,
+                                              int64_t memory_tokens, int64_t num_tokens,
+                                              int64_t skip_prefix_n_tokens, int64_t num_blocks, int64_t block_size,
+                                              int64_t num_heads, int64_t head_size, void* stream);
+int lmcache_paged_to_kv_buffer_two_x_nl_float(void* memory_tensor, const void* cache, const int64_t* slot_mapping,
+                                              int64_t kv_axis, int64_t layer_index, int64_t num_layers,
+                                              int64_t memory_tokens, int64_t num_tokens,
+                                              int64_t skip_prefix_n_tokens, int64_t num_blocks, int64_t block_size,
+                                              int64_t num_heads, int64_t head_size, void* stream);
+int lmcache_kv_buffer_to_paged_two_x_nl_u16(const void* memory_tensor, void* cache, const int64_t* slot_mapping,
+                                            int64_t kv_axis, int64_t layer_index, int64_t num_layers,
+                                            int64_t memory_tokens, int64_t num_tokens, int64_t skip_prefix_n_tokens,
+                                            int64_t num_blocks, int64_t block_size, int64_t num_heads,
+                                            int64_t head_size, void* stream);
+int lmcache_paged_to_kv_buffer_two_x_nl_u16(void* memory_tensor, const void* cache, const int64_t* slot_mapping,
+                                            int64_t kv_axis, int64_t layer_index, int64_t num_layers,
+                                            int64_t memory_tokens, int64_t num_tokens, int64_t skip_prefix_n_tokens,
+                                            int64_t num_blocks, int64_t block_size, int64_t num_heads,
+                                            int64_t head_size, void* stream);
+int lmcache_kv_buffer_to_paged_two_x_nl_coalesced_u16(const void* memory_tensor, const uint64_t* cache_ptrs,
+                                                      const int64_t* slot_mapping, int64_t num_layers,
+                                                      int64_t memory_tokens, int64_t num_tokens,
+                                                      int64_t skip_prefix_n_tokens, int64_t num_blocks,
+                                                      int64_t block_size, int64_t num_heads, int64_t head_size,
+                                                      void* stream);
+int lmcache_paged_to_kv_buffer_two_x_nl_coalesced_u16(void* memory_tensor, const uint64_t* cache_ptrs,
+                                                      const int64_t* slot_mapping, int64_t num_layers,
+                                                      int64_t memory_tokens, int64_t num_tokens, int64_t num_blocks,
+                                                      int64_t block_size, int64_t num_heads, int64_t head_size,
+                                                      void* stream);
+
+/* ---- LMCache per-layer list caches [2,NB,BS,NH,HS] (binding lmcache_kv_transfer.py:874-993;
+ * replaces kv_transfer_float.mu:2310-2600, lmcache_kv_transfer_extended.mu:495-515) ---- */
+int lmcache_kv_buffer_to_paged_list_float(const void* memory_tensor, void* kvcache, const int64_t* slot_mapping,
+                                          int64_t layer_index, int64_t num_layers, int64_t memory_tokens,
+                                          int64_t num_tokens, int64_t skip_prefix, int64_t num_blocks,
+                                          int64_t block_size, int64_t num_heads, int64_t head_size, void* stream);
+int lmcache_paged_to_kv_buffer_list_float(void* memory_tensor, const void* kvcache, const int64_t* slot_mapping,
+                                          int64_t layer_index, int64_t num_layers, int64_t memory_tokens,
+                                          int64_t num_tokens, int64_t skip_prefix, int64_t num_blocks,
+                                          int64_t block_size, int64_t num_heads, int64_t head_size, void* stream);
+int lmcache_kv_buffer_to_paged_list_u16(const void* memory_tensor, void* kvcache, const int64_t* slot_mapping,
+                                        int64_t layer_index, int64_t num_layers, int64_t memory_tokens,
+                                        int64_t num_tokens, int64_t skip_prefix, int64_t num_blocks,
+                                        int64_t block_size, int64_t num_heads, int64_t head_size, void* stream);
+int lmcache_paged_to_kv_buffer_list_u16(void* memory_tensor, const void* kvcache, const int64_t* slot_mapping,
+                                        int64_t layer_index, int64_t num_layers, int64_t memory_tokens,
+                                        int64_t num_tokens, int64_t skip_prefix, int64_t num_blocks,
+                                        int64_t block_size, int64_t num_heads, int64_t head_size, void* stream);
+int lmcache_kv_buffer_to_paged_list2_u16(const void* memory_tensor, void* kvcache0, void* kvcache1,
+                                         const int64_t* slot_mapping, int64_t memory_tokens, int64_t num_tokens,
+                                         int64_t skip_prefix, int64_t num_blocks, int64_t block_size,
+                                         int64_t num_heads, int64_t head_size, void* stream);
+int lmcache_paged_to_kv_buffer_list2_u16(void* memory_tensor, const void* kvcache0, const void* kvcache1,
+                                         const int64_t* slot_mapping, int64_t memory_tokens, int64_t num_tokens,
+                                         int64_t skip_prefix, int64_t num_blocks, int64_t block_size,
+                                         int64_t num_heads, int64_t head_size, void* stream);
+
+/* ---- LMCache MLA per-layer lists [NB,BS,HS] <-> [1,NL,M,HS] (binding lmcache_kv_transfer.py:920-950;
+ * replaces lmcache_kv_transfer_extended.mu:541-575) ---- */
+#define MUSA_AITER_KV_HIP_MLA_LIST_DECLS(SUFFIX)                                                                    \
+  int lmcache_mla_buffer_to_paged_list_##SUFFIX(const void* memory_tensor, void* kvcache,                          \
+                                                const int64_t* slot_mapping, int64_t layer_index,                  \
+                                                int64_t memory_tokens, int64_t num_tokens, int64_t skip_prefix,    \
+                                                int64_t num_blocks, int64_t block_size, int64_t head_size,         \
+                                                void* stream);                                                     \
+  int lmcache_mla_paged_to_buffer_list_##SUFFIX(void* memory_tensor, const void* kvcache,                          \
+                                                const int64_t* slot_mapping, int64_t layer_index,                  \
+                                                int64_t memory_tokens, int64_t num_tokens, int64_t num_blocks,     \
+                                                int64_t block_size, int64_t head_size, void* stream);
+
+MUSA_AITER_KV_HIP_MLA_LIST_DECLS(float)
+MUSA_AITER_KV_HIP_MLA_LIST_DECLS(half)
+MUSA_AITER_KV_HIP_MLA_LIST_DECLS(bfloat16)
+MUSA_AITER_KV_HIP_MLA_LIST_DECLS(u16)
+
+/* ---- DSV4 opaque byte rows (binding kv_transfer.py:4209-4253, :4310-4406;
+ * replaces kv_transfer_float.mu:3088-3275).  Out-of-range rows are skipped.
+ * The layer-table entry takes device arrays of per-layer base addresses. ---- */
+int musa_aiter_kv_copy_paged_rows_u8(const void* src, void* dst, const int64_t* src_indices,
+                                     const int64_t* dst_indices, int64_t num_rows, int64_t item_bytes,
+                                     int64_t src_num_rows, int64_t dst_num_rows, void* stream);
+int musa_aiter_kv_copy_paged_rows_layer_table_u8(const uint64_t* src_ptr_table, const uint64_t* dst_ptr_table,
+                                                 const int64_t* src_indices, const int64_t* dst_indices,
+                                                 int64_t num_rows, int64_t item_bytes, int64_t num_layers,
+                                                 int64_t src_num_rows, int64_t dst_num_rows, void* stream);
+int musa_aiter_kv_copy_paged_rows_contig_layers_u8(const void* src_base, void* dst_base, const int64_t* src_indices,
+                                                   const int64_t* dst_indices, int64_t num_rows, int64_t item_bytes,
+                                                   int64_t num_layers, int64_t src_num_rows, int64_t dst_num_rows,
+                                                   void* stream);
+
+/* ---- LMCache DSV4 strided block transfer (binding lmcache_kv_transfer.py:1355-1400;
+ * replaces kv_transfer_float.mu:3302-3405).  paged_ptrs: host array of num_layers (<= 128)
+ * device page bases; direction 0 staging->pages, 1 pages->staging; mode 0 plain rows,
+ * mode 1 values block then scales block (value_bytes + scale_bytes == row_bytes). ---- */
+int lmcache_kv_strided_block_transfer(void* staging, const uint64_t* paged_ptrs, const int64_t* block_ids,
+                                      int64_t direction, int64_t num_layers, int64_t idx_start, int64_t n_valid,
+                                      int64_t offset_in_object, int64_t staging_tokens, int64_t block_size,
+                                      int64_t row_bytes, int64_t paged_block_stride, int64_t mode,
+                                      int64_t value_bytes, int64_t scale_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MUSA_AITER_KV_HIP_H_ */

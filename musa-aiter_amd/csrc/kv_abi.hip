@@ -1,0 +1,759 @@
+// C-ABI of libmusa_aiter_kv_hip.so.
+//
+// The exported names and argument orders are the ones the reference's ctypes
+// shims bind (musa_aiter/ops/kv_transfer.py, ops/lmcache_kv_transfer.py), so
+// a reference build can load this library in place of its MUSA one.  Every
+// entry point returns the HIP status as an int (0 = success); callers that
+// bind with restype=None keep working.  The library never synchronises the
+// caller's stream except when its duplicate-slot scratch has to grow.
+//
+// Two generic entry points (musa_aiter_hip_paged_tiles and
+// musa_aiter_hip_copy_rows[_table]) carry the strides and flags the Python
+// host layer needs (fill_skipped="preserve", merged layouts, non-contiguous
+// LMCache buffers, skip prefixes); the reference-named symbols are thin
+// wrappers over the same launchers.
+#include <map>
+#include <mutex>
+#include <utility>
+#include <vector>
+
+#include "kv_hip_common.h"
+#include "kv_launch.h"
+#include "musa_aiter_kv_hip.h"
+
+using kvhip::PagedTileParams;
+using kvhip::RowCopyParams;
+
+namespace {
+
+// ----- duplicate-slot claim scratch (one array per device and stream) ------------
+
+struct ClaimScratch {
+  uint64_t* owner = nullptr;
+  int64_t capacity = 0;
+  uint32_t epoch = 0;
+};
+
+std::mutex g_claim_mu;
+std::map<std::pair<int, uintptr_t>, ClaimScratch>* g_claims = nullptr;
+
+// Runs the claim pass for `n` indices into a destination of `rows` rows and
+// returns the tag array and epoch the copy kernel must check.  A call that
+// cannot collide (n <= 1) skips the pass.
+hipError_t prepare_claims(const int64_t* idx, int64_t n, int64_t rows, hipStream_t stream, const uint64_t** owner,
+                          uint32_t* epoch) {
+  *owner = nullptr;
+  *epoch = 0;
+  if (n <= 1 || rows <= 0 || idx == nullptr) return hipSuccess;
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  std::lock_guard<std::mutex> lock(g_claim_mu);
+  if (g_claims == nullptr) g_claims = new std::map<std::pair<int, uintptr_t>, ClaimScratch>();
+  ClaimScratch& cs = (*g_claims)[{dev, reinterpret_cast<uintptr_t>(stream)}];
+  if (cs.capacity < rows) {
+    int64_t cap = cs.capacity * 2;
+    if (cap < rows) cap = rows;
+    if (cap < (int64_t{1} << 16)) cap = int64_t{1} << 16;
+    if (cs.owner != nullptr) {
+      err = hipStreamSynchronize(stream);
+      if (err != hipSuccess) return err;
+      err = hipFree(cs.owner);
+      cs.owner = nullptr;
+      cs.capacity = 0;
+      if (err != hipSuccess) return err;
+    }
+    err = hipMalloc(reinterpret_cast<void**>(&cs.owner), static_cast<size_t>(cap) * sizeof(uint64_t));
+    if (err != hipSuccess) {
+      cs.owner = nullptr;
+      return err;
+    }
+    cs.capacity = cap;
+    cs.epoch = 0;
+    err = kvhip::launch_fill_u64(cs.owner, cap, 0, stream);
+    if (err != hipSuccess) return err;
+  }
+  if (cs.epoch == 0xFFFFFFFFu) {
+    err = kvhip::launch_fill_u64(cs.owner, cs.capacity, 0, stream);
+    if (err != hipSuccess) return err;
+    cs.epoch = 0;
+  }
+  cs.epoch += 1;
+  err = kvhip::launch_claim(idx, n, rows, cs.owner, cs.epoch, stream);
+  if (err != hipSuccess) return err;
+  *owner = cs.owner;
+  *epoch = cs.epoch;
+  return hipSuccess;
+}
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ----- paged-A helpers -------------------------------------------------------------------
+
+int paged_tiles(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtype, void* kc, void* vc, void* kl,
+                void* vl, const int64_t* slots, int64_t nl, int64_t t, int64_t nb, int64_t nh, int64_t hd, int64_t bs,
+                int64_t tok_stride_elems, int64_t layer_stride_elems, const float* ks, const float* vs,
+                int scale_mode, int fill_zeros, int dedupe, hipStream_t stream) {
+  if (t <= 0 || nl <= 0) return hipSuccess;
+  PagedTileParams p{};
+  p.scatter = scatter;
+  p.codec = codec;
+  p.cache_elt = cache_elt;
+  p.lin_elt = lin_elt;
+  p.lin_dtype = lin_dtype;
+  p.cache[0] = kc;
+  p.cache[1] = vc;
+  p.lin[0] = kl;
+  p.lin[1] = vl;
+  p.slots = slots;
+  p.num_layers = nl;
+  p.num_tokens = t;
+  p.num_blocks = nb;
+  p.num_heads = nh;
+  p.head_dim = hd;
+  p.block_size = bs;
+  p.lin_token_stride = tok_stride_elems * lin_elt;
+  p.lin_layer_stride = layer_stride_elems * lin_elt;
+  p.scale[0] = ks;
+  p.scale[1] = vs;
+  p.scale_mode = scale_mode;
+  p.fill_zeros = fill_zeros;
+  if (scatter && dedupe) {
+    hipError_t err = prepare_claims(slots, t, nb * bs, stream, &p.owner, &p.epoch);
+    if (err != hipSuccess) return err;
+  }
+  return kvhip::launch_paged_tiles(p, stream);
+}
+
+int copy_gather(int elt, void* kc, void* vc, const int64_t* slots, void* ok, void* ov, int64_t nl, int64_t t,
+                int64_t nb, int64_t nh, int64_t hd, int64_t bs, int64_t tok_stride, int64_t layer_stride,
+                hipStream_t stream) {
+  return paged_tiles(0, kvhip::kCopy, elt, elt, kvhip::kLinBF16, kc, vc, ok, ov, slots, nl, t, nb, nh, hd, bs,
+                     tok_stride, layer_stride, nullptr, nullptr, 0, 1, 0, stream);
+}
+
+int copy_scatter(int elt, const void* kl, const void* vl, const int64_t* slots, void* kc, void* vc, int64_t nl,
+                 int64_t t, int64_t nb, int64_t nh, int64_t hd, int64_t bs, int64_t tok_stride, int64_t layer_stride,
+                 hipStream_t stream) {
+  return paged_tiles(1, kvhip::kCopy, elt, elt, kvhip::kLinBF16, kc, vc, const_cast<void*>(kl),
+                     const_cast<void*>(vl), slots, nl, t, nb, nh, hd, bs, tok_stride, layer_stride, nullptr, nullptr,
+                     0, 0, 1, stream);
+}
+
+// dtype codes of the reference FP8 ABI: 1 = float16, 2 = bfloat16; this
+// library also accepts 3 = float32.
+bool fp8_lin_dtype(int code, int* lin_dtype, int* lin_elt) {
+  switch (code) {
+    case 1: *lin_dtype = kvhip::kLinF16; *lin_elt = 2; return true;
+    case 2: *lin_dtype = kvhip::kLinBF16; *lin_elt = 2; return true;
+    case 3: *lin_dtype = kvhip::kLinF32; *lin_elt = 4; return true;
+    default: return false;
+  }
+}
+
+int fp8_scatter(int codec, const void* kl, const void* vl, const int64_t* slots, void* kc, void* vc, const float* ks,
+                const float* vs, int64_t nl, int64_t t, int64_t nb, int64_t nh, int64_t hd, int64_t bs, int dtype_code,
+                int scale_mode, hipStream_t stream) {
+  int ldt = 0, lelt = 0;
+  if (!fp8_lin_dtype(dtype_code, &ldt, &lelt)) return hipErrorInvalidValue;
+  return paged_tiles(1, codec, 1, lelt, ldt, kc, vc, const_cast<void*>(kl), const_cast<void*>(vl), slots, nl, t, nb,
+                     nh, hd, bs, nh * hd, t * nh * hd, ks, vs, scale_mode, 0, 1, stream);
+}
+
+int fp8_gather(int codec, const void* kc, const void* vc, const int64_t* slots, const float* ks, const float* vs,
+               void* ok, void* ov, int64_t nl, int64_t t, int64_t nb, int64_t nh, int64_t hd, int64_t bs,
+               int dtype_code, int scale_mode, hipStream_t stream) {
+  int ldt = 0, lelt = 0;
+  if (!fp8_lin_dtype(dtype_code, &ldt, &lelt)) return hipErrorInvalidValue;
+  return paged_tiles(0, codec, 1, lelt, ldt, const_cast<void*>(kc), const_cast<void*>(vc), ok, ov, slots, nl, t, nb,
+                     nh, hd, bs, nh * hd, t * nh * hd, ks, vs, scale_mode, 1, 0, stream);
+}
+
+// ----- row helpers ---------------------------------------------------------------------------
+
+// Gather rows of `planes` slot-addressed caches into directly addressed
+// linear rows; rows [num_tokens, rows_out) and skipped tokens are zeroed.
+int rows_gather(const uint64_t* cache_planes, const uint64_t* lin_planes, int64_t np, const int64_t* slots,
+                int64_t t, int64_t rows_out, int64_t lin_offset, int64_t lin_rows, int64_t slot_rows,
+                int64_t row_bytes, int64_t cache_stride, int64_t lin_stride, hipStream_t stream) {
+  RowCopyParams p{};
+  p.src_planes = cache_planes;
+  p.dst_planes = lin_planes;
+  p.num_planes = np;
+  p.src_idx = slots;
+  p.num_tokens = t;
+  p.num_rows_out = rows_out;
+  p.dst_offset = lin_offset;
+  p.src_rows = slot_rows;
+  p.dst_rows = lin_rows;
+  p.row_bytes = row_bytes;
+  p.src_stride = cache_stride;
+  p.dst_stride = lin_stride;
+  p.zero_invalid = 1;
+  return kvhip::launch_row_copy(p, stream);
+}
+
+int rows_scatter(const uint64_t* lin_planes, const uint64_t* cache_planes, int64_t np, const int64_t* slots,
+                 int64_t t, int64_t lin_offset, int64_t lin_rows, int64_t slot_rows, int64_t row_bytes,
+                 int64_t lin_stride, int64_t cache_stride, hipStream_t stream) {
+  RowCopyParams p{};
+  p.src_planes = lin_planes;
+  p.dst_planes = cache_planes;
+  p.num_planes = np;
+  p.dst_idx = slots;
+  p.num_tokens = t;
+  p.num_rows_out = t;
+  p.src_offset = lin_offset;
+  p.src_rows = lin_rows;
+  p.dst_rows = slot_rows;
+  p.row_bytes = row_bytes;
+  p.src_stride = lin_stride;
+  p.dst_stride = cache_stride;
+  hipError_t err = prepare_claims(slots, t, slot_rows, stream, &p.owner, &p.epoch);
+  if (err != hipSuccess) return err;
+  return kvhip::launch_row_copy(p, stream);
+}
+
+uint64_t addr(const void* base, int64_t byte_offset) {
+  return reinterpret_cast<uint64_t>(base) + static_cast<uint64_t>(byte_offset);
+}
+
+// LMCache legacy 6-D cache [NL, 2, NB, BS, NH, HS] <-> buffer [2, NL, T, NH*HS].
+int lmcache_6d(int scatter, int elt, const void* buffer, const void* paged, const int64_t* slots, int64_t nl,
+               int64_t t, int64_t nb, int64_t bs, int64_t nh, int64_t hs, hipStream_t stream) {
+  if (nl <= 0 || t <= 0) return hipSuccess;
+  const int64_t row = nh * hs * elt;
+  std::vector<uint64_t> cache_planes, lin_planes;
+  for (int64_t kv = 0; kv < 2; ++kv)
+    for (int64_t l = 0; l < nl; ++l) {
+      cache_planes.push_back(addr(paged, ((l * 2 + kv) * nb * bs) * row));
+      lin_planes.push_back(addr(buffer, (kv * nl + l) * t * row));
+    }
+  if (scatter)
+    return rows_scatter(lin_planes.data(), cache_planes.data(), 2 * nl, slots, t, 0, t, nb * bs, row, row, row,
+                        stream);
+  return rows_gather(cache_planes.data(), lin_planes.data(), 2 * nl, slots, t, t, 0, t, nb * bs, row, row, row,
+                     stream);
+}
+
+// LMCache MLA [NL, NB, BS, D] <-> [NL, T, D].
+int lmcache_mla(int scatter, int elt, const void* buffer, const void* paged, const int64_t* slots, int64_t nl,
+                int64_t t, int64_t nb, int64_t bs, int64_t d, hipStream_t stream) {
+  if (nl <= 0 || t <= 0) return hipSuccess;
+  const int64_t row = d * elt;
+  std::vector<uint64_t> cache_planes, lin_planes;
+  for (int64_t l = 0; l < nl; ++l) {
+    cache_planes.push_back(addr(paged, l * nb * bs * row));
+    lin_planes.push_back(addr(buffer, l * t * row));
+  }
+  if (scatter)
+    return rows_scatter(lin_planes.data(), cache_planes.data(), nl, slots, t, 0, t, nb * bs, row, row, row, stream);
+  return rows_gather(cache_planes.data(), lin_planes.data(), nl, slots, t, t, 0, t, nb * bs, row, row, row, stream);
+}
+
+// Split K/V planes of one layer for 2xNL / list layouts: buffer [2, NL, M, H].
+int lmcache_planes(int scatter, int elt, const void* memory, const uint64_t* cache_planes, const int64_t* axes,
+                   const int64_t* layers, int64_t np, const int64_t* slots, int64_t nl, int64_t m, int64_t t,
+                   int64_t skip, int64_t nb, int64_t bs, int64_t hidden, int zero_tail, hipStream_t stream) {
+  if (t <= 0 || np <= 0) return hipSuccess;
+  const int64_t row = hidden * elt;
+  std::vector<uint64_t> lin_planes(np);
+  for (int64_t i = 0; i < np; ++i) lin_planes[i] = addr(memory, (axes[i] * nl + layers[i]) * m * row);
+  if (scatter)
+    return rows_scatter(lin_planes.data(), cache_planes, np, slots, t, skip, m, nb * bs, row, row, row, stream);
+  const int64_t rows_out = zero_tail ? (m - skip) : t;
+  return rows_gather(cache_planes, lin_planes.data(), np, slots, t, rows_out, skip, m, nb * bs, row, row, row, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+// ----- identity / ABI probes ----------------------------------------------------------------
+
+int musa_aiter_kv_transfer_abi_version() { return 1; }
+int native_lmcache_kv_transfer_abi_version() { return 1; }
+int musa_aiter_fp8_kv_cache_abi_version() { return 1; }
+int musa_aiter_dsv4_kv_copy_abi_version() { return 1; }
+const char* musa_aiter_hip_backend_name() { return "rocm-hip"; }
+const char* musa_aiter_hip_error_string(int code) { return hipGetErrorString(static_cast<hipError_t>(code)); }
+
+// ----- generic entries used by the Python host layer ----------------------------------------
+
+int musa_aiter_hip_paged_tiles(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtype, void* key_cache,
+                               void* value_cache, void* key_linear, void* value_linear, const int64_t* slot_mapping,
+                               int64_t num_layers, int64_t num_tokens, int64_t num_blocks, int64_t num_heads,
+                               int64_t head_dim, int64_t block_size, int64_t lin_token_stride,
+                               int64_t lin_layer_stride, const float* k_scale, const float* v_scale, int scale_mode,
+                               int fill_zeros, int dedupe, void* stream) {
+  return paged_tiles(scatter, codec, cache_elt, lin_elt, lin_dtype, key_cache, value_cache, key_linear, value_linear,
+                     slot_mapping, num_layers, num_tokens, num_blocks, num_heads, head_dim, block_size,
+                     lin_token_stride, lin_layer_stride, k_scale, v_scale, scale_mode, fill_zeros, dedupe,
+                     as_stream(stream));
+}
+
+int musa_aiter_hip_copy_rows(const uint64_t* src_planes, const uint64_t* dst_planes, const uint64_t* src_table,
+                             const uint64_t* dst_table, int64_t num_planes, const int64_t* src_idx,
+                             const int64_t* dst_idx, int64_t num_tokens, int64_t num_rows_out, int64_t src_offset,
+                             int64_t dst_offset, int64_t src_rows, int64_t dst_rows, int64_t row_bytes,
+                             int64_t src_stride, int64_t dst_stride, int zero_invalid, int dedupe, void* stream) {
+  RowCopyParams p{};
+  p.src_planes = src_planes;
+  p.dst_planes = dst_planes;
+  p.src_table = src_table;
+  p.dst_table = dst_table;
+  p.num_planes = num_planes;
+  p.src_idx = src_idx;
+  p.dst_idx = dst_idx;
+  p.num_tokens = num_tokens;
+  p.num_rows_out = num_rows_out;
+  p.src_offset = src_offset;
+  p.dst_offset = dst_offset;
+  p.src_rows = src_rows;
+  p.dst_rows = dst_rows;
+  p.row_bytes = row_bytes;
+  p.src_stride = src_stride;
+  p.dst_stride = dst_stride;
+  p.zero_invalid = zero_invalid;
+  if (dedupe && dst_idx != nullptr) {
+    hipError_t err = prepare_claims(dst_idx, num_tokens, dst_rows, as_stream(stream), &p.owner, &p.epoch);
+    if (err != hipSuccess) return err;
+  }
+  return kvhip::launch_row_copy(p, as_stream(stream));
+}
+
+// ----- paged-A copies (kv_transfer.py:350-376, :410-436, :480-508, :542-570) ----------------
+
+#define KVHIP_PAGED_COPY(SUFFIX, ELT)                                                                              \
+  int musa_aiter_kv_paged_to_linear_##SUFFIX(const void* key_cache, const void* value_cache,                      \
+                                             const int64_t* slot_mapping, void* out_k, void* out_v,               \
+                                             int64_t num_tokens, int64_t num_blocks, int64_t num_heads,           \
+                                             int64_t head_dim, int64_t block_size, void* stream) {                \
+    return copy_gather(ELT, const_cast<void*>(key_cache), const_cast<void*>(value_cache), slot_mapping, out_k,    \
+                       out_v, 1, num_tokens, num_blocks, num_heads, head_dim, block_size, num_heads * head_dim, 0, \
+                       as_stream(stream));                                                                        \
+  }                                                                                                               \
+  int musa_aiter_kv_linear_to_paged_##SUFFIX(const void* key_linear, const void* value_linear,                    \
+                                             const int64_t* slot_mapping, void* key_cache, void* value_cache,     \
+                                             int64_t num_tokens, int64_t num_blocks, int64_t num_heads,           \
+                                             int64_t head_dim, int64_t block_size, void* stream) {                \
+    return copy_scatter(ELT, key_linear, value_linear, slot_mapping, key_cache, value_cache, 1, num_tokens,       \
+                        num_blocks, num_heads, head_dim, block_size, num_heads * head_dim, 0, as_stream(stream)); \
+  }                                                                                                               \
+  int musa_aiter_kv_paged_to_linear_multi_layer_##SUFFIX(                                                         \
+      const void* key_cache, const void* value_cache, const int64_t* slot_mapping, void* out_k, void* out_v,      \
+      int64_t num_layers, int64_t num_tokens, int64_t num_blocks, int64_t num_heads, int64_t head_dim,            \
+      int64_t block_size, void* stream) {                                                                         \
+    return copy_gather(ELT, const_cast<void*>(key_cache), const_cast<void*>(value_cache), slot_mapping, out_k,    \
+                       out_v, num_layers, num_tokens, num_blocks, num_heads, head_dim, block_size,                \
+                       num_heads * head_dim, num_tokens * num_heads * head_dim, as_stream(stream));               \
+  }                                                                                                               \
+  int musa_aiter_kv_linear_to_paged_multi_layer_##SUFFIX(                                                         \
+      const void* key_linear, const void* value_linear, const int64_t* slot_mapping, void* key_cache,             \
+      void* value_cache, int64_t num_layers, int64_t num_tokens, int64_t num_blocks, int64_t num_heads,           \
+      int64_t head_dim, int64_t block_size, void* stream) {                                                       \
+    return copy_scatter(ELT, key_linear, value_linear, slot_mapping, key_cache, value_cache, num_layers,          \
+                        num_tokens, num_blocks, num_heads, head_dim, block_size, num_heads * head_dim,            \
+                        num_tokens * num_heads * head_dim, as_stream(stream));                                    \
+  }                                                                                                               \
+  int musa_aiter_kv_paged_to_merged_linear_##SUFFIX(const void* key_cache, const void* value_cache,               \
+                                                    const int64_t* slot_mapping, void* out, int64_t num_tokens,   \
+                                                    int64_t num_blocks, int64_t num_heads, int64_t head_dim,      \
+                                                    int64_t block_size, void* stream) {                           \
+    const int64_t row = num_heads * head_dim;                                                                     \
+    return copy_gather(ELT, const_cast<void*>(key_cache), const_cast<void*>(value_cache), slot_mapping, out,      \
+                       static_cast<uint8_t*>(out) + row * ELT, 1, num_tokens, num_blocks, num_heads, head_dim,    \
+                       block_size, 2 * row, 0, as_stream(stream));                                                \
+  }                                                                                                               \
+  int musa_aiter_kv_merged_linear_to_paged_##SUFFIX(const void* merged, const int64_t* slot_mapping,              \
+                                                    void* key_cache, void* value_cache, int64_t num_tokens,       \
+                                                    int64_t num_blocks, int64_t num_heads, int64_t head_dim,      \
+                                                    int64_t block_size, void* stream) {                           \
+    const int64_t row = num_heads * head_dim;                                                                     \
+    return copy_scatter(ELT, merged, static_cast<const uint8_t*>(merged) + row * ELT, slot_mapping, key_cache,    \
+                        value_cache, 1, num_tokens, num_blocks, num_heads, head_dim, block_size, 2 * row, 0,      \
+                        as_stream(stream));                                                                       \
+  }                                                                                                               \
+  int musa_aiter_kv_paged_to_merged_linear_multi_layer_##SUFFIX(                                                  \
+      const void* key_cache, const void* value_cache, const int64_t* slot_mapping, void* out, int64_t num_layers, \
+      int64_t num_tokens, int64_t num_blocks, int64_t num_heads, int64_t head_dim, int64_t block_size,            \
+      void* stream) {                                                                                             \
+    const int64_t row = num_heads * head_dim;                                                                     \
+    return copy_gather(ELT, const_cast<void*>(key_cache), const_cast<void*>(value_cache), slot_mapping, out,      \
+                       static_cast<uint8_t*>(out) + row * ELT, num_layers, num_tokens, num_blocks, num_heads,     \
+                       head_dim, block_size, 2 * row, 2 * row * num_tokens, as_stream(stream));                   \
+  }                                                                                                               \
+  int musa_aiter_kv_merged_linear_to_paged_multi_layer_##SUFFIX(                                                  \
+      const void* merged, const int64_t* slot_mapping, void* key_cache, void* value_cache, int64_t num_layers,    \
+      int64_t num_tokens, int64_t num_blocks, int64_t num_heads, int64_t head_dim, int64_t block_size,            \
+      void* stream) {                                                                                             \
+    const int64_t row = num_heads * head_dim;                                                                     \
+    return copy_scatter(ELT, merged, static_cast<const uint8_t*>(merged) + row * ELT, slot_mapping, key_cache,    \
+                        value_cache, num_layers, num_tokens, num_blocks, num_heads, head_dim, block_size,         \
+                        2 * row, 2 * row * num_tokens, as_stream(stream));                                        \
+  }                                                                                                               \
+  int musa_aiter_kv_paged_to_mla_linear_##SUFFIX(const void* kv_cache, const void* pe_cache,                     \
+                                                 const int64_t* slot_mapping, void* out_kv, void* out_pe,         \
+                                                 int64_t num_tokens, int64_t num_blocks, int64_t block_size,      \
+                                                 int64_t kv_dim, int64_t pe_dim, void* stream) {                  \
+    const uint64_t kc = addr(kv_cache, 0), pc = addr(pe_cache, 0), ko = addr(out_kv, 0), po = addr(out_pe, 0);   \
+    const int64_t slots = num_blocks * block_size;                                                                \
+    int err = rows_gather(&kc, &ko, 1, slot_mapping, num_tokens, num_tokens, 0, num_tokens, slots, kv_dim * ELT,  \
+                          kv_dim * ELT, kv_dim * ELT, as_stream(stream));                                         \
+    if (err != 0) return err;                                                                                     \
+    return rows_gather(&pc, &po, 1, slot_mapping, num_tokens, num_tokens, 0, num_tokens, slots, pe_dim * ELT,     \
+                       pe_dim * ELT, pe_dim * ELT, as_stream(stream));                                            \
+  }                                                                                                               \
+  int musa_aiter_kv_mla_linear_to_paged_##SUFFIX(const void* kv_linear, const void* pe_linear,                   \
+                                                 const int64_t* slot_mapping, void* kv_cache, void* pe_cache,     \
+                                                 int64_t num_tokens, int64_t num_blocks, int64_t block_size,      \
+                                                 int64_t kv_dim, int64_t pe_dim, void* stream) {                  \
+    const uint64_t src[2] = {addr(kv_linear, 0), addr(pe_linear, 0)};                                             \
+    const uint64_t dst[2] = {addr(kv_cache, 0), addr(pe_cache, 0)};                                               \
+    const int64_t slots = num_blocks * block_size;                                                                \
+    RowCopyParams p{};                                                                                            \
+    p.num_planes = 1;                                                                                             \
+    p.dst_idx = slot_mapping;                                                                                     \
+    p.num_tokens = num_tokens;                                                                                    \
+    p.num_rows_out = num_tokens;                                                                                  \
+    p.src_rows = num_tokens;                                                                                      \
+    p.dst_rows = slots;                                                                                           \
+    int err = prepare_claims(slot_mapping, num_tokens, slots, as_stream(stream), &p.owner, &p.epoch);             \
+    if (err != 0) return err;                                                                                     \
+    const int64_t dims[2] = {kv_dim, pe_dim};                                                                     \
+    for (int i = 0; i < 2; ++i) {                                                                                 \
+      p.src_planes = &src[i];                                                                                     \
+      p.dst_planes = &dst[i];                                                                                     \
+      p.row_bytes = dims[i] * ELT;                                                                                \
+      p.src_stride = dims[i] * ELT;                                                                               \
+      p.dst_stride = dims[i] * ELT;                                                                               \
+      err = kvhip::launch_row_copy(p, as_stream(stream));                                                         \
+      if (err != 0) return err;                                                                                   \
+    }                                                                                                             \
+    return 0;                                                                                                     \
+  }
+
+KVHIP_PAGED_COPY(float, 4)
+KVHIP_PAGED_COPY(half, 2)
+KVHIP_PAGED_COPY(bfloat16, 2)
+#undef KVHIP_PAGED_COPY
+
+// ----- FP8 quant-store / dequant-gather (kv_transfer.py:2446-2480 and the other FP8 shims) -----
+
+#define KVHIP_FP8(FMT, CODEC)                                                                                      \
+  int musa_aiter_kv_linear_to_paged_fp8_##FMT(const void* key_linear, const void* value_linear,                   \
+                                              const int64_t* slot_mapping, void* key_cache, void* value_cache,    \
+                                              const float* k_scale, const float* v_scale, int64_t num_tokens,     \
+                                              int64_t num_blocks, int64_t num_heads, int64_t head_dim,            \
+                                              int64_t block_size, int dtype_code, void* stream) {                 \
+    return fp8_scatter(CODEC, key_linear, value_linear, slot_mapping, key_cache, value_cache, k_scale, v_scale,   \
+                       1, num_tokens, num_blocks, num_heads, head_dim, block_size, dtype_code, 0,                 \
+                       as_stream(stream));                                                                        \
+  }                                                                                                               \
+  int musa_aiter_kv_linear_to_paged_fp8_vec4_##FMT(                                                               \
+      const void* key_linear, const void* value_linear, const int64_t* slot_mapping, void* key_cache,             \
+      void* value_cache, const float* k_scale, const float* v_scale, int64_t num_tokens, int64_t num_blocks,      \
+      int64_t num_heads, int64_t head_dim, int64_t block_size, int dtype_code, void* stream, int scale_mode) {    \
+    return fp8_scatter(CODEC, key_linear, value_linear, slot_mapping, key_cache, value_cache, k_scale, v_scale,   \
+                       1, num_tokens, num_blocks, num_heads, head_dim, block_size, dtype_code, scale_mode,        \
+                       as_stream(stream));                                                                        \
+  }                                                                                                               \
+  int musa_aiter_kv_paged_fp8_to_linear_##FMT(const void* key_cache, const void* value_cache,                     \
+                                              const int64_t* slot_mapping, const float* k_scale,                  \
+                                              const float* v_scale, void* out_k, void* out_v, int64_t num_tokens, \
+                                              int64_t num_blocks, int64_t num_heads, int64_t head_dim,            \
+                                              int64_t block_size, int dtype_code, void* stream) {                 \
+    return fp8_gather(CODEC, key_cache, value_cache, slot_mapping, k_scale, v_scale, out_k, out_v, 1, num_tokens, \
+                      num_blocks, num_heads, head_dim, block_size, dtype_code, 0, as_stream(stream));             \
+  }                                                                                                               \
+  int musa_aiter_kv_paged_fp8_to_linear_vec4_##FMT(                                                               \
+      const void* key_cache, const void* value_cache, const int64_t* slot_mapping, const float* k_scale,          \
+      const float* v_scale, void* out_k, void* out_v, int64_t num_tokens, int64_t num_blocks, int64_t num_heads,  \
+      int64_t head_dim, int64_t block_size, int dtype_code, void* stream, int scale_mode) {                       \
+    return fp8_gather(CODEC, key_cache, value_cache, slot_mapping, k_scale, v_scale, out_k, out_v, 1, num_tokens, \
+                      num_blocks, num_heads, head_dim, block_size, dtype_code, scale_mode, as_stream(stream));    \
+  }                                                                                                               \
+  int musa_aiter_kv_linear_to_paged_fp8_multi_layer_##FMT(                                                        \
+      const void* key_linear, const void* value_linear, const int64_t* slot_mapping, void* key_cache,             \
+      void* value_cache, const float* k_scale, const float* v_scale, int64_t num_layers, int64_t num_tokens,      \
+      int64_t num_blocks, int64_t num_heads, int64_t head_dim, int64_t block_size, int dtype_code, void* stream,  \
+      int scale_mode) {                                                                                           \
+    return fp8_scatter(CODEC, key_linear, value_linear, slot_mapping, key_cache, value_cache, k_scale, v_scale,   \
+                       num_layers, num_tokens, num_blocks, num_heads, head_dim, block_size, dtype_code,           \
+                       scale_mode, as_stream(stream));                                                            \
+  }                                                                                                               \
+  int musa_aiter_kv_paged_fp8_to_linear_multi_layer_##FMT(                                                        \
+      const void* key_cache, const void* value_cache, const int64_t* slot_mapping, const float* k_scale,          \
+      const float* v_scale, void* out_k, void* out_v, int64_t num_layers, int64_t num_tokens, int64_t num_blocks, \
+      int64_t num_heads, int64_t head_dim, int64_t block_size, int dtype_code, void* stream, int scale_mode) {    \
+    return fp8_gather(CODEC, key_cache, value_cache, slot_mapping, k_scale, v_scale, out_k, out_v, num_layers,    \
+                      num_tokens, num_blocks, num_heads, head_dim, block_size, dtype_code, scale_mode,            \
+                      as_stream(stream));                                                                         \
+  }
+
+KVHIP_FP8(e4m3, kvhip::kE4M3)
+KVHIP_FP8(e5m2, kvhip::kE5M2)
+#undef KVHIP_FP8
+
+// Shape-specialised gathers of the reference (scalar scale); one kernel family
+// serves all of them here.
+#define KVHIP_FP8_SHAPE(HD, BS, FMT, CODEC)                                                                        \
+  int musa_aiter_kv_paged_fp8_to_linear_hd##HD##_bs##BS##_##FMT(                                                  \
+      const void* key_cache, const void* value_cache, const int64_t* slot_mapping, const float* k_scale,          \
+      const float* v_scale, void* out_k, void* out_v, int64_t num_tokens, int64_t num_blocks, int64_t num_heads,  \
+      int dtype_code, void* stream) {                                                                             \
+    return fp8_gather(CODEC, key_cache, value_cache, slot_mapping, k_scale, v_scale, out_k, out_v, 1, num_tokens, \
+                      num_blocks, num_heads, HD, BS, dtype_code, 0, as_stream(stream));                           \
+  }
+
+KVHIP_FP8_SHAPE(64, 16, e4m3, kvhip::kE4M3)
+KVHIP_FP8_SHAPE(64, 16, e5m2, kvhip::kE5M2)
+KVHIP_FP8_SHAPE(128, 16, e4m3, kvhip::kE4M3)
+KVHIP_FP8_SHAPE(128, 16, e5m2, kvhip::kE5M2)
+KVHIP_FP8_SHAPE(128, 32, e4m3, kvhip::kE4M3)
+KVHIP_FP8_SHAPE(128, 32, e5m2, kvhip::kE5M2)
+#undef KVHIP_FP8_SHAPE
+
+// ----- LMCache legacy 6-D and MLA (lmcache_kv_transfer.py:628-696) -----------------------------
+
+#define KVHIP_LMCACHE_DENSE(SUFFIX, ELT)                                                                          \
+  int lmcache_kv_buffer_to_paged##SUFFIX(const void* kv_buffer, void* paged_kv_cache, const int64_t* slot_mapping, \
+                                         int64_t num_layers, int64_t num_tokens, int64_t num_blocks,               \
+                                         int64_t block_size, int64_t num_heads, int64_t head_size, void* stream) { \
+    return lmcache_6d(1, ELT, kv_buffer, paged_kv_cache, slot_mapping, num_layers, num_tokens, num_blocks,        \
+                      block_size, num_heads, head_size, as_stream(stream));                                       \
+  }                                                                                                               \
+  int lmcache_paged_to_kv_buffer##SUFFIX(const void* paged_kv_cache, void* kv_buffer, const int64_t* slot_mapping, \
+                                         int64_t num_layers, int64_t num_tokens, int64_t num_blocks,               \
+                                         int64_t block_size, int64_t num_heads, int64_t head_size, void* stream) { \
+    return lmcache_6d(0, ELT, kv_buffer, paged_kv_cache, slot_mapping, num_layers, num_tokens, num_blocks,        \
+                      block_size, num_heads, head_size, as_stream(stream));                                       \
+  }                                                                                                               \
+  int lmcache_kv_buffer_to_paged_mla##SUFFIX(const void* kv_buffer, void* paged_kv_cache,                         \
+                                             const int64_t* slot_mapping, int64_t num_layers, int64_t num_tokens, \
+                                             int64_t num_blocks, int64_t block_size, int64_t hidden_size,         \
+                                             void* stream) {                                                      \
+    return lmcache_mla(1, ELT, kv_buffer, paged_kv_cache, slot_mapping, num_layers, num_tokens, num_blocks,       \
+                       block_size, hidden_size, as_stream(stream));                                               \
+  }                                                                                                               \
+  int lmcache_paged_to_kv_buffer_mla##SUFFIX(const void* paged_kv_cache, void* kv_buffer,                         \
+                                             const int64_t* slot_mapping, int64_t num_layers, int64_t num_tokens, \
+                                             int64_t num_blocks, int64_t block_size, int64_t hidden_size,         \
+                                             void* stream) {                                                      \
+    return lmcache_mla(0, ELT, kv_buffer, paged_kv_cache, slot_mapping, num_layers, num_tokens, num_blocks,       \
+                       block_size, hidden_size, as_stream(stream));                                               \
+  }
+
+KVHIP_LMCACHE_DENSE(, 4)
+KVHIP_LMCACHE_DENSE(_u16, 2)
+#undef KVHIP_LMCACHE_DENSE
+
+// ----- LMCache SGLang-MP 2 x NL (lmcache_kv_transfer.py:713-761; kv_transfer_float.mu:2072-2156) --
+
+#define KVHIP_TWO_X_NL(SUFFIX, ELT)                                                                               \
+  int lmcache_kv_buffer_to_paged_two_x_nl_##SUFFIX(                                                               \
+      const void* memory_tensor, void* cache, const int64_t* slot_mapping, int64_t kv_axis, int64_t layer_index,  \
+      int64_t num_layers, int64_t memory_tokens, int64_t num_tokens, int64_t skip_prefix_n_tokens,                \
+      int64_t num_blocks, int64_t block_size, int64_t num_heads, int64_t head_size, void* stream) {               \
+    const uint64_t plane = addr(cache, 0);                                                                        \
+    return lmcache_planes(1, ELT, memory_tensor, &plane, &kv_axis, &layer_index, 1, slot_mapping, num_layers,     \
+                          memory_tokens, num_tokens, skip_prefix_n_tokens, num_blocks, block_size,                \
+                          num_heads * head_size, 0, as_stream(stream));                                           \
+  }                                                                                                               \
+  int lmcache_paged_to_kv_buffer_two_x_nl_##SUFFIX(                                                               \
+      void* memory_tensor, const void* cache, const int64_t* slot_mapping, int64_t kv_axis, int64_t layer_index,  \
+      int64_t num_layers, int64_t memory_tokens, int64_t num_tokens, int64_t skip_prefix_n_tokens,                \
+      int64_t num_blocks, int64_t block_size, int64_t num_heads, int64_t head_size, void* stream) {               \
+    const uint64_t plane = addr(cache, 0);                                                                        \
+    return lmcache_planes(0, ELT, memory_tensor, &plane, &kv_axis, &layer_index, 1, slot_mapping, num_layers,     \
+                          memory_tokens, num_tokens, skip_prefix_n_tokens, num_blocks, block_size,                \
+                          num_heads * head_size, 0, as_stream(stream));                                           \
+  }
+
+KVHIP_TWO_X_NL(float, 4)
+KVHIP_TWO_X_NL(u16, 2)
+#undef KVHIP_TWO_X_NL
+
+int lmcache_kv_buffer_to_paged_two_x_nl_coalesced_u16(const void* memory_tensor, const uint64_t* cache_ptrs,
+                                                      const int64_t* slot_mapping, int64_t num_layers,
+                                                      int64_t memory_tokens, int64_t num_tokens,
+                                                      int64_t skip_prefix_n_tokens, int64_t num_blocks,
+                                                      int64_t block_size, int64_t num_heads, int64_t head_size,
+                                                      void* stream) {
+  if (num_layers <= 0) return hipSuccess;
+  std::vector<int64_t> axes(2 * num_layers), layers(2 * num_layers);
+  for (int64_t i = 0; i < 2 * num_layers; ++i) {
+    axes[i] = i / num_layers;
+    layers[i] = i % num_layers;
+  }
+  return lmcache_planes(1, 2, memory_tensor, cache_ptrs, axes.data(), layers.data(), 2 * num_layers, slot_mapping,
+                        num_layers, memory_tokens, num_tokens, skip_prefix_n_tokens, num_blocks, block_size,
+                        num_heads * head_size, 0, as_stream(stream));
+}
+
+int lmcache_paged_to_kv_buffer_two_x_nl_coalesced_u16(void* memory_tensor, const uint64_t* cache_ptrs,
+                                                      const int64_t* slot_mapping, int64_t num_layers,
+                                                      int64_t memory_tokens, int64_t num_tokens, int64_t num_blocks,
+                                                      int64_t block_size, int64_t num_heads, int64_t head_size,
+                                                      void* stream) {
+  if (num_layers <= 0) return hipSuccess;
+  std::vector<int64_t> axes(2 * num_layers), layers(2 * num_layers);
+  for (int64_t i = 0; i < 2 * num_layers; ++i) {
+    axes[i] = i / num_layers;
+    layers[i] = i % num_layers;
+  }
+  return lmcache_planes(0, 2, memory_tensor, cache_ptrs, axes.data(), layers.data(), 2 * num_layers, slot_mapping,
+                        num_layers, memory_tokens, num_tokens, 0, num_blocks, block_size, num_heads * head_size, 0,
+                        as_stream(stream));
+}
+
+// ----- LMCache per-layer list caches [2, NB, BS, NH, HS] (lmcache_kv_transfer.py:874-993) ------
+
+#define KVHIP_LIST(SUFFIX, ELT)                                                                                   \
+  int lmcache_kv_buffer_to_paged_list_##SUFFIX(const void* memory_tensor, void* kvcache,                          \
+                                               const int64_t* slot_mapping, int64_t layer_index,                  \
+                                               int64_t num_layers, int64_t memory_tokens, int64_t num_tokens,     \
+                                               int64_t skip_prefix, int64_t num_blocks, int64_t block_size,       \
+                                               int64_t num_heads, int64_t head_size, void* stream) {              \
+    const int64_t plane_bytes = num_blocks * block_size * num_heads * head_size * ELT;                            \
+    const uint64_t planes[2] = {addr(kvcache, 0), addr(kvcache, plane_bytes)};                                    \
+    const int64_t axes[2] = {0, 1}, layers[2] = {layer_index, layer_index};                                       \
+    return lmcache_planes(1, ELT, memory_tensor, planes, axes, layers, 2, slot_mapping, num_layers,               \
+                          memory_tokens, num_tokens, skip_prefix, num_blocks, block_size, num_heads * head_size,  \
+                          0, as_stream(stream));                                                                  \
+  }                                                                                                               \
+  int lmcache_paged_to_kv_buffer_list_##SUFFIX(void* memory_tensor, const void* kvcache,                          \
+                                               const int64_t* slot_mapping, int64_t layer_index,                  \
+                                               int64_t num_layers, int64_t memory_tokens, int64_t num_tokens,     \
+                                               int64_t skip_prefix, int64_t num_blocks, int64_t block_size,       \
+                                               int64_t num_heads, int64_t head_size, void* stream) {              \
+    const int64_t plane_bytes = num_blocks * block_size * num_heads * head_size * ELT;                            \
+    const uint64_t planes[2] = {addr(kvcache, 0), addr(kvcache, plane_bytes)};                                    \
+    const int64_t axes[2] = {0, 1}, layers[2] = {layer_index, layer_index};                                       \
+    return lmcache_planes(0, ELT, memory_tensor, planes, axes, layers, 2, slot_mapping, num_layers,               \
+                          memory_tokens, num_tokens, skip_prefix, num_blocks, block_size, num_heads * head_size,  \
+                          0, as_stream(stream));                                                                  \
+  }
+
+KVHIP_LIST(float, 4)
+KVHIP_LIST(u16, 2)
+#undef KVHIP_LIST
+
+static int list2(int scatter, const void* memory_tensor, const void* kvcache0, const void* kvcache1,
+                 const int64_t* slot_mapping, int64_t memory_tokens, int64_t num_tokens, int64_t skip_prefix,
+                 int64_t num_blocks, int64_t block_size, int64_t num_heads, int64_t head_size, void* stream) {
+  const int64_t plane_bytes = num_blocks * block_size * num_heads * head_size * 2;
+  const uint64_t planes[4] = {addr(kvcache0, 0), addr(kvcache1, 0), addr(kvcache0, plane_bytes),
+                              addr(kvcache1, plane_bytes)};
+  const int64_t axes[4] = {0, 0, 1, 1}, layers[4] = {0, 1, 0, 1};
+  return lmcache_planes(scatter, 2, memory_tensor, planes, axes, layers, 4, slot_mapping, 2, memory_tokens,
+                        num_tokens, skip_prefix, num_blocks, block_size, num_heads * head_size, 0,
+                        as_stream(stream));
+}
+
+int lmcache_kv_buffer_to_paged_list2_u16(const void* memory_tensor, void* kvcache0, void* kvcache1,
+                                         const int64_t* slot_mapping, int64_t memory_tokens, int64_t num_tokens,
+                                         int64_t skip_prefix, int64_t num_blocks, int64_t block_size,
+                                         int64_t num_heads, int64_t head_size, void* stream) {
+  return list2(1, memory_tensor, kvcache0, kvcache1, slot_mapping, memory_tokens, num_tokens, skip_prefix,
+               num_blocks, block_size, num_heads, head_size, stream);
+}
+
+int lmcache_paged_to_kv_buffer_list2_u16(void* memory_tensor, const void* kvcache0, const void* kvcache1,
+                                         const int64_t* slot_mapping, int64_t memory_tokens, int64_t num_tokens,
+                                         int64_t skip_prefix, int64_t num_blocks, int64_t block_size,
+                                         int64_t num_heads, int64_t head_size, void* stream) {
+  return list2(0, memory_tensor, kvcache0, kvcache1, slot_mapping, memory_tokens, num_tokens, skip_prefix,
+               num_blocks, block_size, num_heads, head_size, stream);
+}
+
+// ----- LMCache MLA list caches [NB, BS, HS] <-> [1, NL, M, HS] (lmcache_kv_transfer.py:920-950) -----
+
+#define KVHIP_MLA_LIST(SUFFIX, ELT)                                                                               \
+  int lmcache_mla_buffer_to_paged_list_##SUFFIX(const void* memory_tensor, void* kvcache,                         \
+                                                const int64_t* slot_mapping, int64_t layer_index,                 \
+                                                int64_t memory_tokens, int64_t num_tokens, int64_t skip_prefix,   \
+                                                int64_t num_blocks, int64_t block_size, int64_t head_size,        \
+                                                void* stream) {                                                   \
+    const uint64_t plane = addr(kvcache, 0);                                                                      \
+    const int64_t axis = 0;                                                                                       \
+    return lmcache_planes(1, ELT, memory_tensor, &plane, &axis, &layer_index, 1, slot_mapping, 1, memory_tokens,  \
+                          num_tokens, skip_prefix, num_blocks, block_size, head_size, 0, as_stream(stream));      \
+  }                                                                                                               \
+  int lmcache_mla_paged_to_buffer_list_##SUFFIX(void* memory_tensor, const void* kvcache,                         \
+                                                const int64_t* slot_mapping, int64_t layer_index,                 \
+                                                int64_t memory_tokens, int64_t num_tokens, int64_t num_blocks,    \
+                                                int64_t block_size, int64_t head_size, void* stream) {            \
+    const uint64_t plane = addr(kvcache, 0);                                                                      \
+    const int64_t axis = 0;                                                                                       \
+    return lmcache_planes(0, ELT, memory_tensor, &plane, &axis, &layer_index, 1, slot_mapping, 1, memory_tokens,  \
+                          num_tokens, 0, num_blocks, block_size, head_size, 0, as_stream(stream));                \
+  }
+
+KVHIP_MLA_LIST(float, 4)
+KVHIP_MLA_LIST(half, 2)
+KVHIP_MLA_LIST(bfloat16, 2)
+KVHIP_MLA_LIST(u16, 2)
+#undef KVHIP_MLA_LIST
+
+// ----- DSV4 opaque byte rows (kv_transfer.py:4209-4406) --------------------------------------------
+
+int musa_aiter_kv_copy_paged_rows_u8(const void* src, void* dst, const int64_t* src_indices,
+                                     const int64_t* dst_indices, int64_t num_rows, int64_t item_bytes,
+                                     int64_t src_num_rows, int64_t dst_num_rows, void* stream) {
+  const uint64_t s = addr(src, 0), d = addr(dst, 0);
+  return musa_aiter_hip_copy_rows(&s, &d, nullptr, nullptr, 1, src_indices, dst_indices, num_rows, num_rows, 0, 0,
+                                  src_num_rows, dst_num_rows, item_bytes, item_bytes, item_bytes, 0, 1, stream);
+}
+
+int musa_aiter_kv_copy_paged_rows_layer_table_u8(const uint64_t* src_ptr_table, const uint64_t* dst_ptr_table,
+                                                 const int64_t* src_indices, const int64_t* dst_indices,
+                                                 int64_t num_rows, int64_t item_bytes, int64_t num_layers,
+                                                 int64_t src_num_rows, int64_t dst_num_rows, void* stream) {
+  return musa_aiter_hip_copy_rows(nullptr, nullptr, src_ptr_table, dst_ptr_table, num_layers, src_indices,
+                                  dst_indices, num_rows, num_rows, 0, 0, src_num_rows, dst_num_rows, item_bytes,
+                                  item_bytes, item_bytes, 0, 1, stream);
+}
+
+int musa_aiter_kv_copy_paged_rows_contig_layers_u8(const void* src_base, void* dst_base, const int64_t* src_indices,
+                                                   const int64_t* dst_indices, int64_t num_rows, int64_t item_bytes,
+                                                   int64_t num_layers, int64_t src_num_rows, int64_t dst_num_rows,
+                                                   void* stream) {
+  if (num_layers <= 0) return hipSuccess;
+  std::vector<uint64_t> s(num_layers), d(num_layers);
+  for (int64_t l = 0; l < num_layers; ++l) {
+    s[l] = addr(src_base, l * src_num_rows * item_bytes);
+    d[l] = addr(dst_base, l * dst_num_rows * item_bytes);
+  }
+  return musa_aiter_hip_copy_rows(s.data(), d.data(), nullptr, nullptr, num_layers, src_indices, dst_indices,
+                                  num_rows, num_rows, 0, 0, src_num_rows, dst_num_rows, item_bytes, item_bytes,
+                                  item_bytes, 0, 1, stream);
+}
+
+// ----- LMCache DSV4 strided block transfer (lmcache_kv_transfer.py:1355-1400) ----------------------
+
+int lmcache_kv_strided_block_transfer(void* staging, const uint64_t* paged_ptrs, const int64_t* block_ids,
+                                      int64_t direction, int64_t num_layers, int64_t idx_start, int64_t n_valid,
+                                      int64_t offset_in_object, int64_t staging_tokens, int64_t block_size,
+                                      int64_t row_bytes, int64_t paged_block_stride, int64_t mode,
+                                      int64_t value_bytes, int64_t scale_bytes, void* stream) {
+  kvhip::StridedBlockParams p{};
+  p.staging = static_cast<uint8_t*>(staging);
+  p.paged_ptrs = paged_ptrs;
+  p.block_ids = block_ids;
+  p.direction = direction;
+  p.num_layers = num_layers;
+  p.idx_start = idx_start;
+  p.n_valid = n_valid;
+  p.offset_in_object = offset_in_object;
+  p.staging_tokens = staging_tokens;
+  p.block_size = block_size;
+  p.row_bytes = row_bytes;
+  p.paged_block_stride = paged_block_stride;
+  p.mode = mode;
+  p.value_bytes = value_bytes;
+  p.scale_bytes = scale_bytes;
+  return kvhip::launch_strided_blocks(p, as_stream(stream));
+}
+
+}  // extern "C"

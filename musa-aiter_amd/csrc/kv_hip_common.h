@@ -1,0 +1,214 @@
+// Shared device helpers for the MI355X (gfx950) KV-cache movement kernels.
+//
+// Everything here is written for CDNA4 wave64 execution: 64-lane ballots,
+// 16-byte global_load/store_dwordx4 payload moves and scalar (wave-uniform)
+// slot resolution.  No MFMA is used: the path is a bandwidth-bound copy.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kvhip {
+
+constexpr int kWave = 64;
+constexpr int kWavesPerBlock = 4;
+constexpr int kBlockThreads = kWave * kWavesPerBlock;
+
+using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------
+// Vector memory helpers.  The payload is streamed exactly once, so the loads
+// and stores are tagged non-temporal: they bypass the MALL/L2 retention
+// policy that would otherwise evict the slot tables and claim arrays.
+// ---------------------------------------------------------------------------
+template <int VEC>
+struct VecType;
+template <>
+struct VecType<16> { using T = u32x4; };
+template <>
+struct VecType<8> { using T = u32x2; };
+template <>
+struct VecType<4> { using T = uint32_t; };
+template <>
+struct VecType<2> { using T = uint16_t; };
+template <>
+struct VecType<1> { using T = uint8_t; };
+
+template <int VEC>
+__device__ __forceinline__ typename VecType<VEC>::T ldv(const uint8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const typename VecType<VEC>::T*>(p));
+}
+
+template <int VEC>
+__device__ __forceinline__ void stv(uint8_t* p, typename VecType<VEC>::T v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<typename VecType<VEC>::T*>(p));
+}
+
+__device__ __forceinline__ u32x4 ld16(const uint8_t* p) { return ldv<16>(p); }
+__device__ __forceinline__ void st16(uint8_t* p, u32x4 v) { stv<16>(p, v); }
+
+// ---------------------------------------------------------------------------
+// Wave-level helpers (wave64).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
+
+__device__ __forceinline__ int wave_in_block() {
+  return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+}
+
+__device__ __forceinline__ uint64_t ballot(bool pred) {
+  return static_cast<uint64_t>(__ballot(pred));
+}
+
+__device__ __forceinline__ int64_t readlane64(int64_t v, int lane) {
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(v), lane);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32), lane);
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Value of a 64-bit per-lane quantity held by lane (lane_id - 1); lane 0 gets its own.
+__device__ __forceinline__ int64_t from_prev_lane(int64_t v) {
+  return __shfl_up(static_cast<long long>(v), 1);
+}
+
+// ---------------------------------------------------------------------------
+// Claim tags for last-writer-wins scatter.  A scatter that may see duplicate
+// destination slots first records, per destination slot, the largest
+// (epoch, token+1) pair among the tokens targeting it; only the token whose
+// tag survives writes.  The epoch advances per call so the array never needs
+// clearing between calls on one stream.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t claim_tag(uint32_t epoch, int64_t token) {
+  return (static_cast<uint64_t>(epoch) << 32) | static_cast<uint64_t>(token + 1);
+}
+
+// ---------------------------------------------------------------------------
+// 16-bit element access inside a 16-byte register vector.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t half_of(uint32_t w, int hi) { return hi ? (w >> 16) : (w & 0xFFFFu); }
+
+__device__ __forceinline__ uint32_t elem16(const u32x4& v, int idx) {
+  return half_of(v[idx >> 1], idx & 1);
+}
+
+__device__ __forceinline__ uint32_t elem8(const u32x4& v, int idx) {
+  return (v[idx >> 2] >> (8 * (idx & 3))) & 0xFFu;
+}
+
+// Pack the 16-bit lanes `lo` (bits 0..15 used) and `hi` into one dword.
+__device__ __forceinline__ uint32_t pack16(uint32_t lo, uint32_t hi) { return (lo & 0xFFFFu) | (hi << 16); }
+
+// ---------------------------------------------------------------------------
+// Floating-point conversions with the exact rounding torch uses on the CPU:
+// bf16 and fp16 are produced round-to-nearest-even; widening is exact.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t b) {
+  _Float16 h = __builtin_bit_cast(_Float16, static_cast<uint16_t>(b));
+  return static_cast<float>(h);
+}
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;  // canonical quiet NaN, as c10::BFloat16
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  const _Float16 h = static_cast<_Float16>(f);
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h));
+}
+
+// Linear-side element types for the FP8 codec paths.
+enum LinDtype : int { kLinF32 = 0, kLinF16 = 1, kLinBF16 = 2 };
+
+template <int LDT>
+__device__ __forceinline__ float lin_to_f32(uint32_t bits) {
+  if constexpr (LDT == kLinBF16) return bf16_bits_to_f32(bits);
+  else if constexpr (LDT == kLinF16) return f16_bits_to_f32(bits);
+  else return __uint_as_float(bits);
+}
+
+template <int LDT>
+__device__ __forceinline__ uint32_t f32_to_lin(float f) {
+  if constexpr (LDT == kLinBF16) return f32_to_bf16_bits(f);
+  else if constexpr (LDT == kLinF16) return f32_to_f16_bits(f);
+  else return __float_as_uint(f);
+}
+
+// ---------------------------------------------------------------------------
+// FP8 codec with the reference's exact rules (musa_aiter/ops/kv_transfer.py
+// :2161-2200, the PyTorch implementation, not its MUSA kernels):
+//   * w = x / scale (IEEE fp32 division, round to nearest even);
+//   * sign = (w < 0); non-finite w encodes as a signed-by-`w<0` zero;
+//   * |w| is clamped to (2 - 2^-M) * 2^Emax  (E4M3 480, E5M2 114688);
+//   * |w| below 2^(1-bias) flushes to a signed zero (no subnormals);
+//   * the mantissa is rounded half-to-even, carrying into the exponent.
+// Decoding maps exponent field 0 to a signed zero and every other code to
+// (1 + m/2^M) * 2^(E-bias), including the all-ones patterns.
+// ---------------------------------------------------------------------------
+enum Codec : int { kCopy = 0, kE4M3 = 1, kE5M2 = 2 };
+
+template <int CODEC>
+struct Fp8Fmt;
+
+template <>
+struct Fp8Fmt<kE4M3> {
+  static constexpr int kMant = 3;
+  static constexpr uint32_t kMaxBits = 0x43F00000u;     // 480.0f
+  static constexpr uint32_t kMinNormBits = 0x3C800000u; // 2^-6
+  static constexpr int kShift = 23 - kMant;             // 20
+  static constexpr uint32_t kExpOffset = 127 - 7;       // fp32 bias - fp8 bias
+  static constexpr uint32_t kExpMask = 0x78u;
+};
+
+template <>
+struct Fp8Fmt<kE5M2> {
+  static constexpr int kMant = 2;
+  static constexpr uint32_t kMaxBits = 0x47E00000u;     // 114688.0f
+  static constexpr uint32_t kMinNormBits = 0x38800000u; // 2^-14
+  static constexpr int kShift = 23 - kMant;             // 21
+  static constexpr uint32_t kExpOffset = 127 - 15;
+  static constexpr uint32_t kExpMask = 0x7Cu;
+};
+
+// Encode w (already the correctly rounded quotient x/scale) to an FP8 byte.
+template <int CODEC>
+__device__ __forceinline__ uint32_t fp8_encode(float w) {
+  using F = Fp8Fmt<CODEC>;
+  const uint32_t bits = __float_as_uint(w);
+  const uint32_t sign = (w < 0.0f) ? 0x80u : 0u;
+  uint32_t a = bits & 0x7FFFFFFFu;
+  const bool normal = (a >= F::kMinNormBits) && (a < 0x7F800000u);
+  a = a < F::kMaxBits ? a : F::kMaxBits;
+  const uint32_t lsb = (a >> F::kShift) & 1u;
+  // Round the fp32 mantissa to kMant bits (half to even) and re-bias the
+  // exponent in one add: the carry out of the mantissa lands in the exponent.
+  const uint32_t body =
+      (a + ((1u << (F::kShift - 1)) - 1u) + lsb - (F::kExpOffset << 23)) >> F::kShift;
+  return sign | (normal ? body : 0u);
+}
+
+template <int CODEC>
+__device__ __forceinline__ float fp8_decode(uint32_t byte) {
+  using F = Fp8Fmt<CODEC>;
+  uint32_t bits = ((byte & 0x7Fu) << F::kShift) + (F::kExpOffset << 23);
+  bits = (byte & F::kExpMask) ? bits : 0u;
+  bits |= (byte & 0x80u) << 24;
+  return __uint_as_float(bits);
+}
+
+// Division x / s rounded to nearest even, as torch's CPU `/` on float32.
+// The default HIP compilation mode emits the correctly rounded
+// v_div_scale/v_div_fmas/v_div_fixup sequence for this operator.
+__device__ __forceinline__ float div_rn(float x, float s) { return x / s; }
+
+}  // namespace kvhip

@@ -1,0 +1,94 @@
+// Host-side launcher interfaces shared by the kernel translation units and
+// the C-ABI layer.  Nothing here is exported from the shared library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kvhip {
+
+constexpr int kMaxPlanes = 128;
+
+// Paged-A layout [NL, NB, NH, HD, BS] (block_size innermost) <-> token-major
+// linear rows.  K and V are the two planes of every layer.
+struct PagedTileParams {
+  int scatter;         // 0: paged -> linear (gather), 1: linear -> paged (scatter)
+  int codec;           // Codec: copy, fp8 e4m3, fp8 e5m2
+  int cache_elt;       // bytes per cache element (1 for fp8 codecs)
+  int lin_elt;         // bytes per linear element
+  int lin_dtype;       // LinDtype, used by the fp8 codecs
+  void* cache[2];      // K, V caches (layer 0)
+  void* lin[2];        // K, V linear bases (layer 0, token 0)
+  const int64_t* slots;
+  int64_t num_layers;
+  int64_t num_tokens;
+  int64_t num_blocks;
+  int64_t num_heads;
+  int64_t head_dim;
+  int64_t block_size;
+  int64_t lin_token_stride;  // bytes
+  int64_t lin_layer_stride;  // bytes
+  const float* scale[2];
+  int scale_mode;            // 0 scalar, 1 [NH], 2 [NL, NH]
+  int fill_zeros;            // gather: write zeros for skipped tokens
+  const uint64_t* owner;     // scatter claim tags (nullable)
+  uint32_t epoch;
+};
+
+hipError_t launch_paged_tiles(const PagedTileParams& p, hipStream_t stream);
+
+// Row copies between two row-addressed planes: token-major caches
+// ([NB, BS, ...] slot rows), linear buffers and opaque byte rows.  Either side
+// is addressed directly (row = token + offset) or through an index vector.
+struct RowCopyParams {
+  const uint64_t* src_planes;   // host array (nullable when src_table is set)
+  const uint64_t* dst_planes;
+  const uint64_t* src_table;    // device array of plane bases (nullable)
+  const uint64_t* dst_table;
+  int64_t num_planes;
+  const int64_t* src_idx;       // device (nullable => direct)
+  const int64_t* dst_idx;
+  int64_t num_tokens;           // index entries
+  int64_t num_rows_out;         // >= num_tokens for a direct, zero-filled tail
+  int64_t src_offset;
+  int64_t dst_offset;
+  int64_t src_rows;             // valid row range of each side
+  int64_t dst_rows;
+  int64_t row_bytes;
+  int64_t src_stride;           // bytes between rows
+  int64_t dst_stride;
+  int zero_invalid;             // direct destination: zero rows whose source is skipped
+  const uint64_t* owner;        // claim tags over destination rows (nullable)
+  uint32_t epoch;
+};
+
+hipError_t launch_row_copy(const RowCopyParams& p, hipStream_t stream);
+
+// Marks, for every destination row named by `idx`, the last token (in token
+// order) that targets it.
+hipError_t launch_claim(const int64_t* idx, int64_t n, int64_t rows, uint64_t* owner, uint32_t epoch,
+                        hipStream_t stream);
+hipError_t launch_fill_u64(uint64_t* p, int64_t n, uint64_t value, hipStream_t stream);
+
+// Block-granular byte copies between an LMCache staging object and padded pages.
+struct StridedBlockParams {
+  uint8_t* staging;
+  const uint64_t* paged_ptrs;   // host array, num_layers entries
+  const int64_t* block_ids;
+  int64_t direction;            // 0: staging -> pages, 1: pages -> staging
+  int64_t num_layers;
+  int64_t idx_start;
+  int64_t n_valid;
+  int64_t offset_in_object;
+  int64_t staging_tokens;
+  int64_t block_size;
+  int64_t row_bytes;
+  int64_t paged_block_stride;
+  int64_t mode;                 // 0 plain rows, 1 values block then scales block
+  int64_t value_bytes;
+  int64_t scale_bytes;
+};
+
+hipError_t launch_strided_blocks(const StridedBlockParams& p, hipStream_t stream);
+
+}  // namespace kvhip

@@ -1,0 +1,330 @@
+// Row-granular KV transfers for MI355X (gfx950).
+//
+// Every token-major layout of the path reduces to "copy one row of R bytes
+// per (plane, token)": SGLang-MP split caches [NB, BS, NH, HS] <-> LMCache
+// [2, NL, T, NH*HS] buffers, the per-layer list and legacy 6-D caches, the
+// MLA latent rows [NB, BS, D] and the opaque DSV4 byte rows.  One side of the
+// copy is indexed by a slot/row vector (or both, for byte rows); slot < 0
+// skips the token.
+//
+// One wave owns one token.  Its source and destination rows are resolved once
+// (scalar loads) and the wave streams the row of every plane in its plane
+// group with VEC-byte vectors, U vectors in flight per lane.  Skipped tokens
+// of a directly addressed destination are zero filled; an indexed destination
+// can be protected by claim tags so duplicate slots keep last-writer-wins.
+#include "kv_hip_common.h"
+#include "kv_launch.h"
+
+namespace kvhip {
+
+struct RowArgs {
+  uint64_t src_planes[kMaxPlanes];
+  uint64_t dst_planes[kMaxPlanes];
+  const uint64_t* src_table;
+  const uint64_t* dst_table;
+  const int64_t* src_idx;
+  const int64_t* dst_idx;
+  const uint64_t* owner;
+  int64_t num_tokens;
+  int64_t num_rows_out;
+  int64_t src_offset;
+  int64_t dst_offset;
+  int64_t src_rows;
+  int64_t dst_rows;
+  int64_t row_bytes;
+  int64_t src_stride;
+  int64_t dst_stride;
+  int32_t plane_base;       // first plane of this launch in the table arrays
+  int32_t num_planes;       // planes in this launch
+  int32_t planes_per_wave;
+  int32_t zero_invalid;
+  uint32_t epoch;
+};
+
+constexpr int kRowUnroll = 4;
+
+template <int VEC>
+__global__ __launch_bounds__(kBlockThreads) void row_copy_kernel(const RowArgs a) {
+  using V = typename VecType<VEC>::T;
+  const int lane = lane_id();
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();
+  if (u >= a.num_rows_out) return;
+  const int p0 = static_cast<int>(blockIdx.y) * a.planes_per_wave;
+  if (p0 >= a.num_planes) return;
+  const int np = (a.num_planes - p0) < a.planes_per_wave ? (a.num_planes - p0) : a.planes_per_wave;
+
+  int64_t srow = -1;
+  int64_t drow = u + a.dst_offset;
+  bool valid = false;
+  if (u < a.num_tokens) {
+    srow = a.src_idx ? a.src_idx[u] : u + a.src_offset;
+    if (a.dst_idx) drow = a.dst_idx[u];
+    valid = srow >= 0 && srow < a.src_rows && drow >= 0 && drow < a.dst_rows;
+    if (valid && a.owner != nullptr) valid = (a.owner[drow] == claim_tag(a.epoch, u));
+  }
+  srow = uniform64(srow);
+  drow = uniform64(drow);
+  valid = __builtin_amdgcn_readfirstlane(static_cast<int>(valid)) != 0;
+
+  const int chunks = static_cast<int>(a.row_bytes / VEC);
+  const int iters_per_plane = (chunks + kWave - 1) / kWave;
+  const int iters = np * iters_per_plane;
+
+  if (!valid) {
+    // Only a directly addressed destination row inside its extent is cleared.
+    if (!a.zero_invalid || a.dst_idx != nullptr || drow < 0 || drow >= a.dst_rows) return;
+    const V zero{};
+    for (int it = 0; it < iters; ++it) {
+      const int p = it / iters_per_plane;
+      const int c = (it - p * iters_per_plane) * kWave + lane;
+      const int pp = a.plane_base + p0 + p;
+      uint8_t* const dp = reinterpret_cast<uint8_t*>(a.dst_table ? a.dst_table[pp] : a.dst_planes[pp - a.plane_base]);
+      if (c < chunks) stv<VEC>(dp + drow * a.dst_stride + static_cast<int64_t>(c) * VEC, zero);
+    }
+    return;
+  }
+
+  for (int it0 = 0; it0 < iters; it0 += kRowUnroll) {
+    V v[kRowUnroll];
+#pragma unroll
+    for (int k = 0; k < kRowUnroll; ++k) {
+      const int it = it0 + k;
+      if (it < iters) {
+        const int p = it / iters_per_plane;
+        const int c = (it - p * iters_per_plane) * kWave + lane;
+        const int pp = a.plane_base + p0 + p;
+        const uint8_t* const sp =
+            reinterpret_cast<const uint8_t*>(a.src_table ? a.src_table[pp] : a.src_planes[pp - a.plane_base]);
+        if (c < chunks) v[k] = ldv<VEC>(sp + srow * a.src_stride + static_cast<int64_t>(c) * VEC);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kRowUnroll; ++k) {
+      const int it = it0 + k;
+      if (it < iters) {
+        const int p = it / iters_per_plane;
+        const int c = (it - p * iters_per_plane) * kWave + lane;
+        const int pp = a.plane_base + p0 + p;
+        uint8_t* const dp = reinterpret_cast<uint8_t*>(a.dst_table ? a.dst_table[pp] : a.dst_planes[pp - a.plane_base]);
+        if (c < chunks) stv<VEC>(dp + drow * a.dst_stride + static_cast<int64_t>(c) * VEC, v[k]);
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kBlockThreads) void claim_kernel(const int64_t* idx, int64_t n, int64_t rows,
+                                                              uint64_t* owner, uint32_t epoch) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int64_t s = idx[i];
+  if (s < 0 || s >= rows) return;
+  atomicMax(reinterpret_cast<unsigned long long*>(owner + s), static_cast<unsigned long long>(claim_tag(epoch, i)));
+}
+
+__global__ __launch_bounds__(kBlockThreads) void fill_u64_kernel(uint64_t* p, int64_t n, uint64_t value) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    p[i] = value;
+}
+
+// ----- strided block transfer ------------------------------------------------------
+// Staging [NL, staging_tokens, row_bytes] <-> per-layer pages addressed by block
+// id.  Mode 0 pages hold plain rows at block*stride + t*row_bytes; mode 1 pages
+// hold all value parts first (t*value_bytes) then all scale parts
+// (bs*value_bytes + t*scale_bytes).  Semantics follow the reference kernel text
+// csrc/kvcache/kv_transfer_float.mu:3281-3358 (there is no Python reference).
+struct StridedArgs {
+  uint64_t layers[kMaxPlanes];
+  uint8_t* staging;
+  const int64_t* block_ids;
+  int64_t direction;
+  int64_t idx_start;
+  int64_t offset_in_object;
+  int64_t staging_tokens;
+  int64_t block_size;
+  int64_t row_bytes;
+  int64_t paged_block_stride;
+  int64_t mode;
+  int64_t value_bytes;
+  int64_t scale_bytes;
+  int64_t n_valid;
+};
+
+template <int VEC>
+__global__ __launch_bounds__(kBlockThreads) void strided_block_kernel(const StridedArgs a) {
+  const int64_t p = blockIdx.x;
+  const int layer = static_cast<int>(blockIdx.y);
+  if (p >= a.n_valid) return;
+  const int64_t blk = a.block_ids[a.idx_start + p];
+  uint8_t* const page = reinterpret_cast<uint8_t*>(a.layers[layer]) + blk * a.paged_block_stride;
+  uint8_t* const stage =
+      a.staging + ((static_cast<int64_t>(layer) * a.staging_tokens) + a.offset_in_object + p * a.block_size) * a.row_bytes;
+  if (a.mode == 0) {
+    // Rows of one block are contiguous on both sides.
+    const int64_t n = a.block_size * a.row_bytes / VEC;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+      if (a.direction == 0) stv<VEC>(page + i * VEC, ldv<VEC>(stage + i * VEC));
+      else stv<VEC>(stage + i * VEC, ldv<VEC>(page + i * VEC));
+    }
+    return;
+  }
+  const int64_t row_words = a.row_bytes / VEC;
+  const int64_t value_words = a.value_bytes / VEC;
+  const int64_t n = a.block_size * row_words;
+  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+    const int64_t t = i / row_words;
+    const int64_t w = i - t * row_words;
+    uint8_t* const sp = stage + t * a.row_bytes + w * VEC;
+    uint8_t* const pp = (w < value_words)
+                            ? page + t * a.value_bytes + w * VEC
+                            : page + a.block_size * a.value_bytes + t * a.scale_bytes + (w - value_words) * VEC;
+    if (a.direction == 0) stv<VEC>(pp, ldv<VEC>(sp));
+    else stv<VEC>(sp, ldv<VEC>(pp));
+  }
+}
+
+// ----- host launchers -----------------------------------------------------------------
+
+namespace {
+
+int vec_for(uint64_t bits) {
+  if ((bits & 15u) == 0) return 16;
+  if ((bits & 7u) == 0) return 8;
+  if ((bits & 3u) == 0) return 4;
+  if ((bits & 1u) == 0) return 2;
+  return 1;
+}
+
+template <int VEC>
+hipError_t launch_rows_vec(const RowArgs& a, int64_t plane_groups, hipStream_t stream) {
+  const int64_t blocks = (a.num_rows_out + kWavesPerBlock - 1) / kWavesPerBlock;
+  hipLaunchKernelGGL(row_copy_kernel<VEC>, dim3(static_cast<uint32_t>(blocks), static_cast<uint32_t>(plane_groups)),
+                     dim3(kBlockThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_row_copy(const RowCopyParams& p, hipStream_t stream) {
+  if (p.num_rows_out <= 0 || p.num_planes <= 0 || p.row_bytes <= 0) return hipSuccess;
+  if (p.num_rows_out > (int64_t{1} << 32)) return hipErrorInvalidValue;
+  if (p.row_bytes > (int64_t{1} << 30)) return hipErrorInvalidValue;
+  const bool src_host = p.src_table == nullptr;
+  const bool dst_host = p.dst_table == nullptr;
+  if ((src_host && p.src_planes == nullptr) || (dst_host && p.dst_planes == nullptr)) return hipErrorInvalidValue;
+
+  // Vector width: the largest power of two dividing the row size, both
+  // strides and every plane base known on the host.
+  uint64_t bits = static_cast<uint64_t>(p.row_bytes) | static_cast<uint64_t>(p.src_stride) |
+                  static_cast<uint64_t>(p.dst_stride);
+  for (int64_t i = 0; i < p.num_planes; ++i) {
+    if (src_host) bits |= p.src_planes[i];
+    if (dst_host) bits |= p.dst_planes[i];
+  }
+  // Device-resident tables: their bases are not visible here, so only byte
+  // granularity is assumed unless the rows themselves force a finer width.
+  if (!src_host || !dst_host) bits |= 1u;
+  const int vec = vec_for(bits);
+
+  const int64_t chunks = p.row_bytes / vec;
+  // Plane group per wave: enough work per wave (>= ~16 KB) without starving
+  // the grid of waves.
+  int ppw = static_cast<int>((16384 + p.row_bytes - 1) / p.row_bytes);
+  if (ppw < 1) ppw = 1;
+  if (ppw > 16) ppw = 16;
+  (void)chunks;
+
+  for (int64_t base = 0; base < p.num_planes; base += kMaxPlanes) {
+    const int64_t n = (p.num_planes - base) < kMaxPlanes ? (p.num_planes - base) : kMaxPlanes;
+    RowArgs a{};
+    for (int64_t i = 0; i < n; ++i) {
+      a.src_planes[i] = src_host ? p.src_planes[base + i] : 0;
+      a.dst_planes[i] = dst_host ? p.dst_planes[base + i] : 0;
+    }
+    a.src_table = p.src_table;
+    a.dst_table = p.dst_table;
+    a.src_idx = p.src_idx;
+    a.dst_idx = p.dst_idx;
+    a.owner = p.owner;
+    a.num_tokens = p.num_tokens;
+    a.num_rows_out = p.num_rows_out;
+    a.src_offset = p.src_offset;
+    a.dst_offset = p.dst_offset;
+    a.src_rows = p.src_rows;
+    a.dst_rows = p.dst_rows;
+    a.row_bytes = p.row_bytes;
+    a.src_stride = p.src_stride;
+    a.dst_stride = p.dst_stride;
+    a.plane_base = static_cast<int32_t>(base);
+    a.num_planes = static_cast<int32_t>(n);
+    a.planes_per_wave = ppw < n ? ppw : static_cast<int32_t>(n);
+    a.zero_invalid = p.zero_invalid;
+    a.epoch = p.epoch;
+    const int64_t groups = (n + a.planes_per_wave - 1) / a.planes_per_wave;
+    hipError_t err;
+    switch (vec) {
+      case 16: err = launch_rows_vec<16>(a, groups, stream); break;
+      case 8: err = launch_rows_vec<8>(a, groups, stream); break;
+      case 4: err = launch_rows_vec<4>(a, groups, stream); break;
+      case 2: err = launch_rows_vec<2>(a, groups, stream); break;
+      default: err = launch_rows_vec<1>(a, groups, stream); break;
+    }
+    if (err != hipSuccess) return err;
+  }
+  return hipSuccess;
+}
+
+hipError_t launch_claim(const int64_t* idx, int64_t n, int64_t rows, uint64_t* owner, uint32_t epoch,
+                        hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  const int64_t blocks = (n + kBlockThreads - 1) / kBlockThreads;
+  hipLaunchKernelGGL(claim_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kBlockThreads), 0, stream, idx, n, rows,
+                     owner, epoch);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_u64(uint64_t* p, int64_t n, uint64_t value, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  int64_t blocks = (n + kBlockThreads - 1) / kBlockThreads;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(fill_u64_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kBlockThreads), 0, stream, p, n,
+                     value);
+  return hipGetLastError();
+}
+
+hipError_t launch_strided_blocks(const StridedBlockParams& p, hipStream_t stream) {
+  if (p.n_valid <= 0 || p.num_layers <= 0 || p.num_layers > kMaxPlanes || p.block_size <= 0 ||
+      p.staging_tokens <= 0 || p.row_bytes <= 0 || (p.row_bytes & 3) != 0 || p.paged_block_stride <= 0)
+    return hipErrorInvalidValue;
+  if (p.mode != 0 && (p.value_bytes <= 0 || p.scale_bytes <= 0 || (p.value_bytes & 3) != 0 ||
+                      (p.scale_bytes & 3) != 0 || p.value_bytes + p.scale_bytes != p.row_bytes))
+    return hipErrorInvalidValue;
+  if (p.n_valid > 0x7FFFFFFF) return hipErrorInvalidValue;
+  StridedArgs a{};
+  uint64_t bits = reinterpret_cast<uint64_t>(p.staging) | static_cast<uint64_t>(p.row_bytes) |
+                  static_cast<uint64_t>(p.paged_block_stride);
+  for (int64_t i = 0; i < p.num_layers; ++i) {
+    a.layers[i] = p.paged_ptrs[i];
+    bits |= p.paged_ptrs[i];
+  }
+  if (p.mode != 0) bits |= static_cast<uint64_t>(p.value_bytes) | static_cast<uint64_t>(p.scale_bytes);
+  a.staging = p.staging;
+  a.block_ids = p.block_ids;
+  a.direction = p.direction;
+  a.idx_start = p.idx_start;
+  a.offset_in_object = p.offset_in_object;
+  a.staging_tokens = p.staging_tokens;
+  a.block_size = p.block_size;
+  a.row_bytes = p.row_bytes;
+  a.paged_block_stride = p.paged_block_stride;
+  a.mode = p.mode;
+  a.value_bytes = p.value_bytes;
+  a.scale_bytes = p.scale_bytes;
+  a.n_valid = p.n_valid;
+  const dim3 grid(static_cast<uint32_t>(p.n_valid), static_cast<uint32_t>(p.num_layers));
+  if ((bits & 15u) == 0) hipLaunchKernelGGL(strided_block_kernel<16>, grid, dim3(kBlockThreads), 0, stream, a);
+  else hipLaunchKernelGGL(strided_block_kernel<4>, grid, dim3(kBlockThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace kvhip

@@ -1,0 +1,202 @@
+"""ctypes boundary to ``libmusa_aiter_kv_hip.so`` (the gfx950 HIP kernels).
+
+The library is built in-tree by ``musa-aiter_amd/build.py`` into
+``musa_aiter/_lib``.  There is no fallback: if the library is missing or a
+launch fails, the calling op raises.  torch is imported before the library is
+opened so both share torch's HIP runtime (same ``libamdhip64.so.7`` soname),
+which keeps torch's stream handles and allocations valid in the kernels.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_NAME = "libmusa_aiter_kv_hip.so"
+LIB_PATH = Path(__file__).resolve().parent.parent / "_lib" / LIB_NAME
+BACKEND = "rocm-hip"
+
+_c_void_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_u64p = ctypes.POINTER(ctypes.c_uint64)
+
+# Generic entry points used by the host layer: name -> argtypes.
+_SIGNATURES: dict[str, list] = {
+    "musa_aiter_hip_paged_tiles": [
+        _i32, _i32, _i32, _i32, _i32,            # scatter, codec, cache_elt, lin_elt, lin_dtype
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # key_cache, value_cache, key_linear, value_linear
+        _c_void_p,                               # slot_mapping
+        _i64, _i64, _i64, _i64, _i64, _i64,      # layers, tokens, blocks, heads, head_dim, block_size
+        _i64, _i64,                              # linear token / layer stride (elements)
+        _c_void_p, _c_void_p, _i32,              # k_scale, v_scale, scale_mode
+        _i32, _i32, _c_void_p,                   # fill_zeros, dedupe, stream
+    ],
+    "musa_aiter_hip_copy_rows": [
+        _u64p, _u64p, _c_void_p, _c_void_p, _i64,  # host planes, device tables, planes
+        _c_void_p, _c_void_p,                    # src_idx, dst_idx
+        _i64, _i64, _i64, _i64, _i64, _i64,      # tokens, rows_out, src_off, dst_off, src_rows, dst_rows
+        _i64, _i64, _i64,                        # row_bytes, src_stride, dst_stride
+        _i32, _i32, _c_void_p,                   # zero_invalid, dedupe, stream
+    ],
+    "lmcache_kv_strided_block_transfer": [
+        _c_void_p, _u64p, _c_void_p,
+        _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+        _c_void_p,
+    ],
+    "musa_aiter_hip_error_string": [_i32],
+    "musa_aiter_hip_backend_name": [],
+    "musa_aiter_kv_transfer_abi_version": [],
+    "native_lmcache_kv_transfer_abi_version": [],
+    "musa_aiter_fp8_kv_cache_abi_version": [],
+    "musa_aiter_dsv4_kv_copy_abi_version": [],
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+_fns: dict[str, object] = {}
+
+
+class HipBackendError(RuntimeError):
+    """Raised when the HIP library is missing or a launch reports an error."""
+
+
+def library() -> ctypes.CDLL:
+    """Load the HIP library once; raise if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise HipBackendError(
+                    f"{LIB_NAME} is not built (expected at {LIB_PATH}); "
+                    "run `python musa-aiter_amd/build.py` to compile the gfx950 kernels"
+                )
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, argtypes in _SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.argtypes = argtypes
+                if name == "musa_aiter_hip_error_string" or name == "musa_aiter_hip_backend_name":
+                    fn.restype = ctypes.c_char_p
+                else:
+                    fn.restype = ctypes.c_int
+                _fns[name] = fn
+            _lib = lib
+    return _lib
+
+
+def fn(name: str):
+    library()
+    return _fns[name]
+
+
+def is_available() -> bool:
+    try:
+        library()
+    except (HipBackendError, OSError):
+        return False
+    return True
+
+
+def check(rc: int, op: str) -> None:
+    if rc != 0:
+        msg = fn("musa_aiter_hip_error_string")(int(rc))
+        text = msg.decode() if isinstance(msg, bytes) else str(msg)
+        raise HipBackendError(f"{op}: HIP launch failed with error {rc} ({text})")
+
+
+def stream_ptr(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def u64_array(values) -> ctypes.Array:
+    vals = [int(v) for v in values]
+    return (ctypes.c_uint64 * max(1, len(vals)))(*vals)
+
+
+def paged_tiles(
+    *,
+    op: str,
+    scatter: bool,
+    codec: int,
+    cache_elt: int,
+    lin_elt: int,
+    lin_dtype: int,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    key_linear: torch.Tensor,
+    value_linear: torch.Tensor,
+    slots: torch.Tensor,
+    num_layers: int,
+    num_tokens: int,
+    num_blocks: int,
+    num_heads: int,
+    head_dim: int,
+    block_size: int,
+    lin_token_stride: int,
+    lin_layer_stride: int,
+    k_scale: torch.Tensor | None = None,
+    v_scale: torch.Tensor | None = None,
+    scale_mode: int = 0,
+    fill_zeros: bool = True,
+    dedupe: bool = True,
+) -> None:
+    if num_tokens <= 0 or num_layers <= 0:
+        return
+    device = key_cache.device
+    with torch.cuda.device(device):
+        rc = fn("musa_aiter_hip_paged_tiles")(
+            int(scatter), int(codec), int(cache_elt), int(lin_elt), int(lin_dtype),
+            ptr(key_cache), ptr(value_cache), ptr(key_linear), ptr(value_linear), ptr(slots),
+            int(num_layers), int(num_tokens), int(num_blocks), int(num_heads), int(head_dim), int(block_size),
+            int(lin_token_stride), int(lin_layer_stride),
+            ptr(k_scale), ptr(v_scale), int(scale_mode),
+            int(bool(fill_zeros)), int(bool(dedupe)), stream_ptr(device),
+        )
+    check(rc, op)
+
+
+def copy_rows(
+    *,
+    op: str,
+    device: torch.device,
+    src_planes=None,
+    dst_planes=None,
+    src_table: torch.Tensor | None = None,
+    dst_table: torch.Tensor | None = None,
+    num_planes: int,
+    src_idx: torch.Tensor | None,
+    dst_idx: torch.Tensor | None,
+    num_tokens: int,
+    num_rows_out: int,
+    src_offset: int = 0,
+    dst_offset: int = 0,
+    src_rows: int,
+    dst_rows: int,
+    row_bytes: int,
+    src_stride: int,
+    dst_stride: int,
+    zero_invalid: bool,
+    dedupe: bool = True,
+) -> None:
+    if num_rows_out <= 0 or num_planes <= 0 or row_bytes <= 0:
+        return
+    src_arr = u64_array(src_planes) if src_planes is not None else None
+    dst_arr = u64_array(dst_planes) if dst_planes is not None else None
+    with torch.cuda.device(device):
+        rc = fn("musa_aiter_hip_copy_rows")(
+            src_arr, dst_arr, ptr(src_table), ptr(dst_table), int(num_planes),
+            ptr(src_idx), ptr(dst_idx),
+            int(num_tokens), int(num_rows_out), int(src_offset), int(dst_offset), int(src_rows), int(dst_rows),
+            int(row_bytes), int(src_stride), int(dst_stride),
+            int(bool(zero_invalid)), int(bool(dedupe)), stream_ptr(device),
+        )
+    check(rc, op)

@@ -1,0 +1,63 @@
+"""The C-ABI library loads (no GPU needed) and exports every function include/*.h declares.
+
+Declarations are read from the header itself, with its declaration macros
+expanded for their dtype / format suffixes, so a symbol added to the header
+without an implementation (or renamed on one side) fails here.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import re
+
+from musa_aiter.ops import _hip
+
+HEADER = pathlib.Path(__file__).resolve().parents[1] / "include" / "musa_aiter_kv_hip.h"
+
+
+def _declared_symbols() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = text.replace("\\\n", " ")
+    macros = {}
+    for m in re.finditer(r"#define\s+(\w+)\((\w+)\)\s+(.*)", text):
+        macros[m.group(1)] = (m.group(2), m.group(3))
+    expanded = []
+    for line in text.splitlines():
+        m = re.match(r"\s*(\w+)\((\w+)\)\s*$", line)
+        if m and m.group(1) in macros:
+            param, body = macros[m.group(1)]
+            expanded.append(body.replace(f"##{param}", m.group(2)))
+        elif not line.lstrip().startswith("#"):
+            expanded.append(line)
+    body = "\n".join(expanded)
+    return set(re.findall(r"(?:int|const char\*)\s+(\w+)\s*\(", body))
+
+
+def test_header_declares_expected_families():
+    names = _declared_symbols()
+    assert len(names) == 88
+    for required in ("musa_aiter_kv_paged_to_linear_bfloat16", "musa_aiter_kv_linear_to_paged_multi_layer_half",
+                     "musa_aiter_kv_paged_fp8_to_linear_vec4_e5m2", "lmcache_paged_to_kv_buffer_two_x_nl_coalesced_u16",
+                     "lmcache_mla_paged_to_buffer_list_bfloat16", "musa_aiter_kv_copy_paged_rows_layer_table_u8",
+                     "lmcache_kv_strided_block_transfer", "musa_aiter_hip_paged_tiles"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_hip.LIB_PATH))
+    missing = sorted(name for name in _declared_symbols() if not hasattr(lib, name))
+    assert missing == []
+
+
+def test_probes_callable_without_gpu():
+    lib = ctypes.CDLL(str(_hip.LIB_PATH))
+    for name in ("musa_aiter_kv_transfer_abi_version", "native_lmcache_kv_transfer_abi_version",
+                 "musa_aiter_fp8_kv_cache_abi_version", "musa_aiter_dsv4_kv_copy_abi_version"):
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_int
+        assert fn() == 1
+    name = lib.musa_aiter_hip_backend_name
+    name.restype = ctypes.c_char_p
+    assert name() == b"rocm-hip"

@@ -1,0 +1,167 @@
+"""GPU parity: fused FP8 quant-store / dequant-gather vs the oracle, bit-exact.
+
+The linear inputs enumerate every bf16 (or fp16) bit pattern, so each test
+covers the whole input domain of the encoder for its scales, including
+subnormals, +-0, +-Inf and NaNs; scales include per-head amax/448 values and
+powers of two +-1 ulp.  Dequantised outputs are compared bit-for-bit with the
+oracle (stricter than the 1-ulp bound the path promises).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import musa_aiter
+from oracle import kv_oracle as ko
+from tests.kvgen import bits, make_slots
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+NH, HD, BS = 8, 128, 16
+LIN_DTYPES = {"bfloat16": torch.bfloat16, "float16": torch.float16, "float32": torch.float32}
+
+
+def _all_patterns(dtype: torch.dtype) -> torch.Tensor:
+    """[512, NH, HD] tensor holding every 16-bit pattern once (bf16/fp16) or a spread of fp32 values."""
+    if dtype == torch.float32:
+        gen = torch.Generator().manual_seed(0)
+        raw = torch.randint(-(2 ** 31), 2 ** 31 - 1, (512 * NH * HD,), dtype=torch.int32, generator=gen)
+        return raw.view(torch.float32).reshape(512, NH, HD)
+    raw = torch.arange(-(2 ** 15), 2 ** 15, dtype=torch.int32).to(torch.int16)
+    return raw.view(dtype).reshape(-1, NH, HD)
+
+
+def _lin_f32(x: torch.Tensor) -> np.ndarray:
+    return x.to(torch.float32).numpy()
+
+
+def _scales(kind: str, rng: np.random.Generator) -> torch.Tensor:
+    if kind == "scalar":
+        return torch.tensor(1.7 / 448.0, dtype=torch.float32)
+    if kind == "per_head":
+        vals = np.array([1.0, 0.125, 2.0 / 448.0, 50.0 / 448.0, np.nextafter(np.float32(2.0), np.float32(0.0)),
+                         np.nextafter(np.float32(0.5), np.float32(1.0)), 3.0, 7.3e-5], dtype=np.float32)
+        return torch.from_numpy(vals)
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("lin", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("scale_kind", ["scalar", "per_head"])
+def test_quant_store_then_dequant_gather_exhaustive(fmt, lin, scale_kind):
+    dtype = LIN_DTYPES[lin]
+    rng = np.random.default_rng(31)
+    x = _all_patterns(dtype)
+    tokens = x.shape[0]
+    slots, nb = make_slots("sequences", rng, block_size=BS, tokens=tokens)
+    slots[rng.random(tokens) < 0.05] = -1
+    xv = x.flip(0).contiguous()
+    ks, vs = _scales(scale_kind, rng), _scales(scale_kind, rng).flip(0).contiguous()
+    kc = torch.zeros(nb, NH, HD, BS, dtype=torch.uint8)
+    vc = torch.zeros_like(kc)
+    kc_d, vc_d = kc.to(DEV), vc.to(DEV)
+    s_d = torch.from_numpy(slots).to(DEV)
+    musa_aiter.kv_linear_to_paged_fp8(x.to(DEV), xv.to(DEV), kc_d, vc_d, s_d, ks.to(DEV), vs.to(DEV), fp8_format=fmt)
+    want_k, want_v = kc.numpy().copy(), vc.numpy().copy()
+    ko.linear_to_paged_fp8(_lin_f32(x), want_k, slots, ks.numpy(), fmt)
+    ko.linear_to_paged_fp8(_lin_f32(xv), want_v, slots, vs.numpy(), fmt)
+    got_k, got_v = kc_d.cpu().numpy(), vc_d.cpu().numpy()
+    assert np.array_equal(got_k, want_k), np.argwhere(got_k != want_k)[:5]
+    assert np.array_equal(got_v, want_v)
+    for out_name, out_dtype in LIN_DTYPES.items():
+        rk, rv = musa_aiter.kv_paged_fp8_to_linear(kc_d, vc_d, s_d, ks.to(DEV), vs.to(DEV), out_dtype=out_dtype,
+                                                   fp8_format=fmt)
+        assert np.array_equal(bits(rk), ko.paged_fp8_to_linear(want_k, slots, ks.numpy(), fmt, out_name))
+        assert np.array_equal(bits(rv), ko.paged_fp8_to_linear(want_v, slots, vs.numpy(), fmt, out_name))
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_multi_layer_layer_head_scales_and_merged(fmt):
+    layers, tokens = 3, 600
+    rng = np.random.default_rng(32)
+    slots, nb = make_slots("skips", rng, block_size=BS, tokens=tokens)
+    gen = torch.Generator().manual_seed(2)
+    kl = (torch.randn((layers, tokens, NH, HD), generator=gen) * 2.0).to(torch.bfloat16)
+    vl = (torch.randn((layers, tokens, NH, HD), generator=gen) * 2.0).to(torch.bfloat16)
+    ks = torch.rand((layers, NH), generator=gen) * 0.02 + 1e-3
+    vs = torch.rand((layers, NH), generator=gen) * 0.02 + 1e-3
+    kc = torch.zeros(layers, nb, NH, HD, BS, dtype=torch.uint8, device=DEV)
+    vc = torch.zeros_like(kc)
+    s_d = torch.from_numpy(slots).to(DEV)
+    merged = torch.stack((kl, vl), dim=2).to(DEV)
+    musa_aiter.kv_merged_linear_to_paged_fp8_multi_layer(merged, kc, vc, s_d, ks.to(DEV), vs.to(DEV), fp8_format=fmt)
+    want_k = np.zeros((layers, nb, NH, HD, BS), np.uint8)
+    want_v = np.zeros_like(want_k)
+    for layer in range(layers):
+        ko.linear_to_paged_fp8(_lin_f32(kl[layer]), want_k[layer], slots, ks.numpy(), fmt, layer=layer)
+        ko.linear_to_paged_fp8(_lin_f32(vl[layer]), want_v[layer], slots, vs.numpy(), fmt, layer=layer)
+    assert np.array_equal(kc.cpu().numpy(), want_k)
+    assert np.array_equal(vc.cpu().numpy(), want_v)
+    out = musa_aiter.kv_paged_fp8_to_merged_linear_multi_layer(kc, vc, s_d, ks.to(DEV), vs.to(DEV), fp8_format=fmt)
+    for layer in range(layers):
+        assert np.array_equal(bits(out[layer, :, 0]),
+                              ko.paged_fp8_to_linear(want_k[layer], slots, ks.numpy(), fmt, "bfloat16", layer=layer))
+        assert np.array_equal(bits(out[layer, :, 1]),
+                              ko.paged_fp8_to_linear(want_v[layer], slots, vs.numpy(), fmt, "bfloat16", layer=layer))
+
+
+def test_float8_dtype_caches_and_block_size_32():
+    bs, tokens = 32, 500
+    rng = np.random.default_rng(33)
+    slots, nb = make_slots("sequences", rng, block_size=bs, tokens=tokens)
+    gen = torch.Generator().manual_seed(3)
+    kl = torch.randn((tokens, NH, HD), generator=gen).to(torch.float16)
+    kc = torch.zeros(nb, NH, HD, bs, dtype=torch.float8_e4m3fn, device=DEV)
+    vc = torch.zeros_like(kc)
+    s_d = torch.from_numpy(slots).to(DEV)
+    musa_aiter.kv_linear_to_paged_fp8(kl.to(DEV), kl.to(DEV), kc, vc, s_d, 0.02, 0.02)
+    want = np.zeros((nb, NH, HD, bs), np.uint8)
+    ko.linear_to_paged_fp8(_lin_f32(kl), want, slots, np.float32(0.02), "e4m3")
+    assert np.array_equal(kc.view(torch.uint8).cpu().numpy(), want)
+
+
+def test_reference_fp8_roundtrip_tolerances():
+    # op_tests/test_kv_transfer.py:402-427 scenario and tolerances, on the GPU path.
+    nb, kvh, d, blk = 3, 2, 8, 4
+    t = 5
+    k_lin = torch.linspace(-1.5, 1.5, steps=t * kvh * d, dtype=torch.float32).reshape(t, kvh, d)
+    v_lin = torch.linspace(1.25, -1.25, steps=t * kvh * d, dtype=torch.float32).reshape(t, kvh, d)
+    k_cache = torch.zeros(nb, kvh, d, blk, dtype=torch.uint8, device=DEV)
+    v_cache = torch.zeros_like(k_cache)
+    slots = torch.tensor([0, 7, -1, 5, 9], dtype=torch.int32, device=DEV)
+    scale = torch.tensor(0.125, dtype=torch.float32)
+    musa_aiter.kv_linear_to_paged_fp8(k_lin.to(DEV), v_lin.to(DEV), k_cache, v_cache, slots, scale, scale)
+    rk, rv = musa_aiter.kv_paged_fp8_to_linear(k_cache, v_cache, slots, scale, scale, out_dtype=torch.float32)
+    valid = (slots >= 0).cpu()
+    torch.testing.assert_close(rk.cpu()[valid], k_lin[valid], atol=0.065, rtol=0.08)
+    torch.testing.assert_close(rv.cpu()[valid], v_lin[valid], atol=0.065, rtol=0.08)
+    assert rk.cpu()[~valid].abs().max() == 0
+
+
+def test_raw_symbol_scalar_scale_matches_api():
+    # The reference-named C symbol, bound with ctypes exactly as the reference's shim does.
+    import ctypes
+
+    from musa_aiter.ops import _hip
+
+    lib = _hip.library()
+    tokens = 100
+    rng = np.random.default_rng(34)
+    slots, nb = make_slots("sequences", rng, block_size=BS, tokens=tokens)
+    gen = torch.Generator().manual_seed(4)
+    kl = torch.randn((tokens, NH, HD), generator=gen).to(torch.bfloat16).to(DEV)
+    kc = torch.zeros(nb, NH, HD, BS, dtype=torch.uint8, device=DEV)
+    vc = torch.zeros_like(kc)
+    scale = torch.tensor(0.01, dtype=torch.float32, device=DEV)
+    s_d = torch.from_numpy(slots).to(DEV)
+    fn = lib.musa_aiter_kv_linear_to_paged_fp8_e4m3
+    fn.argtypes = [ctypes.c_void_p] * 7 + [ctypes.c_longlong] * 5 + [ctypes.c_int, ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+    rc = fn(kl.data_ptr(), kl.data_ptr(), s_d.data_ptr(), kc.data_ptr(), vc.data_ptr(), scale.data_ptr(),
+            scale.data_ptr(), tokens, nb, NH, HD, BS, 2, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    want = np.zeros((nb, NH, HD, BS), np.uint8)
+    ko.linear_to_paged_fp8(_lin_f32(kl.cpu()), want, slots, np.float32(0.01), "e4m3")
+    assert np.array_equal(kc.cpu().numpy(), want)

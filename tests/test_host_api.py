@@ -1,0 +1,206 @@
+"""Host-side contract of the public API (CPU only, no kernel launches).
+
+Mirrors the reference's error contracts (op_tests/test_kv_transfer.py:490-560,
+test_lmcache_kv_transfer.py:213-296, test_kv_copy_paged_rows*.py): validation
+raises ValueError / TypeError / IndexError before any launch, and tensors that
+are not on a ROCm device are rejected with RuntimeError instead of silently
+taking a CPU path.  Also pins the registry rows, the dispatch trace format,
+the CLI and the layout descriptors.
+"""
+
+from __future__ import annotations
+
+import subprocess
+import sys
+
+import pytest
+import torch
+
+import musa_aiter
+from musa_aiter import registry
+from musa_aiter.dispatch import DispatchRecord, emit
+
+
+def test_validation_errors_precede_device_check():
+    kc = torch.zeros(2, 1, 4, 4)
+    vc = torch.zeros(2, 1, 4, 4)
+    with pytest.raises(ValueError, match="4-D"):
+        musa_aiter.kv_paged_to_linear(torch.zeros(2, 4, 4), vc, torch.tensor([0]))
+    with pytest.raises(ValueError, match="shapes must match"):
+        musa_aiter.kv_paged_to_linear(kc, torch.zeros(2, 1, 4, 2), torch.tensor([0]))
+    with pytest.raises(ValueError, match="integer-valued"):
+        musa_aiter.kv_paged_to_linear(kc, vc, torch.tensor([0.0]))
+    with pytest.raises(ValueError, match="1-D"):
+        musa_aiter.kv_paged_to_linear(kc, vc, torch.tensor([[0]]))
+    with pytest.raises(ValueError, match="preserve requires"):
+        musa_aiter.kv_paged_to_linear(kc, vc, torch.tensor([0]), fill_skipped="preserve")
+    with pytest.raises(ValueError, match="last dims must match"):
+        musa_aiter.kv_linear_to_paged(torch.zeros(2, 1, 3), torch.zeros(2, 1, 3), kc, vc, torch.tensor([0, 1]))
+    with pytest.raises(ValueError, match="layer count mismatch"):
+        musa_aiter.kv_linear_to_paged_multi_layer(torch.zeros(3, 2, 1, 4), torch.zeros(3, 2, 1, 4),
+                                                  torch.zeros(2, 2, 1, 4, 4), torch.zeros(2, 2, 1, 4, 4),
+                                                  torch.tensor([0, 1]))
+
+
+def test_cpu_tensors_are_rejected_not_computed():
+    kc = torch.zeros(2, 1, 4, 4)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        musa_aiter.kv_paged_to_linear(kc, kc.clone(), torch.tensor([0, 3]))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        musa_aiter.kv_linear_to_paged(torch.zeros(1, 1, 4), torch.zeros(1, 1, 4), kc, kc.clone(), torch.tensor([0]))
+    caches = [[torch.zeros(1, 2, 1, 4) for _ in range(2)] for _ in range(2)]
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        musa_aiter.lmcache_kv_paged_to_buffer(caches, torch.zeros(2, 2, 2, 4), torch.tensor([0, 1]), 2, 1, 4)
+
+
+def test_fp8_validation_contract():
+    # op_tests/test_kv_transfer.py:490-519
+    k_lin = torch.zeros(2, 1, 4)
+    k_cache = torch.zeros(1, 1, 4, 2, dtype=torch.uint8)
+    slots = torch.tensor([0, 1], dtype=torch.int32)
+    for bad in (0.0, -1.0, float("inf")):
+        with pytest.raises(ValueError, match="positive and finite"):
+            musa_aiter.kv_linear_to_paged_fp8(k_lin, k_lin, k_cache, k_cache.clone(), slots, bad, 1.0)
+    with pytest.raises(ValueError, match="uint8"):
+        musa_aiter.kv_linear_to_paged_fp8(k_lin, k_lin, k_cache.float(), k_cache, slots, 1.0, 1.0)
+    with pytest.raises(ValueError, match="unsupported FP8"):
+        musa_aiter.kv_linear_to_paged_fp8(k_lin, k_lin, k_cache, k_cache, slots, 1.0, 1.0, fp8_format="bad")
+    with pytest.raises(ValueError, match=r"scalar or \[kv_heads\]"):
+        musa_aiter.kv_linear_to_paged_fp8(k_lin, k_lin, k_cache, k_cache, slots, torch.ones(3), 1.0)
+
+
+def test_slot_bounds_contract():
+    # op_tests/test_kv_transfer.py:522-560
+    kc = torch.zeros(2, 1, 4, 4)
+    with pytest.raises(ValueError, match="out of bounds"):
+        musa_aiter.kv_paged_to_linear(kc, kc.clone(), torch.tensor([0, 8]))
+    big = torch.zeros(2, 2, 1, 4, 4)
+    with pytest.raises(ValueError, match="out of bounds"):
+        musa_aiter.kv_linear_to_paged_multi_layer(torch.zeros(2, 2, 1, 4), torch.zeros(2, 2, 1, 4), big, big.clone(),
+                                                  torch.tensor([0, 13]))
+
+
+def test_lmcache_contracts():
+    # op_tests/test_lmcache_kv_transfer.py:213-241, :276-295
+    memory = torch.zeros(2, 2, 2, 4)
+    bad_layers = [[torch.zeros(1, 2, 1, 4), torch.zeros(1, 2, 1, 4)], [torch.zeros(1, 2, 1, 4)]]
+    with pytest.raises(ValueError, match="layer"):
+        musa_aiter.lmcache_kv_paged_to_buffer(bad_layers, memory, torch.tensor([0, 1]), 2, 1, 4)
+    good = [[torch.zeros(1, 2, 1, 4) for _ in range(2)] for _ in range(2)]
+    with pytest.raises(ValueError, match="int32 or int64"):
+        musa_aiter.lmcache_kv_paged_to_buffer(good, memory, torch.tensor([0.0, 1.0]), 2, 1, 4)
+    with pytest.raises(ValueError, match="transfer range"):
+        musa_aiter.lmcache_kv_buffer_to_paged_two_x_nl(memory, good, torch.tensor([0, 1]), 1, 2, 1, 4)
+    with pytest.raises(ValueError, match="out of range"):
+        musa_aiter.lmcache_kv_buffer_to_paged(torch.zeros(2, 1, 2, 4), torch.zeros(1, 2, 1, 4, 1, 4),
+                                              torch.tensor([0, 8], dtype=torch.int32))
+    with pytest.raises(ValueError, match="rank"):
+        musa_aiter.lmcache_kv_buffer_to_paged(torch.zeros(1, 2, 3), torch.zeros(1, 2, 1, 4, 1, 4), torch.tensor([0]))
+    with pytest.raises(TypeError):
+        musa_aiter.lmcache_kv_buffer_to_paged(memory, [torch.zeros(2, 1, 2, 1, 4)], torch.tensor([0, 1]), 0, 2)
+
+
+def test_byte_row_contracts():
+    src = torch.zeros(4, 8, dtype=torch.uint8)
+    with pytest.raises(TypeError):
+        musa_aiter.kv_copy_paged_rows([1], src, torch.tensor([0]), torch.tensor([0]))
+    with pytest.raises(ValueError, match="uint8"):
+        musa_aiter.kv_copy_paged_rows(src.float(), src, torch.tensor([0]), torch.tensor([0]))
+    with pytest.raises(IndexError, match="out of bounds"):
+        musa_aiter.kv_copy_paged_rows(src, src.clone(), torch.tensor([4]), torch.tensor([0]))
+    with pytest.raises(IndexError, match="negative"):
+        musa_aiter.kv_copy_paged_rows(src, src.clone(), torch.tensor([0]), torch.tensor([-1]))
+    layout = musa_aiter.InterleavedFp8Layout(value_bytes=4, scale_bytes=2, scale_granularity=2)
+    with pytest.raises(ValueError, match="layout.item_bytes"):
+        musa_aiter.kv_copy_paged_rows(src, src.clone(), torch.tensor([0]), torch.tensor([0]), layout=layout)
+    with pytest.raises(ValueError, match="direction"):
+        musa_aiter.kv_copy_paged_rows_multi_pool([], torch.tensor([0]), direction="X")
+
+
+def test_strided_block_transfer_rejects_without_launch():
+    ids = torch.zeros(4, dtype=torch.int64)
+    assert musa_aiter.lmcache_kv_strided_block_transfer(0, [0], ids, 0, 1, 0, 1, 0, 4, 2, 6, 16, 0) is False
+    assert musa_aiter.lmcache_kv_strided_block_transfer(0, [0], ids, 0, 1, 0, 1, 0, 4, 2, 8, 16, 0) is False
+
+
+def test_kvcache_registry_rows_and_backend():
+    caps = registry.list_capabilities(family="kvcache")
+    names = {c.name for c in caps}
+    assert names == {
+        "kv_paged_to_linear", "kv_linear_to_paged", "kv_paged_to_linear_multi_layer", "kv_linear_to_paged_multi_layer",
+        "kv_paged_to_merged_linear", "kv_merged_linear_to_paged", "kv_paged_to_merged_linear_multi_layer",
+        "kv_merged_linear_to_paged_multi_layer", "kv_linear_to_paged_fp8", "kv_paged_fp8_to_linear",
+        "kv_linear_to_paged_fp8_multi_layer", "kv_paged_fp8_to_linear_multi_layer", "kv_merged_linear_to_paged_fp8",
+        "kv_paged_fp8_to_merged_linear", "kv_merged_linear_to_paged_fp8_multi_layer",
+        "kv_paged_fp8_to_merged_linear_multi_layer", "kv_paged_to_mla_linear", "kv_mla_linear_to_paged",
+        "kv_paged_to_mla_linear_multi_layer", "kv_mla_linear_to_paged_multi_layer", "kv_copy_paged_rows",
+        "kv_copy_paged_rows_layer_table", "kv_copy_paged_rows_multi_pool", "lmcache_kv_paged_to_buffer_two_x_nl",
+        "lmcache_kv_buffer_to_paged_two_x_nl", "lmcache_kv_paged_to_buffer", "lmcache_kv_buffer_to_paged",
+        "lmcache_paged_to_kv_buffer", "lmcache_kv_buffer_to_paged_mla", "lmcache_paged_to_kv_buffer_mla",
+        "lmcache_mla_buffer_to_paged", "lmcache_mla_paged_to_buffer", "lmcache_kv_strided_block_transfer",
+    }
+    for cap in caps:
+        assert cap.backends == ("rocm-hip",)
+        assert callable(getattr(musa_aiter, cap.name))
+
+
+def test_dispatch_trace_format(monkeypatch, capsys):
+    monkeypatch.setenv("MUSA_AITER_TRACE_DISPATCH", "1")
+    emit(DispatchRecord("kv_paged_to_linear", "rocm-hip", "cuda:0", "torch.bfloat16", "why"))
+    err = capsys.readouterr().err
+    assert err.strip() == ("[MUSA_AITER DISPATCH] op=kv_paged_to_linear backend=rocm-hip device=cuda:0 "
+                           "dtype=torch.bfloat16 reason=why")
+    monkeypatch.setenv("MUSA_AITER_TRACE_DISPATCH", "0")
+    emit(DispatchRecord("x", "y", "z", "w", "v"))
+    assert capsys.readouterr().err == ""
+
+
+def test_policy_and_gate(monkeypatch):
+    from musa_aiter.policy import FallbackPolicy, current_policy
+
+    monkeypatch.setenv("MUSA_AITER_FALLBACK_POLICY", "1")
+    assert current_policy() is FallbackPolicy.REQUIRE_NATIVE
+    with pytest.raises(RuntimeError):
+        musa_aiter.ensure_reference_allowed("op")
+    musa_aiter.ensure_reference_allowed("op", native_available=True)
+    monkeypatch.setenv("MUSA_AITER_NATIVE_KV_TRANSFER", "1")
+    d = musa_aiter.decide_native_gate("op", ["MUSA_AITER_NATIVE_KV_TRANSFER"], available=False, native_required=True)
+    assert (d.mode, d.reason) == ("error", "native_unavailable")
+
+
+def test_cli_list_ops():
+    out = subprocess.run([sys.executable, "-m", "musa_aiter.cli", "list-ops", "--family", "kvcache"],
+                         capture_output=True, text=True, check=True,
+                         env={**__import__("os").environ, "PYTHONPATH": ":".join(sys.path)}).stdout
+    assert "kv_paged_to_linear_multi_layer" in out and "backends=rocm-hip" in out
+
+
+def test_layout_descriptors():
+    spec = musa_aiter.InterleavedFp8Layout(value_bytes=128, scale_bytes=4, scale_granularity=16).as_kv_layout_spec(
+        num_layers=2, num_blocks=8, block_size=16)
+    facts = spec.format_facts()
+    assert (facts.value_bytes, facts.scale_bytes, facts.requires_transform) == (128, 4, True)
+    lin = musa_aiter.KVLayoutSpec.linear(num_layers=2, num_tokens=4, num_heads=8, head_size=128, dtype_name="bfloat16")
+    assert lin.row_bytes == 2048 and lin.format_facts().supports_direct_batch
+    with pytest.raises(ValueError):
+        musa_aiter.KVLayoutSpec.linear(num_layers=1, num_tokens=1, num_heads=1, head_size=1, dtype_name="int7")
+    fmt = musa_aiter.describe_lmcache_format(torch.zeros(2, 3, 5, 16, dtype=torch.bfloat16))
+    assert fmt.format is musa_aiter.LMCacheFormat.KV_2LTD and fmt.spec.num_tokens == 5
+    assert musa_aiter.describe_lmcache_format(torch.zeros(7, 2, 4)).spec.num_tokens == 7
+    split = musa_aiter.describe_sglang_split_list([[torch.zeros(4, 16, 2, 8)] * 3, [torch.zeros(4, 16, 2, 8)] * 3])
+    assert split.spec.pointer_table_length == 6
+    plan = musa_aiter.KVTransferPlan(lin, lin, "d2d", 4, 0, (musa_aiter.KVTransferEntry(0, 0, 8),
+                                                             musa_aiter.KVTransferEntry(0, 4, 8)), None, True, None)
+    with pytest.raises(ValueError, match="overlap"):
+        musa_aiter.validate_transfer_plan(plan)
+    ok_plan = musa_aiter.KVTransferPlan(lin, lin, "d2d", 4, 0, (musa_aiter.KVTransferEntry(0, 0, 8),), None, True, None)
+    decision = musa_aiter.select_kv_backend(ok_plan, capabilities=musa_aiter.KVBackendCapabilities(reference=False),
+                                            require_native=True)
+    assert decision.backend is musa_aiter.KVBackend.REJECTED
+    assert musa_aiter.select_kv_backend(ok_plan, capabilities=musa_aiter.hip_capabilities()).accepted
+
+
+def test_abi_version_probes():
+    assert musa_aiter.native_lmcache_kv_transfer_abi_version() == 1
+    assert musa_aiter.native_kv_transfer_abi_version() == 1
+    assert musa_aiter.native_fp8_kv_cache_abi_version() == 1
