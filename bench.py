@@ -54,6 +54,19 @@ def make_slots(seed: int, num_seqs: int, lo: int, hi: int, num_blocks: int, bloc
     return sequence_slots(rng, lengths, num_blocks=num_blocks, block_size=block_size)
 
 
+def make_covering_slots(seed: int, tokens: int, lo: int, hi: int, num_blocks: int, block_size: int) -> np.ndarray:
+    """Slots of random sequences (lengths uniform in [lo, hi]) drawn until ``tokens`` are covered, truncated."""
+    from tests.kvgen import sequence_slots
+
+    rng = np.random.default_rng(seed)
+    lengths, covered = [], 0
+    while covered < tokens:
+        lengths.append(int(rng.integers(lo, hi + 1)))
+        covered += lengths[-1]
+    lengths[-1] -= covered - tokens
+    return sequence_slots(rng, lengths, num_blocks=num_blocks, block_size=block_size)
+
+
 class EventTimer:
     """Accumulates device time between HIP events recorded on torch's current stream."""
 
@@ -223,7 +236,7 @@ def bench_config4(steps: int, warmup: int) -> dict:
     gen = torch.Generator(device=dev).manual_seed(4)
     cache = torch.randn((2, nl, nb, BS, NH, HD), generator=gen, device=dev, dtype=torch.bfloat16)
     kvcaches = [list(cache[0].unbind(0)), list(cache[1].unbind(0))]
-    slots_np = make_slots(1004, 64, 128, 4096, nb, BS)[: chunk * nchunks]
+    slots_np = make_covering_slots(1004, chunk * nchunks, 128, 4096, nb, BS)
     slots = torch.from_numpy(slots_np).to(dev)
     memory = torch.empty((2, nl, chunk * nchunks, ROW), dtype=torch.bfloat16, device=dev)
     chunks = [(slots[i * chunk:(i + 1) * chunk].contiguous(), memory[:, :, i * chunk:(i + 1) * chunk])
@@ -232,6 +245,7 @@ def bench_config4(steps: int, warmup: int) -> dict:
         for s, m in chunks:
             musa_aiter.lmcache_kv_paged_to_buffer_two_x_nl(kvcaches, m, s, BS, NH, HD)
     torch.cuda.synchronize()
+    log(f"config 4: {chunk * nchunks} tokens in {nchunks} chunks, warmup done")
     tg, tb, ts = EventTimer(), EventTimer(), EventTimer()
     for _ in range(steps):
         for s, m in chunks:

@@ -25,8 +25,9 @@ SOURCES = ("kv_paged_tiles.hip", "kv_rows.hip", "kv_abi.hip")
 ARCH = os.environ.get("MUSA_AITER_HIP_ARCH", "gfx950")
 
 # Packed fp32 VALU forms are disabled for the whole library; fp32 division
-# stays correctly rounded and denormals are preserved (no fast-math), which
-# the FP8 codec relies on for bit-exact parity.
+# stays correctly rounded, denormals are preserved (no fast-math) and no
+# floating-point contraction is allowed, which the FP8 codec relies on for
+# bit-exact parity with the reference's separately rounded torch ops.
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -39,6 +40,7 @@ HIPCC_FLAGS = [
     "-Xclang",
     "-packed-fp32-ops",
     "-fno-fast-math",
+    "-ffp-contract=off",
     "-fno-gpu-flush-denormals-to-zero",
     f"-I{ROOT.parent / 'include'}",
 ]

@@ -18,9 +18,12 @@ using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
 using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------
-// Vector memory helpers.  The payload is streamed exactly once, so the loads
-// and stores are tagged non-temporal: they bypass the MALL/L2 retention
-// policy that would otherwise evict the slot tables and claim arrays.
+// Vector memory helpers.  Two cache policies:
+//  * stream (non-temporal): for accesses whose wave instruction covers whole
+//    cache lines (coalesced token rows); the data is touched exactly once.
+//  * cached: for strided accesses where one instruction touches many lines
+//    partially and later instructions of the same wave finish those lines;
+//    L2 must keep and merge them (write-combining for partial-line stores).
 // ---------------------------------------------------------------------------
 template <int VEC>
 struct VecType;
@@ -45,8 +48,12 @@ __device__ __forceinline__ void stv(uint8_t* p, typename VecType<VEC>::T v) {
   __builtin_nontemporal_store(v, reinterpret_cast<typename VecType<VEC>::T*>(p));
 }
 
+// Streaming 16-byte accesses (whole lines per wave instruction).
 __device__ __forceinline__ u32x4 ld16(const uint8_t* p) { return ldv<16>(p); }
 __device__ __forceinline__ void st16(uint8_t* p, u32x4 v) { stv<16>(p, v); }
+// Cached 16-byte accesses (strided, partial lines per wave instruction).
+__device__ __forceinline__ u32x4 ld16_cached(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16_cached(uint8_t* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
 // ---------------------------------------------------------------------------
 // Wave-level helpers (wave64).
@@ -123,6 +130,10 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
 }
 
 __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  // Keep the fp32 value opaque so the backend cannot fold a preceding fp32
+  // multiply and this conversion into v_fma_mix with a +0.0 addend, which
+  // would turn a -0.0 product into +0.0 (torch keeps the sign of zero).
+  __asm__ volatile("" : "+v"(f));
   const _Float16 h = static_cast<_Float16>(f);
   return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h));
 }

@@ -198,7 +198,7 @@ __global__ __launch_bounds__(kBlockThreads) void paged_tile_kernel(const TileArg
             const int lo = (jb + jj) * CG;
             if (lo < c1 && lo + CG > c0) {
 #pragma unroll
-              for (int q = 0; q < RPL; ++q) d[jj][q] = ld16(crow + (q * BS + lo) * ELT_C);
+              for (int q = 0; q < RPL; ++q) d[jj][q] = ld16_cached(crow + (q * BS + lo) * ELT_C);
             }
           }
 #pragma unroll
@@ -228,7 +228,7 @@ __global__ __launch_bounds__(kBlockThreads) void paged_tile_kernel(const TileArg
           if (lo >= c0 && lo + CG <= c1) {
 #pragma unroll
             for (int q = 0; q < RPL; ++q)
-              st16(cgrp + q * BS * ELT_C, scatter_row<ELT_C, ELT_L, CODEC, LDT, CG>(in, q, sc));
+              st16_cached(cgrp + q * BS * ELT_C, scatter_row<ELT_C, ELT_L, CODEC, LDT, CG>(in, q, sc));
           } else {
 #pragma unroll
             for (int q = 0; q < RPL; ++q) {
