@@ -130,16 +130,127 @@ __device__ __forceinline__ void store_elem(uint8_t* p, uint32_t v) {
   else *reinterpret_cast<uint32_t*>(p) = v;
 }
 
+// Element `idx` of a 16-byte cache piece, in cache encoding.
+template <int ELT>
+__device__ __forceinline__ uint32_t piece_elem(const u32x4& v, int idx) {
+  if constexpr (ELT == 1) return elem8(v, idx);
+  else if constexpr (ELT == 2) return elem16(v, idx);
+  else return v[idx];
+}
+
+// ----- LDS staging of one block run ----------------------------------------------
+//
+// A chunk is 64 lane tiles of RPL rows x CG block columns: kChunkRows cache
+// rows of one block, i.e. RPL KiB of contiguous cache bytes.  The cache side
+// of a chunk moves as RPL coalesced wave instructions (lane l takes piece
+// k*64 + l); the lane tiles are exchanged through the wave's private LDS
+// region, so both the cache and the linear side issue whole cache lines.
+// Piece s of the chunk lives at LDS slot lds_slot(s): the low four bits are
+// XOR-swizzled with the row group so that 16 consecutive lanes hit 16
+// distinct 16-byte bank groups in both access patterns.
+
+constexpr int log2_const(int v) { return v <= 1 ? 0 : 1 + log2_const(v / 2); }
+
+template <int RPL, int NCG>
+__device__ __forceinline__ int lds_slot(int s) {
+  constexpr int kGroupShift = log2_const(RPL * NCG);
+  return s ^ (((s >> kGroupShift) * NCG) & 15);
+}
+
+// Orders the wave's LDS writes before its later LDS reads (and the reads
+// before the next writes).  LDS executes one wave's requests in issue order;
+// the wait plus the code-motion barrier keep the compiler from reordering.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), other counters untouched
+  __builtin_amdgcn_wave_barrier();
+}
+
+template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS, bool SCATTER>
+__device__ __forceinline__ void staged_run(const TileArgs& a, uint8_t* const cache_blk, uint8_t* const lin_run,
+                                           const int c0, const int c1, const int kv, const int layer,
+                                           u32x4* const lds) {
+  constexpr int RPL = 16 / ELT_L;
+  constexpr int CG = 16 / ELT_C;
+  constexpr int NCG = BS / CG;
+  constexpr int kChunkRows = (kWave / NCG) * RPL;
+  const int lane = lane_id();
+  const int rg = lane / NCG;
+  const int ct = lane % NCG;
+  const bool full = (c0 == 0) && (c1 == BS);
+
+  for (int64_t r0 = 0; r0 < a.nrows; r0 += kChunkRows) {
+    uint8_t* const chunk = cache_blk + r0 * BS * ELT_C;
+    const int64_t trow = r0 + rg * RPL;  // first cache row of this lane's tile
+    const bool tile_in = trow < a.nrows;
+    float sc = 1.0f;
+    if constexpr (CODEC != kCopy) {
+      if (tile_in) sc = load_scale(a, kv, layer, trow / a.head_dim);
+    }
+    uint8_t* const lrow = lin_run + trow * ELT_L;
+
+    if constexpr (!SCATTER) {
+      u32x4 v[RPL];
+#pragma unroll
+      for (int k = 0; k < RPL; ++k) {
+        const int pc = k * kWave + lane;
+        if (r0 + pc / NCG < a.nrows) v[k] = ld16(chunk + pc * 16);
+      }
+#pragma unroll
+      for (int k = 0; k < RPL; ++k) lds[lds_slot<RPL, NCG>(k * kWave + lane)] = v[k];
+      wave_lds_sync();
+      u32x4 d[RPL];
+#pragma unroll
+      for (int q = 0; q < RPL; ++q) d[q] = lds[lds_slot<RPL, NCG>((rg * RPL + q) * NCG + ct)];
+      wave_lds_sync();
+      if (tile_in) {
+#pragma unroll
+        for (int cc = 0; cc < CG; ++cc) {
+          const int c = ct * CG + cc;
+          if (c >= c0 && c < c1)
+            st16(lrow + static_cast<int64_t>(c - c0) * a.lin_token_stride,
+                 gather_column<ELT_C, ELT_L, CODEC, LDT, RPL>(d, cc, sc));
+        }
+      }
+    } else {
+      u32x4 in[CG];
+#pragma unroll
+      for (int cc = 0; cc < CG; ++cc) {
+        const int c = ct * CG + cc;
+        in[cc] = u32x4{0u, 0u, 0u, 0u};
+        if (tile_in && c >= c0 && c < c1) in[cc] = ld16(lrow + static_cast<int64_t>(c - c0) * a.lin_token_stride);
+      }
+#pragma unroll
+      for (int q = 0; q < RPL; ++q)
+        lds[lds_slot<RPL, NCG>((rg * RPL + q) * NCG + ct)] = scatter_row<ELT_C, ELT_L, CODEC, LDT, CG>(in, q, sc);
+      wave_lds_sync();
+#pragma unroll
+      for (int k = 0; k < RPL; ++k) {
+        const int pc = k * kWave + lane;
+        const u32x4 w = lds[lds_slot<RPL, NCG>(pc)];
+        if (r0 + pc / NCG >= a.nrows) continue;
+        uint8_t* const dst = chunk + pc * 16;
+        const int lo = (pc % NCG) * CG;
+        if (full || (lo >= c0 && lo + CG <= c1)) {
+          st16(dst, w);
+        } else {
+#pragma unroll
+          for (int cc = 0; cc < CG; ++cc)
+            if (lo + cc >= c0 && lo + cc < c1) store_elem<ELT_C>(dst + cc * ELT_C, piece_elem<ELT_C>(w, cc));
+        }
+      }
+      wave_lds_sync();
+    }
+  }
+}
+
 // ----- the tile kernel ---------------------------------------------------------
 
 template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS, bool SCATTER>
 __global__ __launch_bounds__(kBlockThreads) void paged_tile_kernel(const TileArgs a) {
   constexpr int RPL = 16 / ELT_L;  // cache rows per lane tile
   constexpr int CG = 16 / ELT_C;   // block columns per 16-byte group
-  constexpr int NCG = BS / CG;     // 16-byte groups per cache row
   static_assert(BS % CG == 0, "block row must be a whole number of 16-byte groups");
   static_assert(kTileTokens + BS + 1 <= kWave, "run window must fit one wave");
-  constexpr int kBatch = (NCG < 2) ? NCG : 2;  // column groups in flight per lane
 
   const int lane = lane_id();
   const int64_t tile = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();
@@ -170,6 +281,8 @@ __global__ __launch_bounds__(kBlockThreads) void paged_tile_kernel(const TileArg
   uint64_t heads = vmask & ~cmask & window;
 
   const int ngroups = static_cast<int>(a.nrows / RPL);
+  __shared__ u32x4 lds_all[kWavesPerBlock * kWave * RPL];
+  u32x4* const lds = lds_all + wave_in_block() * (kWave * RPL);
 
   while (heads) {
     const int i = __builtin_ctzll(heads);
@@ -182,49 +295,48 @@ __global__ __launch_bounds__(kBlockThreads) void paged_tile_kernel(const TileArg
     const int64_t tf = t0 - 1 + i;
     const int c1 = c0 + len;
 
+    // Runs that touch every 16-byte column group of the block row go through
+    // LDS (whole-line traffic on both sides); shorter runs use lane tiles
+    // that load or store only the column groups they cover.
+    if (c0 < CG && c1 > BS - CG) {
+      staged_run<ELT_C, ELT_L, CODEC, LDT, BS, SCATTER>(a, cache + blk * a.nrows * BS * ELT_C,
+                                                        lin + tf * a.lin_token_stride, c0, c1, kv, layer, lds);
+      continue;
+    }
+
+    const int j0 = c0 / CG;
+    const int j1 = (c1 - 1) / CG;
     for (int g = lane; g < ngroups; g += kWave) {
       const int64_t r0 = static_cast<int64_t>(g) * RPL;
       float sc = 1.0f;
       if constexpr (CODEC != kCopy) sc = load_scale(a, kv, layer, r0 / a.head_dim);
       uint8_t* const crow = cache + (blk * a.nrows + r0) * BS * ELT_C;
       uint8_t* const lrow = lin + tf * a.lin_token_stride + r0 * ELT_L;
-
-      if constexpr (!SCATTER) {
+      // One 16-byte column group at a time keeps the register tile at RPL
+      // (gather) or CG (scatter) vectors.
+#pragma unroll 1
+      for (int j = j0; j <= j1; ++j) {
+        const int lo = j * CG;
+        uint8_t* const cgrp = crow + lo * ELT_C;
+        if constexpr (!SCATTER) {
+          u32x4 d[RPL];
 #pragma unroll
-        for (int jb = 0; jb < NCG; jb += kBatch) {
-          u32x4 d[kBatch][RPL];
+          for (int q = 0; q < RPL; ++q) d[q] = ld16_cached(cgrp + q * BS * ELT_C);
 #pragma unroll
-          for (int jj = 0; jj < kBatch; ++jj) {
-            const int lo = (jb + jj) * CG;
-            if (lo < c1 && lo + CG > c0) {
-#pragma unroll
-              for (int q = 0; q < RPL; ++q) d[jj][q] = ld16_cached(crow + (q * BS + lo) * ELT_C);
-            }
+          for (int cc = 0; cc < CG; ++cc) {
+            const int c = lo + cc;
+            if (c >= c0 && c < c1)
+              st16(lrow + static_cast<int64_t>(c - c0) * a.lin_token_stride,
+                   gather_column<ELT_C, ELT_L, CODEC, LDT, RPL>(d, cc, sc));
           }
-#pragma unroll
-          for (int jj = 0; jj < kBatch; ++jj) {
-            const int lo = (jb + jj) * CG;
-#pragma unroll
-            for (int cc = 0; cc < CG; ++cc) {
-              const int c = lo + cc;
-              if (c >= c0 && c < c1)
-                st16(lrow + static_cast<int64_t>(c - c0) * a.lin_token_stride,
-                     gather_column<ELT_C, ELT_L, CODEC, LDT, RPL>(d[jj], cc, sc));
-            }
-          }
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < NCG; ++j) {
-          const int lo = j * CG;
-          if (lo >= c1 || lo + CG <= c0) continue;
+        } else {
           u32x4 in[CG];
 #pragma unroll
           for (int cc = 0; cc < CG; ++cc) {
             const int c = lo + cc;
+            in[cc] = u32x4{0u, 0u, 0u, 0u};
             if (c >= c0 && c < c1) in[cc] = ld16(lrow + static_cast<int64_t>(c - c0) * a.lin_token_stride);
           }
-          uint8_t* const cgrp = crow + lo * ELT_C;
           if (lo >= c0 && lo + CG <= c1) {
 #pragma unroll
             for (int q = 0; q < RPL; ++q)
