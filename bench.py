@@ -26,6 +26,7 @@ import argparse
 import ctypes
 import json
 import os
+import re
 import sys
 import time
 
@@ -65,6 +66,21 @@ def make_covering_slots(seed: int, tokens: int, lo: int, hi: int, num_blocks: in
         covered += lengths[-1]
     lengths[-1] -= covered - tokens
     return sequence_slots(rng, lengths, num_blocks=num_blocks, block_size=block_size)
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "paged_tile_kernel_cfg2_traffic.md")
+
+
+def profiled_traffic(direction: str) -> int | None:
+    """HBM bytes per launch of the cfg 2 kernel for one direction, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes (scaled by the plain-copy calibration); None if absent."""
+    try:
+        with open(TRAFFIC_PROFILE) as fh:
+            text = fh.read()
+    except OSError:
+        return None
+    m = re.search(rf"traffic_bytes_per_launch\.{direction} = (\d+)", text)
+    return int(m.group(1)) if m else None
 
 
 class EventTimer:
@@ -269,6 +285,25 @@ def bench_config4(steps: int, warmup: int) -> dict:
             "note": "per-chunk times include the host-side Python call overhead between events"}
 
 
+def device_copy(mib: int, reps: int = 5) -> dict:
+    """Plain device-to-device copy of a known size (torch ``copy_``): the achievable copy rate of this
+    GPU and the calibration kernel for the FETCH_SIZE / WRITE_SIZE traffic counters."""
+    dev = torch.device("cuda", 0)
+    src = torch.empty(mib << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    timer = EventTimer()
+    for _ in range(reps):
+        e = timer.start()
+        dst.copy_(src)
+        timer.stop(e)
+    torch.cuda.synchronize()
+    ms = np.array(timer.ms())
+    nbytes = 2 * (mib << 20)
+    return {"bytes_read_plus_written": nbytes, "avg_ms": float(ms.mean()), "gbs": nbytes / (ms.mean() * 1e-3) / 1e9}
+
+
 def cpu_baseline(slots_np: np.ndarray, kc: torch.Tensor, vc: torch.Tensor) -> dict:
     """Time the numpy oracle on a bounded sample of configs[1]: all tokens, first 2 layers, both directions."""
     from oracle import kv_oracle as ko
@@ -298,6 +333,8 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--configs", default="2,3,4", help="comma list of BASELINE configs to run (2 is the headline)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--copy-mib", type=int, default=1024,
+                        help="size of the plain device copy timed first (0 = skip)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X only; --gpus {args.gpus} is not supported (the path does not shard "
@@ -309,6 +346,10 @@ def main() -> int:
     torch.cuda.set_device(0)
     configs = {int(c) for c in args.configs.split(",") if c}
     extra = {}
+    if args.copy_mib > 0:
+        extra["device_copy"] = device_copy(args.copy_mib)
+        log(f"device copy of {args.copy_mib} MiB: {extra['device_copy']['gbs']:.0f} GB/s (read+write)")
+        torch.cuda.empty_cache()
     c2 = bench_config2(args.steps, args.warmup)
     slots_np, kc, vc = c2.pop("_tensors")
     log(f"config 2: scatter {c2['scatter']['gbs']:.0f} GB/s, gather {c2['gather']['gbs']:.0f} GB/s")
@@ -353,7 +394,9 @@ def main() -> int:
         "parity_roundtrip": c2["parity_roundtrip"],
         "roofline": {"bound": "hbm", "kernel": f"paged_tile_kernel ({c2['dominant']}, 64 planes)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(c2["dominant"]),
+                     "traffic_source": "rocprofv3 FETCH_SIZE x2.000 + WRITE_SIZE x1.000 per dispatch "
+                                       "(profiles/paged_tile_kernel_cfg2_traffic.md)",
                      "bytes_per_launch": c2["bytes_per_direction"], "avg_launch_ms": round(c2["dominant_avg_ms"], 4)},
         "cpu_baseline": cpu,
         "extra": extra,

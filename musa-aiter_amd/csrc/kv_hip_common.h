@@ -222,4 +222,93 @@ __device__ __forceinline__ float fp8_decode(uint32_t byte) {
 // v_div_scale/v_div_fmas/v_div_fixup sequence for this operator.
 __device__ __forceinline__ float div_rn(float x, float s) { return x / s; }
 
+// ---------------------------------------------------------------------------
+// Quantiser quotient with a hoisted reciprocal.  For one scale s the lane
+// computes r = RN(1/s) once (an exact division); per element
+//   q0 = x*r,  q1 = q0 + RN(x - s*q0)*r,  q = q1 + RN(x - s*q1)*r
+// (residuals exact through FMA) equals RN(x/s) whenever s and |x| lie in
+// [2^-60, 2^60] (x = +-0 gives +0, which the encoder treats like -0): the
+// first correction makes q1 faithful, the second is Markstein's final
+// correction with a correctly rounded reciprocal.  No over- or underflow can
+// occur in that range.  Elements outside it use div_rn.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kFastLoBits = 0x21800000u;  // 2^-60
+constexpr uint32_t kFastHiBits = 0x5D800000u;  // 2^60
+
+__device__ __forceinline__ bool fast_scale_ok(float s) {
+  return (__float_as_uint(s) - kFastLoBits) < (kFastHiBits - kFastLoBits);
+}
+
+__device__ __forceinline__ float quot_fast(float x, float s, float r) {
+  const float q0 = x * r;
+  const float e0 = __builtin_fmaf(-s, q0, x);
+  const float q1 = __builtin_fmaf(e0, r, q0);
+  const float e1 = __builtin_fmaf(-s, q1, x);
+  return __builtin_fmaf(e1, r, q1);
+}
+
+// Encoder for a quotient known to be +0 or finite with 2^-120 <= |w| < 2^126
+// (the fast range): the sign is the sign bit and no non-finite check is needed.
+template <int CODEC>
+__device__ __forceinline__ uint32_t fp8_encode_fast(float w) {
+  using F = Fp8Fmt<CODEC>;
+  const uint32_t bits = __float_as_uint(w);
+  uint32_t a = bits & 0x7FFFFFFFu;
+  const bool normal = a >= F::kMinNormBits;
+  a = a < F::kMaxBits ? a : F::kMaxBits;
+  const uint32_t lsb = (a >> F::kShift) & 1u;
+  const uint32_t body =
+      (a + ((1u << (F::kShift - 1)) - 1u) + lsb - (F::kExpOffset << 23)) >> F::kShift;
+  return ((bits >> 24) & 0x80u) | (normal ? body : 0u);
+}
+
+// Magnitude range of a tile's linear inputs, tracked on the raw bits: the
+// minimum of (|x| - 1) (so zeros drop out) and the maximum of |x|.  16-bit
+// inputs are tracked two per dword with packed 16-bit integer min/max.
+using u16x2 = unsigned short __attribute__((ext_vector_type(2)));
+
+template <int LDT>
+struct InputRange {
+  static constexpr bool kWide = (LDT == kLinF32);
+  uint32_t lo32 = 0xFFFFFFFFu;
+  uint32_t hi32 = 0u;
+  u16x2 lo16 = {0xFFFF, 0xFFFF};
+  u16x2 hi16 = {0, 0};
+
+  __device__ __forceinline__ void add(const u32x4& v) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      if constexpr (kWide) {
+        const uint32_t a = v[w] & 0x7FFFFFFFu;
+        lo32 = min(lo32, a - 1u);
+        hi32 = max(hi32, a);
+      } else {
+        const u16x2 a = __builtin_bit_cast(u16x2, v[w] & 0x7FFF7FFFu);
+        if constexpr (LDT == kLinBF16) lo16 = __builtin_elementwise_min(lo16, a - u16x2{1, 1});
+        hi16 = __builtin_elementwise_max(hi16, a);
+      }
+    }
+  }
+
+  __device__ __forceinline__ uint32_t lo() const {
+    if constexpr (kWide) return lo32;
+    else return lo16.x < lo16.y ? lo16.x : lo16.y;
+  }
+  __device__ __forceinline__ uint32_t hi() const {
+    if constexpr (kWide) return hi32;
+    else return hi16.x > hi16.y ? hi16.x : hi16.y;
+  }
+
+  // True when every tracked input is zero or has 2^-60 <= |x| < 2^60.
+  __device__ __forceinline__ bool in_fast_range() const {
+    if constexpr (LDT == kLinF32) {
+      return lo() >= kFastLoBits - 1u && hi() < kFastHiBits;
+    } else if constexpr (LDT == kLinBF16) {
+      return lo() >= (kFastLoBits >> 16) - 1u && hi() < (kFastHiBits >> 16);
+    } else {
+      return hi() < 0x7C00u;  // every finite fp16 value is zero or within [2^-24, 65504]
+    }
+  }
+};
+
 }  // namespace kvhip

@@ -86,8 +86,10 @@ __device__ __forceinline__ u32x4 gather_column(const u32x4 (&d)[RPL], int cc, fl
 
 // Scatter: in[cc] holds the 16-byte linear piece (rows r0..r0+RPL-1) of the
 // token in block column cc; element (q, cc) of the tile in cache encoding.
-template <int ELT_C, int ELT_L, int CODEC, int LDT>
-__device__ __forceinline__ uint32_t scatter_elem(const u32x4& in_cc, int q, float sc) {
+// FAST selects the hoisted-reciprocal quotient (r = RN(1/sc)); the caller
+// guarantees the fast range for the scale and every input of the tile.
+template <int ELT_C, int ELT_L, int CODEC, int LDT, bool FAST = false>
+__device__ __forceinline__ uint32_t scatter_elem(const u32x4& in_cc, int q, float sc, float r = 0.0f) {
   if constexpr (CODEC == kCopy && ELT_C == 2) {
     return elem16(in_cc, q);
   } else if constexpr (CODEC == kCopy && ELT_C == 4) {
@@ -96,31 +98,56 @@ __device__ __forceinline__ uint32_t scatter_elem(const u32x4& in_cc, int q, floa
     float x;
     if constexpr (ELT_L == 2) x = lin_to_f32<LDT>(elem16(in_cc, q));
     else x = __uint_as_float(in_cc[q]);
-    return fp8_encode<CODEC>(div_rn(x, sc));
+    if constexpr (FAST) return fp8_encode_fast<CODEC>(quot_fast(x, sc, r));
+    else return fp8_encode<CODEC>(div_rn(x, sc));
   }
 }
 
-template <int ELT_C, int ELT_L, int CODEC, int LDT, int CG>
-__device__ __forceinline__ u32x4 scatter_row(const u32x4 (&in)[CG], int q, float sc) {
+template <int ELT_C, int ELT_L, int CODEC, int LDT, int CG, bool FAST = false>
+__device__ __forceinline__ u32x4 scatter_row(const u32x4 (&in)[CG], int q, float sc, float r = 0.0f) {
   u32x4 o;
   if constexpr (ELT_C == 2) {
 #pragma unroll
     for (int w = 0; w < 4; ++w)
-      o[w] = pack16(scatter_elem<ELT_C, ELT_L, CODEC, LDT>(in[2 * w], q, sc),
-                    scatter_elem<ELT_C, ELT_L, CODEC, LDT>(in[2 * w + 1], q, sc));
+      o[w] = pack16(scatter_elem<ELT_C, ELT_L, CODEC, LDT, FAST>(in[2 * w], q, sc, r),
+                    scatter_elem<ELT_C, ELT_L, CODEC, LDT, FAST>(in[2 * w + 1], q, sc, r));
   } else if constexpr (ELT_C == 4) {
 #pragma unroll
-    for (int w = 0; w < 4; ++w) o[w] = scatter_elem<ELT_C, ELT_L, CODEC, LDT>(in[w], q, sc);
+    for (int w = 0; w < 4; ++w) o[w] = scatter_elem<ELT_C, ELT_L, CODEC, LDT, FAST>(in[w], q, sc, r);
   } else {
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       uint32_t acc = 0;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) acc |= scatter_elem<ELT_C, ELT_L, CODEC, LDT>(in[4 * w + b], q, sc) << (8 * b);
+      for (int b = 0; b < 4; ++b)
+        acc |= scatter_elem<ELT_C, ELT_L, CODEC, LDT, FAST>(in[4 * w + b], q, sc, r) << (8 * b);
       o[w] = acc;
     }
   }
   return o;
+}
+
+// Writes the RPL cache rows of one lane tile through `put(q, row)`.  FP8
+// tiles whose scale and inputs are all in the fast range use the hoisted
+// reciprocal; any other tile divides exactly.
+template <int ELT_C, int ELT_L, int CODEC, int LDT, int CG, int RPL, typename Put>
+__device__ __forceinline__ void encode_tile(const u32x4 (&in)[CG], float sc, Put put) {
+  if constexpr (CODEC == kCopy) {
+#pragma unroll
+    for (int q = 0; q < RPL; ++q) put(q, scatter_row<ELT_C, ELT_L, CODEC, LDT, CG>(in, q, sc));
+  } else {
+    InputRange<LDT> range;
+#pragma unroll
+    for (int cc = 0; cc < CG; ++cc) range.add(in[cc]);
+    if (fast_scale_ok(sc) && range.in_fast_range()) {
+      const float r = 1.0f / sc;
+#pragma unroll
+      for (int q = 0; q < RPL; ++q) put(q, scatter_row<ELT_C, ELT_L, CODEC, LDT, CG, true>(in, q, sc, r));
+    } else {
+#pragma unroll
+      for (int q = 0; q < RPL; ++q) put(q, scatter_row<ELT_C, ELT_L, CODEC, LDT, CG>(in, q, sc));
+    }
+  }
 }
 
 template <int ELT>
@@ -219,9 +246,8 @@ __device__ __forceinline__ void staged_run(const TileArgs& a, uint8_t* const cac
         in[cc] = u32x4{0u, 0u, 0u, 0u};
         if (tile_in && c >= c0 && c < c1) in[cc] = ld16(lrow + static_cast<int64_t>(c - c0) * a.lin_token_stride);
       }
-#pragma unroll
-      for (int q = 0; q < RPL; ++q)
-        lds[lds_slot<RPL, NCG>((rg * RPL + q) * NCG + ct)] = scatter_row<ELT_C, ELT_L, CODEC, LDT, CG>(in, q, sc);
+      encode_tile<ELT_C, ELT_L, CODEC, LDT, CG, RPL>(
+          in, sc, [&](int q, const u32x4& row) { lds[lds_slot<RPL, NCG>((rg * RPL + q) * NCG + ct)] = row; });
       wave_lds_sync();
 #pragma unroll
       for (int k = 0; k < RPL; ++k) {
@@ -338,9 +364,8 @@ __global__ __launch_bounds__(kBlockThreads) void paged_tile_kernel(const TileArg
             if (c >= c0 && c < c1) in[cc] = ld16(lrow + static_cast<int64_t>(c - c0) * a.lin_token_stride);
           }
           if (lo >= c0 && lo + CG <= c1) {
-#pragma unroll
-            for (int q = 0; q < RPL; ++q)
-              st16_cached(cgrp + q * BS * ELT_C, scatter_row<ELT_C, ELT_L, CODEC, LDT, CG>(in, q, sc));
+            encode_tile<ELT_C, ELT_L, CODEC, LDT, CG, RPL>(
+                in, sc, [&](int q, const u32x4& row) { st16_cached(cgrp + q * BS * ELT_C, row); });
           } else {
 #pragma unroll
             for (int q = 0; q < RPL; ++q) {

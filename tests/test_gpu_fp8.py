@@ -165,3 +165,50 @@ def test_raw_symbol_scalar_scale_matches_api():
     want = np.zeros((nb, NH, HD, BS), np.uint8)
     ko.linear_to_paged_fp8(_lin_f32(kl.cpu()), want, slots, np.float32(0.01), "e4m3")
     assert np.array_equal(kc.cpu().numpy(), want)
+
+
+def _fast_range_inputs(lin: str, rng: np.random.Generator) -> torch.Tensor:
+    """Inputs whose every lane tile lies in the quantiser's hoisted-reciprocal range (zero allowed)."""
+    if lin == "float32":
+        mag = np.exp2(rng.uniform(-60.0, 60.0, size=48 * NH * HD)).astype(np.float32)
+        vals = np.where(rng.random(mag.size) < 0.5, -mag, mag).astype(np.float32)
+        vals[rng.random(vals.size) < 0.01] = 0.0
+        return torch.from_numpy(vals.reshape(-1, NH, HD))
+    dtype = LIN_DTYPES[lin]
+    raw = torch.arange(0, 2 ** 16, dtype=torch.int32).to(torch.int16).view(dtype).float()
+    finite = torch.isfinite(raw) & ((raw == 0) | ((raw.abs() >= 2.0 ** -60) & (raw.abs() < 2.0 ** 60)))
+    vals = raw[finite].to(dtype)
+    vals = vals[torch.from_numpy(rng.permutation(vals.numel()))]
+    pad = (-vals.numel()) % (NH * HD)
+    vals = torch.cat([vals, vals[:pad]])
+    return vals.reshape(-1, NH, HD)
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("lin", ["bfloat16", "float16", "float32"])
+def test_quant_store_fast_reciprocal_range_many_scales(fmt, lin):
+    """Tiles in the hoisted-reciprocal range, log-uniform per-head scales and the range edges."""
+    rng = np.random.default_rng(41)
+    x = _fast_range_inputs(lin, rng)
+    tokens = x.shape[0]
+    slots, nb = make_slots("sequences", rng, block_size=BS, tokens=tokens)
+    s_d = torch.from_numpy(slots).to(DEV)
+    edges = np.array([2.0 ** -60, np.nextafter(np.float32(2.0 ** 60), np.float32(0.0)), 2.0 ** -61, 2.0 ** 60],
+                     dtype=np.float32)
+    for rep in range(6):
+        ks = np.exp2(rng.uniform(-50.0, 50.0, size=NH)).astype(np.float32)
+        ks *= np.float32(1.0) + rng.random(NH).astype(np.float32)
+        if rep == 0:
+            ks[:4] = edges
+        vs = np.exp2(rng.uniform(-12.0, 4.0, size=NH)).astype(np.float32)
+        kc_d = torch.zeros(nb, NH, HD, BS, dtype=torch.uint8, device=DEV)
+        vc_d = torch.zeros_like(kc_d)
+        musa_aiter.kv_linear_to_paged_fp8(x.to(DEV), x.flip(0).contiguous().to(DEV), kc_d, vc_d, s_d,
+                                          torch.from_numpy(ks).to(DEV), torch.from_numpy(vs).to(DEV), fp8_format=fmt)
+        want_k = np.zeros((nb, NH, HD, BS), np.uint8)
+        want_v = np.zeros_like(want_k)
+        ko.linear_to_paged_fp8(_lin_f32(x), want_k, slots, ks, fmt)
+        ko.linear_to_paged_fp8(_lin_f32(x.flip(0).contiguous()), want_v, slots, vs, fmt)
+        got_k, got_v = kc_d.cpu().numpy(), vc_d.cpu().numpy()
+        assert np.array_equal(got_k, want_k), (rep, np.argwhere(got_k != want_k)[:5])
+        assert np.array_equal(got_v, want_v), (rep, np.argwhere(got_v != want_v)[:5])
