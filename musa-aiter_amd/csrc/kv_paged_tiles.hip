@@ -41,6 +41,7 @@ struct TileArgs {
   int32_t fill_zeros;
   uint32_t epoch;
   int32_t block_size;          // used by the generic kernel only
+  int64_t split_rows;          // cache rows per grid z-slice (tile kernel)
 };
 
 constexpr int kTileTokens = 16;
@@ -195,7 +196,8 @@ __device__ __forceinline__ void wave_lds_sync() {
 template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS, bool SCATTER>
 __device__ __forceinline__ void staged_run(const TileArgs& a, uint8_t* const cache_blk, uint8_t* const lin_run,
                                            const int c0, const int c1, const int kv, const int layer,
-                                           u32x4* const lds) {
+                                           u32x4* const lds, const int64_t r_begin, const int64_t r_end,
+                                           const int rot) {
   constexpr int RPL = 16 / ELT_L;
   constexpr int CG = 16 / ELT_C;
   constexpr int NCG = BS / CG;
@@ -205,7 +207,13 @@ __device__ __forceinline__ void staged_run(const TileArgs& a, uint8_t* const cac
   const int ct = lane % NCG;
   const bool full = (c0 == 0) && (c1 == BS);
 
-  for (int64_t r0 = 0; r0 < a.nrows; r0 += kChunkRows) {
+  // Chunks are visited starting at chunk `rot` (different per wave), so the
+  // waves in flight spread over all address phases of the block and of the
+  // token rows instead of all streaming the same offsets at the same time.
+  const int nchunks = static_cast<int>((r_end - r_begin + kChunkRows - 1) / kChunkRows);
+  int chunk_id = rot % nchunks;
+  for (int ci = 0; ci < nchunks; ++ci, chunk_id = (chunk_id + 1 == nchunks) ? 0 : chunk_id + 1) {
+    const int64_t r0 = r_begin + static_cast<int64_t>(chunk_id) * kChunkRows;
     uint8_t* const chunk = cache_blk + r0 * BS * ELT_C;
     const int64_t trow = r0 + rg * RPL;  // first cache row of this lane's tile
     const bool tile_in = trow < a.nrows;
@@ -287,6 +295,10 @@ __global__ __launch_bounds__(kBlockThreads) void paged_tile_kernel(const TileArg
   const int kv = plane & 1;
   uint8_t* const cache = a.cache[kv] + static_cast<int64_t>(layer) * a.cache_layer_stride;
   uint8_t* const lin = a.lin[kv] + static_cast<int64_t>(layer) * a.lin_layer_stride;
+  // The z-slice of the grid picks a range of cache rows (a whole number of
+  // LDS chunks), so one run is spread over several independent waves.
+  const int64_t r_begin = static_cast<int64_t>(blockIdx.z) * a.split_rows;
+  const int64_t r_end = (r_begin + a.split_rows < a.nrows) ? r_begin + a.split_rows : a.nrows;
 
   // Slot window: lane i holds token t0 - 1 + i.
   const int64_t t = t0 - 1 + lane;
@@ -306,7 +318,7 @@ __global__ __launch_bounds__(kBlockThreads) void paged_tile_kernel(const TileArg
   const uint64_t window = ((1ull << ntile) - 1ull) << 1;
   uint64_t heads = vmask & ~cmask & window;
 
-  const int ngroups = static_cast<int>(a.nrows / RPL);
+  const int ngroups = static_cast<int>(r_end / RPL);
   __shared__ u32x4 lds_all[kWavesPerBlock * kWave * RPL];
   u32x4* const lds = lds_all + wave_in_block() * (kWave * RPL);
 
@@ -326,13 +338,14 @@ __global__ __launch_bounds__(kBlockThreads) void paged_tile_kernel(const TileArg
     // that load or store only the column groups they cover.
     if (c0 < CG && c1 > BS - CG) {
       staged_run<ELT_C, ELT_L, CODEC, LDT, BS, SCATTER>(a, cache + blk * a.nrows * BS * ELT_C,
-                                                        lin + tf * a.lin_token_stride, c0, c1, kv, layer, lds);
+                                                        lin + tf * a.lin_token_stride, c0, c1, kv, layer, lds,
+                                                        r_begin, r_end, static_cast<int>(tile & 0xFFFF));
       continue;
     }
 
     const int j0 = c0 / CG;
     const int j1 = (c1 - 1) / CG;
-    for (int g = lane; g < ngroups; g += kWave) {
+    for (int g = static_cast<int>(r_begin / RPL) + lane; g < ngroups; g += kWave) {
       const int64_t r0 = static_cast<int64_t>(g) * RPL;
       float sc = 1.0f;
       if constexpr (CODEC != kCopy) sc = load_scale(a, kv, layer, r0 / a.head_dim);
@@ -386,13 +399,14 @@ __global__ __launch_bounds__(kBlockThreads) void paged_tile_kernel(const TileArg
   if constexpr (!SCATTER) {
     if (a.fill_zeros) {
       uint64_t skipped = ~vmask & window;
-      const int64_t row_bytes = a.nrows * ELT_L;
+      const int64_t row_bytes = r_end * ELT_L;
       const u32x4 zero = {0u, 0u, 0u, 0u};
       while (skipped) {
         const int i = __builtin_ctzll(skipped);
         skipped &= skipped - 1;
         uint8_t* const row = lin + (t0 - 1 + i) * a.lin_token_stride;
-        for (int64_t k = static_cast<int64_t>(lane) * 16; k < row_bytes; k += kWave * 16) st16(row + k, zero);
+        for (int64_t k = r_begin * ELT_L + static_cast<int64_t>(lane) * 16; k < row_bytes; k += kWave * 16)
+          st16(row + k, zero);
       }
     }
   }
@@ -463,13 +477,22 @@ hipError_t launch_elem(const TileArgs& a, int64_t planes, hipStream_t stream) {
   return hipGetLastError();
 }
 
+constexpr int kChunksPerSplit = 1;
+
 template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS, bool SCATTER>
-hipError_t launch_tile(const TileArgs& a, int64_t planes, hipStream_t stream) {
+hipError_t launch_tile(const TileArgs& a_in, int64_t planes, hipStream_t stream) {
+  constexpr int RPL = 16 / ELT_L;
+  constexpr int NCG = BS / (16 / ELT_C);
+  constexpr int64_t kChunkRows = (kWave / NCG) * RPL;
+  TileArgs a = a_in;
+  a.split_rows = kChunkRows * kChunksPerSplit;
+  const int64_t splits = (a.nrows + a.split_rows - 1) / a.split_rows;
+  if (splits > 65535) return hipErrorInvalidValue;
   const int64_t tiles = (a.num_tokens + kTileTokens - 1) / kTileTokens;
   const int64_t blocks = (tiles + kWavesPerBlock - 1) / kWavesPerBlock;
   hipLaunchKernelGGL((paged_tile_kernel<ELT_C, ELT_L, CODEC, LDT, BS, SCATTER>),
-                     dim3(static_cast<uint32_t>(blocks), static_cast<uint32_t>(planes)), dim3(kBlockThreads), 0,
-                     stream, a);
+                     dim3(static_cast<uint32_t>(blocks), static_cast<uint32_t>(planes), static_cast<uint32_t>(splits)),
+                     dim3(kBlockThreads), 0, stream, a);
   return hipGetLastError();
 }
 
