@@ -56,6 +56,34 @@ __device__ __forceinline__ u32x4 ld16_cached(const uint8_t* p) { return *reinter
 __device__ __forceinline__ void st16_cached(uint8_t* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
 // ---------------------------------------------------------------------------
+// Raw buffer accesses (gfx9-family descriptor, stride 0).  The descriptor
+// covers 2 GiB from a wave-uniform base; a lane that passes kOffOob as its
+// offset turns its access into a hardware no-op (loads return zero, stores
+// are dropped), so masked lanes need no branch.  Keeping the memory
+// instructions unconditional lets the compiler count outstanding loads
+// exactly, which keeps a prefetched load in flight across LDS barriers.
+// ---------------------------------------------------------------------------
+using buf_t = __amdgpu_buffer_rsrc_t;
+constexpr uint32_t kOffOob = 0x80000000u;
+constexpr int kBufNT = 2;  // cache policy bits: non-temporal
+
+__device__ __forceinline__ buf_t make_buf(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7FFFFFFF, 0x00020000);
+}
+__device__ __forceinline__ u32x4 buf_ld16(buf_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kBufNT);
+}
+__device__ __forceinline__ void buf_st16(buf_t r, uint32_t off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kBufNT);
+}
+template <int ELT>
+__device__ __forceinline__ void buf_st_elem(buf_t r, uint32_t off, uint32_t v) {
+  if constexpr (ELT == 1) __builtin_amdgcn_raw_buffer_store_b8(static_cast<uint8_t>(v), r, off, 0, 0);
+  else if constexpr (ELT == 2) __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(v), r, off, 0, 0);
+  else __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
 // Wave-level helpers (wave64).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }

@@ -1,0 +1,67 @@
+// Kernel arguments and element helpers shared by the paged-A tile kernels
+// (kv_paged_tiles.hip: workgroup-cooperative kernel, generic element kernel;
+// kv_paged_waves.hip: per-wave gather kernel).
+#pragma once
+
+#include "kv_hip_common.h"
+
+namespace kvhip {
+
+struct TileArgs {
+  uint8_t* cache[2];
+  uint8_t* lin[2];
+  const int64_t* slots;
+  const float* scale[2];
+  const uint64_t* owner;
+  int64_t num_tokens;
+  int64_t num_slots;
+  int64_t nrows;               // NH * HD
+  int64_t head_dim;
+  int64_t num_heads;
+  int64_t cache_layer_stride;  // bytes
+  int64_t lin_layer_stride;    // bytes
+  int64_t lin_token_stride;    // bytes
+  int32_t scale_mode;
+  int32_t fill_zeros;
+  uint32_t epoch;
+  int32_t block_size;          // used by the generic kernel only
+};
+
+constexpr int kTileTokens = 16;
+
+__device__ __forceinline__ float load_scale(const TileArgs& a, int kv, int layer, int64_t head) {
+  const float* s = a.scale[kv];
+  if (a.scale_mode == 0) return s[0];
+  if (a.scale_mode == 1) return s[head];
+  return s[static_cast<int64_t>(layer) * a.num_heads + head];
+}
+
+template <int ELT>
+__device__ __forceinline__ void store_elem(uint8_t* p, uint32_t v) {
+  if constexpr (ELT == 1) *p = static_cast<uint8_t>(v);
+  else if constexpr (ELT == 2) *reinterpret_cast<uint16_t*>(p) = static_cast<uint16_t>(v);
+  else *reinterpret_cast<uint32_t*>(p) = v;
+}
+
+template <int ELT>
+__device__ __forceinline__ uint32_t load_elem(const uint8_t* p) {
+  if constexpr (ELT == 1) return *p;
+  else if constexpr (ELT == 2) return *reinterpret_cast<const uint16_t*>(p);
+  else return *reinterpret_cast<const uint32_t*>(p);
+}
+
+// Element `idx` of a 16-byte piece holding ELT-byte elements.
+template <int ELT>
+__device__ __forceinline__ uint32_t piece_elem(const u32x4& v, int idx) {
+  if constexpr (ELT == 1) return elem8(v, idx);
+  else if constexpr (ELT == 2) return elem16(v, idx);
+  else return v[idx];
+}
+
+// Per-wave LDS-staged gather (kv_paged_waves.hip), used for the FP8
+// dequant-gather: its in-register 8x16 byte transposes need an eighth of the
+// LDS instructions of the cooperative kernel's column reads.
+template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS>
+hipError_t launch_wave_gather(const TileArgs& a, int64_t planes, hipStream_t stream);
+
+}  // namespace kvhip

@@ -6,301 +6,138 @@
 //
 // Design.  A "run" is a maximal set of consecutive tokens whose slots are
 // consecutive inside one block (tokens of one sequence filling one block).
-// One wave owns the runs that start inside its 16-token tile.  For a run the
-// wave walks the NH*HD cache rows in lane tiles of RPL rows x (16 bytes of
-// block columns): every lane issues RPL 16-byte loads of block rows, transposes
-// the tile in registers (v_perm byte selects, no LDS), applies the fused FP8
-// codec if any, and writes 16-byte pieces of token rows.  Both the loads and
-// the stores are full 16-byte vectors; partial column groups only occur at the
-// first/last block of a sequence, where the scatter falls back to element
-// stores so neighbouring slots are never touched.
-//
-// Slots are resolved once per wave (one 64-lane window load), K and V and the
-// layers are separate grid planes, and skipped tokens (slot < 0) are zero
-// filled by the wave that owns them.
+// For one run, the block's rows [r0, r0 + kRows) are a contiguous 4 KiB
+// region of the cache and a [BS tokens x kRows] slab of the linear rows: a
+// small 2-D transpose.  One 256-thread workgroup owns the runs that start in
+// its 16-token tile, for one such row chunk of one (layer, K|V) plane:
+//   * every thread moves exactly one 16-byte cache piece (whole lines per
+//     wave instruction) and ELT_L/ELT_C 16-byte linear pieces (RPL rows of
+//     one token, 256-1024 contiguous bytes per token per wave instruction);
+//   * the two orientations meet in a padded LDS tile: cache pieces are
+//     written/read as rows, linear pieces as RPL column elements;
+//   * the FP8 codec is applied on the linear side (encode before the LDS
+//     write, decode after the LDS read), one scale per linear piece.
+// Each wave keeps at most a few hundred bytes per lane in flight and lives for
+// one chunk, the access shape that reaches the highest HBM copy rate on
+// MI355X.  Partial runs store only their own block columns (element stores at
+// the edges), so neighbouring slots are never touched.  Skipped tokens
+// (slot < 0) are zero filled by the workgroup that owns them.
 #include "kv_hip_common.h"
 #include "kv_launch.h"
+#include "kv_paged_args.h"
 
 namespace kvhip {
 
-struct TileArgs {
-  uint8_t* cache[2];
-  uint8_t* lin[2];
-  const int64_t* slots;
-  const float* scale[2];
-  const uint64_t* owner;
-  int64_t num_tokens;
-  int64_t num_slots;
-  int64_t nrows;               // NH * HD
-  int64_t head_dim;
-  int64_t num_heads;
-  int64_t cache_layer_stride;  // bytes
-  int64_t lin_layer_stride;    // bytes
-  int64_t lin_token_stride;    // bytes
-  int32_t scale_mode;
-  int32_t fill_zeros;
-  uint32_t epoch;
-  int32_t block_size;          // used by the generic kernel only
-  int64_t split_rows;          // cache rows per grid z-slice (tile kernel)
+// ----- the cooperative tile kernel ------------------------------------------------
+
+constexpr int kCoopThreads = 256;
+
+template <int ELT_C, int ELT_L, int BS>
+struct CoopShape {
+  static constexpr int CG = 16 / ELT_C;               // block columns per cache piece
+  static constexpr int NCG = BS / CG;                 // cache pieces per cache row
+  static constexpr int ROWB = BS * ELT_C;             // bytes per cache row of a block
+  static constexpr int kRows = kCoopThreads * 16 / ROWB;  // cache rows per chunk (4 KiB)
+  static constexpr int RPL = 16 / ELT_L;              // rows per linear piece
+  static constexpr int G = kRows / RPL;               // linear pieces per token per chunk
+  static constexpr int PPT = ELT_L / ELT_C;           // linear pieces per thread
+  static constexpr int PITCH = ROWB + 4;              // LDS bytes per cache row (one pad dword)
+  static_assert(BS % CG == 0, "block row must be a whole number of 16-byte pieces");
+  static_assert(BS * G == kCoopThreads * PPT, "linear pieces must cover the chunk");
+  static_assert(G % 8 == 0, "row groups come in eights");
+
+  // Linear piece p of a chunk -> (block column, row group).  Eight
+  // consecutive pieces are eight row groups of one token (128 contiguous
+  // bytes of its row); a wave covers eight tokens.  In the LDS tile the
+  // eight row groups of a wave start 8 rows apart, which with the padded
+  // pitch spreads a column read over distinct banks.
+  __device__ static __forceinline__ int col(int p) { return (p >> 3) % BS; }
+  __device__ static __forceinline__ int grp(int p) { return (p & 7) + 8 * (p / (8 * BS)); }
 };
 
-constexpr int kTileTokens = 16;
-
-__device__ __forceinline__ float load_scale(const TileArgs& a, int kv, int layer, int64_t head) {
-  const float* s = a.scale[kv];
-  if (a.scale_mode == 0) return s[0];
-  if (a.scale_mode == 1) return s[head];
-  return s[static_cast<int64_t>(layer) * a.num_heads + head];
-}
-
-// ----- lane-tile transposes ---------------------------------------------------
-
-// Gather: d[q] holds 16 bytes of cache row (r0+q) for one column group; return
-// the 16-byte linear piece (rows r0..r0+RPL-1) of block column `cc`.
-template <int ELT_C, int ELT_L, int CODEC, int LDT, int RPL>
-__device__ __forceinline__ u32x4 gather_column(const u32x4 (&d)[RPL], int cc, float sc) {
-  u32x4 o;
-  if constexpr (CODEC == kCopy && ELT_C == 2) {
-    static_assert(RPL == 8, "bf16/fp16 tiles are 8x8");
-#pragma unroll
-    for (int k = 0; k < 4; ++k) o[k] = pack16(elem16(d[2 * k], cc), elem16(d[2 * k + 1], cc));
-  } else if constexpr (CODEC == kCopy && ELT_C == 4) {
-    static_assert(RPL == 4, "fp32 tiles are 4x4");
-#pragma unroll
-    for (int k = 0; k < 4; ++k) o[k] = d[k][cc];
-  } else {
-    static_assert(ELT_C == 1, "fp8 caches hold one byte per element");
-    if constexpr (ELT_L == 2) {
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t lo = f32_to_lin<LDT>(fp8_decode<CODEC>(elem8(d[2 * k], cc)) * sc);
-        const uint32_t hi = f32_to_lin<LDT>(fp8_decode<CODEC>(elem8(d[2 * k + 1], cc)) * sc);
-        o[k] = pack16(lo, hi);
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < 4; ++k) o[k] = __float_as_uint(fp8_decode<CODEC>(elem8(d[k], cc)) * sc);
-    }
-  }
-  return o;
-}
-
-// Scatter: in[cc] holds the 16-byte linear piece (rows r0..r0+RPL-1) of the
-// token in block column cc; element (q, cc) of the tile in cache encoding.
-// FAST selects the hoisted-reciprocal quotient (r = RN(1/sc)); the caller
-// guarantees the fast range for the scale and every input of the tile.
-template <int ELT_C, int ELT_L, int CODEC, int LDT, bool FAST = false>
-__device__ __forceinline__ uint32_t scatter_elem(const u32x4& in_cc, int q, float sc, float r = 0.0f) {
-  if constexpr (CODEC == kCopy && ELT_C == 2) {
-    return elem16(in_cc, q);
-  } else if constexpr (CODEC == kCopy && ELT_C == 4) {
-    return in_cc[q];
-  } else {
-    float x;
-    if constexpr (ELT_L == 2) x = lin_to_f32<LDT>(elem16(in_cc, q));
-    else x = __uint_as_float(in_cc[q]);
-    if constexpr (FAST) return fp8_encode_fast<CODEC>(quot_fast(x, sc, r));
-    else return fp8_encode<CODEC>(div_rn(x, sc));
-  }
-}
-
-template <int ELT_C, int ELT_L, int CODEC, int LDT, int CG, bool FAST = false>
-__device__ __forceinline__ u32x4 scatter_row(const u32x4 (&in)[CG], int q, float sc, float r = 0.0f) {
-  u32x4 o;
-  if constexpr (ELT_C == 2) {
-#pragma unroll
-    for (int w = 0; w < 4; ++w)
-      o[w] = pack16(scatter_elem<ELT_C, ELT_L, CODEC, LDT, FAST>(in[2 * w], q, sc, r),
-                    scatter_elem<ELT_C, ELT_L, CODEC, LDT, FAST>(in[2 * w + 1], q, sc, r));
-  } else if constexpr (ELT_C == 4) {
-#pragma unroll
-    for (int w = 0; w < 4; ++w) o[w] = scatter_elem<ELT_C, ELT_L, CODEC, LDT, FAST>(in[w], q, sc, r);
-  } else {
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      uint32_t acc = 0;
-#pragma unroll
-      for (int b = 0; b < 4; ++b)
-        acc |= scatter_elem<ELT_C, ELT_L, CODEC, LDT, FAST>(in[4 * w + b], q, sc, r) << (8 * b);
-      o[w] = acc;
-    }
-  }
-  return o;
-}
-
-// Writes the RPL cache rows of one lane tile through `put(q, row)`.  FP8
-// tiles whose scale and inputs are all in the fast range use the hoisted
-// reciprocal; any other tile divides exactly.
-template <int ELT_C, int ELT_L, int CODEC, int LDT, int CG, int RPL, typename Put>
-__device__ __forceinline__ void encode_tile(const u32x4 (&in)[CG], float sc, Put put) {
-  if constexpr (CODEC == kCopy) {
-#pragma unroll
-    for (int q = 0; q < RPL; ++q) put(q, scatter_row<ELT_C, ELT_L, CODEC, LDT, CG>(in, q, sc));
-  } else {
-    InputRange<LDT> range;
-#pragma unroll
-    for (int cc = 0; cc < CG; ++cc) range.add(in[cc]);
-    if (fast_scale_ok(sc) && range.in_fast_range()) {
-      const float r = 1.0f / sc;
-#pragma unroll
-      for (int q = 0; q < RPL; ++q) put(q, scatter_row<ELT_C, ELT_L, CODEC, LDT, CG, true>(in, q, sc, r));
-    } else {
-#pragma unroll
-      for (int q = 0; q < RPL; ++q) put(q, scatter_row<ELT_C, ELT_L, CODEC, LDT, CG>(in, q, sc));
-    }
-  }
-}
-
-template <int ELT>
-__device__ __forceinline__ void store_elem(uint8_t* p, uint32_t v) {
-  if constexpr (ELT == 1) *p = static_cast<uint8_t>(v);
-  else if constexpr (ELT == 2) *reinterpret_cast<uint16_t*>(p) = static_cast<uint16_t>(v);
-  else *reinterpret_cast<uint32_t*>(p) = v;
-}
-
-// Element `idx` of a 16-byte cache piece, in cache encoding.
-template <int ELT>
-__device__ __forceinline__ uint32_t piece_elem(const u32x4& v, int idx) {
-  if constexpr (ELT == 1) return elem8(v, idx);
-  else if constexpr (ELT == 2) return elem16(v, idx);
-  else return v[idx];
-}
-
-// ----- LDS staging of one block run ----------------------------------------------
-//
-// A chunk is 64 lane tiles of RPL rows x CG block columns: kChunkRows cache
-// rows of one block, i.e. RPL KiB of contiguous cache bytes.  The cache side
-// of a chunk moves as RPL coalesced wave instructions (lane l takes piece
-// k*64 + l); the lane tiles are exchanged through the wave's private LDS
-// region, so both the cache and the linear side issue whole cache lines.
-// Piece s of the chunk lives at LDS slot lds_slot(s): the low four bits are
-// XOR-swizzled with the row group so that 16 consecutive lanes hit 16
-// distinct 16-byte bank groups in both access patterns.
-
-constexpr int log2_const(int v) { return v <= 1 ? 0 : 1 + log2_const(v / 2); }
-
-template <int RPL, int NCG>
-__device__ __forceinline__ int lds_slot(int s) {
-  constexpr int kGroupShift = log2_const(RPL * NCG);
-  return s ^ (((s >> kGroupShift) * NCG) & 15);
-}
-
-// Orders the wave's LDS writes before its later LDS reads (and the reads
-// before the next writes).  LDS executes one wave's requests in issue order;
-// the wait plus the code-motion barrier keep the compiler from reordering.
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), other counters untouched
-  __builtin_amdgcn_wave_barrier();
-}
-
-template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS, bool SCATTER>
-__device__ __forceinline__ void staged_run(const TileArgs& a, uint8_t* const cache_blk, uint8_t* const lin_run,
-                                           const int c0, const int c1, const int kv, const int layer,
-                                           u32x4* const lds, const int64_t r_begin, const int64_t r_end,
-                                           const int rot) {
+// Linear piece (RPL rows of block column c) assembled from the LDS tile, in
+// the linear element type.
+template <int ELT_C, int ELT_L, int CODEC, int LDT, int PITCH>
+__device__ __forceinline__ u32x4 lds_column_piece(const uint8_t* tile, int row0, int c, float sc) {
   constexpr int RPL = 16 / ELT_L;
-  constexpr int CG = 16 / ELT_C;
-  constexpr int NCG = BS / CG;
-  constexpr int kChunkRows = (kWave / NCG) * RPL;
-  const int lane = lane_id();
-  const int rg = lane / NCG;
-  const int ct = lane % NCG;
-  const bool full = (c0 == 0) && (c1 == BS);
-
-  // Chunks are visited starting at chunk `rot` (different per wave), so the
-  // waves in flight spread over all address phases of the block and of the
-  // token rows instead of all streaming the same offsets at the same time.
-  const int nchunks = static_cast<int>((r_end - r_begin + kChunkRows - 1) / kChunkRows);
-  int chunk_id = rot % nchunks;
-  for (int ci = 0; ci < nchunks; ++ci, chunk_id = (chunk_id + 1 == nchunks) ? 0 : chunk_id + 1) {
-    const int64_t r0 = r_begin + static_cast<int64_t>(chunk_id) * kChunkRows;
-    uint8_t* const chunk = cache_blk + r0 * BS * ELT_C;
-    const int64_t trow = r0 + rg * RPL;  // first cache row of this lane's tile
-    const bool tile_in = trow < a.nrows;
-    float sc = 1.0f;
-    if constexpr (CODEC != kCopy) {
-      if (tile_in) sc = load_scale(a, kv, layer, trow / a.head_dim);
+  const uint8_t* p = tile + row0 * PITCH + c * ELT_C;
+  u32x4 o;
+  if constexpr (CODEC == kCopy && ELT_C == 2) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = pack16(load_elem<2>(p + (2 * k) * PITCH), load_elem<2>(p + (2 * k + 1) * PITCH));
+  } else if constexpr (CODEC == kCopy && ELT_C == 4) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = load_elem<4>(p + k * PITCH);
+  } else if constexpr (ELT_L == 2) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t lo = f32_to_lin<LDT>(fp8_decode<CODEC>(load_elem<1>(p + (2 * k) * PITCH)) * sc);
+      const uint32_t hi = f32_to_lin<LDT>(fp8_decode<CODEC>(load_elem<1>(p + (2 * k + 1) * PITCH)) * sc);
+      o[k] = pack16(lo, hi);
     }
-    uint8_t* const lrow = lin_run + trow * ELT_L;
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = __float_as_uint(fp8_decode<CODEC>(load_elem<1>(p + k * PITCH)) * sc);
+  }
+  static_assert(RPL * ELT_L == 16, "a linear piece is 16 bytes");
+  return o;
+}
 
-    if constexpr (!SCATTER) {
-      u32x4 v[RPL];
+// Writes the RPL elements of one linear piece into column c of the LDS tile,
+// in cache encoding.  FAST selects the hoisted-reciprocal FP8 quotient.
+template <int ELT_C, int ELT_L, int CODEC, int LDT, int PITCH, bool FAST>
+__device__ __forceinline__ void lds_put_column(uint8_t* tile, int row0, int c, const u32x4& in, float sc, float r) {
+  constexpr int RPL = 16 / ELT_L;
+  uint8_t* p = tile + row0 * PITCH + c * ELT_C;
 #pragma unroll
-      for (int k = 0; k < RPL; ++k) {
-        const int pc = k * kWave + lane;
-        if (r0 + pc / NCG < a.nrows) v[k] = ld16(chunk + pc * 16);
-      }
-#pragma unroll
-      for (int k = 0; k < RPL; ++k) lds[lds_slot<RPL, NCG>(k * kWave + lane)] = v[k];
-      wave_lds_sync();
-      u32x4 d[RPL];
-#pragma unroll
-      for (int q = 0; q < RPL; ++q) d[q] = lds[lds_slot<RPL, NCG>((rg * RPL + q) * NCG + ct)];
-      wave_lds_sync();
-      if (tile_in) {
-#pragma unroll
-        for (int cc = 0; cc < CG; ++cc) {
-          const int c = ct * CG + cc;
-          if (c >= c0 && c < c1)
-            st16(lrow + static_cast<int64_t>(c - c0) * a.lin_token_stride,
-                 gather_column<ELT_C, ELT_L, CODEC, LDT, RPL>(d, cc, sc));
-        }
-      }
+  for (int i = 0; i < RPL; ++i) {
+    uint32_t v;
+    if constexpr (CODEC == kCopy) {
+      v = piece_elem<ELT_L>(in, i);
     } else {
-      u32x4 in[CG];
-#pragma unroll
-      for (int cc = 0; cc < CG; ++cc) {
-        const int c = ct * CG + cc;
-        in[cc] = u32x4{0u, 0u, 0u, 0u};
-        if (tile_in && c >= c0 && c < c1) in[cc] = ld16(lrow + static_cast<int64_t>(c - c0) * a.lin_token_stride);
-      }
-      encode_tile<ELT_C, ELT_L, CODEC, LDT, CG, RPL>(
-          in, sc, [&](int q, const u32x4& row) { lds[lds_slot<RPL, NCG>((rg * RPL + q) * NCG + ct)] = row; });
-      wave_lds_sync();
-#pragma unroll
-      for (int k = 0; k < RPL; ++k) {
-        const int pc = k * kWave + lane;
-        const u32x4 w = lds[lds_slot<RPL, NCG>(pc)];
-        if (r0 + pc / NCG >= a.nrows) continue;
-        uint8_t* const dst = chunk + pc * 16;
-        const int lo = (pc % NCG) * CG;
-        if (full || (lo >= c0 && lo + CG <= c1)) {
-          st16(dst, w);
-        } else {
-#pragma unroll
-          for (int cc = 0; cc < CG; ++cc)
-            if (lo + cc >= c0 && lo + cc < c1) store_elem<ELT_C>(dst + cc * ELT_C, piece_elem<ELT_C>(w, cc));
-        }
-      }
-      wave_lds_sync();
+      const float x = (ELT_L == 2) ? lin_to_f32<LDT>(elem16(in, i)) : __uint_as_float(in[i]);
+      if constexpr (FAST) v = fp8_encode_fast<CODEC>(quot_fast(x, sc, r));
+      else v = fp8_encode<CODEC>(div_rn(x, sc));
     }
+    store_elem<ELT_C>(p + i * PITCH, v);
   }
 }
 
-// ----- the tile kernel ---------------------------------------------------------
+// Workgroup barrier for the LDS tile only: waits for this wave's LDS
+// accesses, not for its outstanding global loads (the next chunk's prefetch
+// stays in flight across the barrier).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Chunks of one run handled by one workgroup (grid z covers the rest).
+constexpr int kChunksPerGroup = 4;
 
 template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS, bool SCATTER>
-__global__ __launch_bounds__(kBlockThreads) void paged_tile_kernel(const TileArgs a) {
-  constexpr int RPL = 16 / ELT_L;  // cache rows per lane tile
-  constexpr int CG = 16 / ELT_C;   // block columns per 16-byte group
-  static_assert(BS % CG == 0, "block row must be a whole number of 16-byte groups");
+__global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs a) {
+  using S = CoopShape<ELT_C, ELT_L, BS>;
+  constexpr int CG = S::CG, NCG = S::NCG, ROWB = S::ROWB, kRows = S::kRows;
+  constexpr int RPL = S::RPL, PPT = S::PPT, PITCH = S::PITCH;
   static_assert(kTileTokens + BS + 1 <= kWave, "run window must fit one wave");
+  __shared__ __align__(16) uint8_t tile[kRows * PITCH];
 
+  const int tid = static_cast<int>(threadIdx.x);
   const int lane = lane_id();
-  const int64_t tile = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();
-  const int64_t t0 = tile * kTileTokens;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kTileTokens;
   if (t0 >= a.num_tokens) return;
   const int plane = static_cast<int>(blockIdx.y);
   const int layer = plane >> 1;
   const int kv = plane & 1;
+  // Rows [rb, re) of the block, in chunks of kRows.
+  const int64_t rb = static_cast<int64_t>(blockIdx.z) * (kRows * kChunksPerGroup);
+  const int64_t re = (rb + kRows * kChunksPerGroup < a.nrows) ? rb + kRows * kChunksPerGroup : a.nrows;
+  const int nchunks = static_cast<int>((re - rb + kRows - 1) / kRows);
   uint8_t* const cache = a.cache[kv] + static_cast<int64_t>(layer) * a.cache_layer_stride;
   uint8_t* const lin = a.lin[kv] + static_cast<int64_t>(layer) * a.lin_layer_stride;
-  // The z-slice of the grid picks a range of cache rows (a whole number of
-  // LDS chunks), so one run is spread over several independent waves.
-  const int64_t r_begin = static_cast<int64_t>(blockIdx.z) * a.split_rows;
-  const int64_t r_end = (r_begin + a.split_rows < a.nrows) ? r_begin + a.split_rows : a.nrows;
 
-  // Slot window: lane i holds token t0 - 1 + i.
+  // Slot window, identical in every wave: lane i holds token t0 - 1 + i.
   const int64_t t = t0 - 1 + lane;
   int64_t s = -1;
   if (t >= 0 && t < a.num_tokens) s = a.slots[t];
@@ -318,9 +155,32 @@ __global__ __launch_bounds__(kBlockThreads) void paged_tile_kernel(const TileArg
   const uint64_t window = ((1ull << ntile) - 1ull) << 1;
   uint64_t heads = vmask & ~cmask & window;
 
-  const int ngroups = static_cast<int>(r_end / RPL);
-  __shared__ u32x4 lds_all[kWavesPerBlock * kWave * RPL];
-  u32x4* const lds = lds_all + wave_in_block() * (kWave * RPL);
+  // This thread's cache piece (row pr, column group pg) and linear pieces
+  // (block column lc[j], row group lq[j]) within every chunk.
+  const int pr = tid / NCG;
+  const int pg = tid % NCG;
+  int lc[PPT], lq[PPT];
+#pragma unroll
+  for (int j = 0; j < PPT; ++j) {
+    lc[j] = S::col(tid + j * kCoopThreads);
+    lq[j] = S::grp(tid + j * kCoopThreads);
+  }
+  auto prow_in = [&](int k) { return rb + static_cast<int64_t>(k) * kRows + pr < re; };
+  auto lrow_in = [&](int k, int j) {
+    return rb + static_cast<int64_t>(k) * kRows + static_cast<int64_t>(lq[j]) * RPL < re;
+  };
+  // FP8 scale of linear piece j in chunk k.  The row is clamped into the
+  // block so the load is unconditional (the value of an out-of-range piece is
+  // never used); chunk k+1's scales are fetched together with its payload.
+  auto piece_scale = [&](int k, int j) -> float {
+    if constexpr (CODEC == kCopy) {
+      return 1.0f;
+    } else {
+      int64_t row = rb + static_cast<int64_t>(k) * kRows + static_cast<int64_t>(lq[j]) * RPL;
+      row = row < a.nrows ? row : a.nrows - 1;
+      return load_scale(a, kv, layer, row / a.head_dim);
+    }
+  };
 
   while (heads) {
     const int i = __builtin_ctzll(heads);
@@ -330,68 +190,102 @@ __global__ __launch_bounds__(kBlockThreads) void paged_tile_kernel(const TileArg
     const int64_t sh = readlane64(s, i);
     const int64_t blk = sh / BS;
     const int c0 = static_cast<int>(sh - blk * BS);
-    const int64_t tf = t0 - 1 + i;
     const int c1 = c0 + len;
+    const int64_t tf = t0 - 1 + i;
+    // Wave-uniform descriptors: the block's rows [rb, re) and the run's
+    // first linear row at row rb.  Offsets of masked lanes are kOffOob.
+    const buf_t cbuf = make_buf(cache + (blk * a.nrows + rb) * ROWB);
+    const buf_t lbuf = make_buf(lin + tf * a.lin_token_stride + rb * ELT_L);
+    auto coff = [&](int k) -> uint32_t {
+      return prow_in(k) ? static_cast<uint32_t>(k * kRows * ROWB + tid * 16) : kOffOob;
+    };
+    auto loff = [&](int k, int j) -> uint32_t {
+      const int c = lc[j];
+      return (c >= c0 && c < c1 && lrow_in(k, j))
+                 ? static_cast<uint32_t>((c - c0) * a.lin_token_stride + k * kRows * ELT_L + lq[j] * 16)
+                 : kOffOob;
+    };
 
-    // Runs that touch every 16-byte column group of the block row go through
-    // LDS (whole-line traffic on both sides); shorter runs use lane tiles
-    // that load or store only the column groups they cover.
-    if (c0 < CG && c1 > BS - CG) {
-      staged_run<ELT_C, ELT_L, CODEC, LDT, BS, SCATTER>(a, cache + blk * a.nrows * BS * ELT_C,
-                                                        lin + tf * a.lin_token_stride, c0, c1, kv, layer, lds,
-                                                        r_begin, r_end, static_cast<int>(tile & 0xFFFF));
-      continue;
-    }
-
-    const int j0 = c0 / CG;
-    const int j1 = (c1 - 1) / CG;
-    for (int g = static_cast<int>(r_begin / RPL) + lane; g < ngroups; g += kWave) {
-      const int64_t r0 = static_cast<int64_t>(g) * RPL;
-      float sc = 1.0f;
-      if constexpr (CODEC != kCopy) sc = load_scale(a, kv, layer, r0 / a.head_dim);
-      uint8_t* const crow = cache + (blk * a.nrows + r0) * BS * ELT_C;
-      uint8_t* const lrow = lin + tf * a.lin_token_stride + r0 * ELT_L;
-      // One 16-byte column group at a time keeps the register tile at RPL
-      // (gather) or CG (scatter) vectors.
-#pragma unroll 1
-      for (int j = j0; j <= j1; ++j) {
-        const int lo = j * CG;
-        uint8_t* const cgrp = crow + lo * ELT_C;
-        if constexpr (!SCATTER) {
-          u32x4 d[RPL];
+    if constexpr (!SCATTER) {
+      u32x4 nxt = buf_ld16(cbuf, coff(0));
+      float scn[PPT];
 #pragma unroll
-          for (int q = 0; q < RPL; ++q) d[q] = ld16_cached(cgrp + q * BS * ELT_C);
+      for (int j = 0; j < PPT; ++j) scn[j] = piece_scale(0, j);
+      for (int k = 0; k < nchunks; ++k) {
+        const u32x4 cur = nxt;
+        float scc[PPT];
 #pragma unroll
-          for (int cc = 0; cc < CG; ++cc) {
-            const int c = lo + cc;
-            if (c >= c0 && c < c1)
-              st16(lrow + static_cast<int64_t>(c - c0) * a.lin_token_stride,
-                   gather_column<ELT_C, ELT_L, CODEC, LDT, RPL>(d, cc, sc));
+        for (int j = 0; j < PPT; ++j) scc[j] = scn[j];
+        nxt = buf_ld16(cbuf, (k + 1 < nchunks) ? coff(k + 1) : kOffOob);
+#pragma unroll
+        for (int j = 0; j < PPT; ++j) scn[j] = piece_scale(k + 1 < nchunks ? k + 1 : k, j);
+        if (prow_in(k)) {
+          uint32_t* const d = reinterpret_cast<uint32_t*>(tile + pr * PITCH + pg * 16);
+          d[0] = cur[0]; d[1] = cur[1]; d[2] = cur[2]; d[3] = cur[3];
+        }
+        lds_barrier();
+#pragma unroll
+        for (int j = 0; j < PPT; ++j)
+          buf_st16(lbuf, loff(k, j),
+                   lds_column_piece<ELT_C, ELT_L, CODEC, LDT, PITCH>(tile, lq[j] * RPL, lc[j], scc[j]));
+        lds_barrier();
+      }
+    } else {
+      u32x4 nxt[PPT];
+      float scn[PPT];
+#pragma unroll
+      for (int j = 0; j < PPT; ++j) {
+        nxt[j] = buf_ld16(lbuf, loff(0, j));
+        scn[j] = piece_scale(0, j);
+      }
+      const bool full_run = (c0 == 0) && (c1 == BS);
+      for (int k = 0; k < nchunks; ++k) {
+        u32x4 in[PPT];
+        float scc[PPT];
+#pragma unroll
+        for (int j = 0; j < PPT; ++j) {
+          in[j] = nxt[j];
+          scc[j] = scn[j];
+          nxt[j] = buf_ld16(lbuf, (k + 1 < nchunks) ? loff(k + 1, j) : kOffOob);
+          scn[j] = piece_scale(k + 1 < nchunks ? k + 1 : k, j);
+        }
+#pragma unroll
+        for (int j = 0; j < PPT; ++j) {
+          const int c = lc[j];
+          if (c < c0 || c >= c1 || !lrow_in(k, j)) continue;
+          const float sc = scc[j];
+          bool fast = true;
+          if constexpr (CODEC != kCopy) {
+            InputRange<LDT> range;
+            range.add(in[j]);
+            fast = fast_scale_ok(sc) && range.in_fast_range();
           }
-        } else {
-          u32x4 in[CG];
-#pragma unroll
-          for (int cc = 0; cc < CG; ++cc) {
-            const int c = lo + cc;
-            in[cc] = u32x4{0u, 0u, 0u, 0u};
-            if (c >= c0 && c < c1) in[cc] = ld16(lrow + static_cast<int64_t>(c - c0) * a.lin_token_stride);
-          }
-          if (lo >= c0 && lo + CG <= c1) {
-            encode_tile<ELT_C, ELT_L, CODEC, LDT, CG, RPL>(
-                in, sc, [&](int q, const u32x4& row) { st16_cached(cgrp + q * BS * ELT_C, row); });
+          if (fast) {
+            const float r = (CODEC != kCopy) ? 1.0f / sc : 0.0f;
+            lds_put_column<ELT_C, ELT_L, CODEC, LDT, PITCH, CODEC != kCopy>(tile, lq[j] * RPL, c, in[j], sc, r);
           } else {
-#pragma unroll
-            for (int q = 0; q < RPL; ++q) {
-#pragma unroll
-              for (int cc = 0; cc < CG; ++cc) {
-                const int c = lo + cc;
-                if (c >= c0 && c < c1)
-                  store_elem<ELT_C>(cgrp + (q * BS + cc) * ELT_C,
-                                    scatter_elem<ELT_C, ELT_L, CODEC, LDT>(in[cc], q, sc));
-              }
-            }
+            lds_put_column<ELT_C, ELT_L, CODEC, LDT, PITCH, false>(tile, lq[j] * RPL, c, in[j], sc, 0.0f);
           }
         }
+        lds_barrier();
+        const uint32_t* const d = reinterpret_cast<const uint32_t*>(tile + pr * PITCH + pg * 16);
+        const u32x4 w = {d[0], d[1], d[2], d[3]};
+        const uint32_t off = coff(k);
+        const int lo = pg * CG;
+        if (full_run) {
+          buf_st16(cbuf, off, w);
+        } else {
+          // Whole pieces inside the run go as one vector; edge pieces store
+          // only their in-run columns.
+          const bool whole = lo >= c0 && lo + CG <= c1;
+          buf_st16(cbuf, whole ? off : kOffOob, w);
+#pragma unroll
+          for (int cc = 0; cc < CG; ++cc) {
+            const bool mine = !whole && off != kOffOob && lo + cc >= c0 && lo + cc < c1;
+            buf_st_elem<ELT_C>(cbuf, mine ? off + cc * ELT_C : kOffOob, piece_elem<ELT_C>(w, cc));
+          }
+        }
+        lds_barrier();
       }
     }
   }
@@ -399,13 +293,12 @@ __global__ __launch_bounds__(kBlockThreads) void paged_tile_kernel(const TileArg
   if constexpr (!SCATTER) {
     if (a.fill_zeros) {
       uint64_t skipped = ~vmask & window;
-      const int64_t row_bytes = r_end * ELT_L;
       const u32x4 zero = {0u, 0u, 0u, 0u};
       while (skipped) {
         const int i = __builtin_ctzll(skipped);
         skipped &= skipped - 1;
         uint8_t* const row = lin + (t0 - 1 + i) * a.lin_token_stride;
-        for (int64_t k = r_begin * ELT_L + static_cast<int64_t>(lane) * 16; k < row_bytes; k += kWave * 16)
+        for (int64_t k = rb * ELT_L + static_cast<int64_t>(tid) * 16; k < re * ELT_L; k += kCoopThreads * 16)
           st16(row + k, zero);
       }
     }
@@ -413,13 +306,6 @@ __global__ __launch_bounds__(kBlockThreads) void paged_tile_kernel(const TileArg
 }
 
 // ----- generic element-wise kernel (any block size / alignment) ----------------
-
-template <int ELT>
-__device__ __forceinline__ uint32_t load_elem(const uint8_t* p) {
-  if constexpr (ELT == 1) return *p;
-  else if constexpr (ELT == 2) return *reinterpret_cast<const uint16_t*>(p);
-  else return *reinterpret_cast<const uint32_t*>(p);
-}
 
 template <int ELT_C, int ELT_L, int CODEC, int LDT, bool SCATTER>
 __global__ __launch_bounds__(kBlockThreads) void paged_elem_kernel(const TileArgs a) {
@@ -477,22 +363,16 @@ hipError_t launch_elem(const TileArgs& a, int64_t planes, hipStream_t stream) {
   return hipGetLastError();
 }
 
-constexpr int kChunksPerSplit = 1;
-
 template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS, bool SCATTER>
-hipError_t launch_tile(const TileArgs& a_in, int64_t planes, hipStream_t stream) {
-  constexpr int RPL = 16 / ELT_L;
-  constexpr int NCG = BS / (16 / ELT_C);
-  constexpr int64_t kChunkRows = (kWave / NCG) * RPL;
-  TileArgs a = a_in;
-  a.split_rows = kChunkRows * kChunksPerSplit;
-  const int64_t splits = (a.nrows + a.split_rows - 1) / a.split_rows;
-  if (splits > 65535) return hipErrorInvalidValue;
+hipError_t launch_tile(const TileArgs& a, int64_t planes, hipStream_t stream) {
+  using S = CoopShape<ELT_C, ELT_L, BS>;
+  const int64_t chunks = (a.nrows + S::kRows * kChunksPerGroup - 1) / (S::kRows * kChunksPerGroup);
+  if (chunks > 65535) return hipErrorInvalidValue;
   const int64_t tiles = (a.num_tokens + kTileTokens - 1) / kTileTokens;
-  const int64_t blocks = (tiles + kWavesPerBlock - 1) / kWavesPerBlock;
+  if (tiles > 0x7FFFFFFF) return hipErrorInvalidValue;
   hipLaunchKernelGGL((paged_tile_kernel<ELT_C, ELT_L, CODEC, LDT, BS, SCATTER>),
-                     dim3(static_cast<uint32_t>(blocks), static_cast<uint32_t>(planes), static_cast<uint32_t>(splits)),
-                     dim3(kBlockThreads), 0, stream, a);
+                     dim3(static_cast<uint32_t>(tiles), static_cast<uint32_t>(planes), static_cast<uint32_t>(chunks)),
+                     dim3(kCoopThreads), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -502,8 +382,14 @@ hipError_t dispatch_bs(const TileArgs& a, int64_t bs, bool fast, int64_t planes,
     if constexpr (ELT_C != 1) {
       if (bs == 8) return launch_tile<ELT_C, ELT_L, CODEC, LDT, 8, SCATTER>(a, planes, stream);
     }
-    if (bs == 16) return launch_tile<ELT_C, ELT_L, CODEC, LDT, 16, SCATTER>(a, planes, stream);
-    if (bs == 32) return launch_tile<ELT_C, ELT_L, CODEC, LDT, 32, SCATTER>(a, planes, stream);
+    if constexpr (ELT_C == 1 && !SCATTER) {
+      // FP8 dequant-gather: per-wave kernel (kv_paged_waves.hip).
+      if (bs == 16) return launch_wave_gather<ELT_C, ELT_L, CODEC, LDT, 16>(a, planes, stream);
+      if (bs == 32) return launch_wave_gather<ELT_C, ELT_L, CODEC, LDT, 32>(a, planes, stream);
+    } else {
+      if (bs == 16) return launch_tile<ELT_C, ELT_L, CODEC, LDT, 16, SCATTER>(a, planes, stream);
+      if (bs == 32) return launch_tile<ELT_C, ELT_L, CODEC, LDT, 32, SCATTER>(a, planes, stream);
+    }
   }
   return launch_elem<ELT_C, ELT_L, CODEC, LDT, SCATTER>(a, planes, stream);
 }
