@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""KV-copy throughput on one MI355X: BASELINE.json configs[1] (headline) plus configs 3 and 4.
+"""KV-copy throughput on one MI355X: BASELINE.json configs[1] (headline) plus configs 1, 3, 4 and 5.
 
 Headline workload: 32 layers of Llama-3-8B KV caches
 [8192 blocks, 16, 8 kv-heads, 128] bf16 (paged layout [NB, NH, HD, BS]),
@@ -15,9 +15,16 @@ once, outside the timed region.
 ``value`` = algorithmic bytes (payload read + payload written + 8 B per slot)
 of K steps / device time of the K steps between HIP events, in GB/s.
 ``roofline`` is reported for the dominant kernel (the direction with the
-larger total time) against the 8 TB/s HBM peak.  ``cpu_baseline`` times the
+larger total time) against the 8 TB/s HBM peak; its ``traffic`` comes from the
+committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes.  ``cpu_baseline`` times the
 numpy oracle (oracle/kv_oracle.py, a port of the reference algorithm) on a
 bounded sample of the same workload on this host and scales by bytes.
+
+The other configs are reported under ``extra`` with the same byte convention.
+Their launches are short (0.01-0.3 ms), so they are timed in batches of
+back-to-back launches between two events (host launch overhead hidden behind
+device work); each is also checked against the oracle or by a round trip
+outside the timed region.
 """
 
 from __future__ import annotations
@@ -101,6 +108,34 @@ class EventTimer:
 
     def ms(self) -> list[float]:
         return [a.elapsed_time(b) for a, b in self.pairs]
+
+
+def batched_ms(fn, launches: int = 20, reps: int = 5) -> np.ndarray:
+    """Per-launch device ms of ``fn`` from ``reps`` batches of ``launches`` back-to-back calls."""
+    per = []
+    for _ in range(reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(launches):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        per.append(e0.elapsed_time(e1) / launches)
+    return np.array(per)
+
+
+def rate(nbytes: int, ms: np.ndarray, tokens: int | None = None) -> dict:
+    out = {"p50_ms": float(np.median(ms)), "min_ms": float(ms.min()), "max_ms": float(ms.max()),
+           "gbs": nbytes / (np.median(ms) * 1e-3) / 1e9}
+    out["pct_of_peak"] = round(100.0 * out["gbs"] / HBM_PEAK_GBS, 2)
+    if tokens is not None:
+        out["tokens_per_ms"] = tokens / float(np.median(ms))
+    return out
+
+
+def _stream() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
 def _bind(lib, name: str, nargs_ptr: int, nargs_i64: int):
@@ -190,9 +225,40 @@ def bench_config2(steps: int, warmup: int) -> dict:
     }
 
 
-def bench_config3(steps: int, warmup: int) -> dict:
-    """FP8 E4M3 quant-store into a uint8 paged cache and dequant-gather to bf16, per-head scales."""
-    import musa_aiter
+def bench_config1() -> dict:
+    """Single-layer paged->linear K/V gather, fp16, 1024 blocks, 32 seqs len U[1,512]."""
+    from musa_aiter.ops import _hip
+    from oracle import kv_oracle as ko
+    from tests.kvgen import bits
+
+    dev = torch.device("cuda", 0)
+    nb = 1024
+    slots_np = make_slots(1001, 32, 1, 512, nb, BS)
+    t = int(slots_np.shape[0])
+    gen = torch.Generator(device=dev).manual_seed(1)
+    kc = torch.randn((nb, NH, HD, BS), generator=gen, device=dev, dtype=torch.float16)
+    vc = torch.randn((nb, NH, HD, BS), generator=gen, device=dev, dtype=torch.float16)
+    slots = torch.from_numpy(slots_np).to(dev)
+    ok = torch.empty((t, NH, HD), dtype=torch.float16, device=dev)
+    ov = torch.empty_like(ok)
+    fn = _bind(_hip.library(), "musa_aiter_kv_paged_to_linear_half", 5, 5)
+    args = (kc.data_ptr(), vc.data_ptr(), slots.data_ptr(), ok.data_ptr(), ov.data_ptr(), t, nb, NH, HD, BS)
+    _check(fn(*args, _stream()), "cfg1 gather")
+    torch.cuda.synchronize()
+    parity = bool(np.array_equal(bits(ok), ko.paged_to_linear(bits(kc), slots_np))
+                  and np.array_equal(bits(ov), ko.paged_to_linear(bits(vc), slots_np)))
+    ms = batched_ms(lambda: _check(fn(*args, _stream()), "cfg1 gather"), launches=50)
+    nbytes = 2 * (2 * t * ROW * 2) + 8 * t
+    return {"tokens": t, "bytes_per_call": nbytes, "gather": rate(nbytes, ms, t), "parity_vs_oracle": parity,
+            "api": "musa_aiter_kv_paged_to_linear_half"}
+
+
+def bench_config3() -> dict:
+    """FP8 quant-store into uint8 paged caches and dequant-gather to bf16: E4M3 per-head scales
+    (headline), E4M3 scalar scale, E5M2 per-head scales, through the reference-named vec4 C-ABI entries."""
+    from musa_aiter.ops import _hip
+    from oracle import kv_oracle as ko
+    from tests.kvgen import bits
 
     dev = torch.device("cuda", 0)
     slots_np = make_slots(1003, 64, 128, 4096, NB, BS)
@@ -204,48 +270,60 @@ def bench_config3(steps: int, warmup: int) -> dict:
     for x in (kl, vl):
         x.mul_(torch.where(torch.rand(x.shape, generator=gen, device=dev) < 0.01, 50.0, 1.0))
     kl, vl = kl.to(torch.bfloat16), vl.to(torch.bfloat16)
-    ks = (kl.float().abs().amax(dim=(0, 2)) / 448.0).contiguous()
-    vs = (vl.float().abs().amax(dim=(0, 2)) / 448.0).contiguous()
+    amax_k = kl.float().abs().amax(dim=(0, 2))
+    amax_v = vl.float().abs().amax(dim=(0, 2))
     kc = torch.zeros((NB, NH, HD, BS), dtype=torch.uint8, device=dev)
     vc = torch.zeros_like(kc)
     ok = torch.empty_like(kl)
     ov = torch.empty_like(vl)
-    for _ in range(warmup):
-        musa_aiter.kv_linear_to_paged_fp8(kl, vl, kc, vc, slots, ks, vs)
-        musa_aiter.kv_paged_fp8_to_linear(kc, vc, slots, ks, vs, out_k=ok, out_v=ov)
-    torch.cuda.synchronize()
-    # Time the device work only: bind the generic entry with validated arguments.
-    from musa_aiter.ops import _hip
+    lib = _hip.library()
+    nbytes = 2 * t * ROW * (2 + 1) + 8 * t
+    sample = min(t, 2048)
+    out = {"tokens": t, "bytes_per_call": nbytes}
+    variants = (("e4m3_per_head", "e4m3", 1, 448.0), ("e4m3_scalar", "e4m3", 0, 448.0),
+                ("e5m2_per_head", "e5m2", 1, 57344.0))
+    for name, fmt, mode, fmax in variants:
+        if mode == 1:
+            ks, vs = (amax_k / fmax).contiguous(), (amax_v / fmax).contiguous()
+        else:
+            ks, vs = (amax_k.max() / fmax).reshape(1).contiguous(), (amax_v.max() / fmax).reshape(1).contiguous()
+        q = _bind(lib, f"musa_aiter_kv_linear_to_paged_fp8_vec4_{fmt}", 7, 5)
+        d = _bind(lib, f"musa_aiter_kv_paged_fp8_to_linear_vec4_{fmt}", 7, 5)
+        q.argtypes = q.argtypes[:-1] + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int]
+        d.argtypes = d.argtypes[:-1] + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int]
+        qa = (kl.data_ptr(), vl.data_ptr(), slots.data_ptr(), kc.data_ptr(), vc.data_ptr(), ks.data_ptr(),
+              vs.data_ptr(), t, NB, NH, HD, BS, 2)
+        da = (kc.data_ptr(), vc.data_ptr(), slots.data_ptr(), ks.data_ptr(), vs.data_ptr(), ok.data_ptr(),
+              ov.data_ptr(), t, NB, NH, HD, BS, 2)
+        _check(q(*qa, _stream(), mode), name)
+        _check(d(*da, _stream(), mode), name)
+        torch.cuda.synchronize()
+        # Parity on a sample of tokens, outside the timed region: cache bytes vs the oracle's encoder,
+        # dequantised rows vs the oracle's decoder.
+        s_np = slots_np[:sample]
+        blk, off = s_np // BS, s_np % BS
+        got = kc.cpu().numpy()[blk, :, :, off]                    # [sample, NH, HD]
+        x = kl[:sample].float().cpu().numpy()
+        scale = ks.cpu().numpy().reshape(-1, 1) if mode == 1 else ks.cpu().numpy()[0]
+        want = ko.fp8_quantize(x, scale, fmt)
+        deq = bits(ok[:sample])
+        want_deq = ko.to_storage(ko.fp8_dequantize_f32(want, scale, fmt), "bfloat16")
+        parity = bool(np.array_equal(got, want) and np.array_equal(deq, want_deq))
+        mq = batched_ms(lambda: _check(q(*qa, _stream(), mode), name))
+        md = batched_ms(lambda: _check(d(*da, _stream(), mode), name))
+        out[name] = {"quant_store": rate(nbytes, mq, t), "dequant_gather": rate(nbytes, md, t),
+                     "scale_rule": f"amax/{fmax:g}" + (" per kv-head" if mode == 1 else " over all heads"),
+                     "parity_sample_tokens": sample, "parity_vs_oracle": parity}
+        log(f"config 3 {name}: quant {out[name]['quant_store']['gbs']:.0f} GB/s, "
+            f"dequant {out[name]['dequant_gather']['gbs']:.0f} GB/s, parity {parity}")
+    return out
 
-    tq, td = EventTimer(), EventTimer()
-    for _ in range(steps * 4):
-        e0 = tq.start()
-        _hip.paged_tiles(op="bench", scatter=True, codec=1, cache_elt=1, lin_elt=2, lin_dtype=2, key_cache=kc,
-                         value_cache=vc, key_linear=kl, value_linear=vl, slots=slots, num_layers=1, num_tokens=t,
-                         num_blocks=NB, num_heads=NH, head_dim=HD, block_size=BS, lin_token_stride=ROW,
-                         lin_layer_stride=t * ROW, k_scale=ks, v_scale=vs, scale_mode=1, fill_zeros=False)
-        tq.stop(e0)
-        e1 = td.start()
-        _hip.paged_tiles(op="bench", scatter=False, codec=1, cache_elt=1, lin_elt=2, lin_dtype=2, key_cache=kc,
-                         value_cache=vc, key_linear=ok, value_linear=ov, slots=slots, num_layers=1, num_tokens=t,
-                         num_blocks=NB, num_heads=NH, head_dim=HD, block_size=BS, lin_token_stride=ROW,
-                         lin_layer_stride=t * ROW, k_scale=ks, v_scale=vs, scale_mode=1, fill_zeros=True)
-        td.stop(e1)
-    torch.cuda.synchronize()
-    quant_bytes = 2 * t * ROW * (2 + 1) + 8 * t
-    mq, md = np.array(tq.ms()), np.array(td.ms())
-    err = float(((ok.float() - kl.float()).abs() / (kl.float().abs() + 1e-3)).median())
-    return {"tokens": t, "bytes_per_call": quant_bytes,
-            "quant_store": {"avg_ms": float(mq.mean()), "gbs": quant_bytes / (mq.mean() * 1e-3) / 1e9,
-                            "tokens_per_ms": t / mq.mean()},
-            "dequant_gather": {"avg_ms": float(md.mean()), "gbs": quant_bytes / (md.mean() * 1e-3) / 1e9,
-                               "tokens_per_ms": t / md.mean()},
-            "median_rel_err_roundtrip": err}
 
-
-def bench_config4(steps: int, warmup: int) -> dict:
+def bench_config4() -> dict:
     """SGLang-MP [2, 32, 4096, 16, 8, 128] bf16 <-> LMCache [2, 32, 256, 1024], 16 chunks."""
     import musa_aiter
+    from oracle import kv_oracle as ko
+    from tests.kvgen import bits
 
     dev = torch.device("cuda", 0)
     nl, nb, chunk, nchunks = 32, 4096, 256, 16
@@ -257,32 +335,95 @@ def bench_config4(steps: int, warmup: int) -> dict:
     memory = torch.empty((2, nl, chunk * nchunks, ROW), dtype=torch.bfloat16, device=dev)
     chunks = [(slots[i * chunk:(i + 1) * chunk].contiguous(), memory[:, :, i * chunk:(i + 1) * chunk])
               for i in range(nchunks)]
-    for _ in range(warmup):
-        for s, m in chunks:
-            musa_aiter.lmcache_kv_paged_to_buffer_two_x_nl(kvcaches, m, s, BS, NH, HD)
+    for s_c, m in chunks:
+        musa_aiter.lmcache_kv_paged_to_buffer_two_x_nl(kvcaches, m, s_c, BS, NH, HD)
     torch.cuda.synchronize()
-    log(f"config 4: {chunk * nchunks} tokens in {nchunks} chunks, warmup done")
-    tg, tb, ts = EventTimer(), EventTimer(), EventTimer()
-    for _ in range(steps):
-        for s, m in chunks:
-            e = tg.start()
-            musa_aiter.lmcache_kv_paged_to_buffer_two_x_nl(kvcaches, m, s, BS, NH, HD)
-            tg.stop(e)
-        e = tb.start()
-        musa_aiter.lmcache_kv_paged_to_buffer_two_x_nl(kvcaches, memory, slots, BS, NH, HD)
-        tb.stop(e)
-        e = ts.start()
-        musa_aiter.lmcache_kv_buffer_to_paged_two_x_nl(memory, kvcaches, slots, 0, BS, NH, HD)
-        ts.stop(e)
-    torch.cuda.synchronize()
+    # Parity (outside timing): layers 0 and 31 of K and V, all 16 chunks, vs the oracle's 2xNL gather.
+    layers = (0, nl - 1)
+    sub = [[bits(cache[axis, layer]) for layer in layers] for axis in (0, 1)]
+    want = np.zeros((2, len(layers), chunk * nchunks, ROW), dtype=np.uint16)
+    ko.two_x_nl_to_buffer(sub, want, slots_np)
+    parity = bool(np.array_equal(bits(memory[:, list(layers)]), want))
+    log(f"config 4: {chunk * nchunks} tokens in {nchunks} chunks, parity {parity}")
+
+    def per_chunk_gather():
+        for s_c, m in chunks:
+            musa_aiter.lmcache_kv_paged_to_buffer_two_x_nl(kvcaches, m, s_c, BS, NH, HD)
+
+    mg = batched_ms(per_chunk_gather, launches=5, reps=5) / nchunks
+    mb = batched_ms(lambda: musa_aiter.lmcache_kv_paged_to_buffer_two_x_nl(kvcaches, memory, slots, BS, NH, HD),
+                    launches=10)
+    ms = batched_ms(lambda: musa_aiter.lmcache_kv_buffer_to_paged_two_x_nl(memory, kvcaches, slots, 0, BS, NH, HD),
+                    launches=10)
     per_chunk = 2 * (2 * nl * chunk * ROW * 2) + 8 * chunk
-    mg, mb, ms = np.array(tg.ms()), np.array(tb.ms()), np.array(ts.ms())
-    return {"chunk_tokens": chunk, "chunks": nchunks, "bytes_per_chunk": per_chunk,
-            "gather_per_chunk": {"avg_ms": float(mg.mean()), "p50_ms": float(np.median(mg)),
-                                 "gbs": per_chunk / (np.median(mg) * 1e-3) / 1e9},
-            "gather_batched_16": {"avg_ms": float(mb.mean()), "gbs": per_chunk * nchunks / (mb.mean() * 1e-3) / 1e9},
-            "scatter_batched_16": {"avg_ms": float(ms.mean()), "gbs": per_chunk * nchunks / (ms.mean() * 1e-3) / 1e9},
-            "note": "per-chunk times include the host-side Python call overhead between events"}
+    return {"chunk_tokens": chunk, "chunks": nchunks, "bytes_per_chunk": per_chunk, "parity_vs_oracle": parity,
+            "gather_per_chunk_call": rate(per_chunk, mg, chunk),
+            "gather_batched_16": rate(per_chunk * nchunks, mb, chunk * nchunks),
+            "scatter_batched_16": rate(per_chunk * nchunks, ms, chunk * nchunks),
+            "note": "per-chunk calls go through the Python API (validation, pointer tables) back to back; "
+                    "batched = one call for all 16 chunks"}
+
+
+def bench_config5() -> dict:
+    """MLA flat rows, 61 layers, BS=64, 128 seqs len U[256,8192]: bf16 576-value rows through
+    lmcache_{paged_to_kv_buffer,kv_buffer_to_paged}_mla_u16, and 656-byte FP8 rows through
+    musa_aiter_kv_copy_paged_rows_contig_layers_u8."""
+    from musa_aiter.ops import _hip
+    from tests.kvgen import sequence_slots
+
+    dev = torch.device("cuda", 0)
+    nl, bs, hs, rowb8 = 61, 64, 576, 656
+    rng = np.random.default_rng(1005)
+    lengths = [int(x) for x in rng.integers(256, 8193, size=128)]
+    nb = sum((n + bs - 1) // bs for n in lengths)
+    slots_np = sequence_slots(rng, lengths, num_blocks=nb, block_size=bs)
+    t = int(slots_np.shape[0])
+    slots = torch.from_numpy(slots_np).to(dev)
+    lib = _hip.library()
+    out = {"tokens": t, "num_blocks": nb, "layers": nl}
+    gen = torch.Generator(device=dev).manual_seed(5)
+
+    paged = torch.randn((nl, nb, bs, hs), generator=gen, device=dev, dtype=torch.bfloat16)
+    buf = torch.empty((nl, t, hs), dtype=torch.bfloat16, device=dev)
+    g = _bind(lib, "lmcache_paged_to_kv_buffer_mla_u16", 3, 5)
+    sct = _bind(lib, "lmcache_kv_buffer_to_paged_mla_u16", 3, 5)
+    ga = (paged.data_ptr(), buf.data_ptr(), slots.data_ptr(), nl, t, nb, bs, hs)
+    sa = (buf.data_ptr(), paged.data_ptr(), slots.data_ptr(), nl, t, nb, bs, hs)
+    before = paged.view(torch.int16).sum(dtype=torch.int64).item()
+    _check(g(*ga, _stream()), "cfg5 gather")
+    _check(sct(*sa, _stream()), "cfg5 scatter")
+    torch.cuda.synchronize()
+    pick = rng.integers(0, t, size=256)
+    flat = paged.view(nl, nb * bs, hs)
+    sample_ok = bool(torch.equal(buf[:, torch.from_numpy(pick).to(dev)],
+                                 flat[:, torch.from_numpy(slots_np[pick]).to(dev)]))
+    parity = sample_ok and before == paged.view(torch.int16).sum(dtype=torch.int64).item()
+    mg = batched_ms(lambda: _check(g(*ga, _stream()), "cfg5 gather"), launches=3, reps=3)
+    ms = batched_ms(lambda: _check(sct(*sa, _stream()), "cfg5 scatter"), launches=3, reps=3)
+    nbytes = 2 * nl * t * hs * 2 + 8 * t
+    out["bf16_576"] = {"bytes_per_call": nbytes, "gather": rate(nbytes, mg, t), "scatter": rate(nbytes, ms, t),
+                       "parity": parity, "parity_check": "256 sampled tokens x 61 layers equal to their slot rows; "
+                                                          "scatter of the gathered rows leaves the cache checksum unchanged"}
+    log(f"config 5 bf16: gather {out['bf16_576']['gather']['gbs']:.0f} GB/s, "
+        f"scatter {out['bf16_576']['scatter']['gbs']:.0f} GB/s, parity {parity}")
+    del paged, buf, flat
+    torch.cuda.empty_cache()
+
+    src = torch.randint(0, 256, (nl, nb * bs, rowb8), generator=gen, device=dev, dtype=torch.uint8)
+    dst = torch.empty((nl, t, rowb8), dtype=torch.uint8, device=dev)
+    rows = torch.arange(t, dtype=torch.int64, device=dev)
+    cp = _bind(lib, "musa_aiter_kv_copy_paged_rows_contig_layers_u8", 4, 5)
+    ca = (src.data_ptr(), dst.data_ptr(), slots.data_ptr(), rows.data_ptr(), t, rowb8, nl, nb * bs, t)
+    _check(cp(*ca, _stream()), "cfg5 rows")
+    torch.cuda.synchronize()
+    parity8 = bool(torch.equal(dst[:, torch.from_numpy(pick).to(dev)], src[:, torch.from_numpy(slots_np[pick]).to(dev)]))
+    mr = batched_ms(lambda: _check(cp(*ca, _stream()), "cfg5 rows"), launches=3, reps=3)
+    nbytes8 = 2 * nl * t * rowb8 + 2 * 8 * t
+    out["fp8_656_rows"] = {"bytes_per_call": nbytes8, "gather": rate(nbytes8, mr, t), "parity": parity8}
+    log(f"config 5 fp8 rows: gather {out['fp8_656_rows']['gather']['gbs']:.0f} GB/s, parity {parity8}")
+    del src, dst
+    torch.cuda.empty_cache()
+    return out
 
 
 def device_copy(mib: int, reps: int = 5) -> dict:
@@ -331,7 +472,8 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--configs", default="2,3,4", help="comma list of BASELINE configs to run (2 is the headline)")
+    parser.add_argument("--configs", default="1,2,3,4,5",
+                        help="comma list of BASELINE configs to run (2, the headline, always runs)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--copy-mib", type=int, default=1024,
                         help="size of the plain device copy timed first (0 = skip)")
@@ -360,13 +502,14 @@ def main() -> int:
         log(f"cpu baseline {cpu['value']:.2f} GB/s")
     del kc, vc
     torch.cuda.empty_cache()
-    if 3 in configs:
-        extra["config3_fp8_e4m3_per_head"] = bench_config3(max(1, args.steps // 2), max(1, args.warmup))
-        log(f"config 3: {json.dumps(extra['config3_fp8_e4m3_per_head'])}")
-        torch.cuda.empty_cache()
-    if 4 in configs:
-        extra["config4_lmcache_two_x_nl"] = bench_config4(max(1, args.steps // 4), max(1, args.warmup // 2))
-        log(f"config 4: {json.dumps(extra['config4_lmcache_two_x_nl'])}")
+    runners = {1: ("config1_fp16_single_layer_gather", bench_config1), 3: ("config3_fp8", bench_config3),
+               4: ("config4_lmcache_two_x_nl", bench_config4), 5: ("config5_mla_rows", bench_config5)}
+    for cfg in sorted(configs - {2}):
+        if cfg not in runners:
+            continue
+        key, fn = runners[cfg]
+        extra[key] = fn()
+        log(f"config {cfg}: {json.dumps(extra[key])}")
         torch.cuda.empty_cache()
     dom = c2[c2["dominant"]]
     achieved = c2["bytes_per_direction"] / (c2["dominant_avg_ms"] * 1e-3) / 1e9
