@@ -7,11 +7,15 @@
 // copy is indexed by a slot/row vector (or both, for byte rows); slot < 0
 // skips the token.
 //
-// One wave owns one token.  Its source and destination rows are resolved once
-// (scalar loads) and the wave streams the row of every plane in its plane
-// group with VEC-byte vectors, U vectors in flight per lane.  Skipped tokens
-// of a directly addressed destination are zero filled; an indexed destination
-// can be protected by claim tags so duplicate slots keep last-writer-wins.
+// One block covers a few whole rows of one plane (grid y = plane): the rows
+// are cut into VEC-byte pieces (VEC = the widest power of two dividing the
+// row size, strides and plane bases) and the flattened (token, piece) range is
+// spread over the 256 threads, one or two pieces each.  Every lane does useful
+// work for any row size, and each wave keeps only a vector or two per lane in
+// flight, the access shape that reaches the highest HBM copy rate on MI355X.
+// Skipped tokens of a directly addressed destination are zero filled; an
+// indexed destination can be protected by claim tags so duplicate slots keep
+// last-writer-wins.
 #include "kv_hip_common.h"
 #include "kv_launch.h"
 
@@ -36,77 +40,64 @@ struct RowArgs {
   int64_t dst_stride;
   int32_t plane_base;       // first plane of this launch in the table arrays
   int32_t num_planes;       // planes in this launch
-  int32_t planes_per_wave;
   int32_t zero_invalid;
   uint32_t epoch;
 };
 
-constexpr int kRowUnroll = 4;
-
+// One block covers `tokens_per_block` whole rows of one plane, split into
+// VEC-byte pieces: thread i of the block moves pieces i, i + 256, ... of the
+// flattened (token, piece) range, so every lane does useful work whatever the
+// row size and each wave keeps only one or two vectors per lane in flight.
+// The piece -> token split divides small integers with a float reciprocal
+// and one exact correction step.
 template <int VEC>
-__global__ __launch_bounds__(kBlockThreads) void row_copy_kernel(const RowArgs a) {
+__global__ __launch_bounds__(kBlockThreads) void row_flat_kernel(const RowArgs a, const int32_t pieces,
+                                                                 const int32_t tokens_per_block,
+                                                                 const float inv_pieces) {
   using V = typename VecType<VEC>::T;
-  const int lane = lane_id();
-  const int64_t u = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();
-  if (u >= a.num_rows_out) return;
-  const int p0 = static_cast<int>(blockIdx.y) * a.planes_per_wave;
-  if (p0 >= a.num_planes) return;
-  const int np = (a.num_planes - p0) < a.planes_per_wave ? (a.num_planes - p0) : a.planes_per_wave;
+  const int64_t t_base = static_cast<int64_t>(blockIdx.x) * tokens_per_block;
+  const int pp = a.plane_base + static_cast<int>(blockIdx.y);
+  const uint8_t* const sp =
+      reinterpret_cast<const uint8_t*>(a.src_table ? a.src_table[pp] : a.src_planes[pp - a.plane_base]);
+  uint8_t* const dp = reinterpret_cast<uint8_t*>(a.dst_table ? a.dst_table[pp] : a.dst_planes[pp - a.plane_base]);
+  // Plane bases read from device tables may be less aligned than VEC: such a
+  // plane is copied byte by byte (uniform branch).
+  const bool narrow = VEC > 1 && ((reinterpret_cast<uintptr_t>(sp) | reinterpret_cast<uintptr_t>(dp)) & (VEC - 1));
+  const int total = tokens_per_block * pieces;
 
-  int64_t srow = -1;
-  int64_t drow = u + a.dst_offset;
-  bool valid = false;
-  if (u < a.num_tokens) {
-    srow = a.src_idx ? a.src_idx[u] : u + a.src_offset;
-    if (a.dst_idx) drow = a.dst_idx[u];
-    valid = srow >= 0 && srow < a.src_rows && drow >= 0 && drow < a.dst_rows;
-    if (valid && a.owner != nullptr) valid = (a.owner[drow] == claim_tag(a.epoch, u));
-  }
-  srow = uniform64(srow);
-  drow = uniform64(drow);
-  valid = __builtin_amdgcn_readfirstlane(static_cast<int>(valid)) != 0;
+  for (int l = static_cast<int>(threadIdx.x); l < total; l += kBlockThreads) {
+    int lt = static_cast<int>(static_cast<float>(l) * inv_pieces);
+    if (lt * pieces > l) --lt;
+    else if ((lt + 1) * pieces <= l) ++lt;
+    const int c = l - lt * pieces;
+    const int64_t u = t_base + lt;
+    if (u >= a.num_rows_out) break;
 
-  const int chunks = static_cast<int>(a.row_bytes / VEC);
-  const int iters_per_plane = (chunks + kWave - 1) / kWave;
-  const int iters = np * iters_per_plane;
-
-  if (!valid) {
-    // Only a directly addressed destination row inside its extent is cleared.
-    if (!a.zero_invalid || a.dst_idx != nullptr || drow < 0 || drow >= a.dst_rows) return;
-    const V zero{};
-    for (int it = 0; it < iters; ++it) {
-      const int p = it / iters_per_plane;
-      const int c = (it - p * iters_per_plane) * kWave + lane;
-      const int pp = a.plane_base + p0 + p;
-      uint8_t* const dp = reinterpret_cast<uint8_t*>(a.dst_table ? a.dst_table[pp] : a.dst_planes[pp - a.plane_base]);
-      if (c < chunks) stv<VEC>(dp + drow * a.dst_stride + static_cast<int64_t>(c) * VEC, zero);
+    int64_t srow = -1;
+    int64_t drow = u + a.dst_offset;
+    bool valid = false;
+    if (u < a.num_tokens) {
+      srow = a.src_idx ? a.src_idx[u] : u + a.src_offset;
+      if (a.dst_idx) drow = a.dst_idx[u];
+      valid = srow >= 0 && srow < a.src_rows && drow >= 0 && drow < a.dst_rows;
+      if (valid && a.owner != nullptr) valid = (a.owner[drow] == claim_tag(a.epoch, u));
     }
-    return;
-  }
-
-  for (int it0 = 0; it0 < iters; it0 += kRowUnroll) {
-    V v[kRowUnroll];
+    const int64_t doff = drow * a.dst_stride + static_cast<int64_t>(c) * VEC;
+    if (valid) {
+      const int64_t soff = srow * a.src_stride + static_cast<int64_t>(c) * VEC;
+      if (!narrow) {
+        stv<VEC>(dp + doff, ldv<VEC>(sp + soff));
+      } else {
 #pragma unroll
-    for (int k = 0; k < kRowUnroll; ++k) {
-      const int it = it0 + k;
-      if (it < iters) {
-        const int p = it / iters_per_plane;
-        const int c = (it - p * iters_per_plane) * kWave + lane;
-        const int pp = a.plane_base + p0 + p;
-        const uint8_t* const sp =
-            reinterpret_cast<const uint8_t*>(a.src_table ? a.src_table[pp] : a.src_planes[pp - a.plane_base]);
-        if (c < chunks) v[k] = ldv<VEC>(sp + srow * a.src_stride + static_cast<int64_t>(c) * VEC);
+        for (int b = 0; b < VEC; ++b) dp[doff + b] = sp[soff + b];
       }
-    }
+    } else if (a.zero_invalid && a.dst_idx == nullptr && drow >= 0 && drow < a.dst_rows) {
+      // Only a directly addressed destination row inside its extent is cleared.
+      if (!narrow) {
+        stv<VEC>(dp + doff, V{});
+      } else {
 #pragma unroll
-    for (int k = 0; k < kRowUnroll; ++k) {
-      const int it = it0 + k;
-      if (it < iters) {
-        const int p = it / iters_per_plane;
-        const int c = (it - p * iters_per_plane) * kWave + lane;
-        const int pp = a.plane_base + p0 + p;
-        uint8_t* const dp = reinterpret_cast<uint8_t*>(a.dst_table ? a.dst_table[pp] : a.dst_planes[pp - a.plane_base]);
-        if (c < chunks) stv<VEC>(dp + drow * a.dst_stride + static_cast<int64_t>(c) * VEC, v[k]);
+        for (int b = 0; b < VEC; ++b) dp[doff + b] = 0;
       }
     }
   }
@@ -195,11 +186,19 @@ int vec_for(uint64_t bits) {
   return 1;
 }
 
+// Rows per block: about two pieces per thread, at least one row, and the
+// flattened range kept well inside 32-bit arithmetic.
 template <int VEC>
-hipError_t launch_rows_vec(const RowArgs& a, int64_t plane_groups, hipStream_t stream) {
-  const int64_t blocks = (a.num_rows_out + kWavesPerBlock - 1) / kWavesPerBlock;
-  hipLaunchKernelGGL(row_copy_kernel<VEC>, dim3(static_cast<uint32_t>(blocks), static_cast<uint32_t>(plane_groups)),
-                     dim3(kBlockThreads), 0, stream, a);
+hipError_t launch_rows_vec(const RowArgs& a, int64_t planes, hipStream_t stream) {
+  const int64_t pieces = a.row_bytes / VEC;
+  if (pieces > (int64_t{1} << 22)) return hipErrorInvalidValue;
+  int64_t tpb = (2 * kBlockThreads) / pieces;
+  if (tpb < 1) tpb = 1;
+  const int64_t blocks = (a.num_rows_out + tpb - 1) / tpb;
+  if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(row_flat_kernel<VEC>, dim3(static_cast<uint32_t>(blocks), static_cast<uint32_t>(planes)),
+                     dim3(kBlockThreads), 0, stream, a, static_cast<int32_t>(pieces), static_cast<int32_t>(tpb),
+                     1.0f / static_cast<float>(pieces));
   return hipGetLastError();
 }
 
@@ -221,18 +220,8 @@ hipError_t launch_row_copy(const RowCopyParams& p, hipStream_t stream) {
     if (src_host) bits |= p.src_planes[i];
     if (dst_host) bits |= p.dst_planes[i];
   }
-  // Device-resident tables: their bases are not visible here, so only byte
-  // granularity is assumed unless the rows themselves force a finer width.
-  if (!src_host || !dst_host) bits |= 1u;
+  // Plane bases held in device tables are checked per plane by the kernel.
   const int vec = vec_for(bits);
-
-  const int64_t chunks = p.row_bytes / vec;
-  // Plane group per wave: enough work per wave (>= ~16 KB) without starving
-  // the grid of waves.
-  int ppw = static_cast<int>((16384 + p.row_bytes - 1) / p.row_bytes);
-  if (ppw < 1) ppw = 1;
-  if (ppw > 16) ppw = 16;
-  (void)chunks;
 
   for (int64_t base = 0; base < p.num_planes; base += kMaxPlanes) {
     const int64_t n = (p.num_planes - base) < kMaxPlanes ? (p.num_planes - base) : kMaxPlanes;
@@ -257,17 +246,15 @@ hipError_t launch_row_copy(const RowCopyParams& p, hipStream_t stream) {
     a.dst_stride = p.dst_stride;
     a.plane_base = static_cast<int32_t>(base);
     a.num_planes = static_cast<int32_t>(n);
-    a.planes_per_wave = ppw < n ? ppw : static_cast<int32_t>(n);
     a.zero_invalid = p.zero_invalid;
     a.epoch = p.epoch;
-    const int64_t groups = (n + a.planes_per_wave - 1) / a.planes_per_wave;
     hipError_t err;
     switch (vec) {
-      case 16: err = launch_rows_vec<16>(a, groups, stream); break;
-      case 8: err = launch_rows_vec<8>(a, groups, stream); break;
-      case 4: err = launch_rows_vec<4>(a, groups, stream); break;
-      case 2: err = launch_rows_vec<2>(a, groups, stream); break;
-      default: err = launch_rows_vec<1>(a, groups, stream); break;
+      case 16: err = launch_rows_vec<16>(a, n, stream); break;
+      case 8: err = launch_rows_vec<8>(a, n, stream); break;
+      case 4: err = launch_rows_vec<4>(a, n, stream); break;
+      case 2: err = launch_rows_vec<2>(a, n, stream); break;
+      default: err = launch_rows_vec<1>(a, n, stream); break;
     }
     if (err != hipSuccess) return err;
   }
