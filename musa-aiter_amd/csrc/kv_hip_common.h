@@ -290,6 +290,41 @@ __device__ __forceinline__ uint32_t fp8_encode_fast(float w) {
   return ((bits >> 24) & 0x80u) | (normal ? body : 0u);
 }
 
+// Hardware encoder for the fast range.  gfx950's v_cvt_pk_fp8_f32 /
+// v_cvt_pk_bf8_f32 (OCP formats, round to nearest even, no saturation)
+// produce the reference byte for every finite quotient once values below the
+// smallest normal are flushed to a signed zero: checked exhaustively on the
+// device over all finite fp32 inputs.  E4M3 matches everywhere (overflow
+// gives 0x7F|sign, the reference's 480 clamp byte); E5M2 matches up to its
+// largest normal 57344, above which the reference keeps exponent-31 codes and
+// the callers must use fp8_encode_fast instead.
+template <int CODEC>
+__device__ __forceinline__ float fp8_flush_small(float w) {
+  const uint32_t b = __float_as_uint(w);
+  return ((b & 0x7FFFFFFFu) < Fp8Fmt<CODEC>::kMinNormBits) ? __uint_as_float(b & 0x80000000u) : w;
+}
+
+template <int CODEC>
+constexpr uint32_t kHwEncodeMaxBits = (CODEC == kE4M3) ? 0x7F7FFFFFu : 0x47600000u;  // all finite / 57344
+
+// Four quotients -> four bytes (element i in byte i).
+template <int CODEC>
+__device__ __forceinline__ uint32_t fp8_pack4_hw(float w0, float w1, float w2, float w3) {
+  w0 = fp8_flush_small<CODEC>(w0);
+  w1 = fp8_flush_small<CODEC>(w1);
+  w2 = fp8_flush_small<CODEC>(w2);
+  w3 = fp8_flush_small<CODEC>(w3);
+  int r;
+  if constexpr (CODEC == kE4M3) {
+    r = __builtin_amdgcn_cvt_pk_fp8_f32(w0, w1, 0, false);
+    r = __builtin_amdgcn_cvt_pk_fp8_f32(w2, w3, r, true);
+  } else {
+    r = __builtin_amdgcn_cvt_pk_bf8_f32(w0, w1, 0, false);
+    r = __builtin_amdgcn_cvt_pk_bf8_f32(w2, w3, r, true);
+  }
+  return static_cast<uint32_t>(r);
+}
+
 // Magnitude range of a tile's linear inputs, tracked on the raw bits: the
 // minimum of (|x| - 1) (so zeros drop out) and the maximum of |x|.  16-bit
 // inputs are tracked two per dword with packed 16-bit integer min/max.

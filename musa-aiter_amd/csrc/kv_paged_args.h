@@ -25,6 +25,7 @@ struct TileArgs {
   int32_t fill_zeros;
   uint32_t epoch;
   int32_t block_size;          // used by the generic kernel only
+  float inv_head_dim;          // 1 / head_dim, for small-integer division by head_dim
 };
 
 constexpr int kTileTokens = 16;

@@ -89,6 +89,31 @@ template <int ELT_C, int ELT_L, int CODEC, int LDT, int PITCH, bool FAST>
 __device__ __forceinline__ void lds_put_column(uint8_t* tile, int row0, int c, const u32x4& in, float sc, float r) {
   constexpr int RPL = 16 / ELT_L;
   uint8_t* p = tile + row0 * PITCH + c * ELT_C;
+  if constexpr (FAST && CODEC != kCopy) {
+    // Fast range: exact quotients through the hoisted reciprocal, bytes from
+    // the hardware converter (E5M2 pieces above its largest normal keep the
+    // integer encoder).
+    float w[RPL];
+    uint32_t amax = 0;
+#pragma unroll
+    for (int i = 0; i < RPL; ++i) {
+      const float x = (ELT_L == 2) ? lin_to_f32<LDT>(elem16(in, i)) : __uint_as_float(in[i]);
+      w[i] = quot_fast(x, sc, r);
+      if constexpr (CODEC == kE5M2) amax = max(amax, __float_as_uint(w[i]) & 0x7FFFFFFFu);
+    }
+    if (CODEC == kE4M3 || amax <= kHwEncodeMaxBits<CODEC>) {
+#pragma unroll
+      for (int g = 0; g < RPL / 4; ++g) {
+        const uint32_t b = fp8_pack4_hw<CODEC>(w[4 * g], w[4 * g + 1], w[4 * g + 2], w[4 * g + 3]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) store_elem<1>(p + (4 * g + k) * PITCH, b >> (8 * k));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < RPL; ++i) store_elem<1>(p + i * PITCH, fp8_encode_fast<CODEC>(w[i]));
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < RPL; ++i) {
     uint32_t v;
@@ -156,31 +181,40 @@ __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs
   uint64_t heads = vmask & ~cmask & window;
 
   // This thread's cache piece (row pr, column group pg) and linear pieces
-  // (block column lc[j], row group lq[j]) within every chunk.
+  // (block column lc[j], row group lq[j]) within every chunk.  All offsets are
+  // 32-bit and relative to the run's descriptors; per chunk they advance by a
+  // constant.
   const int pr = tid / NCG;
   const int pg = tid % NCG;
+  const int rows_left = static_cast<int>(re - rb);
   int lc[PPT], lq[PPT];
 #pragma unroll
   for (int j = 0; j < PPT; ++j) {
     lc[j] = S::col(tid + j * kCoopThreads);
     lq[j] = S::grp(tid + j * kCoopThreads);
   }
-  auto prow_in = [&](int k) { return rb + static_cast<int64_t>(k) * kRows + pr < re; };
-  auto lrow_in = [&](int k, int j) {
-    return rb + static_cast<int64_t>(k) * kRows + static_cast<int64_t>(lq[j]) * RPL < re;
-  };
-  // FP8 scale of linear piece j in chunk k.  The row is clamped into the
-  // block so the load is unconditional (the value of an out-of-range piece is
-  // never used); chunk k+1's scales are fetched together with its payload.
+  auto prow_in = [&](int k) { return k * kRows + pr < rows_left; };
+  auto lrow_in = [&](int k, int j) { return k * kRows + lq[j] * RPL < rows_left; };
+  // FP8 scale of linear piece j in chunk k: head = row / head_dim by a float
+  // reciprocal and one exact correction (rows < 2^24).  The row is clamped
+  // into the block so the load is unconditional.
   auto piece_scale = [&](int k, int j) -> float {
     if constexpr (CODEC == kCopy) {
       return 1.0f;
     } else {
-      int64_t row = rb + static_cast<int64_t>(k) * kRows + static_cast<int64_t>(lq[j]) * RPL;
-      row = row < a.nrows ? row : a.nrows - 1;
-      return load_scale(a, kv, layer, row / a.head_dim);
+      int row = static_cast<int>(rb) + k * kRows + lq[j] * RPL;
+      row = row < static_cast<int>(a.nrows) ? row : static_cast<int>(a.nrows) - 1;
+      const int hd = static_cast<int>(a.head_dim);
+      int head = static_cast<int>(static_cast<float>(row) * a.inv_head_dim);
+      if (head * hd > row) --head;
+      else if ((head + 1) * hd <= row) ++head;
+      return load_scale(a, kv, layer, head);
     }
   };
+  constexpr uint32_t kCacheStep = kRows * ROWB;     // bytes between chunks, cache side
+  constexpr uint32_t kLinStep = kRows * ELT_L;      // bytes between chunks, linear side
+  const uint32_t cpiece = static_cast<uint32_t>(tid) * 16u;
+  const uint32_t stride32 = static_cast<uint32_t>(a.lin_token_stride);
 
   while (heads) {
     const int i = __builtin_ctzll(heads);
@@ -196,14 +230,16 @@ __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs
     // first linear row at row rb.  Offsets of masked lanes are kOffOob.
     const buf_t cbuf = make_buf(cache + (blk * a.nrows + rb) * ROWB);
     const buf_t lbuf = make_buf(lin + tf * a.lin_token_stride + rb * ELT_L);
-    auto coff = [&](int k) -> uint32_t {
-      return prow_in(k) ? static_cast<uint32_t>(k * kRows * ROWB + tid * 16) : kOffOob;
-    };
+    bool lmine[PPT];
+    uint32_t lbase[PPT];
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      lmine[j] = lc[j] >= c0 && lc[j] < c1;
+      lbase[j] = static_cast<uint32_t>(lc[j] - c0) * stride32 + static_cast<uint32_t>(lq[j]) * 16u;
+    }
+    auto coff = [&](int k) -> uint32_t { return prow_in(k) ? cpiece + k * kCacheStep : kOffOob; };
     auto loff = [&](int k, int j) -> uint32_t {
-      const int c = lc[j];
-      return (c >= c0 && c < c1 && lrow_in(k, j))
-                 ? static_cast<uint32_t>((c - c0) * a.lin_token_stride + k * kRows * ELT_L + lq[j] * 16)
-                 : kOffOob;
+      return (lmine[j] && lrow_in(k, j)) ? lbase[j] + k * kLinStep : kOffOob;
     };
 
     if constexpr (!SCATTER) {
@@ -251,8 +287,7 @@ __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs
         }
 #pragma unroll
         for (int j = 0; j < PPT; ++j) {
-          const int c = lc[j];
-          if (c < c0 || c >= c1 || !lrow_in(k, j)) continue;
+          if (!lmine[j] || !lrow_in(k, j)) continue;
           const float sc = scc[j];
           bool fast = true;
           if constexpr (CODEC != kCopy) {
@@ -262,9 +297,9 @@ __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs
           }
           if (fast) {
             const float r = (CODEC != kCopy) ? 1.0f / sc : 0.0f;
-            lds_put_column<ELT_C, ELT_L, CODEC, LDT, PITCH, CODEC != kCopy>(tile, lq[j] * RPL, c, in[j], sc, r);
+            lds_put_column<ELT_C, ELT_L, CODEC, LDT, PITCH, CODEC != kCopy>(tile, lq[j] * RPL, lc[j], in[j], sc, r);
           } else {
-            lds_put_column<ELT_C, ELT_L, CODEC, LDT, PITCH, false>(tile, lq[j] * RPL, c, in[j], sc, 0.0f);
+            lds_put_column<ELT_C, ELT_L, CODEC, LDT, PITCH, false>(tile, lq[j] * RPL, lc[j], in[j], sc, 0.0f);
           }
         }
         lds_barrier();
@@ -444,11 +479,15 @@ hipError_t launch_paged_tiles(const PagedTileParams& p, hipStream_t stream) {
   a.fill_zeros = p.fill_zeros;
   a.epoch = p.epoch;
   a.block_size = static_cast<int32_t>(p.block_size);
+  a.inv_head_dim = 1.0f / static_cast<float>(p.head_dim);
 
   const int rpl = 16 / p.lin_elt;
   const int cg = 16 / p.cache_elt;
+  // The tile kernels address one run with 32-bit offsets (token stride up to
+  // 32 MiB) and divide row numbers below 2^24 by head_dim in float.
   bool fast = (p.head_dim % rpl == 0) && (p.lin_token_stride % 16 == 0) && (p.lin_layer_stride % 16 == 0) &&
-              (p.block_size % cg == 0);
+              (p.block_size % cg == 0) && (p.lin_token_stride <= (int64_t{1} << 25)) &&
+              (a.nrows < (int64_t{1} << 24));
   for (int i = 0; i < 2; ++i) fast = fast && aligned16(a.cache[i]) && aligned16(a.lin[i]);
 
   const int64_t planes = p.num_layers * 2;
