@@ -307,13 +307,16 @@ __device__ __forceinline__ float fp8_flush_small(float w) {
 template <int CODEC>
 constexpr uint32_t kHwEncodeMaxBits = (CODEC == kE4M3) ? 0x7F7FFFFFu : 0x47600000u;  // all finite / 57344
 
-// Four quotients -> four bytes (element i in byte i).
-template <int CODEC>
+// Four quotients -> four bytes (element i in byte i).  FLUSH may be false
+// when no quotient of the group lies below the smallest normal.
+template <int CODEC, bool FLUSH = true>
 __device__ __forceinline__ uint32_t fp8_pack4_hw(float w0, float w1, float w2, float w3) {
-  w0 = fp8_flush_small<CODEC>(w0);
-  w1 = fp8_flush_small<CODEC>(w1);
-  w2 = fp8_flush_small<CODEC>(w2);
-  w3 = fp8_flush_small<CODEC>(w3);
+  if constexpr (FLUSH) {
+    w0 = fp8_flush_small<CODEC>(w0);
+    w1 = fp8_flush_small<CODEC>(w1);
+    w2 = fp8_flush_small<CODEC>(w2);
+    w3 = fp8_flush_small<CODEC>(w3);
+  }
   int r;
   if constexpr (CODEC == kE4M3) {
     r = __builtin_amdgcn_cvt_pk_fp8_f32(w0, w1, 0, false);
@@ -347,7 +350,7 @@ struct InputRange {
         hi32 = max(hi32, a);
       } else {
         const u16x2 a = __builtin_bit_cast(u16x2, v[w] & 0x7FFF7FFFu);
-        if constexpr (LDT == kLinBF16) lo16 = __builtin_elementwise_min(lo16, a - u16x2{1, 1});
+        lo16 = __builtin_elementwise_min(lo16, a - u16x2{1, 1});
         hi16 = __builtin_elementwise_max(hi16, a);
       }
     }
@@ -360,6 +363,14 @@ struct InputRange {
   __device__ __forceinline__ uint32_t hi() const {
     if constexpr (kWide) return hi32;
     else return hi16.x > hi16.y ? hi16.x : hi16.y;
+  }
+
+  // Smallest nonzero |x| of the tracked inputs (+inf bits when all are zero).
+  __device__ __forceinline__ float min_abs_nonzero() const {
+    const uint32_t m = lo() + 1u;  // wraps to 0 when every input was zero
+    if constexpr (LDT == kLinF32) return m == 0u ? __uint_as_float(0x7F800000u) : __uint_as_float(m);
+    else if constexpr (LDT == kLinBF16) return m > 0xFFFFu ? __uint_as_float(0x7F800000u) : bf16_bits_to_f32(m);
+    else return m > 0xFFFFu ? __uint_as_float(0x7F800000u) : f16_bits_to_f32(m);
   }
 
   // True when every tracked input is zero or has 2^-60 <= |x| < 2^60.

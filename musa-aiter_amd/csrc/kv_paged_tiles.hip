@@ -86,7 +86,8 @@ __device__ __forceinline__ u32x4 lds_column_piece(const uint8_t* tile, int row0,
 // Writes the RPL elements of one linear piece into column c of the LDS tile,
 // in cache encoding.  FAST selects the hoisted-reciprocal FP8 quotient.
 template <int ELT_C, int ELT_L, int CODEC, int LDT, int PITCH, bool FAST>
-__device__ __forceinline__ void lds_put_column(uint8_t* tile, int row0, int c, const u32x4& in, float sc, float r) {
+__device__ __forceinline__ void lds_put_column(uint8_t* tile, int row0, int c, const u32x4& in, float sc, float r,
+                                               bool no_small = false) {
   constexpr int RPL = 16 / ELT_L;
   uint8_t* p = tile + row0 * PITCH + c * ELT_C;
   if constexpr (FAST && CODEC != kCopy) {
@@ -102,11 +103,20 @@ __device__ __forceinline__ void lds_put_column(uint8_t* tile, int row0, int c, c
       if constexpr (CODEC == kE5M2) amax = max(amax, __float_as_uint(w[i]) & 0x7FFFFFFFu);
     }
     if (CODEC == kE4M3 || amax <= kHwEncodeMaxBits<CODEC>) {
+      if (no_small) {
 #pragma unroll
-      for (int g = 0; g < RPL / 4; ++g) {
-        const uint32_t b = fp8_pack4_hw<CODEC>(w[4 * g], w[4 * g + 1], w[4 * g + 2], w[4 * g + 3]);
+        for (int g = 0; g < RPL / 4; ++g) {
+          const uint32_t b = fp8_pack4_hw<CODEC, false>(w[4 * g], w[4 * g + 1], w[4 * g + 2], w[4 * g + 3]);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) store_elem<1>(p + (4 * g + k) * PITCH, b >> (8 * k));
+          for (int k = 0; k < 4; ++k) store_elem<1>(p + (4 * g + k) * PITCH, b >> (8 * k));
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < RPL / 4; ++g) {
+          const uint32_t b = fp8_pack4_hw<CODEC>(w[4 * g], w[4 * g + 1], w[4 * g + 2], w[4 * g + 3]);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) store_elem<1>(p + (4 * g + k) * PITCH, b >> (8 * k));
+        }
       }
     } else {
 #pragma unroll
@@ -290,14 +300,21 @@ __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs
           if (!lmine[j] || !lrow_in(k, j)) continue;
           const float sc = scc[j];
           bool fast = true;
+          bool no_small = false;
           if constexpr (CODEC != kCopy) {
             InputRange<LDT> range;
             range.add(in[j]);
             fast = fast_scale_ok(sc) && range.in_fast_range();
+            // Every nonzero quotient of the piece is at least the smallest
+            // normal when min|x| >= minnorm * s (margin 2^-20 for the rounded
+            // product): no flush to zero is needed.
+            no_small = range.min_abs_nonzero() >=
+                       __uint_as_float(Fp8Fmt<CODEC>::kMinNormBits) * sc * (1.0f + 0x1p-20f);
           }
           if (fast) {
             const float r = (CODEC != kCopy) ? 1.0f / sc : 0.0f;
-            lds_put_column<ELT_C, ELT_L, CODEC, LDT, PITCH, CODEC != kCopy>(tile, lq[j] * RPL, lc[j], in[j], sc, r);
+            lds_put_column<ELT_C, ELT_L, CODEC, LDT, PITCH, CODEC != kCopy>(tile, lq[j] * RPL, lc[j], in[j], sc, r,
+                                                                            no_small);
           } else {
             lds_put_column<ELT_C, ELT_L, CODEC, LDT, PITCH, false>(tile, lq[j] * RPL, lc[j], in[j], sc, 0.0f);
           }
