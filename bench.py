@@ -79,8 +79,8 @@ TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "paged_tile_kernel_cfg2_traffic
 
 
 def profiled_traffic(direction: str) -> int | None:
-    """HBM bytes per launch of the cfg 2 kernel for one direction, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE passes (scaled by the plain-copy calibration); None if absent."""
+    """HBM bytes per launch of a profiled kernel (cfg 2 scatter/gather, cfg 3 FP8 quant/dequant), from the
+    committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes (scaled by the plain-copy calibration); None if absent."""
     try:
         with open(TRAFFIC_PROFILE) as fh:
             text = fh.read()
@@ -311,7 +311,11 @@ def bench_config3() -> dict:
         parity = bool(np.array_equal(got, want) and np.array_equal(deq, want_deq))
         mq = batched_ms(lambda: _check(q(*qa, _stream(), mode), name))
         md = batched_ms(lambda: _check(d(*da, _stream(), mode), name))
-        out[name] = {"quant_store": rate(nbytes, mq, t), "dequant_gather": rate(nbytes, md, t),
+        qr, dr = rate(nbytes, mq, t), rate(nbytes, md, t)
+        if name == "e4m3_per_head":
+            qr["traffic"] = profiled_traffic("fp8_quant")
+            dr["traffic"] = profiled_traffic("fp8_dequant")
+        out[name] = {"quant_store": qr, "dequant_gather": dr,
                      "scale_rule": f"amax/{fmax:g}" + (" per kv-head" if mode == 1 else " over all heads"),
                      "parity_sample_tokens": sample, "parity_vs_oracle": parity}
         log(f"config 3 {name}: quant {out[name]['quant_store']['gbs']:.0f} GB/s, "
