@@ -22,6 +22,8 @@
 // MI355X.  Partial runs store only their own block columns (element stores at
 // the edges), so neighbouring slots are never touched.  Skipped tokens
 // (slot < 0) are zero filled by the workgroup that owns them.
+#include <type_traits>
+
 #include "kv_hip_common.h"
 #include "kv_launch.h"
 #include "kv_paged_args.h"
@@ -157,6 +159,9 @@ __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs
   constexpr int RPL = S::RPL, PPT = S::PPT, PITCH = S::PITCH;
   static_assert(kTileTokens + BS + 1 <= kWave, "run window must fit one wave");
   __shared__ __align__(16) uint8_t tile[kRows * PITCH];
+  // FP8: (scale, RN(1/scale)) of every head the workgroup's rows touch.
+  constexpr int kTabHeads = (CODEC == kCopy) ? 1 : 64;
+  __shared__ float2 scale_tab[kTabHeads];
 
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = lane_id();
@@ -208,19 +213,35 @@ __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs
   // FP8 scale of linear piece j in chunk k: head = row / head_dim by a float
   // reciprocal and one exact correction (rows < 2^24).  The row is clamped
   // into the block so the load is unconditional.
-  auto piece_scale = [&](int k, int j) -> float {
-    if constexpr (CODEC == kCopy) {
-      return 1.0f;
-    } else {
-      int row = static_cast<int>(rb) + k * kRows + lq[j] * RPL;
-      row = row < static_cast<int>(a.nrows) ? row : static_cast<int>(a.nrows) - 1;
-      const int hd = static_cast<int>(a.head_dim);
-      int head = static_cast<int>(static_cast<float>(row) * a.inv_head_dim);
-      if (head * hd > row) --head;
-      else if ((head + 1) * hd <= row) ++head;
-      return load_scale(a, kv, layer, head);
-    }
+  auto head_of = [&](int k, int j) -> int {
+    int row = static_cast<int>(rb) + k * kRows + lq[j] * RPL;
+    row = row < static_cast<int>(a.nrows) ? row : static_cast<int>(a.nrows) - 1;
+    const int hd = static_cast<int>(a.head_dim);
+    int head = static_cast<int>(static_cast<float>(row) * a.inv_head_dim);
+    if (head * hd > row) --head;
+    else if ((head + 1) * hd <= row) ++head;
+    return head;
   };
+  auto piece_scale = [&](int k, int j) -> float {
+    if constexpr (CODEC == kCopy) return 1.0f;
+    else return load_scale(a, kv, layer, head_of(k, j));
+  };
+  // Quantiser: the heads of rows [rb, re) are computed once into LDS, so a
+  // piece looks up its scale and reciprocal instead of loading and dividing.
+  int tab_h0 = 0;
+  bool use_tab = false;
+  if constexpr (CODEC != kCopy && SCATTER) {
+    tab_h0 = static_cast<int>(rb / a.head_dim);
+    const int tab_n = static_cast<int>((re - 1) / a.head_dim) - tab_h0 + 1;
+    use_tab = tab_n <= kTabHeads;
+    if (use_tab) {
+      if (tid < tab_n) {
+        const float sc = load_scale(a, kv, layer, tab_h0 + tid);
+        scale_tab[tid] = make_float2(sc, fast_scale_ok(sc) ? 1.0f / sc : 0.0f);
+      }
+      lds_barrier();
+    }
+  }
   constexpr uint32_t kCacheStep = kRows * ROWB;     // bytes between chunks, cache side
   constexpr uint32_t kLinStep = kRows * ELT_L;      // bytes between chunks, linear side
   const uint32_t cpiece = static_cast<uint32_t>(tid) * 16u;
@@ -277,67 +298,85 @@ __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs
         lds_barrier();
       }
     } else {
-      u32x4 nxt[PPT];
-      float scn[PPT];
-#pragma unroll
-      for (int j = 0; j < PPT; ++j) {
-        nxt[j] = buf_ld16(lbuf, loff(0, j));
-        scn[j] = piece_scale(0, j);
-      }
-      const bool full_run = (c0 == 0) && (c1 == BS);
-      for (int k = 0; k < nchunks; ++k) {
-        u32x4 in[PPT];
-        float scc[PPT];
+      // The chunk loop is instantiated with and without the LDS scale table
+      // so that neither version has data-dependent memory instructions.
+      auto scatter_run = [&](auto tab_tag) {
+        constexpr bool kTab = decltype(tab_tag)::value;
+        u32x4 nxt[PPT];
+        float scn[PPT];
 #pragma unroll
         for (int j = 0; j < PPT; ++j) {
-          in[j] = nxt[j];
-          scc[j] = scn[j];
-          nxt[j] = buf_ld16(lbuf, (k + 1 < nchunks) ? loff(k + 1, j) : kOffOob);
-          scn[j] = piece_scale(k + 1 < nchunks ? k + 1 : k, j);
+          nxt[j] = buf_ld16(lbuf, loff(0, j));
+          if constexpr (!kTab) scn[j] = piece_scale(0, j);
+          else scn[j] = 0.0f;
         }
+        const bool full_run = (c0 == 0) && (c1 == BS);
+        for (int k = 0; k < nchunks; ++k) {
+          u32x4 in[PPT];
+          float scc[PPT];
 #pragma unroll
-        for (int j = 0; j < PPT; ++j) {
-          if (!lmine[j] || !lrow_in(k, j)) continue;
-          const float sc = scc[j];
-          bool fast = true;
-          bool no_small = false;
-          if constexpr (CODEC != kCopy) {
-            InputRange<LDT> range;
-            range.add(in[j]);
-            fast = fast_scale_ok(sc) && range.in_fast_range();
-            // Every nonzero quotient of the piece is at least the smallest
-            // normal when min|x| >= minnorm * s (margin 2^-20 for the rounded
-            // product): no flush to zero is needed.
-            no_small = range.min_abs_nonzero() >=
-                       __uint_as_float(Fp8Fmt<CODEC>::kMinNormBits) * sc * (1.0f + 0x1p-20f);
+          for (int j = 0; j < PPT; ++j) {
+            in[j] = nxt[j];
+            scc[j] = scn[j];
+            nxt[j] = buf_ld16(lbuf, (k + 1 < nchunks) ? loff(k + 1, j) : kOffOob);
+            if constexpr (!kTab) scn[j] = piece_scale(k + 1 < nchunks ? k + 1 : k, j);
           }
-          if (fast) {
-            const float r = (CODEC != kCopy) ? 1.0f / sc : 0.0f;
-            lds_put_column<ELT_C, ELT_L, CODEC, LDT, PITCH, CODEC != kCopy>(tile, lq[j] * RPL, lc[j], in[j], sc, r,
-                                                                            no_small);
+#pragma unroll
+          for (int j = 0; j < PPT; ++j) {
+            if (!lmine[j] || !lrow_in(k, j)) continue;
+            float sc = scc[j];
+            float rtab = 0.0f;
+            if constexpr (kTab) {
+              const float2 e = scale_tab[head_of(k, j) - tab_h0];
+              sc = e.x;
+              rtab = e.y;
+            }
+            bool fast = true;
+            bool no_small = false;
+            if constexpr (CODEC != kCopy) {
+              InputRange<LDT> range;
+              range.add(in[j]);
+              fast = fast_scale_ok(sc) && range.in_fast_range();
+              // Every nonzero quotient of the piece is at least the smallest
+              // normal when min|x| >= minnorm * s (margin 2^-20 for the rounded
+              // product): no flush to zero is needed.
+              no_small = range.min_abs_nonzero() >=
+                         __uint_as_float(Fp8Fmt<CODEC>::kMinNormBits) * sc * (1.0f + 0x1p-20f);
+            }
+            if (fast) {
+              const float r = (CODEC == kCopy) ? 0.0f : (kTab ? rtab : 1.0f / sc);
+              lds_put_column<ELT_C, ELT_L, CODEC, LDT, PITCH, CODEC != kCopy>(tile, lq[j] * RPL, lc[j], in[j], sc, r,
+                                                                              no_small);
+            } else {
+              lds_put_column<ELT_C, ELT_L, CODEC, LDT, PITCH, false>(tile, lq[j] * RPL, lc[j], in[j], sc, 0.0f);
+            }
+          }
+          lds_barrier();
+          const uint32_t* const d = reinterpret_cast<const uint32_t*>(tile + pr * PITCH + pg * 16);
+          const u32x4 w = {d[0], d[1], d[2], d[3]};
+          const uint32_t off = coff(k);
+          const int lo = pg * CG;
+          if (full_run) {
+            buf_st16(cbuf, off, w);
           } else {
-            lds_put_column<ELT_C, ELT_L, CODEC, LDT, PITCH, false>(tile, lq[j] * RPL, lc[j], in[j], sc, 0.0f);
-          }
-        }
-        lds_barrier();
-        const uint32_t* const d = reinterpret_cast<const uint32_t*>(tile + pr * PITCH + pg * 16);
-        const u32x4 w = {d[0], d[1], d[2], d[3]};
-        const uint32_t off = coff(k);
-        const int lo = pg * CG;
-        if (full_run) {
-          buf_st16(cbuf, off, w);
-        } else {
-          // Whole pieces inside the run go as one vector; edge pieces store
-          // only their in-run columns.
-          const bool whole = lo >= c0 && lo + CG <= c1;
-          buf_st16(cbuf, whole ? off : kOffOob, w);
+            // Whole pieces inside the run go as one vector; edge pieces store
+            // only their in-run columns.
+            const bool whole = lo >= c0 && lo + CG <= c1;
+            buf_st16(cbuf, whole ? off : kOffOob, w);
 #pragma unroll
-          for (int cc = 0; cc < CG; ++cc) {
-            const bool mine = !whole && off != kOffOob && lo + cc >= c0 && lo + cc < c1;
-            buf_st_elem<ELT_C>(cbuf, mine ? off + cc * ELT_C : kOffOob, piece_elem<ELT_C>(w, cc));
+            for (int cc = 0; cc < CG; ++cc) {
+              const bool mine = !whole && off != kOffOob && lo + cc >= c0 && lo + cc < c1;
+              buf_st_elem<ELT_C>(cbuf, mine ? off + cc * ELT_C : kOffOob, piece_elem<ELT_C>(w, cc));
+            }
           }
+          lds_barrier();
         }
-        lds_barrier();
+      };
+      if constexpr (CODEC != kCopy) {
+        if (use_tab) scatter_run(std::true_type{});
+        else scatter_run(std::false_type{});
+      } else {
+        scatter_run(std::false_type{});
       }
     }
   }
