@@ -52,6 +52,25 @@ int musa_aiter_hip_paged_tiles(int scatter, int codec, int cache_elt, int lin_el
                                int64_t head_dim, int64_t block_size, int64_t lin_token_stride,
                                int64_t lin_layer_stride, const float* k_scale, const float* v_scale, int scale_mode,
                                int fill_zeros, int dedupe, void* stream);
+/* Paged-A caches [NB, NH, HD, BS] <-> dense [batch, dense_len, NH, HD] tensors addressed through
+ * block tables: dense token (b, pos) uses slot block_tables[b, pos / BS] * BS + pos % BS while
+ * pos < seq_lens[b], the logical block is below max_blocks and the block id lies in [0, num_blocks).
+ * Same codec / element / scale / fill / dedupe arguments as musa_aiter_hip_paged_tiles;
+ * dense_token_stride in dense elements.  batch * dense_len must stay below 2^31. */
+int musa_aiter_hip_paged_dense_tiles(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtype,
+                                     void* key_cache, void* value_cache, void* dense_k, void* dense_v,
+                                     const int64_t* block_tables, const int64_t* seq_lens, int64_t batch,
+                                     int64_t dense_len, int64_t max_blocks, int64_t num_blocks, int64_t num_heads,
+                                     int64_t head_dim, int64_t block_size, int64_t dense_token_stride,
+                                     const float* k_scale, const float* v_scale, int scale_mode, int fill_zeros,
+                                     int dedupe, void* stream);
+/* Dense [batch, dense_len, row_bytes] rows gathered from token-major caches [num_tokens, row_bytes]
+ * through CSR indices (kv_indptr [batch + 1], kv_indices [index_count]); the byte-row form of
+ * musa_aiter_kv_triton_indexed_to_dense_* for any element type. */
+int musa_aiter_hip_csr_dense_rows(const void* key_cache, const void* value_cache, const int64_t* kv_indptr,
+                                  const int64_t* kv_indices, void* out_k, void* out_v, int64_t batch,
+                                  int64_t dense_len, int64_t index_count, int64_t num_tokens, int64_t row_bytes,
+                                  void* stream);
 /* Row copies between plane sets: planes given as host arrays (src_planes/dst_planes)
  * or device arrays (src_table/dst_table); a side is indexed through src_idx/dst_idx
  * or addressed directly (row = token + offset).  zero_invalid zero-fills directly
@@ -112,6 +131,52 @@ int musa_aiter_hip_copy_rows(const uint64_t* src_planes, const uint64_t* dst_pla
 MUSA_AITER_KV_HIP_PAGED_DECLS(float)
 MUSA_AITER_KV_HIP_PAGED_DECLS(half)
 MUSA_AITER_KV_HIP_PAGED_DECLS(bfloat16)
+
+/* ---- Dense preload for attention: block tables / CSR indices -> dense [B, S, NH, HD] --------------
+ * load_and_reshape_flash: binding kv_transfer.py:1369-1440, replaces kv_transfer_float.mu:985-1076
+ *   and :1420-1474; positions >= seq_lens[b] and invalid block ids are written as zeros.
+ * reshape_and_cache_back_flash: binding kv_transfer.py:1443-1524, replaces
+ *   kv_transfer_float.mu:1078-1164 and :1476-1521; the reverse scatter (duplicate destinations:
+ *   the last (batch, position) in row-major order wins, like the reference's Python loop).
+ * triton_indexed_to_dense: binding kv_transfer.py:1220-1288, replaces kv_transfer_float.mu:88-167
+ *   and :1208-1254 (wrappers :1564-1587); caches are token-major [num_tokens, NH, HD]; dense
+ *   token (b, pos) copies row kv_indices[kv_indptr[b] + pos] when that offset lies inside
+ *   [kv_indptr[b], kv_indptr[b + 1]) and [0, index_count) and the row inside [0, num_tokens);
+ *   other rows are zeros. */
+#define MUSA_AITER_KV_HIP_DENSE_DECLS(SUFFIX)                                                                       \
+  int musa_aiter_kv_load_and_reshape_flash_##SUFFIX(                                                               \
+      const void* key_cache, const void* value_cache, const int64_t* block_tables, const int64_t* seq_lens,        \
+      void* out_k, void* out_v, int64_t batch, int64_t dense_len, int64_t max_blocks, int64_t num_blocks,          \
+      int64_t num_heads, int64_t head_dim, int64_t block_size, void* stream);                                      \
+  int musa_aiter_kv_reshape_and_cache_back_flash_##SUFFIX(                                                         \
+      const void* dense_k, const void* dense_v, const int64_t* block_tables, const int64_t* seq_lens,              \
+      void* key_cache, void* value_cache, int64_t batch, int64_t dense_len, int64_t max_blocks,                    \
+      int64_t num_blocks, int64_t num_heads, int64_t head_dim, int64_t block_size, void* stream);                  \
+  int musa_aiter_kv_triton_indexed_to_dense_##SUFFIX(                                                              \
+      const void* key_cache, const void* value_cache, const int64_t* kv_indptr, const int64_t* kv_indices,         \
+      void* out_k, void* out_v, int64_t batch, int64_t dense_len, int64_t index_count, int64_t num_tokens,         \
+      int64_t num_heads, int64_t head_dim, void* stream);
+
+MUSA_AITER_KV_HIP_DENSE_DECLS(float)
+MUSA_AITER_KV_HIP_DENSE_DECLS(half)
+MUSA_AITER_KV_HIP_DENSE_DECLS(bfloat16)
+
+/* ---- Paged block copies between same-layout caches [NB,NH,HD,BS] or [NL,NB,NH,HD,BS] -------------
+ * binding kv_transfer.py:1962-2032 (float/half/bfloat16) and :1798-1868 (FP8 bytes, "_fp8_vec8");
+ * replaces kv_transfer_float.mu:907-983, :1379-1418 (wrappers :1556-1563) and
+ * fp8_kv_cache.mu:1462-1527.  block_mapping is a device int64 [num_pairs, 2] array of
+ * (source, destination) block ids; a pair with a negative or out-of-range id is skipped and a
+ * destination named by several pairs keeps the last pair.  Source and destination blocks of one
+ * call must not overlap (the copy of all pairs runs concurrently). */
+#define MUSA_AITER_KV_HIP_BLOCKS_DECL(NAME)                                                                         \
+  int NAME(const void* src_key_cache, const void* src_value_cache, void* dst_key_cache, void* dst_value_cache,     \
+           const int64_t* block_mapping, int64_t num_pairs, int64_t num_layers, int64_t src_blocks,                \
+           int64_t dst_blocks, int64_t num_heads, int64_t head_dim, int64_t block_size, void* stream);
+
+MUSA_AITER_KV_HIP_BLOCKS_DECL(musa_aiter_kv_copy_paged_blocks_float)
+MUSA_AITER_KV_HIP_BLOCKS_DECL(musa_aiter_kv_copy_paged_blocks_half)
+MUSA_AITER_KV_HIP_BLOCKS_DECL(musa_aiter_kv_copy_paged_blocks_bfloat16)
+MUSA_AITER_KV_HIP_BLOCKS_DECL(musa_aiter_kv_copy_paged_blocks_fp8_vec8)
 
 /* ---- FP8 quant-store / dequant-gather (uint8 paged-A caches) ----------------------------------
  * binding kv_transfer.py:2401-2480 (vec4 scatter), :2485-2555 (scalar scatter), :2560-2640 (hd/bs

@@ -37,14 +37,14 @@ struct ClaimScratch {
 std::mutex g_claim_mu;
 std::map<std::pair<int, uintptr_t>, ClaimScratch>* g_claims = nullptr;
 
-// Runs the claim pass for `n` indices into a destination of `rows` rows and
-// returns the tag array and epoch the copy kernel must check.  A call that
-// cannot collide (n <= 1) skips the pass.
-hipError_t prepare_claims(const int64_t* idx, int64_t n, int64_t rows, hipStream_t stream, const uint64_t** owner,
-                          uint32_t* epoch) {
+// Runs the claim pass for the `n` destinations of `src` into a destination
+// of `rows` rows and returns the tag array and epoch the copy kernel must
+// check.  A call that cannot collide (n <= 1) skips the pass.
+hipError_t prepare_claims(const kvhip::ClaimSource& src, int64_t n, int64_t rows, hipStream_t stream,
+                          const uint64_t** owner, uint32_t* epoch) {
   *owner = nullptr;
   *epoch = 0;
-  if (n <= 1 || rows <= 0 || idx == nullptr) return hipSuccess;
+  if (n <= 1 || rows <= 0 || (src.idx == nullptr && src.bt.block_tables == nullptr)) return hipSuccess;
   int dev = 0;
   hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess) return err;
@@ -79,11 +79,19 @@ hipError_t prepare_claims(const int64_t* idx, int64_t n, int64_t rows, hipStream
     cs.epoch = 0;
   }
   cs.epoch += 1;
-  err = kvhip::launch_claim(idx, n, rows, cs.owner, cs.epoch, stream);
+  err = kvhip::launch_claim(src, n, rows, cs.owner, cs.epoch, stream);
   if (err != hipSuccess) return err;
   *owner = cs.owner;
   *epoch = cs.epoch;
   return hipSuccess;
+}
+
+// Destinations read from one index vector.
+hipError_t prepare_claims(const int64_t* idx, int64_t n, int64_t rows, hipStream_t stream, const uint64_t** owner,
+                          uint32_t* epoch) {
+  kvhip::ClaimSource src;
+  src.idx = idx;
+  return prepare_claims(src, n, rows, stream, owner, epoch);
 }
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
@@ -93,7 +101,8 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 int paged_tiles(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtype, void* kc, void* vc, void* kl,
                 void* vl, const int64_t* slots, int64_t nl, int64_t t, int64_t nb, int64_t nh, int64_t hd, int64_t bs,
                 int64_t tok_stride_elems, int64_t layer_stride_elems, const float* ks, const float* vs,
-                int scale_mode, int fill_zeros, int dedupe, hipStream_t stream) {
+                int scale_mode, int fill_zeros, int dedupe, hipStream_t stream,
+                const kvhip::BlockTableSlots* bt = nullptr) {
   if (t <= 0 || nl <= 0) return hipSuccess;
   PagedTileParams p{};
   p.scatter = scatter;
@@ -118,11 +127,68 @@ int paged_tiles(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtyp
   p.scale[1] = vs;
   p.scale_mode = scale_mode;
   p.fill_zeros = fill_zeros;
+  if (bt != nullptr) p.bt = *bt;
   if (scatter && dedupe) {
-    hipError_t err = prepare_claims(slots, t, nb * bs, stream, &p.owner, &p.epoch);
+    kvhip::ClaimSource src;
+    src.idx = slots;
+    if (bt != nullptr) src.bt = *bt;
+    hipError_t err = prepare_claims(src, t, nb * bs, stream, &p.owner, &p.epoch);
     if (err != hipSuccess) return err;
   }
   return kvhip::launch_paged_tiles(p, stream);
+}
+
+// Paged-A caches <-> dense [batch, dense_len, NH, HD] tensors whose tokens are
+// addressed through block tables (the Flash-style preload); the dense side is
+// token-major with `tok_stride_elems` elements between tokens.
+int dense_tiles(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtype, void* kc, void* vc, void* dk,
+                void* dv, const int64_t* block_tables, const int64_t* seq_lens, int64_t batch, int64_t dense_len,
+                int64_t max_blocks, int64_t nb, int64_t nh, int64_t hd, int64_t bs, int64_t tok_stride_elems,
+                const float* ks, const float* vs, int scale_mode, int fill_zeros, int dedupe, hipStream_t stream) {
+  if (batch <= 0 || dense_len <= 0) return hipSuccess;
+  if (block_tables == nullptr || seq_lens == nullptr || max_blocks < 0 || max_blocks >= (int64_t{1} << 31) ||
+      dense_len >= (int64_t{1} << 31) || batch >= ((int64_t{1} << 31) - 1) / dense_len + 1)
+    return hipErrorInvalidValue;
+  kvhip::BlockTableSlots bt{};
+  bt.block_tables = block_tables;
+  bt.seq_lens = seq_lens;
+  bt.num_blocks = nb;
+  bt.dense_len = static_cast<uint32_t>(dense_len);
+  bt.max_blocks = static_cast<int32_t>(max_blocks);
+  bt.block_size = static_cast<int32_t>(bs);
+  return paged_tiles(scatter, codec, cache_elt, lin_elt, lin_dtype, kc, vc, dk, dv, nullptr, 1, batch * dense_len,
+                     nb, nh, hd, bs, tok_stride_elems, 0, ks, vs, scale_mode, fill_zeros, dedupe, stream, &bt);
+}
+
+// Dense [batch, dense_len, NH, HD] rows gathered from a token-major cache
+// [num_tokens, NH, HD] through a CSR index table; rows without a valid index
+// are zeroed.
+int csr_dense_rows(const void* kc, const void* vc, const int64_t* indptr, const int64_t* indices, void* ok, void* ov,
+                   int64_t batch, int64_t dense_len, int64_t index_count, int64_t num_tokens, int64_t row,
+                   hipStream_t stream) {
+  if (batch <= 0 || dense_len <= 0 || row <= 0) return hipSuccess;
+  if (indptr == nullptr || indices == nullptr || dense_len >= (int64_t{1} << 31) ||
+      batch >= ((int64_t{1} << 31) - 1) / dense_len + 1)
+    return hipErrorInvalidValue;
+  const uint64_t src[2] = {reinterpret_cast<uint64_t>(kc), reinterpret_cast<uint64_t>(vc)};
+  const uint64_t dst[2] = {reinterpret_cast<uint64_t>(ok), reinterpret_cast<uint64_t>(ov)};
+  RowCopyParams p{};
+  p.src_planes = src;
+  p.dst_planes = dst;
+  p.num_planes = 2;
+  p.src_idx = indices;
+  p.src_indptr = indptr;
+  p.dense_len = dense_len;
+  p.index_count = index_count;
+  p.num_tokens = batch * dense_len;
+  p.num_rows_out = batch * dense_len;
+  p.src_rows = num_tokens;
+  p.dst_rows = batch * dense_len;
+  p.row_bytes = row;
+  p.src_stride = row;
+  p.dst_stride = row;
+  p.zero_invalid = 1;
+  return kvhip::launch_row_copy(p, stream);
 }
 
 int copy_gather(int elt, void* kc, void* vc, const int64_t* slots, void* ok, void* ov, int64_t nl, int64_t t,
@@ -218,6 +284,48 @@ uint64_t addr(const void* base, int64_t byte_offset) {
   return reinterpret_cast<uint64_t>(base) + static_cast<uint64_t>(byte_offset);
 }
 
+// Whole paged blocks copied between same-layout caches [NL, NB, NH, HD, BS]
+// (NL = 1 for single-layer caches): `mapping` holds [num_pairs, 2] (source,
+// destination) block ids.  A pair with a negative or out-of-range id is
+// skipped; a destination named by several pairs keeps the last one.  One
+// block of one plane is one row of nh * hd * bs * elt bytes.
+int copy_blocks(int64_t elt, const void* sk, const void* sv, void* dk, void* dv, const int64_t* mapping,
+                int64_t num_pairs, int64_t nl, int64_t src_blocks, int64_t dst_blocks, int64_t nh, int64_t hd,
+                int64_t bs, hipStream_t stream) {
+  if (num_pairs <= 0 || nl <= 0) return hipSuccess;
+  if (mapping == nullptr || nh <= 0 || hd <= 0 || bs <= 0 || src_blocks < 0 || dst_blocks < 0)
+    return hipErrorInvalidValue;
+  const int64_t row = nh * hd * bs * elt;
+  std::vector<uint64_t> src, dst;
+  for (int64_t kv = 0; kv < 2; ++kv)
+    for (int64_t l = 0; l < nl; ++l) {
+      src.push_back(addr(kv == 0 ? sk : sv, l * src_blocks * row));
+      dst.push_back(addr(kv == 0 ? dk : dv, l * dst_blocks * row));
+    }
+  RowCopyParams p{};
+  p.src_planes = src.data();
+  p.dst_planes = dst.data();
+  p.num_planes = 2 * nl;
+  p.src_idx = mapping;
+  p.dst_idx = mapping + 1;
+  p.idx_stride = 2;
+  p.num_tokens = num_pairs;
+  p.num_rows_out = num_pairs;
+  p.src_rows = src_blocks;
+  p.dst_rows = dst_blocks;
+  p.row_bytes = row;
+  p.src_stride = row;
+  p.dst_stride = row;
+  kvhip::ClaimSource claims;
+  claims.idx = mapping + 1;
+  claims.idx_stride = 2;
+  claims.src_idx = mapping;
+  claims.src_rows = src_blocks;
+  hipError_t err = prepare_claims(claims, num_pairs, dst_blocks, stream, &p.owner, &p.epoch);
+  if (err != hipSuccess) return err;
+  return kvhip::launch_row_copy(p, stream);
+}
+
 // LMCache legacy 6-D cache [NL, 2, NB, BS, NH, HS] <-> buffer [2, NL, T, NH*HS].
 int lmcache_6d(int scatter, int elt, const void* buffer, const void* paged, const int64_t* slots, int64_t nl,
                int64_t t, int64_t nb, int64_t bs, int64_t nh, int64_t hs, hipStream_t stream) {
@@ -292,6 +400,27 @@ int musa_aiter_hip_paged_tiles(int scatter, int codec, int cache_elt, int lin_el
                      as_stream(stream));
 }
 
+int musa_aiter_hip_paged_dense_tiles(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtype,
+                                     void* key_cache, void* value_cache, void* dense_k, void* dense_v,
+                                     const int64_t* block_tables, const int64_t* seq_lens, int64_t batch,
+                                     int64_t dense_len, int64_t max_blocks, int64_t num_blocks, int64_t num_heads,
+                                     int64_t head_dim, int64_t block_size, int64_t dense_token_stride,
+                                     const float* k_scale, const float* v_scale, int scale_mode, int fill_zeros,
+                                     int dedupe, void* stream) {
+  return dense_tiles(scatter, codec, cache_elt, lin_elt, lin_dtype, key_cache, value_cache, dense_k, dense_v,
+                     block_tables, seq_lens, batch, dense_len, max_blocks, num_blocks, num_heads, head_dim,
+                     block_size, dense_token_stride, k_scale, v_scale, scale_mode, fill_zeros, dedupe,
+                     as_stream(stream));
+}
+
+int musa_aiter_hip_csr_dense_rows(const void* key_cache, const void* value_cache, const int64_t* kv_indptr,
+                                  const int64_t* kv_indices, void* out_k, void* out_v, int64_t batch,
+                                  int64_t dense_len, int64_t index_count, int64_t num_tokens, int64_t row_bytes,
+                                  void* stream) {
+  return csr_dense_rows(key_cache, value_cache, kv_indptr, kv_indices, out_k, out_v, batch, dense_len, index_count,
+                        num_tokens, row_bytes, as_stream(stream));
+}
+
 int musa_aiter_hip_copy_rows(const uint64_t* src_planes, const uint64_t* dst_planes, const uint64_t* src_table,
                              const uint64_t* dst_table, int64_t num_planes, const int64_t* src_idx,
                              const int64_t* dst_idx, int64_t num_tokens, int64_t num_rows_out, int64_t src_offset,
@@ -316,7 +445,11 @@ int musa_aiter_hip_copy_rows(const uint64_t* src_planes, const uint64_t* dst_pla
   p.dst_stride = dst_stride;
   p.zero_invalid = zero_invalid;
   if (dedupe && dst_idx != nullptr) {
-    hipError_t err = prepare_claims(dst_idx, num_tokens, dst_rows, as_stream(stream), &p.owner, &p.epoch);
+    kvhip::ClaimSource claims;
+    claims.idx = dst_idx;
+    claims.src_idx = src_idx;
+    claims.src_rows = src_rows;
+    hipError_t err = prepare_claims(claims, num_tokens, dst_rows, as_stream(stream), &p.owner, &p.epoch);
     if (err != hipSuccess) return err;
   }
   return kvhip::launch_row_copy(p, as_stream(stream));
@@ -437,6 +570,58 @@ KVHIP_PAGED_COPY(float, 4)
 KVHIP_PAGED_COPY(half, 2)
 KVHIP_PAGED_COPY(bfloat16, 2)
 #undef KVHIP_PAGED_COPY
+
+// ----- dense preload (kv_transfer.py:1220-1288, :1369-1440, :1443-1524) -----------------------
+
+#define KVHIP_DENSE(SUFFIX, ELT)                                                                                   \
+  int musa_aiter_kv_load_and_reshape_flash_##SUFFIX(                                                              \
+      const void* key_cache, const void* value_cache, const int64_t* block_tables, const int64_t* seq_lens,       \
+      void* out_k, void* out_v, int64_t batch, int64_t dense_len, int64_t max_blocks, int64_t num_blocks,         \
+      int64_t num_heads, int64_t head_dim, int64_t block_size, void* stream) {                                    \
+    return dense_tiles(0, kvhip::kCopy, ELT, ELT, kvhip::kLinBF16, const_cast<void*>(key_cache),                  \
+                       const_cast<void*>(value_cache), out_k, out_v, block_tables, seq_lens, batch, dense_len,    \
+                       max_blocks, num_blocks, num_heads, head_dim, block_size, num_heads * head_dim, nullptr,    \
+                       nullptr, 0, 1, 0, as_stream(stream));                                                     \
+  }                                                                                                               \
+  int musa_aiter_kv_reshape_and_cache_back_flash_##SUFFIX(                                                        \
+      const void* dense_k, const void* dense_v, const int64_t* block_tables, const int64_t* seq_lens,             \
+      void* key_cache, void* value_cache, int64_t batch, int64_t dense_len, int64_t max_blocks,                   \
+      int64_t num_blocks, int64_t num_heads, int64_t head_dim, int64_t block_size, void* stream) {                \
+    return dense_tiles(1, kvhip::kCopy, ELT, ELT, kvhip::kLinBF16, key_cache, value_cache,                        \
+                       const_cast<void*>(dense_k), const_cast<void*>(dense_v), block_tables, seq_lens, batch,     \
+                       dense_len, max_blocks, num_blocks, num_heads, head_dim, block_size, num_heads * head_dim,  \
+                       nullptr, nullptr, 0, 0, 1, as_stream(stream));                                            \
+  }                                                                                                               \
+  int musa_aiter_kv_triton_indexed_to_dense_##SUFFIX(                                                             \
+      const void* key_cache, const void* value_cache, const int64_t* kv_indptr, const int64_t* kv_indices,        \
+      void* out_k, void* out_v, int64_t batch, int64_t dense_len, int64_t index_count, int64_t num_tokens,        \
+      int64_t num_heads, int64_t head_dim, void* stream) {                                                        \
+    if (num_heads <= 0 || head_dim <= 0) return hipSuccess;                                                       \
+    return csr_dense_rows(key_cache, value_cache, kv_indptr, kv_indices, out_k, out_v, batch, dense_len,          \
+                          index_count, num_tokens, num_heads * head_dim * ELT, as_stream(stream));               \
+  }
+
+KVHIP_DENSE(float, 4)
+KVHIP_DENSE(half, 2)
+KVHIP_DENSE(bfloat16, 2)
+#undef KVHIP_DENSE
+
+// ----- paged block copies (kv_transfer.py:1798-1868 FP8, :1962-2032) ---------------------------
+
+#define KVHIP_BLOCKS(NAME, ELT)                                                                                    \
+  int NAME(const void* src_key_cache, const void* src_value_cache, void* dst_key_cache, void* dst_value_cache,    \
+           const int64_t* block_mapping, int64_t num_pairs, int64_t num_layers, int64_t src_blocks,               \
+           int64_t dst_blocks, int64_t num_heads, int64_t head_dim, int64_t block_size, void* stream) {           \
+    return copy_blocks(ELT, src_key_cache, src_value_cache, dst_key_cache, dst_value_cache, block_mapping,        \
+                       num_pairs, num_layers, src_blocks, dst_blocks, num_heads, head_dim, block_size,            \
+                       as_stream(stream));                                                                        \
+  }
+
+KVHIP_BLOCKS(musa_aiter_kv_copy_paged_blocks_float, 4)
+KVHIP_BLOCKS(musa_aiter_kv_copy_paged_blocks_half, 2)
+KVHIP_BLOCKS(musa_aiter_kv_copy_paged_blocks_bfloat16, 2)
+KVHIP_BLOCKS(musa_aiter_kv_copy_paged_blocks_fp8_vec8, 1)
+#undef KVHIP_BLOCKS
 
 // ----- FP8 quant-store / dequant-gather (kv_transfer.py:2446-2480 and the other FP8 shims) -----
 

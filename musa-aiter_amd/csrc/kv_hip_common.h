@@ -125,6 +125,52 @@ __device__ __forceinline__ uint64_t claim_tag(uint32_t epoch, int64_t token) {
 }
 
 // ---------------------------------------------------------------------------
+// Block-table addressing of a dense [batch, dense_len] token range (the
+// Flash-style preload, reference csrc/kvcache/kv_transfer_float.mu:985-1037):
+// token t = b * dense_len + pos lives in slot
+//   block_tables[b, pos / block_size] * block_size + pos % block_size
+// while pos < seq_lens[b], the logical block is below max_blocks and the block
+// id lies in [0, num_blocks); otherwise it has no slot (-1).  The host keeps
+// batch * dense_len, max_blocks and block_size below 2^31.
+// ---------------------------------------------------------------------------
+struct BlockTableSlots {
+  const int64_t* block_tables;  // [batch, max_blocks]; nullptr: slots come from a vector
+  const int64_t* seq_lens;      // [batch]
+  int64_t num_blocks;
+  uint32_t dense_len;
+  int32_t max_blocks;
+  int32_t block_size;
+};
+
+__device__ __forceinline__ int64_t block_table_slot(const BlockTableSlots& bt, int64_t t) {
+  const uint32_t tt = static_cast<uint32_t>(t);
+  const uint32_t b = tt / bt.dense_len;
+  const int32_t pos = static_cast<int32_t>(tt - b * bt.dense_len);
+  if (pos >= bt.seq_lens[b]) return -1;
+  const int32_t lb = pos / bt.block_size;
+  if (lb >= bt.max_blocks) return -1;
+  const int64_t blk = bt.block_tables[static_cast<int64_t>(b) * bt.max_blocks + lb];
+  if (blk < 0 || blk >= bt.num_blocks) return -1;
+  return blk * bt.block_size + (pos - lb * bt.block_size);
+}
+
+// Row of dense token u = b * dense_len + pos in a CSR index table (SGLang's
+// kv_indptr / kv_indices, reference csrc/kvcache/kv_transfer_float.mu:88-133):
+// indices[indptr[b] + pos] when that offset lies inside both [indptr[b],
+// indptr[b + 1]) and the index vector, else -1.
+__device__ __forceinline__ int64_t csr_row(const int64_t* indptr, const int64_t* indices, uint32_t dense_len,
+                                           int64_t index_count, int64_t u) {
+  const uint32_t uu = static_cast<uint32_t>(u);
+  const uint32_t b = uu / dense_len;
+  const int64_t pos = static_cast<int64_t>(uu - b * dense_len);
+  const int64_t start = indptr[b];
+  const int64_t end = indptr[b + 1];
+  const int64_t off = start + pos;
+  if (start < 0 || end < start || off >= end || off >= index_count) return -1;
+  return indices[off];
+}
+
+// ---------------------------------------------------------------------------
 // 16-bit element access inside a 16-byte register vector.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t half_of(uint32_t w, int hi) { return hi ? (w >> 16) : (w & 0xFFFFu); }

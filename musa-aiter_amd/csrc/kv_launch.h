@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "kv_hip_common.h"
+
 namespace kvhip {
 
 constexpr int kMaxPlanes = 128;
@@ -33,6 +35,7 @@ struct PagedTileParams {
   int fill_zeros;            // gather: write zeros for skipped tokens
   const uint64_t* owner;     // scatter claim tags (nullable)
   uint32_t epoch;
+  BlockTableSlots bt;        // block_tables set: slots derived per dense token, `slots` unused
 };
 
 hipError_t launch_paged_tiles(const PagedTileParams& p, hipStream_t stream);
@@ -60,13 +63,31 @@ struct RowCopyParams {
   int zero_invalid;             // direct destination: zero rows whose source is skipped
   const uint64_t* owner;        // claim tags over destination rows (nullable)
   uint32_t epoch;
+  // CSR source addressing (nullable): token u = b * dense_len + pos reads
+  // row src_idx[src_indptr[b] + pos]; src_idx holds index_count entries.
+  const int64_t* src_indptr;
+  int64_t dense_len;
+  int64_t index_count;
+  int64_t idx_stride;           // elements between index entries (0 or 1: packed vectors)
 };
 
 hipError_t launch_row_copy(const RowCopyParams& p, hipStream_t stream);
 
-// Marks, for every destination row named by `idx`, the last token (in token
-// order) that targets it.
-hipError_t launch_claim(const int64_t* idx, int64_t n, int64_t rows, uint64_t* owner, uint32_t epoch,
+// Destinations of a scatter for the claim pass: token i targets idx[i *
+// idx_stride] (or the block-table slot of dense token i when bt.block_tables
+// is set); with src_idx set, a token whose source src_idx[i * idx_stride]
+// lies outside [0, src_rows) writes nothing and claims nothing.
+struct ClaimSource {
+  const int64_t* idx = nullptr;
+  int64_t idx_stride = 1;
+  BlockTableSlots bt{};
+  const int64_t* src_idx = nullptr;
+  int64_t src_rows = 0;
+};
+
+// Marks, for every destination row, the last token (in token order) that
+// writes it.
+hipError_t launch_claim(const ClaimSource& src, int64_t n, int64_t rows, uint64_t* owner, uint32_t epoch,
                         hipStream_t stream);
 hipError_t launch_fill_u64(uint64_t* p, int64_t n, uint64_t value, hipStream_t stream);
 

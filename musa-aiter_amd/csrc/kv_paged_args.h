@@ -26,7 +26,15 @@ struct TileArgs {
   uint32_t epoch;
   int32_t block_size;          // used by the generic kernel only
   float inv_head_dim;          // 1 / head_dim, for small-integer division by head_dim
+  BlockTableSlots bt;          // block_tables set: slots derived per dense token
 };
+
+// Slot of token t: the slot vector's entry, or the block-table slot of the
+// dense token t.
+__device__ __forceinline__ int64_t slot_at(const TileArgs& a, int64_t t) {
+  if (a.bt.block_tables != nullptr) return block_table_slot(a.bt, t);
+  return a.slots[t];
+}
 
 constexpr int kTileTokens = 16;
 

@@ -180,7 +180,7 @@ __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs
   // Slot window, identical in every wave: lane i holds token t0 - 1 + i.
   const int64_t t = t0 - 1 + lane;
   int64_t s = -1;
-  if (t >= 0 && t < a.num_tokens) s = a.slots[t];
+  if (t >= 0 && t < a.num_tokens) s = slot_at(a, t);
   bool valid = (s >= 0) && (s < a.num_slots);
   if constexpr (SCATTER) {
     if (valid && a.owner != nullptr) valid = (a.owner[s] == claim_tag(a.epoch, t));
@@ -411,7 +411,7 @@ __global__ __launch_bounds__(kBlockThreads) void paged_elem_kernel(const TileArg
        e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int64_t t = e / a.nrows;
     const int64_t r = e - t * a.nrows;
-    const int64_t s = a.slots[t];
+    const int64_t s = slot_at(a, t);
     bool valid = (s >= 0) && (s < a.num_slots);
     if constexpr (SCATTER) {
       if (valid && a.owner != nullptr) valid = (a.owner[s] == claim_tag(a.epoch, t));
@@ -536,6 +536,17 @@ hipError_t launch_paged_tiles(const PagedTileParams& p, hipStream_t stream) {
   a.epoch = p.epoch;
   a.block_size = static_cast<int32_t>(p.block_size);
   a.inv_head_dim = 1.0f / static_cast<float>(p.head_dim);
+  a.bt = p.bt;
+  if (a.bt.block_tables != nullptr) {
+    // Dense tokens are numbered in 32 bits; block ids and sizes stay 32-bit too.
+    if (a.bt.seq_lens == nullptr || a.bt.dense_len == 0 || a.bt.max_blocks < 0 ||
+        p.num_tokens >= (int64_t{1} << 31) || p.block_size >= (int64_t{1} << 31))
+      return hipErrorInvalidValue;
+    a.bt.block_size = static_cast<int32_t>(p.block_size);
+    a.bt.num_blocks = p.num_blocks;
+  } else if (p.slots == nullptr) {
+    return hipErrorInvalidValue;
+  }
 
   const int rpl = 16 / p.lin_elt;
   const int cg = 16 / p.cache_elt;

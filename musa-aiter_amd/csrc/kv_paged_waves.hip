@@ -104,7 +104,7 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_gather_kernel(const 
   // Slot window: lane i holds token t0 - 1 + i.
   const int64_t t = t0 - 1 + lane;
   int64_t s = -1;
-  if (t >= 0 && t < a.num_tokens) s = a.slots[t];
+  if (t >= 0 && t < a.num_tokens) s = slot_at(a, t);
   const bool valid = (s >= 0) && (s < a.num_slots);
   const uint64_t vmask = ballot(valid);
   const int64_t s_prev = from_prev_lane(s);

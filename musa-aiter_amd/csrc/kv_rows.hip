@@ -42,6 +42,10 @@ struct RowArgs {
   int32_t num_planes;       // planes in this launch
   int32_t zero_invalid;
   uint32_t epoch;
+  const int64_t* src_indptr;  // CSR source addressing (nullable)
+  uint32_t dense_len;
+  int64_t index_count;
+  int64_t idx_stride;         // elements between consecutive entries of src_idx / dst_idx
 };
 
 // One block covers `tokens_per_block` whole rows of one plane, split into
@@ -77,8 +81,9 @@ __global__ __launch_bounds__(kBlockThreads) void row_flat_kernel(const RowArgs a
     int64_t drow = u + a.dst_offset;
     bool valid = false;
     if (u < a.num_tokens) {
-      srow = a.src_idx ? a.src_idx[u] : u + a.src_offset;
-      if (a.dst_idx) drow = a.dst_idx[u];
+      if (a.src_indptr != nullptr) srow = csr_row(a.src_indptr, a.src_idx, a.dense_len, a.index_count, u);
+      else srow = a.src_idx ? a.src_idx[u * a.idx_stride] : u + a.src_offset;
+      if (a.dst_idx) drow = a.dst_idx[u * a.idx_stride];
       valid = srow >= 0 && srow < a.src_rows && drow >= 0 && drow < a.dst_rows;
       if (valid && a.owner != nullptr) valid = (a.owner[drow] == claim_tag(a.epoch, u));
     }
@@ -103,11 +108,18 @@ __global__ __launch_bounds__(kBlockThreads) void row_flat_kernel(const RowArgs a
   }
 }
 
-__global__ __launch_bounds__(kBlockThreads) void claim_kernel(const int64_t* idx, int64_t n, int64_t rows,
+__global__ __launch_bounds__(kBlockThreads) void claim_kernel(const int64_t* idx, int64_t idx_stride,
+                                                              const BlockTableSlots bt, const int64_t* src_idx,
+                                                              int64_t src_rows, int64_t n, int64_t rows,
                                                               uint64_t* owner, uint32_t epoch) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const int64_t s = idx[i];
+  // A token whose source is skipped never writes, so it claims nothing.
+  if (src_idx != nullptr) {
+    const int64_t r = src_idx[i * idx_stride];
+    if (r < 0 || r >= src_rows) return;
+  }
+  const int64_t s = bt.block_tables != nullptr ? block_table_slot(bt, i) : idx[i * idx_stride];
   if (s < 0 || s >= rows) return;
   atomicMax(reinterpret_cast<unsigned long long*>(owner + s), static_cast<unsigned long long>(claim_tag(epoch, i)));
 }
@@ -208,6 +220,9 @@ hipError_t launch_row_copy(const RowCopyParams& p, hipStream_t stream) {
   if (p.num_rows_out <= 0 || p.num_planes <= 0 || p.row_bytes <= 0) return hipSuccess;
   if (p.num_rows_out > (int64_t{1} << 32)) return hipErrorInvalidValue;
   if (p.row_bytes > (int64_t{1} << 30)) return hipErrorInvalidValue;
+  if (p.src_indptr != nullptr &&
+      (p.src_idx == nullptr || p.dense_len <= 0 || p.num_tokens >= (int64_t{1} << 31) || p.dst_idx != nullptr))
+    return hipErrorInvalidValue;
   const bool src_host = p.src_table == nullptr;
   const bool dst_host = p.dst_table == nullptr;
   if ((src_host && p.src_planes == nullptr) || (dst_host && p.dst_planes == nullptr)) return hipErrorInvalidValue;
@@ -248,6 +263,10 @@ hipError_t launch_row_copy(const RowCopyParams& p, hipStream_t stream) {
     a.num_planes = static_cast<int32_t>(n);
     a.zero_invalid = p.zero_invalid;
     a.epoch = p.epoch;
+    a.src_indptr = p.src_indptr;
+    a.dense_len = static_cast<uint32_t>(p.dense_len);
+    a.index_count = p.index_count;
+    a.idx_stride = p.idx_stride > 0 ? p.idx_stride : 1;
     hipError_t err;
     switch (vec) {
       case 16: err = launch_rows_vec<16>(a, n, stream); break;
@@ -261,12 +280,13 @@ hipError_t launch_row_copy(const RowCopyParams& p, hipStream_t stream) {
   return hipSuccess;
 }
 
-hipError_t launch_claim(const int64_t* idx, int64_t n, int64_t rows, uint64_t* owner, uint32_t epoch,
+hipError_t launch_claim(const ClaimSource& src, int64_t n, int64_t rows, uint64_t* owner, uint32_t epoch,
                         hipStream_t stream) {
   if (n <= 0) return hipSuccess;
+  if ((src.bt.block_tables == nullptr && src.idx == nullptr) || src.idx_stride < 1) return hipErrorInvalidValue;
   const int64_t blocks = (n + kBlockThreads - 1) / kBlockThreads;
-  hipLaunchKernelGGL(claim_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kBlockThreads), 0, stream, idx, n, rows,
-                     owner, epoch);
+  hipLaunchKernelGGL(claim_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kBlockThreads), 0, stream, src.idx,
+                     src.idx_stride, src.bt, src.src_idx, src.src_rows, n, rows, owner, epoch);
   return hipGetLastError();
 }
 

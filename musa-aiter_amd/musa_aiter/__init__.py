@@ -47,10 +47,14 @@ from musa_aiter.ops.kv_transfer import (
     is_native_fp8_kv_cache_available,
     is_native_fp8_kv_vectorized_available,
     is_native_kv_transfer_available,
+    kv_copy_paged_blocks,
+    kv_copy_paged_blocks_fp8,
     kv_copy_paged_rows,
     kv_copy_paged_rows_layer_table,
     kv_copy_paged_rows_multi_pool,
     kv_linear_to_paged,
+    kv_load_and_dequantize_fp8_flash,
+    kv_load_and_reshape_flash,
     kv_linear_to_paged_fp8,
     kv_linear_to_paged_fp8_multi_layer,
     kv_linear_to_paged_multi_layer,
@@ -70,7 +74,9 @@ from musa_aiter.ops.kv_transfer import (
     kv_paged_to_merged_linear_multi_layer,
     kv_paged_to_mla_linear,
     kv_paged_to_mla_linear_multi_layer,
+    kv_reshape_and_cache_back_flash,
     kv_transfer_stats,
+    kv_triton_indexed_to_dense,
     native_fp8_kv_cache_abi_version,
     native_kv_transfer_abi_version,
     reset_kv_transfer_stats,

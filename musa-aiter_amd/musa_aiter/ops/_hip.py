@@ -35,6 +35,15 @@ _SIGNATURES: dict[str, list] = {
         _c_void_p, _c_void_p, _i32,              # k_scale, v_scale, scale_mode
         _i32, _i32, _c_void_p,                   # fill_zeros, dedupe, stream
     ],
+    "musa_aiter_hip_paged_dense_tiles": [
+        _i32, _i32, _i32, _i32, _i32,            # scatter, codec, cache_elt, lin_elt, lin_dtype
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # key_cache, value_cache, dense_k, dense_v
+        _c_void_p, _c_void_p,                    # block_tables, seq_lens
+        _i64, _i64, _i64, _i64,                  # batch, dense_len, max_blocks, blocks
+        _i64, _i64, _i64, _i64,                  # heads, head_dim, block_size, dense token stride (elements)
+        _c_void_p, _c_void_p, _i32,              # k_scale, v_scale, scale_mode
+        _i32, _i32, _c_void_p,                   # fill_zeros, dedupe, stream
+    ],
     "musa_aiter_hip_copy_rows": [
         _u64p, _u64p, _c_void_p, _c_void_p, _i64,  # host planes, device tables, planes
         _c_void_p, _c_void_p,                    # src_idx, dst_idx
@@ -47,6 +56,12 @@ _SIGNATURES: dict[str, list] = {
         _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
         _c_void_p,
     ],
+    # (key, value, kv_indptr, kv_indices, out_k, out_v, batch, dense_len, index_count, num_tokens,
+    #  row_bytes, stream)
+    "musa_aiter_hip_csr_dense_rows": [_c_void_p] * 6 + [_i64] * 5 + [_c_void_p],
+    # (src_k, src_v, dst_k, dst_v, block_mapping, pairs, layers, src_blocks, dst_blocks, heads,
+    #  head_dim, block_size, stream); the "_fp8_vec8" entry copies one-byte elements.
+    "musa_aiter_kv_copy_paged_blocks_fp8_vec8": [_c_void_p] * 5 + [_i64] * 7 + [_c_void_p],
     "musa_aiter_hip_error_string": [_i32],
     "musa_aiter_hip_backend_name": [],
     "musa_aiter_kv_transfer_abi_version": [],
@@ -198,5 +213,105 @@ def copy_rows(
             int(num_tokens), int(num_rows_out), int(src_offset), int(dst_offset), int(src_rows), int(dst_rows),
             int(row_bytes), int(src_stride), int(dst_stride),
             int(bool(zero_invalid)), int(bool(dedupe)), stream_ptr(device),
+        )
+    check(rc, op)
+
+
+def paged_dense_tiles(
+    *,
+    op: str,
+    scatter: bool,
+    codec: int,
+    cache_elt: int,
+    lin_elt: int,
+    lin_dtype: int,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    dense_k: torch.Tensor,
+    dense_v: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    batch: int,
+    dense_len: int,
+    max_blocks: int,
+    num_blocks: int,
+    num_heads: int,
+    head_dim: int,
+    block_size: int,
+    dense_token_stride: int,
+    k_scale: torch.Tensor | None = None,
+    v_scale: torch.Tensor | None = None,
+    scale_mode: int = 0,
+    fill_zeros: bool = True,
+    dedupe: bool = True,
+) -> None:
+    """Paged-A caches <-> dense [batch, dense_len, heads, head_dim] through int64 block tables."""
+    if batch <= 0 or dense_len <= 0:
+        return
+    device = key_cache.device
+    with torch.cuda.device(device):
+        rc = fn("musa_aiter_hip_paged_dense_tiles")(
+            int(scatter), int(codec), int(cache_elt), int(lin_elt), int(lin_dtype),
+            ptr(key_cache), ptr(value_cache), ptr(dense_k), ptr(dense_v), ptr(block_tables), ptr(seq_lens),
+            int(batch), int(dense_len), int(max_blocks), int(num_blocks), int(num_heads), int(head_dim),
+            int(block_size), int(dense_token_stride), ptr(k_scale), ptr(v_scale), int(scale_mode),
+            int(bool(fill_zeros)), int(bool(dedupe)), stream_ptr(device),
+        )
+    check(rc, op)
+
+
+def csr_dense_rows(
+    *,
+    op: str,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    kv_indptr: torch.Tensor,
+    kv_indices: torch.Tensor,
+    out_k: torch.Tensor,
+    out_v: torch.Tensor,
+    batch: int,
+    dense_len: int,
+    num_tokens: int,
+    row_bytes: int,
+) -> None:
+    """Dense rows gathered from token-major caches through int64 CSR indices (any element type)."""
+    if batch <= 0 or dense_len <= 0 or row_bytes <= 0:
+        return
+    device = key_cache.device
+    with torch.cuda.device(device):
+        rc = fn("musa_aiter_hip_csr_dense_rows")(
+            ptr(key_cache), ptr(value_cache), ptr(kv_indptr), ptr(kv_indices), ptr(out_k), ptr(out_v),
+            int(batch), int(dense_len), int(kv_indices.numel()), int(num_tokens), int(row_bytes),
+            stream_ptr(device),
+        )
+    check(rc, op)
+
+
+def copy_blocks(
+    *,
+    op: str,
+    src_k: torch.Tensor,
+    src_v: torch.Tensor,
+    dst_k: torch.Tensor,
+    dst_v: torch.Tensor,
+    block_mapping: torch.Tensor,
+    num_layers: int,
+    src_blocks: int,
+    dst_blocks: int,
+    block_bytes: int,
+) -> None:
+    """Whole-block byte copies; `block_mapping` is a contiguous int64 [pairs, 2] device tensor.
+
+    Blocks are opaque bytes, so every element type goes through the one-byte
+    entry with the block described as [1 head, block_bytes, 1 position].
+    """
+    pairs = int(block_mapping.shape[0])
+    if pairs <= 0 or num_layers <= 0:
+        return
+    device = dst_k.device
+    with torch.cuda.device(device):
+        rc = fn("musa_aiter_kv_copy_paged_blocks_fp8_vec8")(
+            ptr(src_k), ptr(src_v), ptr(dst_k), ptr(dst_v), ptr(block_mapping), pairs, int(num_layers),
+            int(src_blocks), int(dst_blocks), 1, int(block_bytes), 1, stream_ptr(device),
         )
     check(rc, op)

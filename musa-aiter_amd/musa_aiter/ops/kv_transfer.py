@@ -930,6 +930,433 @@ def kv_merged_linear_to_paged_fp8_multi_layer(
 
 
 # ---------------------------------------------------------------------------
+# Dense preload for attention (reference :1220-1795)
+# ---------------------------------------------------------------------------
+
+_INDEX_DTYPES = (torch.int16, torch.int32, torch.int64)
+
+
+def _first_bad_block(block_tables_cpu: torch.Tensor, seq_lens_cpu: torch.Tensor, bs: int,
+                     nb: int) -> tuple[int, int] | None:
+    """(batch index, block id) of the first block id outside [0, nb) that a sequence uses, in the
+    (batch, logical block) order of the reference's loops (:1578-1585, :1670-1676), or None."""
+    batch, max_blocks = block_tables_cpu.shape
+    if batch == 0 or max_blocks == 0:
+        return None
+    needed = (seq_lens_cpu.clamp(min=0) + bs - 1) // bs
+    used = torch.arange(max_blocks).unsqueeze(0) < needed.unsqueeze(1)
+    bad = used & ((block_tables_cpu < 0) | (block_tables_cpu >= nb))
+    if not bool(bad.any()):
+        return None
+    first = int(bad.reshape(-1).nonzero()[0].item())
+    return first // max_blocks, int(block_tables_cpu.reshape(-1)[first].item())
+
+
+def _flash_dense_len(op: str, cache: torch.Tensor, value_cache: torch.Tensor, block_tables: torch.Tensor,
+                     seq_lens: torch.Tensor, max_seq_len: int | None, bs: int, *,
+                     joint_dtype_message: bool) -> tuple[int, torch.Tensor, torch.Tensor]:
+    """Shared block_tables / seq_lens validation of the Flash-style loads, in the reference's order
+    (:1541-1564 and :1741-1763, whose dtype messages differ); returns (dense_len, seq_lens, tables) on the CPU."""
+    if block_tables.dim() != 2:
+        raise ValueError(f"{op}: block_tables must be [batch, max_blocks]")
+    if seq_lens.dim() != 1 or seq_lens.shape[0] != block_tables.shape[0]:
+        raise ValueError(f"{op}: seq_lens must be [batch]")
+    if (cache.device != value_cache.device or block_tables.device != cache.device
+            or seq_lens.device != cache.device):
+        raise ValueError(f"{op}: all tensors must be on the same device")
+    if joint_dtype_message:
+        if block_tables.dtype not in _INDEX_DTYPES or seq_lens.dtype not in _INDEX_DTYPES:
+            raise ValueError(f"{op}: block_tables and seq_lens must be integer tensors")
+    else:
+        if block_tables.dtype not in _INDEX_DTYPES:
+            raise ValueError(f"{op}: block_tables must use an integer dtype")
+        if seq_lens.dtype not in _INDEX_DTYPES:
+            raise ValueError(f"{op}: seq_lens must use an integer dtype")
+    seq_lens_cpu = seq_lens.to(device="cpu", dtype=torch.long)
+    if seq_lens_cpu.numel() > 0 and int(seq_lens_cpu.min().item()) < 0:
+        raise ValueError(f"{op}: seq_lens must be non-negative")
+    inferred_max = int(seq_lens_cpu.max().item()) if seq_lens_cpu.numel() > 0 else 0
+    dense_len = inferred_max if max_seq_len is None else int(max_seq_len)
+    if dense_len < inferred_max:
+        raise ValueError(f"{op}: max_seq_len is smaller than seq_lens max")
+    if (dense_len + bs - 1) // bs > int(block_tables.shape[1]):
+        raise ValueError(f"{op}: block_tables does not contain enough columns")
+    return dense_len, seq_lens_cpu, block_tables.to(device="cpu", dtype=torch.long)
+
+
+def _dense_out(op: str, out: torch.Tensor | None, which: str, shape: tuple[int, ...], dtype: torch.dtype,
+               device: torch.device, *, exact_dtype: bool = False) -> torch.Tensor:
+    if out is None:
+        # Every dense position is written by the kernel (zeros past seq_lens), so no clearing pass.
+        return torch.empty(shape, dtype=dtype, device=device)
+    dtype_bad = (out.dtype is not dtype) if exact_dtype else (out.dtype != dtype)
+    if tuple(out.shape) != tuple(shape) or dtype_bad or out.device != device:
+        raise ValueError(f"{op}: {which} must match [B, S, kv_heads, head_dim] dtype/device")
+    return out
+
+
+def _dense_work(out: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """The tensor the kernel writes: ``out`` itself when it is contiguous and of ``dtype``."""
+    if out.is_contiguous() and out.dtype is dtype:
+        return out
+    return torch.empty(out.shape, dtype=dtype, device=out.device)
+
+
+def _index_tensor(t: torch.Tensor) -> torch.Tensor:
+    return t.to(dtype=torch.long).contiguous()
+
+
+def kv_triton_indexed_to_dense(
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    kv_indptr: torch.Tensor,
+    kv_indices: torch.Tensor,
+    *,
+    max_seq_len: int,
+    out_k: torch.Tensor | None = None,
+    out_v: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Load SGLang Triton-decode CSR-indexed KV rows into dense ``[B, S, kv_heads, head_dim]`` tensors
+    (reference :1291-1366).
+
+    Sequence b copies ``min(max(end - start, 0), max_seq_len)`` rows
+    ``cache[kv_indices[kv_indptr[b] + i]]``; the rest of its dense rows are zeros.
+    Indices are read on the device (nothing is synchronised, so the call can be
+    captured in a graph); an offset past ``kv_indices`` or a row outside the cache
+    yields a zero row, as in the reference's native kernel
+    (kv_transfer_float.mu:114-128).
+    """
+    op = "kv_triton_indexed_to_dense"
+    if key_cache.dim() != 3 or value_cache.dim() != 3:
+        raise ValueError(f"{op}: key/value cache must be [tokens, kv_heads, head_dim]")
+    if key_cache.shape != value_cache.shape or key_cache.dtype != value_cache.dtype or key_cache.device != value_cache.device:
+        raise ValueError(f"{op}: key/value cache shape, dtype, and device must match")
+    if kv_indptr.dim() != 1 or kv_indptr.numel() < 2:
+        raise ValueError(f"{op}: kv_indptr must be [batch + 1]")
+    if kv_indices.dim() != 1:
+        raise ValueError(f"{op}: kv_indices must be 1-D")
+    if kv_indptr.device != key_cache.device or kv_indices.device != key_cache.device:
+        raise ValueError(f"{op}: all tensors must be on the same device")
+    if kv_indptr.dtype not in _INDEX_DTYPES or kv_indices.dtype not in _INDEX_DTYPES:
+        raise ValueError(f"{op}: indices must use integer dtype")
+    batch = int(kv_indptr.shape[0] - 1)
+    dense_len = int(max_seq_len)
+    if dense_len < 0:
+        raise ValueError(f"{op}: max_seq_len must be non-negative")
+    ntok, nh, hd = map(int, key_cache.shape)
+    shape = (batch, dense_len, nh, hd)
+    for name, out, cache in (("out_k", out_k, key_cache), ("out_v", out_v, value_cache)):
+        if out is not None and (tuple(out.shape) != shape or out.dtype != cache.dtype or out.device != cache.device
+                                or not out.is_contiguous()):
+            raise ValueError(f"{op}: {name} must match [B, S, kv_heads, head_dim] dtype/device and be contiguous")
+    _require_rocm(op, key_cache)
+    if out_k is None:
+        out_k = torch.empty(shape, dtype=key_cache.dtype, device=key_cache.device)
+    if out_v is None:
+        out_v = torch.empty(shape, dtype=value_cache.dtype, device=value_cache.device)
+    _hip.csr_dense_rows(
+        op=op, key_cache=key_cache.contiguous(), value_cache=value_cache.contiguous(),
+        kv_indptr=_index_tensor(kv_indptr), kv_indices=_index_tensor(kv_indices), out_k=out_k, out_v=out_v,
+        batch=batch, dense_len=dense_len, num_tokens=ntok, row_bytes=nh * hd * key_cache.element_size(),
+    )
+    _emit(op, key_cache, "gfx950 CSR-indexed dense KV preload")
+    return out_k, out_v
+
+
+def kv_load_and_reshape_flash(
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    *,
+    max_seq_len: int | None = None,
+    out_k: torch.Tensor | None = None,
+    out_v: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Load paged KV blocks into dense Flash-style ``[B, S, kv_heads, head_dim]`` tensors (reference :1527-1622).
+
+    Dense position ``pos`` of sequence ``b`` holds cache slot
+    ``block_tables[b, pos // block_size] * block_size + pos % block_size`` for
+    ``pos < seq_lens[b]`` and zeros after it.  One launch moves both caches.
+    """
+    op = "kv_load_and_reshape_flash"
+    nb, nh, hd, bs = _validate_paged_shapes(key_cache, value_cache, name=op)
+    dense_len, seq_lens_cpu, tables_cpu = _flash_dense_len(op, key_cache, value_cache, block_tables, seq_lens,
+                                                           max_seq_len, bs, joint_dtype_message=False)
+    batch = int(block_tables.shape[0])
+    shape = (batch, dense_len, nh, hd)
+    out_k = _dense_out(op, out_k, "out_k", shape, key_cache.dtype, key_cache.device)
+    out_v = _dense_out(op, out_v, "out_v", shape, value_cache.dtype, value_cache.device)
+    bad = _first_bad_block(tables_cpu, seq_lens_cpu, bs, nb)
+    if bad is not None:
+        raise ValueError(f"{op}: invalid block id {bad[1]}")
+    elt = _float_elt(op, key_cache, value_cache)
+    _require_rocm(op, key_cache)
+    caches = _CachePair(key_cache, value_cache, writable=False)
+    wk, wv = _dense_work(out_k, key_cache.dtype), _dense_work(out_v, value_cache.dtype)
+    _hip.paged_dense_tiles(
+        op=op, scatter=False, codec=_CODEC_COPY, cache_elt=elt, lin_elt=elt, lin_dtype=0,
+        key_cache=caches.k, value_cache=caches.v, dense_k=wk, dense_v=wv,
+        block_tables=_index_tensor(block_tables), seq_lens=_index_tensor(seq_lens), batch=batch,
+        dense_len=dense_len, max_blocks=int(block_tables.shape[1]), num_blocks=nb, num_heads=nh, head_dim=hd,
+        block_size=bs, dense_token_stride=nh * hd, fill_zeros=True,
+    )
+    if wk is not out_k:
+        out_k.copy_(wk)
+    if wv is not out_v:
+        out_v.copy_(wv)
+    _emit(op, key_cache, "gfx950 block-table dense preload")
+    return out_k, out_v
+
+
+def kv_reshape_and_cache_back_flash(
+    dense_k: torch.Tensor,
+    dense_v: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+) -> bool:
+    """Scatter dense Flash-style KV tensors back into paged cache blocks (reference :1625-1726).
+
+    Positions ``pos < seq_lens[b]`` are written; blocks shared by several
+    sequences keep the last (batch, position) in row-major order, as the
+    reference's batch loop does.  Returns True.
+    """
+    op = "kv_reshape_and_cache_back_flash"
+    if dense_k.dim() != 4 or dense_v.dim() != 4:
+        raise ValueError("dense Flash KV tensors must be [batch, seq, heads, head_dim]")
+    if dense_k.shape != dense_v.shape or dense_k.dtype != dense_v.dtype:
+        raise ValueError("dense K and V tensors must have matching shape and dtype")
+    if dense_k.device != dense_v.device:
+        raise ValueError("dense K and V tensors must be on the same device")
+    nb, nh, hd, bs = _validate_paged_shapes(key_cache, value_cache, name=op)
+    if key_cache.dtype != dense_k.dtype or value_cache.dtype != dense_v.dtype:
+        raise ValueError("dense and paged KV tensors must have matching dtypes")
+    if key_cache.device != dense_k.device or value_cache.device != dense_k.device:
+        raise ValueError("dense and paged KV tensors must be on the same device")
+    if tuple(dense_k.shape[2:]) != (nh, hd):
+        raise ValueError("dense KV head shape does not match paged cache")
+    if block_tables.dim() != 2:
+        raise ValueError(f"{op}: block_tables must be [batch, max_blocks]")
+    if seq_lens.dim() != 1 or seq_lens.shape[0] != block_tables.shape[0]:
+        raise ValueError(f"{op}: seq_lens must be [batch]")
+    if dense_k.shape[0] != block_tables.shape[0]:
+        raise ValueError(f"{op}: dense batch does not match block_tables")
+    if block_tables.device != dense_k.device or seq_lens.device != dense_k.device:
+        raise ValueError(f"{op}: all tensors must be on the same device")
+    if block_tables.dtype not in _INDEX_DTYPES:
+        raise ValueError(f"{op}: block_tables must use an integer dtype")
+    if seq_lens.dtype not in _INDEX_DTYPES:
+        raise ValueError(f"{op}: seq_lens must use an integer dtype")
+    seq_lens_cpu = seq_lens.to(device="cpu", dtype=torch.long)
+    tables_cpu = block_tables.to(device="cpu", dtype=torch.long)
+    batch, dense_len = int(dense_k.shape[0]), int(dense_k.shape[1])
+    max_blocks = int(block_tables.shape[1])
+    # The reference checks each sequence in turn (:1660-1676): length, table width, block ids.
+    bad_len = (seq_lens_cpu < 0) | (seq_lens_cpu > dense_len)
+    bad_width = (seq_lens_cpu.clamp(min=0) + bs - 1) // bs > max_blocks
+    bad_block = _first_bad_block(tables_cpu, torch.where(bad_len | bad_width, 0, seq_lens_cpu), bs, nb)
+    first = [int(bad_len.nonzero()[0].item()) if bool(bad_len.any()) else batch,
+             int(bad_width.nonzero()[0].item()) if bool(bad_width.any()) else batch,
+             bad_block[0] if bad_block is not None else batch]
+    b = min(first)
+    if b < batch:
+        if first[0] == b:
+            raise ValueError(f"{op}: seq_lens exceeds dense sequence length")
+        if first[1] == b:
+            raise ValueError(f"{op}: block_tables does not contain enough columns")
+        raise ValueError(f"{op}: invalid block id {bad_block[1]}")
+    elt = _float_elt(op, dense_k, key_cache)
+    _require_rocm(op, dense_k)
+    caches = _CachePair(key_cache, value_cache, writable=True)
+    _hip.paged_dense_tiles(
+        op=op, scatter=True, codec=_CODEC_COPY, cache_elt=elt, lin_elt=elt, lin_dtype=0,
+        key_cache=caches.k, value_cache=caches.v, dense_k=dense_k.contiguous(), dense_v=dense_v.contiguous(),
+        block_tables=_index_tensor(block_tables), seq_lens=_index_tensor(seq_lens), batch=batch,
+        dense_len=dense_len, max_blocks=max_blocks, num_blocks=nb, num_heads=nh, head_dim=hd, block_size=bs,
+        dense_token_stride=nh * hd, fill_zeros=False,
+    )
+    caches.finish()
+    _emit(op, dense_k, "gfx950 block-table dense write-back")
+    return True
+
+
+def kv_load_and_dequantize_fp8_flash(
+    key_cache_fp8: torch.Tensor,
+    value_cache_fp8: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    k_scale: torch.Tensor | float,
+    v_scale: torch.Tensor | float,
+    *,
+    max_seq_len: int | None = None,
+    out_dtype: torch.dtype = torch.bfloat16,
+    fp8_format: Literal["e4m3", "e5m2"] = "e4m3",
+    out_k: torch.Tensor | None = None,
+    out_v: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Load paged FP8 blocks into dense dequantized ``[B, S, kv_heads, head_dim]`` tensors (reference :1729-1781).
+
+    Each dense position decodes like kv_paged_fp8_to_linear over the
+    sequence's slots (``code * scale`` in fp32, rounded to ``out_dtype``);
+    positions past ``seq_lens[b]`` are zeros.  One launch covers the batch.
+    """
+    op = "kv_load_and_dequantize_fp8_flash"
+    nb, nh, hd, bs = _validate_paged_shapes(key_cache_fp8, value_cache_fp8, name=op)
+    dense_len, seq_lens_cpu, tables_cpu = _flash_dense_len(op, key_cache_fp8, value_cache_fp8, block_tables,
+                                                           seq_lens, max_seq_len, bs, joint_dtype_message=True)
+    batch = int(block_tables.shape[0])
+    shape = (batch, dense_len, nh, hd)
+    out_k = _dense_out(op, out_k, "out_k", shape, out_dtype, key_cache_fp8.device, exact_dtype=True)
+    out_v = _dense_out(op, out_v, "out_v", shape, out_dtype, value_cache_fp8.device, exact_dtype=True)
+    bad = _first_bad_block(tables_cpu, seq_lens_cpu, bs, nb)
+    if bad is not None:
+        raise ValueError(f"{op}: invalid block id {bad[1]}")
+    if batch == 0:
+        return out_k, out_v
+    # The reference decodes through kv_paged_fp8_to_linear, whose checks and messages apply.
+    fp8_format = _normalize_fp8_format(fp8_format)
+    _validate_fp8_cache_tensor(key_cache_fp8, name="kv_paged_fp8_to_linear key_cache_fp8")
+    _validate_fp8_cache_tensor(value_cache_fp8, name="kv_paged_fp8_to_linear value_cache_fp8")
+    ks = _ensure_fp8_scale(k_scale, device=key_cache_fp8.device, name="k_scale", num_heads=nh)
+    vs = _ensure_fp8_scale(v_scale, device=value_cache_fp8.device, name="v_scale", num_heads=nh)
+    _require_rocm(op, key_cache_fp8)
+    ks, vs, mode = _scale_pair(ks, vs, nh)
+    work_dtype = out_dtype if out_dtype in _LIN_DTYPE else torch.float32
+    caches = _CachePair(_fp8_bytes(key_cache_fp8), _fp8_bytes(value_cache_fp8), writable=False)
+    wk, wv = _dense_work(out_k, work_dtype), _dense_work(out_v, work_dtype)
+    _hip.paged_dense_tiles(
+        op=op, scatter=False, codec=_codec(fp8_format), cache_elt=1, lin_elt=_ELT[work_dtype],
+        lin_dtype=_LIN_DTYPE[work_dtype], key_cache=caches.k, value_cache=caches.v, dense_k=wk, dense_v=wv,
+        block_tables=_index_tensor(block_tables), seq_lens=_index_tensor(seq_lens), batch=batch,
+        dense_len=dense_len, max_blocks=int(block_tables.shape[1]), num_blocks=nb, num_heads=nh, head_dim=hd,
+        block_size=bs, dense_token_stride=nh * hd, k_scale=ks, v_scale=vs, scale_mode=mode, fill_zeros=True,
+    )
+    if wk is not out_k:
+        out_k.copy_(wk)
+    if wv is not out_v:
+        out_v.copy_(wv)
+    _emit(op, key_cache_fp8, f"gfx950 block-table {fp8_format.upper()} dequantize preload")
+    return out_k, out_v
+
+
+# ---------------------------------------------------------------------------
+# Paged block copies (reference :1798-2091)
+# ---------------------------------------------------------------------------
+
+
+def _validate_block_copy_shapes(src_key_cache: torch.Tensor, src_value_cache: torch.Tensor,
+                                dst_key_cache: torch.Tensor, dst_value_cache: torch.Tensor, *,
+                                name: str) -> tuple[int, int, bool]:
+    if src_key_cache.shape != src_value_cache.shape:
+        raise ValueError(f"{name}: source key/value cache shapes must match")
+    if dst_key_cache.shape != dst_value_cache.shape:
+        raise ValueError(f"{name}: destination key/value cache shapes must match")
+    if src_key_cache.dim() not in (4, 5) or dst_key_cache.dim() != src_key_cache.dim():
+        raise ValueError(f"{name}: caches must be 4-D single-layer or 5-D multi-layer paged tensors")
+    if src_key_cache.dtype != src_value_cache.dtype or dst_key_cache.dtype != dst_value_cache.dtype:
+        raise ValueError(f"{name}: key/value dtype pairs must match")
+    if src_key_cache.dtype != dst_key_cache.dtype:
+        raise ValueError(f"{name}: source and destination dtypes must match")
+    if src_key_cache.dim() == 4:
+        if src_key_cache.shape[1:] != dst_key_cache.shape[1:]:
+            raise ValueError(f"{name}: single-layer cache tails must match")
+        return int(src_key_cache.shape[0]), int(dst_key_cache.shape[0]), False
+    if src_key_cache.shape[0] != dst_key_cache.shape[0] or src_key_cache.shape[2:] != dst_key_cache.shape[2:]:
+        raise ValueError(f"{name}: multi-layer cache layer count and tails must match")
+    return int(src_key_cache.shape[1]), int(dst_key_cache.shape[1]), True
+
+
+def _ensure_block_mapping_pairs(block_mapping: torch.Tensor, *, src_blocks: int, dst_blocks: int,
+                                name: str) -> torch.Tensor:
+    if block_mapping.dim() != 2 or block_mapping.shape[1] != 2:
+        raise ValueError(f"{name}: block_mapping must be [num_pairs, 2] with source and destination block ids")
+    if block_mapping.dtype not in _INDEX_DTYPES:
+        raise ValueError(f"{name}: block_mapping must use an integer dtype")
+    pairs = block_mapping.to(device="cpu", dtype=torch.long)
+    if pairs.numel() == 0:
+        return pairs
+    valid = (pairs[:, 0] >= 0) & (pairs[:, 1] >= 0)
+    if not bool(valid.any()):
+        return pairs
+    src_max = int(pairs[valid, 0].max().item())
+    dst_max = int(pairs[valid, 1].max().item())
+    if src_max >= src_blocks:
+        raise ValueError(f"{name}: source block index {src_max} out of bounds for {src_blocks} blocks")
+    if dst_max >= dst_blocks:
+        raise ValueError(f"{name}: destination block index {dst_max} out of bounds for {dst_blocks} blocks")
+    return pairs
+
+
+def _copy_blocks(op: str, src_k: torch.Tensor, src_v: torch.Tensor, dst_k: torch.Tensor, dst_v: torch.Tensor,
+                 pairs: torch.Tensor, *, src_blocks: int, dst_blocks: int, multi_layer: bool) -> int:
+    count = int(((pairs[:, 0] >= 0) & (pairs[:, 1] >= 0)).sum().item()) if pairs.numel() else 0
+    if count == 0:
+        return 0
+    _require_rocm(op, src_k, dst_k)
+    if src_k.device != dst_k.device:
+        raise NotImplementedError(f"{op}: source and destination caches must be on one device")
+    dst = _CachePair(dst_k, dst_v, writable=True)
+    nl = int(src_k.shape[0]) if multi_layer else 1
+    tail = src_k.shape[2:] if multi_layer else src_k.shape[1:]
+    block_bytes = src_k.element_size()
+    for extent in tail:
+        block_bytes *= int(extent)
+    _hip.copy_blocks(
+        op=op, src_k=src_k.contiguous(), src_v=src_v.contiguous(), dst_k=dst.k, dst_v=dst.v,
+        block_mapping=pairs.to(device=dst_k.device).contiguous(), num_layers=nl, src_blocks=src_blocks,
+        dst_blocks=dst_blocks, block_bytes=block_bytes,
+    )
+    dst.finish()
+    return count
+
+
+def kv_copy_paged_blocks(
+    src_key_cache: torch.Tensor,
+    src_value_cache: torch.Tensor,
+    dst_key_cache: torch.Tensor,
+    dst_value_cache: torch.Tensor,
+    block_mapping: torch.Tensor,
+) -> int:
+    """Copy selected paged KV cache blocks between same-layout caches (reference :2035-2091).
+
+    ``block_mapping`` is ``[num_pairs, 2]`` (source, destination) block ids;
+    pairs with a negative id are skipped and the number of copied pairs is
+    returned.  A destination named twice keeps the last pair.  Source and
+    destination blocks of one call must not overlap: all pairs copy at once.
+    """
+    op = "kv_copy_paged_blocks"
+    src_blocks, dst_blocks, multi_layer = _validate_block_copy_shapes(
+        src_key_cache, src_value_cache, dst_key_cache, dst_value_cache, name=op)
+    pairs = _ensure_block_mapping_pairs(block_mapping, src_blocks=src_blocks, dst_blocks=dst_blocks, name=op)
+    copied = _copy_blocks(op, src_key_cache, src_value_cache, dst_key_cache, dst_value_cache, pairs,
+                          src_blocks=src_blocks, dst_blocks=dst_blocks, multi_layer=multi_layer)
+    _emit(op, dst_key_cache, "gfx950 whole-block copy")
+    return copied
+
+
+def kv_copy_paged_blocks_fp8(
+    src_key_cache_fp8: torch.Tensor,
+    src_value_cache_fp8: torch.Tensor,
+    dst_key_cache_fp8: torch.Tensor,
+    dst_value_cache_fp8: torch.Tensor,
+    block_mapping: torch.Tensor,
+) -> int:
+    """Raw FP8 paged block copy between same-layout caches (reference :1871-1906); see kv_copy_paged_blocks."""
+    op = "kv_copy_paged_blocks_fp8"
+    src_blocks, dst_blocks, multi_layer = _validate_block_copy_shapes(
+        src_key_cache_fp8, src_value_cache_fp8, dst_key_cache_fp8, dst_value_cache_fp8, name=op)
+    for tensor in (src_key_cache_fp8, src_value_cache_fp8, dst_key_cache_fp8, dst_value_cache_fp8):
+        _validate_fp8_cache_tensor(tensor, name=op)
+    pairs = _ensure_block_mapping_pairs(block_mapping, src_blocks=src_blocks, dst_blocks=dst_blocks, name=op)
+    copied = _copy_blocks(op, src_key_cache_fp8, src_value_cache_fp8, dst_key_cache_fp8, dst_value_cache_fp8, pairs,
+                          src_blocks=src_blocks, dst_blocks=dst_blocks, multi_layer=multi_layer)
+    _emit(op, dst_key_cache_fp8, "gfx950 raw FP8 whole-block copy")
+    return copied
+
+
+# ---------------------------------------------------------------------------
 # MLA / DSA flat caches [NB, BS, D] (reference :3769-4118)
 # ---------------------------------------------------------------------------
 

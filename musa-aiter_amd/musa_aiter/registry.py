@@ -100,6 +100,16 @@ _kv("kv_paged_to_mla_linear", "hip-native", _FLOAT, "MLA flat caches [NB, BS, D]
 _kv("kv_mla_linear_to_paged", "hip-native", _FLOAT, "Token-major kv and rope rows -> MLA flat caches.")
 _kv("kv_paged_to_mla_linear_multi_layer", "hip-native", _FLOAT, "Stacked MLA flat caches -> layer-major rows.")
 _kv("kv_mla_linear_to_paged_multi_layer", "hip-native", _FLOAT, "Layer-major rows -> stacked MLA flat caches.")
+# Dense preload for attention and whole-block copies.
+_kv("kv_load_and_reshape_flash", "hip-native", _FLOAT,
+    "Paged KV blocks -> dense Flash-style [batch, seq, kv_heads, head_dim] through block tables.")
+_kv("kv_load_and_dequantize_fp8_flash", "hip-native", ("uint8", "float8_e4m3fn", "float8_e5m2"),
+    "Paged FP8 blocks -> dense dequantized Flash-style tensors through block tables.")
+_kv("kv_reshape_and_cache_back_flash", "hip-native", _FLOAT,
+    "Dense Flash-style KV tensors -> paged KV blocks through block tables.")
+_kv("kv_copy_paged_blocks", "hip-native", _FLOAT, "Copy selected paged KV blocks between same-layout caches.")
+_kv("kv_copy_paged_blocks_fp8", "hip-native", ("uint8", "float8_e4m3fn", "float8_e5m2"),
+    "Raw FP8 paged KV block copy between same-layout caches.")
 # DSV4 opaque byte rows.
 _kv("kv_copy_paged_rows", "hip-native", ("uint8",), "Opaque byte-row gather/scatter between row pools (per layer).")
 _kv("kv_copy_paged_rows_layer_table", "hip-native", ("uint8",), "Opaque byte-row copy across a layer table, one launch.")

@@ -235,6 +235,145 @@ def paged_fp8_to_linear(cache_u8: np.ndarray, slots: np.ndarray, scale: np.ndarr
 
 
 # ---------------------------------------------------------------------------
+# Dense preload for attention (kv_transfer.py:1291-1781)
+# ---------------------------------------------------------------------------
+
+
+def _logical_blocks(seq_len: int, bs: int, max_blocks: int, num_blocks: int, table_row: np.ndarray):
+    """(start, end, block_id) of every logical block of one sequence (kv_transfer.py:1609-1622).
+
+    The reference's Python path raises on a block id outside [0, num_blocks)
+    (:1581-1585); its native kernels, which C-ABI callers reach, skip such a
+    block and any logical block at or past ``max_blocks``
+    (kv_transfer_float.mu:1006-1030).  Both are expressed by skipping here.
+    """
+    for lb in range((max(seq_len, 0) + bs - 1) // bs):
+        if lb >= max_blocks:
+            break
+        blk = int(table_row[lb])
+        if blk < 0 or blk >= num_blocks:
+            continue
+        start = lb * bs
+        yield start, min(start + bs, seq_len), blk
+
+
+def load_and_reshape_flash(cache: np.ndarray, block_tables: np.ndarray, seq_lens: np.ndarray,
+                           dense_len: int) -> np.ndarray:
+    """kv_load_and_reshape_flash (kv_transfer.py:1599-1622) for one cache: dense [B, S, NH, HD].
+
+    Positions at or past ``seq_lens[b]`` stay zero (``out.zero_()``, :1565-1576).
+    """
+    nb, nh, hd, bs = cache.shape
+    block_tables = np.asarray(block_tables, dtype=np.int64)
+    seq_lens = np.asarray(seq_lens, dtype=np.int64)
+    batch, max_blocks = block_tables.shape
+    out = np.zeros((batch, dense_len, nh, hd), dtype=cache.dtype)
+    for b in range(batch):
+        for start, end, blk in _logical_blocks(int(seq_lens[b]), bs, max_blocks, nb, block_tables[b]):
+            end = min(end, dense_len)
+            if end > start:
+                out[b, start:end] = cache[blk, :, :, :end - start].transpose(2, 0, 1)
+    return out
+
+
+def reshape_and_cache_back_flash(dense: np.ndarray, cache: np.ndarray, block_tables: np.ndarray,
+                                 seq_lens: np.ndarray) -> None:
+    """kv_reshape_and_cache_back_flash's loop (kv_transfer.py:1700-1715) for one cache, in place.
+
+    Later (batch, position) pairs overwrite earlier ones on shared blocks, as
+    the reference's batch-major loop does.
+    """
+    nb, nh, hd, bs = cache.shape
+    block_tables = np.asarray(block_tables, dtype=np.int64)
+    seq_lens = np.asarray(seq_lens, dtype=np.int64)
+    batch, max_blocks = block_tables.shape
+    dense_len = dense.shape[1]
+    for b in range(batch):
+        for start, end, blk in _logical_blocks(int(seq_lens[b]), bs, max_blocks, nb, block_tables[b]):
+            end = min(end, dense_len)
+            if end > start:
+                cache[blk, :, :, :end - start] = dense[b, start:end].transpose(1, 2, 0)
+
+
+def flash_dense_slots(block_tables: np.ndarray, seq_lens: np.ndarray, dense_len: int, block_size: int,
+                      num_blocks: int) -> np.ndarray:
+    """Per-sequence slot vectors of kv_load_and_dequantize_fp8_flash (kv_transfer.py:1766-1776): [B, S]."""
+    block_tables = np.asarray(block_tables, dtype=np.int64)
+    seq_lens = np.asarray(seq_lens, dtype=np.int64)
+    batch, max_blocks = block_tables.shape
+    slots = np.full((batch, dense_len), -1, dtype=np.int64)
+    for b in range(batch):
+        for start, end, blk in _logical_blocks(int(seq_lens[b]), block_size, max_blocks, num_blocks,
+                                               block_tables[b]):
+            end = min(end, dense_len)
+            slots[b, start:end] = blk * block_size + np.arange(end - start)
+    return slots
+
+
+def load_and_dequantize_fp8_flash(cache_u8: np.ndarray, block_tables: np.ndarray, seq_lens: np.ndarray,
+                                  scale: np.ndarray, fmt: str, out_dtype: str, dense_len: int) -> np.ndarray:
+    """kv_load_and_dequantize_fp8_flash (kv_transfer.py:1764-1781) for one cache: one
+    kv_paged_fp8_to_linear per sequence over its slot vector."""
+    nb, nh, hd, bs = cache_u8.shape
+    slots = flash_dense_slots(block_tables, seq_lens, dense_len, bs, nb)
+    rows = [paged_fp8_to_linear(cache_u8, slots[b], scale, fmt, out_dtype) for b in range(slots.shape[0])]
+    if not rows:
+        return np.zeros((0, dense_len, nh, hd), dtype=np.uint16 if out_dtype != "float32" else np.uint32)
+    return np.stack(rows)
+
+
+def triton_indexed_to_dense(cache: np.ndarray, kv_indptr: np.ndarray, kv_indices: np.ndarray,
+                            dense_len: int) -> np.ndarray:
+    """kv_triton_indexed_to_dense (kv_transfer.py:1355-1366) for one token-major cache [N, NH, HD].
+
+    Sequence b copies ``min(max(end - start, 0), dense_len)`` rows
+    ``cache[kv_indices[start + i]]``.  Where the reference's Python path would
+    fail (an offset past ``kv_indices``, a row outside the cache, a negative
+    ``start``) its native kernel writes zeros (kv_transfer_float.mu:114-128);
+    so does this function.
+    """
+    kv_indptr = np.asarray(kv_indptr, dtype=np.int64)
+    kv_indices = np.asarray(kv_indices, dtype=np.int64)
+    n = cache.shape[0]
+    batch = kv_indptr.shape[0] - 1
+    out = np.zeros((batch, dense_len) + cache.shape[1:], dtype=cache.dtype)
+    for b in range(batch):
+        start, end = int(kv_indptr[b]), int(kv_indptr[b + 1])
+        if start < 0:
+            continue
+        copy_len = min(max(end - start, 0), dense_len)
+        for i in range(copy_len):
+            off = start + i
+            if off >= kv_indices.shape[0]:
+                break
+            row = int(kv_indices[off])
+            if 0 <= row < n:
+                out[b, i] = cache[row]
+    return out
+
+
+def copy_paged_blocks(src: np.ndarray, dst: np.ndarray, pairs: np.ndarray, *, multi_layer: bool) -> int:
+    """kv_copy_paged_blocks's pair loop (kv_transfer.py:2078-2091) for one cache, in place.
+
+    Pairs with a negative id are skipped; later pairs overwrite earlier ones.
+    The reference's native kernel (kv_transfer_float.mu:934-937) also skips ids
+    past either cache, which the Python layer rejects beforehand.
+    """
+    copied = 0
+    for s_blk, d_blk in np.asarray(pairs, dtype=np.int64).reshape(-1, 2).tolist():
+        nsrc = src.shape[1] if multi_layer else src.shape[0]
+        ndst = dst.shape[1] if multi_layer else dst.shape[0]
+        if s_blk < 0 or d_blk < 0 or s_blk >= nsrc or d_blk >= ndst:
+            continue
+        if multi_layer:
+            dst[:, d_blk] = src[:, s_blk]
+        else:
+            dst[d_blk] = src[s_blk]
+        copied += 1
+    return copied
+
+
+# ---------------------------------------------------------------------------
 # Token-major flat caches [NB, BS, D] (kv_transfer.py:3786-3838)
 # ---------------------------------------------------------------------------
 

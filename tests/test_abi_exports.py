@@ -28,7 +28,7 @@ def _declared_symbols() -> set[str]:
         m = re.match(r"\s*(\w+)\((\w+)\)\s*$", line)
         if m and m.group(1) in macros:
             param, body = macros[m.group(1)]
-            expanded.append(body.replace(f"##{param}", m.group(2)))
+            expanded.append(re.sub(rf"\b{param}\b", m.group(2), body.replace(f"##{param}", m.group(2))))
         elif not line.lstrip().startswith("#"):
             expanded.append(line)
     body = "\n".join(expanded)
@@ -37,8 +37,10 @@ def _declared_symbols() -> set[str]:
 
 def test_header_declares_expected_families():
     names = _declared_symbols()
-    assert len(names) == 88
-    for required in ("musa_aiter_kv_paged_to_linear_bfloat16", "musa_aiter_kv_linear_to_paged_multi_layer_half",
+    assert len(names) == 103
+    for required in ("musa_aiter_kv_load_and_reshape_flash_half", "musa_aiter_kv_triton_indexed_to_dense_bfloat16",
+                     "musa_aiter_kv_reshape_and_cache_back_flash_float", "musa_aiter_kv_copy_paged_blocks_fp8_vec8",
+                     "musa_aiter_hip_paged_dense_tiles","musa_aiter_kv_paged_to_linear_bfloat16", "musa_aiter_kv_linear_to_paged_multi_layer_half",
                      "musa_aiter_kv_paged_fp8_to_linear_vec4_e5m2", "lmcache_paged_to_kv_buffer_two_x_nl_coalesced_u16",
                      "lmcache_mla_paged_to_buffer_list_bfloat16", "musa_aiter_kv_copy_paged_rows_layer_table_u8",
                      "lmcache_kv_strided_block_transfer", "musa_aiter_hip_paged_tiles"):

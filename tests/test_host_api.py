@@ -133,6 +133,8 @@ def test_kvcache_registry_rows_and_backend():
         "kv_linear_to_paged_fp8_multi_layer", "kv_paged_fp8_to_linear_multi_layer", "kv_merged_linear_to_paged_fp8",
         "kv_paged_fp8_to_merged_linear", "kv_merged_linear_to_paged_fp8_multi_layer",
         "kv_paged_fp8_to_merged_linear_multi_layer", "kv_paged_to_mla_linear", "kv_mla_linear_to_paged",
+        "kv_load_and_reshape_flash", "kv_load_and_dequantize_fp8_flash", "kv_reshape_and_cache_back_flash",
+        "kv_copy_paged_blocks", "kv_copy_paged_blocks_fp8",
         "kv_paged_to_mla_linear_multi_layer", "kv_mla_linear_to_paged_multi_layer", "kv_copy_paged_rows",
         "kv_copy_paged_rows_layer_table", "kv_copy_paged_rows_multi_pool", "lmcache_kv_paged_to_buffer_two_x_nl",
         "lmcache_kv_buffer_to_paged_two_x_nl", "lmcache_kv_paged_to_buffer", "lmcache_kv_buffer_to_paged",
@@ -204,3 +206,85 @@ def test_abi_version_probes():
     assert musa_aiter.native_lmcache_kv_transfer_abi_version() == 1
     assert musa_aiter.native_kv_transfer_abi_version() == 1
     assert musa_aiter.native_fp8_kv_cache_abi_version() == 1
+
+
+def test_dense_preload_validation_contract():
+    # op_tests/test_kv_transfer.py:335-346, test_kv_flash_reverse.py:45-55, kv_transfer.py:1303-1328
+    kc = torch.zeros(2, 1, 2, 4)
+    tables = torch.tensor([[0, 2]], dtype=torch.int32)
+    with pytest.raises(ValueError, match="invalid block id 2"):
+        musa_aiter.kv_load_and_reshape_flash(kc, kc.clone(), tables, torch.tensor([5], dtype=torch.int32),
+                                             out_k=torch.empty(1, 5, 1, 2), out_v=torch.empty(1, 5, 1, 2))
+    with pytest.raises(ValueError, match="max_seq_len is smaller"):
+        musa_aiter.kv_load_and_reshape_flash(kc, kc.clone(), tables, torch.tensor([5]), max_seq_len=4)
+    with pytest.raises(ValueError, match="enough columns"):
+        musa_aiter.kv_load_and_reshape_flash(kc, kc.clone(), tables, torch.tensor([3]), max_seq_len=9)
+    with pytest.raises(ValueError, match="non-negative"):
+        musa_aiter.kv_load_and_reshape_flash(kc, kc.clone(), tables, torch.tensor([-1]))
+    with pytest.raises(ValueError, match="block_tables must use an integer dtype"):
+        musa_aiter.kv_load_and_reshape_flash(kc, kc.clone(), tables.float(), torch.tensor([3]))
+    with pytest.raises(ValueError, match="out_k must match"):
+        musa_aiter.kv_load_and_reshape_flash(kc, kc.clone(), tables, torch.tensor([3]), out_k=torch.empty(1, 4, 1, 2))
+    with pytest.raises(ValueError, match="dense"):
+        musa_aiter.kv_reshape_and_cache_back_flash(torch.zeros(2, 7, 3), torch.zeros(2, 7, 3), torch.zeros(4, 2, 3, 4),
+                                                   torch.zeros(4, 2, 3, 4),
+                                                   torch.tensor([[0, 1], [2, 3]], dtype=torch.int32),
+                                                   torch.tensor([4, 4], dtype=torch.int32))
+    dense = torch.zeros(2, 4, 1, 2)
+    with pytest.raises(ValueError, match="seq_lens exceeds"):
+        musa_aiter.kv_reshape_and_cache_back_flash(dense, dense.clone(), kc, kc.clone(),
+                                                   torch.tensor([[0, 1], [1, 0]]), torch.tensor([4, 5]))
+    with pytest.raises(ValueError, match="invalid block id -1"):
+        musa_aiter.kv_reshape_and_cache_back_flash(dense, dense.clone(), kc, kc.clone(),
+                                                   torch.tensor([[0, 1], [-1, 0]]), torch.tensor([4, 2]))
+    with pytest.raises(ValueError, match="integer tensors"):
+        musa_aiter.kv_load_and_dequantize_fp8_flash(kc.to(torch.uint8), kc.to(torch.uint8), tables,
+                                                    torch.tensor([3.0]), 1.0, 1.0)
+    with pytest.raises(ValueError, match="out_k must match"):
+        musa_aiter.kv_load_and_dequantize_fp8_flash(kc.to(torch.uint8), kc.to(torch.uint8), tables,
+                                                    torch.tensor([3]), 1.0, 1.0, out_k=torch.empty(1, 3, 1, 2))
+    key = torch.zeros(8, 2, 4)
+    with pytest.raises(ValueError, match=r"kv_indptr must be \[batch \+ 1\]"):
+        musa_aiter.ops.kv_transfer.kv_triton_indexed_to_dense(key, key.clone(), torch.tensor([0]), torch.tensor([0]),
+                                                             max_seq_len=2)
+    with pytest.raises(ValueError, match="max_seq_len must be non-negative"):
+        musa_aiter.ops.kv_transfer.kv_triton_indexed_to_dense(key, key.clone(), torch.tensor([0, 1]),
+                                                             torch.tensor([0]), max_seq_len=-1)
+    with pytest.raises(ValueError, match="be contiguous"):
+        musa_aiter.ops.kv_transfer.kv_triton_indexed_to_dense(key, key.clone(), torch.tensor([0, 1]),
+                                                             torch.tensor([0]), max_seq_len=2,
+                                                             out_k=torch.zeros(1, 2, 4, 2).transpose(2, 3))
+
+
+def test_block_copy_validation_contract():
+    # op_tests/test_kv_transfer.py:387-399
+    src = torch.zeros(2, 1, 2, 3)
+    with pytest.raises(ValueError, match="out of bounds"):
+        musa_aiter.kv_copy_paged_blocks(src, src.clone(), src.clone(), src.clone(), torch.tensor([[2, 0]]))
+    with pytest.raises(ValueError, match=r"\[num_pairs, 2\]"):
+        musa_aiter.kv_copy_paged_blocks(src, src.clone(), src.clone(), src.clone(), torch.tensor([0, 1]))
+    with pytest.raises(ValueError, match="tails must match"):
+        musa_aiter.kv_copy_paged_blocks(src, src.clone(), torch.zeros(2, 1, 2, 4), torch.zeros(2, 1, 2, 4),
+                                        torch.tensor([[0, 1]]))
+    with pytest.raises(ValueError, match="FP8 cache storage"):
+        musa_aiter.kv_copy_paged_blocks_fp8(src, src.clone(), src.clone(), src.clone(), torch.tensor([[0, 1]]))
+    # Nothing to copy: no launch, so CPU tensors are fine.
+    assert musa_aiter.kv_copy_paged_blocks(src, src.clone(), src.clone(), src.clone(), torch.tensor([[-1, 0]])) == 0
+
+
+def test_dense_preload_cpu_tensors_are_rejected_not_computed():
+    kc = torch.zeros(2, 1, 2, 4)
+    tables = torch.tensor([[0, 1]])
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        musa_aiter.kv_load_and_reshape_flash(kc, kc.clone(), tables, torch.tensor([5]))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        musa_aiter.kv_reshape_and_cache_back_flash(torch.zeros(1, 5, 1, 2), torch.zeros(1, 5, 1, 2), kc, kc.clone(),
+                                                   tables, torch.tensor([5]))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        musa_aiter.kv_load_and_dequantize_fp8_flash(kc.to(torch.uint8), kc.to(torch.uint8), tables,
+                                                    torch.tensor([5]), 1.0, 1.0)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        musa_aiter.ops.kv_transfer.kv_triton_indexed_to_dense(torch.zeros(4, 1, 2), torch.zeros(4, 1, 2),
+                                                             torch.tensor([0, 2]), torch.tensor([1, 3]), max_seq_len=2)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        musa_aiter.kv_copy_paged_blocks(kc, kc.clone(), kc.clone(), kc.clone(), torch.tensor([[0, 1]]))
