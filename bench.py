@@ -23,8 +23,9 @@ bounded sample of the same workload on this host and scales by bytes.
 The other configs are reported under ``extra`` with the same byte convention.
 Their launches are short (0.01-0.3 ms), so they are timed in batches of
 back-to-back launches between two events (host launch overhead hidden behind
-device work); each is also checked against the oracle or by a round trip
-outside the timed region.
+device work); each is also checked outside the timed region, by torch
+indexing, by the reference's FP8 steps restated in torch (tests/torch_ref.py)
+or by a round trip.  The numpy oracle runs only in the CPU-baseline leg.
 """
 
 from __future__ import annotations
@@ -228,8 +229,7 @@ def bench_config2(steps: int, warmup: int) -> dict:
 def bench_config1() -> dict:
     """Single-layer paged->linear K/V gather, fp16, 1024 blocks, 32 seqs len U[1,512]."""
     from musa_aiter.ops import _hip
-    from oracle import kv_oracle as ko
-    from tests.kvgen import bits
+    from tests.torch_ref import paged_rows
 
     dev = torch.device("cuda", 0)
     nb = 1024
@@ -245,11 +245,11 @@ def bench_config1() -> dict:
     args = (kc.data_ptr(), vc.data_ptr(), slots.data_ptr(), ok.data_ptr(), ov.data_ptr(), t, nb, NH, HD, BS)
     _check(fn(*args, _stream()), "cfg1 gather")
     torch.cuda.synchronize()
-    parity = bool(np.array_equal(bits(ok), ko.paged_to_linear(bits(kc), slots_np))
-                  and np.array_equal(bits(ov), ko.paged_to_linear(bits(vc), slots_np)))
+    parity = bool(torch.equal(ok, paged_rows(kc)[slots]) and torch.equal(ov, paged_rows(vc)[slots]))
     ms = batched_ms(lambda: _check(fn(*args, _stream()), "cfg1 gather"), launches=50)
     nbytes = 2 * (2 * t * ROW * 2) + 8 * t
-    return {"tokens": t, "bytes_per_call": nbytes, "gather": rate(nbytes, ms, t), "parity_vs_oracle": parity,
+    return {"tokens": t, "bytes_per_call": nbytes, "gather": rate(nbytes, ms, t), "parity": parity,
+            "parity_check": "every gathered row equals its slot's cache row (torch indexing)",
             "api": "musa_aiter_kv_paged_to_linear_half"}
 
 
@@ -257,8 +257,7 @@ def bench_config3() -> dict:
     """FP8 quant-store into uint8 paged caches and dequant-gather to bf16: E4M3 per-head scales
     (headline), E4M3 scalar scale, E5M2 per-head scales, through the reference-named vec4 C-ABI entries."""
     from musa_aiter.ops import _hip
-    from oracle import kv_oracle as ko
-    from tests.kvgen import bits
+    from tests import torch_ref
 
     dev = torch.device("cuda", 0)
     slots_np = make_slots(1003, 64, 128, 4096, NB, BS)
@@ -298,17 +297,13 @@ def bench_config3() -> dict:
         _check(q(*qa, _stream(), mode), name)
         _check(d(*da, _stream(), mode), name)
         torch.cuda.synchronize()
-        # Parity on a sample of tokens, outside the timed region: cache bytes vs the oracle's encoder,
-        # dequantised rows vs the oracle's decoder.
-        s_np = slots_np[:sample]
-        blk, off = s_np // BS, s_np % BS
-        got = kc.cpu().numpy()[blk, :, :, off]                    # [sample, NH, HD]
-        x = kl[:sample].float().cpu().numpy()
-        scale = ks.cpu().numpy().reshape(-1, 1) if mode == 1 else ks.cpu().numpy()[0]
-        want = ko.fp8_quantize(x, scale, fmt)
-        deq = bits(ok[:sample])
-        want_deq = ko.to_storage(ko.fp8_dequantize_f32(want, scale, fmt), "bfloat16")
-        parity = bool(np.array_equal(got, want) and np.array_equal(deq, want_deq))
+        # Parity on a sample of tokens, outside the timed region (on the CPU): cache bytes vs the
+        # reference encoder's steps in torch, dequantised rows vs its decoder (tests/torch_ref.py).
+        got = torch_ref.paged_rows(kc)[slots[:sample]].cpu()      # [sample, NH, HD]
+        scale = (ks.reshape(-1, 1) if mode == 1 else ks.reshape(())).cpu()
+        want = torch_ref.fp8_quantize(kl[:sample].cpu(), scale, fmt)
+        want_deq = torch_ref.fp8_dequantize(want, scale, fmt, torch.bfloat16)
+        parity = bool(torch.equal(got, want) and torch.equal(ok[:sample].cpu(), want_deq))
         mq = batched_ms(lambda: _check(q(*qa, _stream(), mode), name))
         md = batched_ms(lambda: _check(d(*da, _stream(), mode), name))
         qr, dr = rate(nbytes, mq, t), rate(nbytes, md, t)
@@ -317,7 +312,9 @@ def bench_config3() -> dict:
             dr["traffic"] = profiled_traffic("fp8_dequant")
         out[name] = {"quant_store": qr, "dequant_gather": dr,
                      "scale_rule": f"amax/{fmax:g}" + (" per kv-head" if mode == 1 else " over all heads"),
-                     "parity_sample_tokens": sample, "parity_vs_oracle": parity}
+                     "parity_sample_tokens": sample, "parity": parity,
+                     "parity_check": "cache bytes and bf16 rows of the sampled tokens equal the reference's "
+                                     "encode/decode steps in torch (tests/torch_ref.py)"}
         log(f"config 3 {name}: quant {out[name]['quant_store']['gbs']:.0f} GB/s, "
             f"dequant {out[name]['dequant_gather']['gbs']:.0f} GB/s, parity {parity}")
     return out
@@ -326,8 +323,6 @@ def bench_config3() -> dict:
 def bench_config4() -> dict:
     """SGLang-MP [2, 32, 4096, 16, 8, 128] bf16 <-> LMCache [2, 32, 256, 1024], 16 chunks."""
     import musa_aiter
-    from oracle import kv_oracle as ko
-    from tests.kvgen import bits
 
     dev = torch.device("cuda", 0)
     nl, nb, chunk, nchunks = 32, 4096, 256, 16
@@ -342,12 +337,8 @@ def bench_config4() -> dict:
     for s_c, m in chunks:
         musa_aiter.lmcache_kv_paged_to_buffer_two_x_nl(kvcaches, m, s_c, BS, NH, HD)
     torch.cuda.synchronize()
-    # Parity (outside timing): layers 0 and 31 of K and V, all 16 chunks, vs the oracle's 2xNL gather.
-    layers = (0, nl - 1)
-    sub = [[bits(cache[axis, layer]) for layer in layers] for axis in (0, 1)]
-    want = np.zeros((2, len(layers), chunk * nchunks, ROW), dtype=np.uint16)
-    ko.two_x_nl_to_buffer(sub, want, slots_np)
-    parity = bool(np.array_equal(bits(memory[:, list(layers)]), want))
+    # Parity (outside timing): every row of the buffer equals its slot's row of the cache (torch indexing).
+    parity = bool(torch.equal(memory, cache.reshape(2, nl, nb * BS, ROW)[:, :, slots]))
     log(f"config 4: {chunk * nchunks} tokens in {nchunks} chunks, parity {parity}")
 
     def per_chunk_gather():
@@ -360,7 +351,7 @@ def bench_config4() -> dict:
     ms = batched_ms(lambda: musa_aiter.lmcache_kv_buffer_to_paged_two_x_nl(memory, kvcaches, slots, 0, BS, NH, HD),
                     launches=10)
     per_chunk = 2 * (2 * nl * chunk * ROW * 2) + 8 * chunk
-    return {"chunk_tokens": chunk, "chunks": nchunks, "bytes_per_chunk": per_chunk, "parity_vs_oracle": parity,
+    return {"chunk_tokens": chunk, "chunks": nchunks, "bytes_per_chunk": per_chunk, "parity": parity,
             "gather_per_chunk_call": rate(per_chunk, mg, chunk),
             "gather_batched_16": rate(per_chunk * nchunks, mb, chunk * nchunks),
             "scatter_batched_16": rate(per_chunk * nchunks, ms, chunk * nchunks),
@@ -430,6 +421,142 @@ def bench_config5() -> dict:
     return out
 
 
+def bench_dense() -> dict:
+    """Dense preload for attention and whole-block copies (the next row after the BASELINE configs).
+
+    Llama-3-8B single-layer caches [8192, 8, 128, 16] bf16, 64 decode sequences with lengths
+    uniform in [128, 4096] and random block tables; dense tensors [64, max_len, 8, 128].
+    Bytes per call: cache rows read for valid positions + every dense row written (zeros past
+    seq_lens) for the loads, valid rows read + written for the write-back, plus index bytes.
+    The block copy moves 1024 random block pairs of a 32-layer cache (disjoint source and
+    destination halves).
+    """
+    from musa_aiter.ops import _hip
+    from tests import torch_ref
+    from tests.kvgen import sequence_lengths
+
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(1006)
+    lengths = np.array(sequence_lengths(rng, 64, 128, 4096, num_blocks=NB, block_size=BS), dtype=np.int64)
+    batch, dense_len = lengths.size, int(lengths.max())
+    need = (lengths + BS - 1) // BS
+    max_blocks = int(need.max())
+    perm = rng.permutation(NB)
+    tables_np = np.zeros((batch, max_blocks), dtype=np.int64)
+    pos = 0
+    for b, k in enumerate(need):
+        tables_np[b, :k] = perm[pos:pos + k]
+        pos += k
+    valid = int(lengths.sum())
+    tables = torch.from_numpy(tables_np).to(dev)
+    seq_lens = torch.from_numpy(lengths).to(dev)
+    gen = torch.Generator(device=dev).manual_seed(6)
+    kc = torch.randn((NB, NH, HD, BS), generator=gen, device=dev, dtype=torch.bfloat16)
+    vc = torch.randn((NB, NH, HD, BS), generator=gen, device=dev, dtype=torch.bfloat16)
+    dk = torch.empty((batch, dense_len, NH, HD), dtype=torch.bfloat16, device=dev)
+    dv = torch.empty_like(dk)
+    lib = _hip.library()
+    out = {"sequences": batch, "dense_len": dense_len, "valid_tokens": valid, "max_blocks": max_blocks}
+    row_b = ROW * 2
+    idx_bytes = tables_np.size * 8 + batch * 8
+
+    # Slot of every valid dense position, for the parity checks (torch indexing, outside timing).
+    j = np.arange(dense_len)
+    mask_np = j[None, :] < lengths[:, None]
+    slots_np = np.where(mask_np, tables_np[np.arange(batch)[:, None], np.minimum(j // BS, max_blocks - 1)[None, :]]
+                        * BS + (j % BS)[None, :], 0)
+    flat_slots = torch.from_numpy(slots_np[mask_np]).to(dev)
+    mask = torch.from_numpy(mask_np).to(dev)
+
+    rows_of = torch_ref.paged_rows
+
+    load = _bind(lib, "musa_aiter_kv_load_and_reshape_flash_bfloat16", 6, 7)
+    la = (kc.data_ptr(), vc.data_ptr(), tables.data_ptr(), seq_lens.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+          batch, dense_len, max_blocks, NB, NH, HD, BS)
+    _check(load(*la, _stream()), "dense load")
+    torch.cuda.synchronize()
+    ok = bool(torch.equal(dk[mask], rows_of(kc)[flat_slots]) and torch.equal(dv[mask], rows_of(vc)[flat_slots])
+              and not bool(dk[~mask].any()) and not bool(dv[~mask].any()))
+    ml = batched_ms(lambda: _check(load(*la, _stream()), "dense load"), launches=5, reps=5)
+    nbytes = 2 * valid * row_b + 2 * batch * dense_len * row_b + idx_bytes
+    out["load_and_reshape_flash"] = {**rate(nbytes, ml, valid), "bytes_per_call": nbytes, "parity": ok}
+
+    back = _bind(lib, "musa_aiter_kv_reshape_and_cache_back_flash_bfloat16", 6, 7)
+    ba = (dk.data_ptr(), dv.data_ptr(), tables.data_ptr(), seq_lens.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+          batch, dense_len, max_blocks, NB, NH, HD, BS)
+    before = kc.view(torch.int16).sum(dtype=torch.int64).item() + vc.view(torch.int16).sum(dtype=torch.int64).item()
+    _check(back(*ba, _stream()), "dense write-back")
+    torch.cuda.synchronize()
+    after = kc.view(torch.int16).sum(dtype=torch.int64).item() + vc.view(torch.int16).sum(dtype=torch.int64).item()
+    mb = batched_ms(lambda: _check(back(*ba, _stream()), "dense write-back"), launches=5, reps=5)
+    nbytes = 4 * valid * row_b + idx_bytes
+    out["reshape_and_cache_back_flash"] = {**rate(nbytes, mb, valid), "bytes_per_call": nbytes,
+                                           "parity": before == after,
+                                           "parity_check": "writing the loaded rows back leaves the caches' checksum "
+                                                           "unchanged"}
+
+    # FP8 E4M3 per-head dequant-load into bf16, through the generic entry.
+    k8 = torch.randint(0, 256, (NB, NH, HD, BS), generator=gen, device=dev, dtype=torch.uint8)
+    v8 = k8.flip(0)
+    ks = torch.rand(NH, generator=gen, device=dev) + 0.01
+    vs = torch.rand(NH, generator=gen, device=dev) + 0.01
+    dq = _hip.fn("musa_aiter_hip_paged_dense_tiles")
+    qa = (0, 1, 1, 2, 2, k8.data_ptr(), v8.data_ptr(), dk.data_ptr(), dv.data_ptr(), tables.data_ptr(),
+          seq_lens.data_ptr(), batch, dense_len, max_blocks, NB, NH, HD, BS, ROW, ks.data_ptr(), vs.data_ptr(), 1,
+          1, 0)
+    _check(dq(*qa, _stream()), "fp8 dense load")
+    torch.cuda.synchronize()
+    want = torch_ref.fp8_dequantize(rows_of(k8)[flat_slots], ks[None, :, None], "e4m3", torch.bfloat16)
+    ok8 = bool(torch.equal(dk[mask], want) and not bool(dk[~mask].any()))
+    del want
+    mq = batched_ms(lambda: _check(dq(*qa, _stream()), "fp8 dense load"), launches=5, reps=5)
+    nbytes = 2 * valid * ROW + 2 * batch * dense_len * row_b + idx_bytes + 2 * NH * 4
+    out["load_and_dequantize_fp8_flash_e4m3"] = {**rate(nbytes, mq, valid), "bytes_per_call": nbytes, "parity": ok8,
+                                                 "parity_check": "valid rows equal the reference decoder's value "
+                                                                 "x per-head scale rounded to bf16 "
+                                                                 "(tests/torch_ref.py)"}
+    del k8, v8
+
+    # SGLang Triton-decode CSR indices over token-major caches [NB*BS, NH, HD].
+    key_tok, val_tok = rows_of(kc).contiguous(), rows_of(vc).contiguous()
+    indptr = torch.from_numpy(np.concatenate([[0], np.cumsum(lengths)])).to(dev)
+    csr = _bind(lib, "musa_aiter_kv_triton_indexed_to_dense_bfloat16", 6, 6)
+    ca = (key_tok.data_ptr(), val_tok.data_ptr(), indptr.data_ptr(), flat_slots.data_ptr(), dk.data_ptr(),
+          dv.data_ptr(), batch, dense_len, valid, NB * BS, NH, HD)
+    _check(csr(*ca, _stream()), "csr dense load")
+    torch.cuda.synchronize()
+    okc = bool(torch.equal(dk[mask], key_tok[flat_slots]) and torch.equal(dv[mask], val_tok[flat_slots])
+               and not bool(dk[~mask].any()))
+    mc = batched_ms(lambda: _check(csr(*ca, _stream()), "csr dense load"), launches=5, reps=5)
+    nbytes = 2 * valid * row_b + 2 * batch * dense_len * row_b + valid * 8 + (batch + 1) * 8
+    out["triton_indexed_to_dense"] = {**rate(nbytes, mc, valid), "bytes_per_call": nbytes, "parity": okc}
+    del key_tok, val_tok, dk, dv, kc, vc
+    torch.cuda.empty_cache()
+
+    # 1024 block pairs of a 32-layer cache; sources in the first half, destinations in the second.
+    nl, nb2, pairs_n = NL, 4096, 1024
+    ck = torch.randn((nl, nb2, NH, HD, BS), generator=gen, device=dev, dtype=torch.bfloat16)
+    cv = torch.randn((nl, nb2, NH, HD, BS), generator=gen, device=dev, dtype=torch.bfloat16)
+    pairs_np = np.stack([rng.permutation(nb2 // 2)[:pairs_n], nb2 // 2 + rng.permutation(nb2 // 2)[:pairs_n]], 1)
+    pairs = torch.from_numpy(np.ascontiguousarray(pairs_np)).to(dev)
+    cp = _bind(lib, "musa_aiter_kv_copy_paged_blocks_bfloat16", 5, 7)
+    pa = (ck.data_ptr(), cv.data_ptr(), ck.data_ptr(), cv.data_ptr(), pairs.data_ptr(), pairs_n, nl, nb2, nb2, NH,
+          HD, BS)
+    _check(cp(*pa, _stream()), "block copy")
+    torch.cuda.synchronize()
+    okb = bool(torch.equal(ck[:, pairs[:, 1]], ck[:, pairs[:, 0]]) and torch.equal(cv[:, pairs[:, 1]],
+                                                                                 cv[:, pairs[:, 0]]))
+    mp = batched_ms(lambda: _check(cp(*pa, _stream()), "block copy"), launches=5, reps=5)
+    nbytes = 2 * 2 * nl * pairs_n * ROW * BS * 2 + pairs_n * 16
+    out["copy_paged_blocks_32_layers"] = {**rate(nbytes, mp), "bytes_per_call": nbytes, "pairs": pairs_n,
+                                          "parity": okb}
+    del ck, cv
+    torch.cuda.empty_cache()
+    log("dense: " + ", ".join(f"{k} {v['gbs']:.0f} GB/s parity {v['parity']}" for k, v in out.items()
+                              if isinstance(v, dict)))
+    return out
+
+
 def device_copy(mib: int, reps: int = 5) -> dict:
     """Plain device-to-device copy of a known size (torch ``copy_``): the achievable copy rate of this
     GPU and the calibration kernel for the FETCH_SIZE / WRITE_SIZE traffic counters."""
@@ -476,8 +603,9 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--configs", default="1,2,3,4,5",
-                        help="comma list of BASELINE configs to run (2, the headline, always runs)")
+    parser.add_argument("--configs", default="1,2,3,4,5,6",
+                        help="comma list of BASELINE configs to run (2, the headline, always runs; 6 = dense "
+                             "preload and block copies)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--copy-mib", type=int, default=1024,
                         help="size of the plain device copy timed first (0 = skip)")
@@ -507,7 +635,8 @@ def main() -> int:
     del kc, vc
     torch.cuda.empty_cache()
     runners = {1: ("config1_fp16_single_layer_gather", bench_config1), 3: ("config3_fp8", bench_config3),
-               4: ("config4_lmcache_two_x_nl", bench_config4), 5: ("config5_mla_rows", bench_config5)}
+               4: ("config4_lmcache_two_x_nl", bench_config4), 5: ("config5_mla_rows", bench_config5),
+               6: ("dense_preload_and_block_copies", bench_dense)}
     for cfg in sorted(configs - {2}):
         if cfg not in runners:
             continue

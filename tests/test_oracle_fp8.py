@@ -25,6 +25,7 @@ import pytest
 import torch
 
 from oracle import kv_oracle as ko
+from tests import torch_ref
 
 FORMATS = {"e4m3": (torch.float8_e4m3fn, 2.0 ** -6, float("inf")), "e5m2": (torch.float8_e5m2, 2.0 ** -14, 73728.0)}
 
@@ -44,24 +45,8 @@ def _all_f16_as_f32() -> np.ndarray:
 
 
 def _torch_steps_quantize(x: torch.Tensor, scale: torch.Tensor, fmt: str) -> torch.Tensor:
-    """The encoder's steps written with torch primitives (op-level cross-check of the numpy primitives)."""
-    _, mant, bias, emax = ko.FP8_FORMATS[fmt]
-    work = x.to(torch.float32) / scale
-    sign = work < 0
-    a = work.abs()
-    a = torch.where(torch.isfinite(a), a, torch.zeros_like(a))
-    clipped = a.clamp(max=(2.0 - 2.0 ** (-mant)) * (2.0 ** emax))
-    nonzero = clipped >= 2.0 ** (1 - bias)
-    safe = torch.where(nonzero, clipped, torch.ones_like(clipped))
-    e = torch.floor(torch.log2(safe)).to(torch.int32).clamp(min=1 - bias, max=emax)
-    base = torch.pow(torch.tensor(2.0, dtype=torch.float32), e.to(torch.float32))
-    m = torch.round((safe / base - 1.0) * (2 ** mant)).to(torch.int32)
-    ovf = m == 2 ** mant
-    e = torch.where(ovf, e + 1, e).clamp(max=emax)
-    m = torch.where(ovf, torch.zeros_like(m), m).clamp(min=0, max=2 ** mant - 1)
-    ef = torch.where(nonzero, e + bias, torch.zeros_like(e))
-    m = torch.where(nonzero, m, torch.zeros_like(m))
-    return ((sign.to(torch.int32) << 7) | (ef << mant) | m).to(torch.uint8)
+    """The encoder's steps written with torch primitives (tests/torch_ref.py; bench.py checks with it)."""
+    return torch_ref.fp8_quantize(x, scale, fmt)
 
 
 @pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
@@ -201,3 +186,14 @@ def test_division_matches_torch_exhaustively():
             ours = (x / np.float32(scale)).astype(np.float32)
         theirs = (torch.from_numpy(x) / torch.tensor(scale, dtype=torch.float32)).numpy()
         assert np.array_equal(ours.view(np.uint32), theirs.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_torch_decode_table_matches_oracle_on_every_code(fmt):
+    # tests/torch_ref.py's decoder (used by bench.py's checks) against the oracle's, all 256 codes and two scales.
+    codes = np.arange(256, dtype=np.uint8)
+    for scale in (1.0, 0.0123):
+        mine = torch_ref.fp8_dequantize(torch.from_numpy(codes), torch.tensor(scale), fmt, torch.float32).numpy()
+        want = ko.fp8_dequantize_f32(codes, np.float32(scale), fmt)
+        assert np.array_equal(mine.view(np.uint32), want.view(np.uint32))
+    assert torch_ref.FP8_FORMATS[fmt] == ko.FP8_FORMATS[fmt]
