@@ -38,22 +38,29 @@ struct VecType<2> { using T = uint16_t; };
 template <>
 struct VecType<1> { using T = uint8_t; };
 
+// Every pointer these helpers see is device (global) memory, never LDS or
+// scratch: the casts to address space 1 let the compiler emit global_load /
+// global_store instead of flat accesses, which also count against lgkmcnt.
+#define KVHIP_GLOBAL __attribute__((address_space(1)))
+
 template <int VEC>
 __device__ __forceinline__ typename VecType<VEC>::T ldv(const uint8_t* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const typename VecType<VEC>::T*>(p));
+  using T = typename VecType<VEC>::T;
+  return __builtin_nontemporal_load((const KVHIP_GLOBAL T*)(p));
 }
 
 template <int VEC>
 __device__ __forceinline__ void stv(uint8_t* p, typename VecType<VEC>::T v) {
-  __builtin_nontemporal_store(v, reinterpret_cast<typename VecType<VEC>::T*>(p));
+  using T = typename VecType<VEC>::T;
+  __builtin_nontemporal_store(v, (KVHIP_GLOBAL T*)(p));
 }
 
 // Streaming 16-byte accesses (whole lines per wave instruction).
 __device__ __forceinline__ u32x4 ld16(const uint8_t* p) { return ldv<16>(p); }
 __device__ __forceinline__ void st16(uint8_t* p, u32x4 v) { stv<16>(p, v); }
 // Cached 16-byte accesses (strided, partial lines per wave instruction).
-__device__ __forceinline__ u32x4 ld16_cached(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
-__device__ __forceinline__ void st16_cached(uint8_t* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+__device__ __forceinline__ u32x4 ld16_cached(const uint8_t* p) { return *(const KVHIP_GLOBAL u32x4*)(p); }
+__device__ __forceinline__ void st16_cached(uint8_t* p, u32x4 v) { *(KVHIP_GLOBAL u32x4*)(p) = v; }
 
 // ---------------------------------------------------------------------------
 // Raw buffer accesses (gfx9-family descriptor, stride 0).  The descriptor

@@ -7,15 +7,16 @@
 // copy is indexed by a slot/row vector (or both, for byte rows); slot < 0
 // skips the token.
 //
-// One block covers a few whole rows of one plane (grid y = plane): the rows
-// are cut into VEC-byte pieces (VEC = the widest power of two dividing the
-// row size, strides and plane bases) and the flattened (token, piece) range is
-// spread over the 256 threads, one or two pieces each.  Every lane does useful
-// work for any row size, and each wave keeps only a vector or two per lane in
-// flight, the access shape that reaches the highest HBM copy rate on MI355X.
-// Skipped tokens of a directly addressed destination are zero filled; an
-// indexed destination can be protected by claim tags so duplicate slots keep
-// last-writer-wins.
+// Rows are cut into VEC-byte pieces (VEC = the widest power of two dividing
+// the row size, strides and plane bases); one block moves 512 consecutive
+// pieces of the flattened (token, piece) range of one plane (grid y = plane),
+// two per thread, whatever the row size: a short row shares a block with its
+// neighbours, a long one spans several blocks.  Each wave keeps only two
+// vectors per lane in flight, the access shape that reaches the highest HBM
+// copy rate on MI355X, and the block resolves the indices of the rows it
+// touches once, into LDS, before streaming.  Skipped tokens of a directly
+// addressed destination are zero filled; an indexed destination can be
+// protected by claim tags so duplicate slots keep last-writer-wins.
 #include "kv_hip_common.h"
 #include "kv_launch.h"
 
@@ -48,18 +49,47 @@ struct RowArgs {
   int64_t idx_stride;         // elements between consecutive entries of src_idx / dst_idx
 };
 
-// One block covers `tokens_per_block` whole rows of one plane, split into
-// VEC-byte pieces: thread i of the block moves pieces i, i + 256, ... of the
-// flattened (token, piece) range, so every lane does useful work whatever the
-// row size and each wave keeps only one or two vectors per lane in flight.
-// The piece -> token split divides small integers with a float reciprocal
-// and one exact correction step.
+// Work of one block: kBlockPieces consecutive VEC-byte pieces of the
+// flattened (row, piece) range of one plane, two per thread.  The rows the
+// range touches (at most kBlockPieces / pieces + 2) are resolved once, into
+// LDS, by the block's first threads: source and destination byte offsets, or
+// a zero-fill / skip mark.  The copy loop then reads only LDS besides the
+// payload, and each thread issues both of its loads before its stores.
+constexpr int kBlockPieces = 2 * kBlockThreads;
+constexpr int kBlockRows = kBlockPieces + 2;
+constexpr int64_t kSkipRow = -1;  // destination offset: the token writes nothing
+constexpr int64_t kZeroRow = -1;  // source offset: the destination row is zero filled
+
+// Byte offsets of token u's source and destination rows, with the skip and
+// zero-fill marks above.
+__device__ __forceinline__ void resolve_row(const RowArgs& a, int64_t u, int64_t* so, int64_t* dof) {
+  *so = kZeroRow;
+  *dof = kSkipRow;
+  int64_t srow = -1;
+  int64_t drow = u + a.dst_offset;
+  bool valid = false;
+  if (u < a.num_tokens) {
+    if (a.src_indptr != nullptr) srow = csr_row(a.src_indptr, a.src_idx, a.dense_len, a.index_count, u);
+    else srow = a.src_idx ? a.src_idx[u * a.idx_stride] : u + a.src_offset;
+    if (a.dst_idx) drow = a.dst_idx[u * a.idx_stride];
+    valid = srow >= 0 && srow < a.src_rows && drow >= 0 && drow < a.dst_rows;
+    if (valid && a.owner != nullptr) valid = (a.owner[drow] == claim_tag(a.epoch, u));
+  }
+  if (valid) {
+    *so = srow * a.src_stride;
+    *dof = drow * a.dst_stride;
+  } else if (a.zero_invalid && a.dst_idx == nullptr && drow >= 0 && drow < a.dst_rows) {
+    // Only a directly addressed destination row inside its extent is cleared.
+    *dof = drow * a.dst_stride;
+  }
+}
+
 template <int VEC>
 __global__ __launch_bounds__(kBlockThreads) void row_flat_kernel(const RowArgs a, const int32_t pieces,
-                                                                 const int32_t tokens_per_block,
                                                                  const float inv_pieces) {
   using V = typename VecType<VEC>::T;
-  const int64_t t_base = static_cast<int64_t>(blockIdx.x) * tokens_per_block;
+  __shared__ int64_t s_src[kBlockRows];
+  __shared__ int64_t s_dst[kBlockRows];
   const int pp = a.plane_base + static_cast<int>(blockIdx.y);
   const uint8_t* const sp =
       reinterpret_cast<const uint8_t*>(a.src_table ? a.src_table[pp] : a.src_planes[pp - a.plane_base]);
@@ -67,43 +97,59 @@ __global__ __launch_bounds__(kBlockThreads) void row_flat_kernel(const RowArgs a
   // Plane bases read from device tables may be less aligned than VEC: such a
   // plane is copied byte by byte (uniform branch).
   const bool narrow = VEC > 1 && ((reinterpret_cast<uintptr_t>(sp) | reinterpret_cast<uintptr_t>(dp)) & (VEC - 1));
-  const int total = tokens_per_block * pieces;
 
-  for (int l = static_cast<int>(threadIdx.x); l < total; l += kBlockThreads) {
-    int lt = static_cast<int>(static_cast<float>(l) * inv_pieces);
-    if (lt * pieces > l) --lt;
-    else if ((lt + 1) * pieces <= l) ++lt;
-    const int c = l - lt * pieces;
-    const int64_t u = t_base + lt;
-    if (u >= a.num_rows_out) break;
+  // Block range [l0, l0 + kBlockPieces) starts at piece r0 of row u0.
+  const int64_t l0 = static_cast<int64_t>(blockIdx.x) * kBlockPieces;
+  const int64_t u0 = l0 / pieces;
+  const int r0 = static_cast<int>(l0 - u0 * pieces);
+  const int64_t total = a.num_rows_out * pieces;
+  const int span = static_cast<int>((total - l0) < kBlockPieces ? (total - l0) : kBlockPieces);
+  const int nrows = (r0 + span - 1) / pieces + 1;
+  for (int i = static_cast<int>(threadIdx.x); i < nrows; i += kBlockThreads) {
+    int64_t so, dof;
+    resolve_row(a, u0 + i, &so, &dof);
+    s_src[i] = so;
+    s_dst[i] = dof;
+  }
+  __syncthreads();
 
-    int64_t srow = -1;
-    int64_t drow = u + a.dst_offset;
-    bool valid = false;
-    if (u < a.num_tokens) {
-      if (a.src_indptr != nullptr) srow = csr_row(a.src_indptr, a.src_idx, a.dense_len, a.index_count, u);
-      else srow = a.src_idx ? a.src_idx[u * a.idx_stride] : u + a.src_offset;
-      if (a.dst_idx) drow = a.dst_idx[u * a.idx_stride];
-      valid = srow >= 0 && srow < a.src_rows && drow >= 0 && drow < a.dst_rows;
-      if (valid && a.owner != nullptr) valid = (a.owner[drow] == claim_tag(a.epoch, u));
+  constexpr int kPer = kBlockPieces / kBlockThreads;
+  V v[kPer];
+  int64_t d[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int m = static_cast<int>(threadIdx.x) + k * kBlockThreads;  // piece within the block
+    d[k] = kSkipRow;
+    v[k] = V{};
+    if (m >= span) continue;
+    // Row and column of piece r0 + m: small integers divided with a float
+    // reciprocal and one exact correction step.
+    const int q = r0 + m;
+    int lt = static_cast<int>(static_cast<float>(q) * inv_pieces);
+    if (lt * pieces > q) --lt;
+    else if ((lt + 1) * pieces <= q) ++lt;
+    const int64_t c = static_cast<int64_t>(q - lt * pieces) * VEC;
+    const int64_t dof = s_dst[lt];
+    if (dof == kSkipRow) continue;
+    d[k] = dof + c;
+    const int64_t so = s_src[lt];
+    if (so == kZeroRow) continue;
+    if (!narrow) {
+      v[k] = ldv<VEC>(sp + so + c);
+    } else {
+#pragma unroll
+      for (int b = 0; b < VEC; ++b) dp[d[k] + b] = sp[so + c + b];
+      d[k] = kSkipRow;
     }
-    const int64_t doff = drow * a.dst_stride + static_cast<int64_t>(c) * VEC;
-    if (valid) {
-      const int64_t soff = srow * a.src_stride + static_cast<int64_t>(c) * VEC;
-      if (!narrow) {
-        stv<VEC>(dp + doff, ldv<VEC>(sp + soff));
-      } else {
+  }
 #pragma unroll
-        for (int b = 0; b < VEC; ++b) dp[doff + b] = sp[soff + b];
-      }
-    } else if (a.zero_invalid && a.dst_idx == nullptr && drow >= 0 && drow < a.dst_rows) {
-      // Only a directly addressed destination row inside its extent is cleared.
-      if (!narrow) {
-        stv<VEC>(dp + doff, V{});
-      } else {
+  for (int k = 0; k < kPer; ++k) {
+    if (d[k] == kSkipRow) continue;
+    if (!narrow) {
+      stv<VEC>(dp + d[k], v[k]);
+    } else {
 #pragma unroll
-        for (int b = 0; b < VEC; ++b) dp[doff + b] = 0;
-      }
+      for (int b = 0; b < VEC; ++b) dp[d[k] + b] = 0;
     }
   }
 }
@@ -198,18 +244,16 @@ int vec_for(uint64_t bits) {
   return 1;
 }
 
-// Rows per block: about two pieces per thread, at least one row, and the
-// flattened range kept well inside 32-bit arithmetic.
+// kBlockPieces pieces per block over the flattened (row, piece) range; the
+// piece -> row split inside a block stays within small 32-bit integers.
 template <int VEC>
 hipError_t launch_rows_vec(const RowArgs& a, int64_t planes, hipStream_t stream) {
   const int64_t pieces = a.row_bytes / VEC;
   if (pieces > (int64_t{1} << 22)) return hipErrorInvalidValue;
-  int64_t tpb = (2 * kBlockThreads) / pieces;
-  if (tpb < 1) tpb = 1;
-  const int64_t blocks = (a.num_rows_out + tpb - 1) / tpb;
+  const int64_t blocks = (a.num_rows_out * pieces + kBlockPieces - 1) / kBlockPieces;
   if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
   hipLaunchKernelGGL(row_flat_kernel<VEC>, dim3(static_cast<uint32_t>(blocks), static_cast<uint32_t>(planes)),
-                     dim3(kBlockThreads), 0, stream, a, static_cast<int32_t>(pieces), static_cast<int32_t>(tpb),
+                     dim3(kBlockThreads), 0, stream, a, static_cast<int32_t>(pieces),
                      1.0f / static_cast<float>(pieces));
   return hipGetLastError();
 }
