@@ -80,6 +80,10 @@ __device__ __forceinline__ buf_t make_buf(const void* base) {
 __device__ __forceinline__ u32x4 buf_ld16(buf_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kBufNT);
 }
+// Per-lane offset `off` plus a wave-uniform offset `soff` (an SGPR operand).
+__device__ __forceinline__ u32x4 buf_ld16(buf_t r, uint32_t off, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, kBufNT);
+}
 __device__ __forceinline__ void buf_st16(buf_t r, uint32_t off, u32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kBufNT);
 }
@@ -353,8 +357,10 @@ __device__ __forceinline__ uint32_t fp8_encode_fast(float w) {
 // the callers must use fp8_encode_fast instead.
 template <int CODEC>
 __device__ __forceinline__ float fp8_flush_small(float w) {
-  const uint32_t b = __float_as_uint(w);
-  return ((b & 0x7FFFFFFFu) < Fp8Fmt<CODEC>::kMinNormBits) ? __uint_as_float(b & 0x80000000u) : w;
+  // |w| < minnorm as one float compare (abs is a free source modifier).
+  return (__builtin_fabsf(w) < __uint_as_float(Fp8Fmt<CODEC>::kMinNormBits))
+             ? __uint_as_float(__float_as_uint(w) & 0x80000000u)
+             : w;
 }
 
 template <int CODEC>
@@ -424,6 +430,13 @@ struct InputRange {
     if constexpr (LDT == kLinF32) return m == 0u ? __uint_as_float(0x7F800000u) : __uint_as_float(m);
     else if constexpr (LDT == kLinBF16) return m > 0xFFFFu ? __uint_as_float(0x7F800000u) : bf16_bits_to_f32(m);
     else return m > 0xFFFFu ? __uint_as_float(0x7F800000u) : f16_bits_to_f32(m);
+  }
+
+  // Largest |x| of the tracked inputs (0 when none was added).
+  __device__ __forceinline__ float max_abs() const {
+    if constexpr (LDT == kLinF32) return __uint_as_float(hi());
+    else if constexpr (LDT == kLinBF16) return bf16_bits_to_f32(hi());
+    else return f16_bits_to_f32(hi());
   }
 
   // True when every tracked input is zero or has 2^-60 <= |x| < 2^60.

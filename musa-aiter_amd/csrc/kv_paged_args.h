@@ -38,6 +38,16 @@ __device__ __forceinline__ int64_t slot_at(const TileArgs& a, int64_t t) {
 
 constexpr int kTileTokens = 16;
 
+// head = row / head_dim for rows below 2^24: a float reciprocal and one
+// exact correction step.
+__device__ __forceinline__ int head_of_row(const TileArgs& a, int row) {
+  const int hd = static_cast<int>(a.head_dim);
+  int head = static_cast<int>(static_cast<float>(row) * a.inv_head_dim);
+  if (head * hd > row) --head;
+  else if ((head + 1) * hd <= row) ++head;
+  return head;
+}
+
 __device__ __forceinline__ float load_scale(const TileArgs& a, int kv, int layer, int64_t head) {
   const float* s = a.scale[kv];
   if (a.scale_mode == 0) return s[0];
@@ -72,5 +82,11 @@ __device__ __forceinline__ uint32_t piece_elem(const u32x4& v, int idx) {
 // LDS instructions of the cooperative kernel's column reads.
 template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS>
 hipError_t launch_wave_gather(const TileArgs& a, int64_t planes, hipStream_t stream);
+
+// Per-wave linear -> paged FP8 quant-store (kv_paged_waves.hip): the
+// converter packs four tokens of one cache row per dword, so the quantised
+// tile leaves the lane already transposed.
+template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS>
+hipError_t launch_wave_scatter(const TileArgs& a, int64_t planes, hipStream_t stream);
 
 }  // namespace kvhip

@@ -477,6 +477,10 @@ hipError_t dispatch_bs(const TileArgs& a, int64_t bs, bool fast, int64_t planes,
       // FP8 dequant-gather: per-wave kernel (kv_paged_waves.hip).
       if (bs == 16) return launch_wave_gather<ELT_C, ELT_L, CODEC, LDT, 16>(a, planes, stream);
       if (bs == 32) return launch_wave_gather<ELT_C, ELT_L, CODEC, LDT, 32>(a, planes, stream);
+    } else if constexpr (ELT_C == 1 && SCATTER) {
+      // FP8 quant-store: per-wave kernel (kv_paged_waves.hip).
+      if (bs == 16) return launch_wave_scatter<ELT_C, ELT_L, CODEC, LDT, 16>(a, planes, stream);
+      if (bs == 32) return launch_wave_scatter<ELT_C, ELT_L, CODEC, LDT, 32>(a, planes, stream);
     } else {
       if (bs == 16) return launch_tile<ELT_C, ELT_L, CODEC, LDT, 16, SCATTER>(a, planes, stream);
       if (bs == 32) return launch_tile<ELT_C, ELT_L, CODEC, LDT, 32, SCATTER>(a, planes, stream);

@@ -204,6 +204,235 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_gather_kernel(const 
   }
 }
 
+// ----- per-wave FP8 quant-store (linear -> paged) ---------------------------------------
+//
+// The mirror image of the gather.  Two lanes share one 16-column group of a
+// block's cache rows: a lane takes RPL cache rows (one head) x 8 block
+// columns of a run.  It loads the 8 linear pieces (RPL elements of one token
+// each; a wave load instruction covers two tokens' 512 contiguous bytes),
+// computes every quotient, and packs row q of four consecutive tokens into
+// one dword with the hardware converter, so its half of row q's 16-byte cache
+// piece leaves the converter already transposed.  The half pieces meet in
+// the wave's LDS region (the gather's swizzle) and leave as coalesced 16-byte
+// wave stores.  Runs that do not fill a whole block store the bytes of their
+// columns one by one.  The exactness conditions of the fast quotient and of
+// the converter are checked per lane on the loaded inputs and made wave
+// uniform.
+
+template <int ELT_L, int BS>
+struct ScatterShape {
+  static constexpr int RPL = 16 / ELT_L;                     // cache rows per lane tile
+  static constexpr int CG = 16;                              // block columns per 16-byte group
+  static constexpr int NCG = BS / CG;                        // 16-byte groups per cache row
+  static constexpr int COLS = CG / 2;                        // block columns per lane
+  static constexpr int kChunkRows = (kWave / (2 * NCG)) * RPL;
+  static constexpr int kPieces = kChunkRows * NCG;           // 16-byte cache pieces per chunk
+  static constexpr int kWaveChunks = 1;                      // chunks per wave (grid z covers the rest)
+  static_assert(BS % CG == 0, "block row must be a whole number of 16-byte groups");
+  static_assert(kPieces % kWave == 0, "chunk pieces must spread evenly over the wave");
+};
+
+// When a full-run tile may use the fast quotient and the converter (with
+// the flush of sub-normal quotients), judged on the raw input bits of the
+// lane.  The fast quotient is RN(x / s) for s and |x| in [2^-60, 2^60].
+// 16-bit inputs only need the upper bound: every nonzero fp16 value is at
+// least 2^-24, and a bf16 value below 2^-60 with s in [2^-45, 2^15] has a
+// quotient below 2^-15 (flushed for both formats, like the exact quotient)
+// and above 2^-149 (so its sign survives as in the exact quotient).
+template <int LDT>
+struct TileBound {
+  uint32_t hi32 = 0u, lo32 = 0xFFFFFFFFu;
+  u16x2 hi16 = {0, 0};
+
+  __device__ __forceinline__ void add(const u32x4& v) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      if constexpr (LDT == kLinF32) {
+        const uint32_t a = v[w] & 0x7FFFFFFFu;
+        lo32 = min(lo32, a - 1u);
+        hi32 = max(hi32, a);
+      } else {
+        hi16 = __builtin_elementwise_max(hi16, __builtin_bit_cast(u16x2, v[w] & 0x7FFF7FFFu));
+      }
+    }
+  }
+  __device__ __forceinline__ uint32_t hi() const {
+    if constexpr (LDT == kLinF32) return hi32;
+    else return hi16.x > hi16.y ? hi16.x : hi16.y;
+  }
+  __device__ __forceinline__ bool fast(float s) const {
+    if constexpr (LDT == kLinF32) {
+      return fast_scale_ok(s) && lo32 >= kFastLoBits - 1u && hi32 < kFastHiBits;
+    } else if constexpr (LDT == kLinBF16) {
+      return (__float_as_uint(s) - 0x29000000u) < (0x47000000u - 0x29000000u) && hi() < (kFastHiBits >> 16);
+    } else {
+      return fast_scale_ok(s) && hi() < 0x7C00u;
+    }
+  }
+  __device__ __forceinline__ float max_abs() const {
+    if constexpr (LDT == kLinF32) return __uint_as_float(hi32);
+    else if constexpr (LDT == kLinBF16) return bf16_bits_to_f32(hi());
+    else return f16_bits_to_f32(hi());
+  }
+};
+
+template <int CODEC>
+__device__ __forceinline__ uint32_t quant_soft(float x, float sc, float r, bool fast) {
+  return fast ? fp8_encode_fast<CODEC>(quot_fast(x, sc, r)) : fp8_encode<CODEC>(div_rn(x, sc));
+}
+
+// One element, checked on its own (edge columns of partial runs).
+template <int CODEC>
+__device__ __forceinline__ uint32_t quant_one(float x, float sc, float r, bool scale_ok) {
+  const uint32_t ax = __float_as_uint(x) & 0x7FFFFFFFu;
+  const bool fast = scale_ok && (ax == 0u || (ax >= kFastLoBits && ax < kFastHiBits));
+  return quant_soft<CODEC>(x, sc, r, fast);
+}
+
+template <int ELT_L, int LDT, int RPL>
+__device__ __forceinline__ float tile_elem(const u32x4& piece, int q) {
+  if constexpr (ELT_L == 2) return lin_to_f32<LDT>(elem16(piece, q));
+  else return __uint_as_float(piece[q]);
+}
+
+template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS>
+__global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const TileArgs a) {
+  static_assert(ELT_C == 1 && CODEC != kCopy, "the per-wave scatter quantises into one-byte caches");
+  using W = ScatterShape<ELT_L, BS>;
+  constexpr int RPL = W::RPL, CG = W::CG, NCG = W::NCG, COLS = W::COLS;
+  constexpr int kChunkRows = W::kChunkRows, kPieces = W::kPieces;
+  static_assert(kTileTokens + BS + 1 <= kWave, "run window must fit one wave");
+  __shared__ u32x4 lds_all[kWavesPerBlock * kPieces];
+  u32x4* const lds = lds_all + wave_in_block() * kPieces;
+
+  const int lane = lane_id();
+  const int64_t tile = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();
+  const int64_t t0 = tile * kTileTokens;
+  if (t0 >= a.num_tokens) return;
+  const int plane = static_cast<int>(blockIdx.y);
+  const int layer = plane >> 1;
+  const int kv = plane & 1;
+  uint8_t* const cache = a.cache[kv] + static_cast<int64_t>(layer) * a.cache_layer_stride;
+  const uint8_t* const lin = a.lin[kv] + static_cast<int64_t>(layer) * a.lin_layer_stride;
+  // This wave's cache rows: up to W::kWaveChunks chunks of kChunkRows rows.
+  const int rw0 = static_cast<int>(blockIdx.z) * (kChunkRows * W::kWaveChunks);
+  const int rw_end = (rw0 + kChunkRows * W::kWaveChunks < a.nrows) ? rw0 + kChunkRows * W::kWaveChunks
+                                                                    : static_cast<int>(a.nrows);
+
+  // Slot window: lane i holds token t0 - 1 + i; a token whose claim lost to a
+  // later duplicate writes nothing.
+  const int64_t t = t0 - 1 + lane;
+  int64_t s = -1;
+  if (t >= 0 && t < a.num_tokens) s = slot_at(a, t);
+  bool valid = (s >= 0) && (s < a.num_slots);
+  if (valid && a.owner != nullptr) valid = (a.owner[s] == claim_tag(a.epoch, t));
+  const uint64_t vmask = ballot(valid);
+  const int64_t s_prev = from_prev_lane(s);
+  const bool prev_valid = lane > 0 && ((vmask >> (lane - 1)) & 1ull);
+  const bool cont = valid && prev_valid && (s == s_prev + 1) && ((s % BS) != 0);
+  const uint64_t cmask = ballot(cont);
+  const int64_t remaining = a.num_tokens - t0;
+  const int ntile = remaining < kTileTokens ? static_cast<int>(remaining) : kTileTokens;
+  const uint64_t window = ((1ull << ntile) - 1ull) << 1;
+  const uint64_t heads = vmask & ~cmask & window;
+  if (heads == 0) return;
+
+  // Lane tile: rows trow .. trow + RPL - 1 of the chunk, block columns lo .. lo + COLS - 1.
+  const int half = lane & 1;
+  const int rg = (lane >> 1) / NCG;
+  const int ct = (lane >> 1) % NCG;
+  const int lo = ct * CG + half * COLS;
+  u32x2* const lds_half = reinterpret_cast<u32x2*>(lds) + half;
+
+#pragma unroll 1
+  for (int r0 = rw0; r0 < rw_end; r0 += kChunkRows) {
+    const int r_end = (r0 + kChunkRows < rw_end) ? r0 + kChunkRows : rw_end;
+    const int trow = r0 + rg * RPL;
+    const bool tile_in = trow < r_end;
+    float sc = 1.0f;
+    if (tile_in) sc = load_scale(a, kv, layer, head_of_row(a, trow));
+    const bool scale_ok = fast_scale_ok(sc);
+    const float r = scale_ok ? 1.0f / sc : 0.0f;
+
+    uint64_t hs = heads;
+    while (hs) {
+      const int i = __builtin_ctzll(hs);
+      hs &= hs - 1;
+      const uint64_t after = cmask >> (i + 1);  // i <= kTileTokens < 63
+      const int len = 1 + __builtin_ctzll(~after);
+      const int64_t sh = readlane64(s, i);
+      const int64_t blk = sh / BS;
+      const int c0 = static_cast<int>(sh - blk * BS);
+      const int c1 = c0 + len;
+      const int64_t tf = t0 - 1 + i;  // token of column c0
+      uint8_t* const chunk = cache + (blk * a.nrows + r0) * BS;
+      const uint8_t* const lrow = lin + tf * a.lin_token_stride + static_cast<int64_t>(trow) * ELT_L;
+
+      if (c0 == 0 && c1 == BS) {
+        // Whole block: full cache pieces, unless some lane of the wave needs the
+        // integer encoders (then the byte path below takes the whole run).
+        // Linear pieces: a descriptor at the run's first token and row r0, a
+        // per-lane offset (row group, column) and a wave-uniform column step;
+        // lanes past the chunk read zeros.
+        const buf_t lbuf = make_buf(lin + tf * a.lin_token_stride + static_cast<int64_t>(r0) * ELT_L);
+        const uint32_t stride32 = static_cast<uint32_t>(a.lin_token_stride);
+        const uint32_t loff = tile_in ? static_cast<uint32_t>(rg * RPL * ELT_L) + static_cast<uint32_t>(lo) * stride32
+                                      : kOffOob;
+        u32x4 in[COLS];
+#pragma unroll
+        for (int c = 0; c < COLS; ++c) in[c] = buf_ld16(lbuf, loff, static_cast<uint32_t>(c) * stride32);
+        TileBound<LDT> bound;
+#pragma unroll
+        for (int c = 0; c < COLS; ++c) bound.add(in[c]);
+        bool soft = !bound.fast(sc);
+        if constexpr (CODEC == kE5M2) {
+          // The converter is exact up to 57344; |q| <= max|x| * r * (1 + 2^-22).
+          soft = soft || bound.max_abs() * r * (1.0f + 0x1p-20f) > __uint_as_float(kHwEncodeMaxBits<CODEC>);
+        }
+        if (ballot(tile_in && soft) == 0) {
+#pragma unroll
+          for (int q = 0; q < RPL; ++q) {
+            uint32_t word[2];
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+              float w[4];
+#pragma unroll
+              for (int k = 0; k < 4; ++k) w[k] = quot_fast(tile_elem<ELT_L, LDT, RPL>(in[4 * g + k], q), sc, r);
+              word[g] = fp8_pack4_hw<CODEC>(w[0], w[1], w[2], w[3]);
+            }
+            lds_half[2 * lds_slot<RPL, NCG>((rg * RPL + q) * NCG + ct)] = u32x2{word[0], word[1]};
+          }
+          wave_lds_sync();
+          const buf_t cbuf = make_buf(chunk);
+#pragma unroll
+          for (int k = 0; k < kPieces / kWave; ++k) {
+            const int pc = k * kWave + lane;
+            const u32x4 v = lds[lds_slot<RPL, NCG>(pc)];
+            buf_st16(cbuf, (r0 + pc / NCG < r_end) ? static_cast<uint32_t>(pc) * 16u : kOffOob, v);
+          }
+          wave_lds_sync();
+          continue;
+        }
+      }
+
+      // Partial block (or a block whose wave needs the integer encoders): the
+      // lane's columns inside the run, byte by byte.
+      const int ca = c0 > lo ? c0 : lo;
+      const int cb = c1 < lo + COLS ? c1 : lo + COLS;
+      if (!tile_in) continue;
+      uint8_t* const crow = chunk + static_cast<int64_t>(rg * RPL) * BS;
+#pragma unroll 1
+      for (int c = ca; c < cb; ++c) {
+        const u32x4 piece = ld16(lrow + static_cast<int64_t>(c - c0) * a.lin_token_stride);
+#pragma unroll
+        for (int q = 0; q < RPL; ++q)
+          crow[q * BS + c] =
+              static_cast<uint8_t>(quant_one<CODEC>(tile_elem<ELT_L, LDT, RPL>(piece, q), sc, r, scale_ok));
+      }
+    }
+  }
+}
+
 }  // namespace
 
 template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS>
@@ -220,9 +449,25 @@ hipError_t launch_wave_gather(const TileArgs& a, int64_t planes, hipStream_t str
   return hipGetLastError();
 }
 
-#define KVHIP_WAVE_GATHER(CODEC, ELT_L, LDT)                                                            \
-  template hipError_t launch_wave_gather<1, ELT_L, CODEC, LDT, 16>(const TileArgs&, int64_t, hipStream_t); \
-  template hipError_t launch_wave_gather<1, ELT_L, CODEC, LDT, 32>(const TileArgs&, int64_t, hipStream_t);
+template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS>
+hipError_t launch_wave_scatter(const TileArgs& a, int64_t planes, hipStream_t stream) {
+  using W = ScatterShape<ELT_L, BS>;
+  const int64_t chunks = (a.nrows + W::kChunkRows * W::kWaveChunks - 1) / (W::kChunkRows * W::kWaveChunks);
+  if (chunks > 65535) return hipErrorInvalidValue;
+  const int64_t tiles = (a.num_tokens + kTileTokens - 1) / kTileTokens;
+  const int64_t blocks = (tiles + kWavesPerBlock - 1) / kWavesPerBlock;
+  if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((paged_wave_scatter_kernel<ELT_C, ELT_L, CODEC, LDT, BS>),
+                     dim3(static_cast<uint32_t>(blocks), static_cast<uint32_t>(planes), static_cast<uint32_t>(chunks)),
+                     dim3(kBlockThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+#define KVHIP_WAVE_GATHER(CODEC, ELT_L, LDT)                                                             \
+  template hipError_t launch_wave_gather<1, ELT_L, CODEC, LDT, 16>(const TileArgs&, int64_t, hipStream_t);  \
+  template hipError_t launch_wave_gather<1, ELT_L, CODEC, LDT, 32>(const TileArgs&, int64_t, hipStream_t);  \
+  template hipError_t launch_wave_scatter<1, ELT_L, CODEC, LDT, 16>(const TileArgs&, int64_t, hipStream_t); \
+  template hipError_t launch_wave_scatter<1, ELT_L, CODEC, LDT, 32>(const TileArgs&, int64_t, hipStream_t);
 KVHIP_WAVE_GATHER(kE4M3, 2, kLinBF16)
 KVHIP_WAVE_GATHER(kE4M3, 2, kLinF16)
 KVHIP_WAVE_GATHER(kE4M3, 4, kLinF32)

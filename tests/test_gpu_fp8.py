@@ -212,3 +212,34 @@ def test_quant_store_fast_reciprocal_range_many_scales(fmt, lin):
         got_k, got_v = kc_d.cpu().numpy(), vc_d.cpu().numpy()
         assert np.array_equal(got_k, want_k), (rep, np.argwhere(got_k != want_k)[:5])
         assert np.array_equal(got_v, want_v), (rep, np.argwhere(got_v != want_v)[:5])
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("bs", [16, 32])
+def test_quant_store_bf16_tiny_inputs_scale_window_edges(fmt, bs):
+    """Every finite bf16 pattern (subnormals and values below 2^-60 included) with per-head scales at and
+    beyond the edges of the bf16 fast window [2^-45, 2^15): the fast tiles, the fallback tiles and the
+    partial runs must all give the reference bytes."""
+    rng = np.random.default_rng(43)
+    raw = torch.arange(0, 2 ** 16, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    vals = raw[torch.isfinite(raw.float())]
+    vals = vals[torch.from_numpy(rng.permutation(vals.numel()))]
+    pad = (-vals.numel()) % (NH * HD)
+    x = torch.cat([vals, vals[:pad]]).reshape(-1, NH, HD)
+    tokens = x.shape[0]
+    slots, nb = make_slots("sequences", rng, block_size=bs, tokens=tokens)
+    s_d = torch.from_numpy(slots).to(DEV)
+    ks = np.array([2.0 ** -46, 2.0 ** -45, np.nextafter(np.float32(2.0 ** 15), np.float32(0.0)), 2.0 ** 15,
+                   2.0 ** 20, 2.0 ** -50, 1.0, 0.01], dtype=np.float32)
+    vs = ks[::-1].copy()
+    kc_d = torch.zeros(nb, NH, HD, bs, dtype=torch.uint8, device=DEV)
+    vc_d = torch.zeros_like(kc_d)
+    musa_aiter.kv_linear_to_paged_fp8(x.to(DEV), x.flip(0).contiguous().to(DEV), kc_d, vc_d, s_d,
+                                      torch.from_numpy(ks).to(DEV), torch.from_numpy(vs).to(DEV), fp8_format=fmt)
+    want_k = np.zeros((nb, NH, HD, bs), np.uint8)
+    want_v = np.zeros_like(want_k)
+    ko.linear_to_paged_fp8(_lin_f32(x), want_k, slots, ks, fmt)
+    ko.linear_to_paged_fp8(_lin_f32(x.flip(0).contiguous()), want_v, slots, vs, fmt)
+    got_k, got_v = kc_d.cpu().numpy(), vc_d.cpu().numpy()
+    assert np.array_equal(got_k, want_k), np.argwhere(got_k != want_k)[:5]
+    assert np.array_equal(got_v, want_v), np.argwhere(got_v != want_v)[:5]
