@@ -1,4 +1,5 @@
-// Paged-A KV cache <-> token-major linear transfers for MI355X (gfx950).
+// Paged-A KV cache <-> token-major linear transfers for MI355X (gfx950):
+// 16- and 32-bit copies, and the dispatch of every paged-A transfer.
 //
 // Cache layout (the reference API layout, musa_aiter/ops/kv_transfer.py:3-14):
 //   [NL, NB, NH, HD, BS]  -- block_size innermost, so one token's head row is
@@ -11,41 +12,38 @@
 // small 2-D transpose.  One 256-thread workgroup owns the runs that start in
 // its 16-token tile, for one such row chunk of one (layer, K|V) plane:
 //   * every thread moves exactly one 16-byte cache piece (whole lines per
-//     wave instruction) and ELT_L/ELT_C 16-byte linear pieces (RPL rows of
-//     one token, 256-1024 contiguous bytes per token per wave instruction);
+//     wave instruction) and one 16-byte linear piece (RPL rows of one token,
+//     256-1024 contiguous bytes per token per wave instruction);
 //   * the two orientations meet in a padded LDS tile: cache pieces are
-//     written/read as rows, linear pieces as RPL column elements;
-//   * the FP8 codec is applied on the linear side (encode before the LDS
-//     write, decode after the LDS read), one scale per linear piece.
+//     written/read as rows, linear pieces as RPL column elements.
 // Each wave keeps at most a few hundred bytes per lane in flight and lives for
 // one chunk, the access shape that reaches the highest HBM copy rate on
 // MI355X.  Partial runs store only their own block columns (element stores at
 // the edges), so neighbouring slots are never touched.  Skipped tokens
-// (slot < 0) are zero filled by the workgroup that owns them.
-#include <type_traits>
-
+// (slot < 0) are zero filled by the workgroup that owns them.  FP8 caches go
+// to the per-wave kernels of kv_paged_waves.hip; any shape or alignment the
+// tiled kernels do not cover goes to the element-wise kernel below.
 #include "kv_hip_common.h"
 #include "kv_launch.h"
 #include "kv_paged_args.h"
 
 namespace kvhip {
 
-// ----- the cooperative tile kernel ------------------------------------------------
+// ----- the cooperative tile kernel (16- and 32-bit copies) ----------------------------
 
 constexpr int kCoopThreads = 256;
 
-template <int ELT_C, int ELT_L, int BS>
+template <int ELT, int BS>
 struct CoopShape {
-  static constexpr int CG = 16 / ELT_C;               // block columns per cache piece
+  static constexpr int CG = 16 / ELT;                 // block columns per cache piece
   static constexpr int NCG = BS / CG;                 // cache pieces per cache row
-  static constexpr int ROWB = BS * ELT_C;             // bytes per cache row of a block
+  static constexpr int ROWB = BS * ELT;               // bytes per cache row of a block
   static constexpr int kRows = kCoopThreads * 16 / ROWB;  // cache rows per chunk (4 KiB)
-  static constexpr int RPL = 16 / ELT_L;              // rows per linear piece
+  static constexpr int RPL = 16 / ELT;                // rows per linear piece
   static constexpr int G = kRows / RPL;               // linear pieces per token per chunk
-  static constexpr int PPT = ELT_L / ELT_C;           // linear pieces per thread
   static constexpr int PITCH = ROWB + 4;              // LDS bytes per cache row (one pad dword)
   static_assert(BS % CG == 0, "block row must be a whole number of 16-byte pieces");
-  static_assert(BS * G == kCoopThreads * PPT, "linear pieces must cover the chunk");
+  static_assert(BS * G == kCoopThreads, "linear pieces must cover the chunk");
   static_assert(G % 8 == 0, "row groups come in eights");
 
   // Linear piece p of a chunk -> (block column, row group).  Eight
@@ -57,87 +55,28 @@ struct CoopShape {
   __device__ static __forceinline__ int grp(int p) { return (p & 7) + 8 * (p / (8 * BS)); }
 };
 
-// Linear piece (RPL rows of block column c) assembled from the LDS tile, in
-// the linear element type.
-template <int ELT_C, int ELT_L, int CODEC, int LDT, int PITCH>
-__device__ __forceinline__ u32x4 lds_column_piece(const uint8_t* tile, int row0, int c, float sc) {
-  constexpr int RPL = 16 / ELT_L;
-  const uint8_t* p = tile + row0 * PITCH + c * ELT_C;
+// Linear piece (RPL rows of block column c) assembled from the LDS tile.
+template <int ELT, int PITCH>
+__device__ __forceinline__ u32x4 lds_column_piece(const uint8_t* tile, int row0, int c) {
+  const uint8_t* p = tile + row0 * PITCH + c * ELT;
   u32x4 o;
-  if constexpr (CODEC == kCopy && ELT_C == 2) {
+  if constexpr (ELT == 2) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) o[k] = pack16(load_elem<2>(p + (2 * k) * PITCH), load_elem<2>(p + (2 * k + 1) * PITCH));
-  } else if constexpr (CODEC == kCopy && ELT_C == 4) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) o[k] = load_elem<4>(p + k * PITCH);
-  } else if constexpr (ELT_L == 2) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t lo = f32_to_lin<LDT>(fp8_decode<CODEC>(load_elem<1>(p + (2 * k) * PITCH)) * sc);
-      const uint32_t hi = f32_to_lin<LDT>(fp8_decode<CODEC>(load_elem<1>(p + (2 * k + 1) * PITCH)) * sc);
-      o[k] = pack16(lo, hi);
-    }
   } else {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) o[k] = __float_as_uint(fp8_decode<CODEC>(load_elem<1>(p + k * PITCH)) * sc);
+    for (int k = 0; k < 4; ++k) o[k] = load_elem<4>(p + k * PITCH);
   }
-  static_assert(RPL * ELT_L == 16, "a linear piece is 16 bytes");
   return o;
 }
 
-// Writes the RPL elements of one linear piece into column c of the LDS tile,
-// in cache encoding.  FAST selects the hoisted-reciprocal FP8 quotient.
-template <int ELT_C, int ELT_L, int CODEC, int LDT, int PITCH, bool FAST>
-__device__ __forceinline__ void lds_put_column(uint8_t* tile, int row0, int c, const u32x4& in, float sc, float r,
-                                               bool no_small = false) {
-  constexpr int RPL = 16 / ELT_L;
-  uint8_t* p = tile + row0 * PITCH + c * ELT_C;
-  if constexpr (FAST && CODEC != kCopy) {
-    // Fast range: exact quotients through the hoisted reciprocal, bytes from
-    // the hardware converter (E5M2 pieces above its largest normal keep the
-    // integer encoder).
-    float w[RPL];
-    uint32_t amax = 0;
+// Writes the RPL elements of one linear piece into column c of the LDS tile.
+template <int ELT, int PITCH>
+__device__ __forceinline__ void lds_put_column(uint8_t* tile, int row0, int c, const u32x4& in) {
+  constexpr int RPL = 16 / ELT;
+  uint8_t* p = tile + row0 * PITCH + c * ELT;
 #pragma unroll
-    for (int i = 0; i < RPL; ++i) {
-      const float x = (ELT_L == 2) ? lin_to_f32<LDT>(elem16(in, i)) : __uint_as_float(in[i]);
-      w[i] = quot_fast(x, sc, r);
-      if constexpr (CODEC == kE5M2) amax = max(amax, __float_as_uint(w[i]) & 0x7FFFFFFFu);
-    }
-    if (CODEC == kE4M3 || amax <= kHwEncodeMaxBits<CODEC>) {
-      if (no_small) {
-#pragma unroll
-        for (int g = 0; g < RPL / 4; ++g) {
-          const uint32_t b = fp8_pack4_hw<CODEC, false>(w[4 * g], w[4 * g + 1], w[4 * g + 2], w[4 * g + 3]);
-#pragma unroll
-          for (int k = 0; k < 4; ++k) store_elem<1>(p + (4 * g + k) * PITCH, b >> (8 * k));
-        }
-      } else {
-#pragma unroll
-        for (int g = 0; g < RPL / 4; ++g) {
-          const uint32_t b = fp8_pack4_hw<CODEC>(w[4 * g], w[4 * g + 1], w[4 * g + 2], w[4 * g + 3]);
-#pragma unroll
-          for (int k = 0; k < 4; ++k) store_elem<1>(p + (4 * g + k) * PITCH, b >> (8 * k));
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < RPL; ++i) store_elem<1>(p + i * PITCH, fp8_encode_fast<CODEC>(w[i]));
-    }
-    return;
-  }
-#pragma unroll
-  for (int i = 0; i < RPL; ++i) {
-    uint32_t v;
-    if constexpr (CODEC == kCopy) {
-      v = piece_elem<ELT_L>(in, i);
-    } else {
-      const float x = (ELT_L == 2) ? lin_to_f32<LDT>(elem16(in, i)) : __uint_as_float(in[i]);
-      if constexpr (FAST) v = fp8_encode_fast<CODEC>(quot_fast(x, sc, r));
-      else v = fp8_encode<CODEC>(div_rn(x, sc));
-    }
-    store_elem<ELT_C>(p + i * PITCH, v);
-  }
+  for (int i = 0; i < RPL; ++i) store_elem<ELT>(p + i * PITCH, piece_elem<ELT>(in, i));
 }
 
 // Workgroup barrier for the LDS tile only: waits for this wave's LDS
@@ -152,16 +91,13 @@ __device__ __forceinline__ void lds_barrier() {
 // Chunks of one run handled by one workgroup (grid z covers the rest).
 constexpr int kChunksPerGroup = 4;
 
-template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS, bool SCATTER>
+template <int ELT, int BS, bool SCATTER>
 __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs a) {
-  using S = CoopShape<ELT_C, ELT_L, BS>;
+  using S = CoopShape<ELT, BS>;
   constexpr int CG = S::CG, NCG = S::NCG, ROWB = S::ROWB, kRows = S::kRows;
-  constexpr int RPL = S::RPL, PPT = S::PPT, PITCH = S::PITCH;
+  constexpr int RPL = S::RPL, PITCH = S::PITCH;
   static_assert(kTileTokens + BS + 1 <= kWave, "run window must fit one wave");
   __shared__ __align__(16) uint8_t tile[kRows * PITCH];
-  // FP8: (scale, RN(1/scale)) of every head the workgroup's rows touch.
-  constexpr int kTabHeads = (CODEC == kCopy) ? 1 : 64;
-  __shared__ float2 scale_tab[kTabHeads];
 
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = lane_id();
@@ -195,55 +131,19 @@ __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs
   const uint64_t window = ((1ull << ntile) - 1ull) << 1;
   uint64_t heads = vmask & ~cmask & window;
 
-  // This thread's cache piece (row pr, column group pg) and linear pieces
-  // (block column lc[j], row group lq[j]) within every chunk.  All offsets are
+  // This thread's cache piece (row pr, column group pg) and linear piece
+  // (block column lc, row group lq) within every chunk.  All offsets are
   // 32-bit and relative to the run's descriptors; per chunk they advance by a
   // constant.
   const int pr = tid / NCG;
   const int pg = tid % NCG;
   const int rows_left = static_cast<int>(re - rb);
-  int lc[PPT], lq[PPT];
-#pragma unroll
-  for (int j = 0; j < PPT; ++j) {
-    lc[j] = S::col(tid + j * kCoopThreads);
-    lq[j] = S::grp(tid + j * kCoopThreads);
-  }
+  const int lc = S::col(tid);
+  const int lq = S::grp(tid);
   auto prow_in = [&](int k) { return k * kRows + pr < rows_left; };
-  auto lrow_in = [&](int k, int j) { return k * kRows + lq[j] * RPL < rows_left; };
-  // FP8 scale of linear piece j in chunk k: head = row / head_dim by a float
-  // reciprocal and one exact correction (rows < 2^24).  The row is clamped
-  // into the block so the load is unconditional.
-  auto head_of = [&](int k, int j) -> int {
-    int row = static_cast<int>(rb) + k * kRows + lq[j] * RPL;
-    row = row < static_cast<int>(a.nrows) ? row : static_cast<int>(a.nrows) - 1;
-    const int hd = static_cast<int>(a.head_dim);
-    int head = static_cast<int>(static_cast<float>(row) * a.inv_head_dim);
-    if (head * hd > row) --head;
-    else if ((head + 1) * hd <= row) ++head;
-    return head;
-  };
-  auto piece_scale = [&](int k, int j) -> float {
-    if constexpr (CODEC == kCopy) return 1.0f;
-    else return load_scale(a, kv, layer, head_of(k, j));
-  };
-  // Quantiser: the heads of rows [rb, re) are computed once into LDS, so a
-  // piece looks up its scale and reciprocal instead of loading and dividing.
-  int tab_h0 = 0;
-  bool use_tab = false;
-  if constexpr (CODEC != kCopy && SCATTER) {
-    tab_h0 = static_cast<int>(rb / a.head_dim);
-    const int tab_n = static_cast<int>((re - 1) / a.head_dim) - tab_h0 + 1;
-    use_tab = tab_n <= kTabHeads;
-    if (use_tab) {
-      if (tid < tab_n) {
-        const float sc = load_scale(a, kv, layer, tab_h0 + tid);
-        scale_tab[tid] = make_float2(sc, fast_scale_ok(sc) ? 1.0f / sc : 0.0f);
-      }
-      lds_barrier();
-    }
-  }
+  auto lrow_in = [&](int k) { return k * kRows + lq * RPL < rows_left; };
   constexpr uint32_t kCacheStep = kRows * ROWB;     // bytes between chunks, cache side
-  constexpr uint32_t kLinStep = kRows * ELT_L;      // bytes between chunks, linear side
+  constexpr uint32_t kLinStep = kRows * ELT;        // bytes between chunks, linear side
   const uint32_t cpiece = static_cast<uint32_t>(tid) * 16u;
   const uint32_t stride32 = static_cast<uint32_t>(a.lin_token_stride);
 
@@ -260,123 +160,51 @@ __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs
     // Wave-uniform descriptors: the block's rows [rb, re) and the run's
     // first linear row at row rb.  Offsets of masked lanes are kOffOob.
     const buf_t cbuf = make_buf(cache + (blk * a.nrows + rb) * ROWB);
-    const buf_t lbuf = make_buf(lin + tf * a.lin_token_stride + rb * ELT_L);
-    bool lmine[PPT];
-    uint32_t lbase[PPT];
-#pragma unroll
-    for (int j = 0; j < PPT; ++j) {
-      lmine[j] = lc[j] >= c0 && lc[j] < c1;
-      lbase[j] = static_cast<uint32_t>(lc[j] - c0) * stride32 + static_cast<uint32_t>(lq[j]) * 16u;
-    }
+    const buf_t lbuf = make_buf(lin + tf * a.lin_token_stride + rb * ELT);
+    const bool lmine = lc >= c0 && lc < c1;
+    const uint32_t lbase = static_cast<uint32_t>(lc - c0) * stride32 + static_cast<uint32_t>(lq) * 16u;
     auto coff = [&](int k) -> uint32_t { return prow_in(k) ? cpiece + k * kCacheStep : kOffOob; };
-    auto loff = [&](int k, int j) -> uint32_t {
-      return (lmine[j] && lrow_in(k, j)) ? lbase[j] + k * kLinStep : kOffOob;
-    };
+    auto loff = [&](int k) -> uint32_t { return (lmine && lrow_in(k)) ? lbase + k * kLinStep : kOffOob; };
 
     if constexpr (!SCATTER) {
       u32x4 nxt = buf_ld16(cbuf, coff(0));
-      float scn[PPT];
-#pragma unroll
-      for (int j = 0; j < PPT; ++j) scn[j] = piece_scale(0, j);
       for (int k = 0; k < nchunks; ++k) {
         const u32x4 cur = nxt;
-        float scc[PPT];
-#pragma unroll
-        for (int j = 0; j < PPT; ++j) scc[j] = scn[j];
         nxt = buf_ld16(cbuf, (k + 1 < nchunks) ? coff(k + 1) : kOffOob);
-#pragma unroll
-        for (int j = 0; j < PPT; ++j) scn[j] = piece_scale(k + 1 < nchunks ? k + 1 : k, j);
         if (prow_in(k)) {
           uint32_t* const d = reinterpret_cast<uint32_t*>(tile + pr * PITCH + pg * 16);
           d[0] = cur[0]; d[1] = cur[1]; d[2] = cur[2]; d[3] = cur[3];
         }
         lds_barrier();
-#pragma unroll
-        for (int j = 0; j < PPT; ++j)
-          buf_st16(lbuf, loff(k, j),
-                   lds_column_piece<ELT_C, ELT_L, CODEC, LDT, PITCH>(tile, lq[j] * RPL, lc[j], scc[j]));
+        buf_st16(lbuf, loff(k), lds_column_piece<ELT, PITCH>(tile, lq * RPL, lc));
         lds_barrier();
       }
     } else {
-      // The chunk loop is instantiated with and without the LDS scale table
-      // so that neither version has data-dependent memory instructions.
-      auto scatter_run = [&](auto tab_tag) {
-        constexpr bool kTab = decltype(tab_tag)::value;
-        u32x4 nxt[PPT];
-        float scn[PPT];
+      u32x4 nxt = buf_ld16(lbuf, loff(0));
+      const bool full_run = (c0 == 0) && (c1 == BS);
+      for (int k = 0; k < nchunks; ++k) {
+        const u32x4 in = nxt;
+        nxt = buf_ld16(lbuf, (k + 1 < nchunks) ? loff(k + 1) : kOffOob);
+        if (lmine && lrow_in(k)) lds_put_column<ELT, PITCH>(tile, lq * RPL, lc, in);
+        lds_barrier();
+        const uint32_t* const d = reinterpret_cast<const uint32_t*>(tile + pr * PITCH + pg * 16);
+        const u32x4 w = {d[0], d[1], d[2], d[3]};
+        const uint32_t off = coff(k);
+        const int lo = pg * CG;
+        if (full_run) {
+          buf_st16(cbuf, off, w);
+        } else {
+          // Whole pieces inside the run go as one vector; edge pieces store
+          // only their in-run columns.
+          const bool whole = lo >= c0 && lo + CG <= c1;
+          buf_st16(cbuf, whole ? off : kOffOob, w);
 #pragma unroll
-        for (int j = 0; j < PPT; ++j) {
-          nxt[j] = buf_ld16(lbuf, loff(0, j));
-          if constexpr (!kTab) scn[j] = piece_scale(0, j);
-          else scn[j] = 0.0f;
+          for (int cc = 0; cc < CG; ++cc) {
+            const bool mine = !whole && off != kOffOob && lo + cc >= c0 && lo + cc < c1;
+            buf_st_elem<ELT>(cbuf, mine ? off + cc * ELT : kOffOob, piece_elem<ELT>(w, cc));
+          }
         }
-        const bool full_run = (c0 == 0) && (c1 == BS);
-        for (int k = 0; k < nchunks; ++k) {
-          u32x4 in[PPT];
-          float scc[PPT];
-#pragma unroll
-          for (int j = 0; j < PPT; ++j) {
-            in[j] = nxt[j];
-            scc[j] = scn[j];
-            nxt[j] = buf_ld16(lbuf, (k + 1 < nchunks) ? loff(k + 1, j) : kOffOob);
-            if constexpr (!kTab) scn[j] = piece_scale(k + 1 < nchunks ? k + 1 : k, j);
-          }
-#pragma unroll
-          for (int j = 0; j < PPT; ++j) {
-            if (!lmine[j] || !lrow_in(k, j)) continue;
-            float sc = scc[j];
-            float rtab = 0.0f;
-            if constexpr (kTab) {
-              const float2 e = scale_tab[head_of(k, j) - tab_h0];
-              sc = e.x;
-              rtab = e.y;
-            }
-            bool fast = true;
-            bool no_small = false;
-            if constexpr (CODEC != kCopy) {
-              InputRange<LDT> range;
-              range.add(in[j]);
-              fast = fast_scale_ok(sc) && range.in_fast_range();
-              // Every nonzero quotient of the piece is at least the smallest
-              // normal when min|x| >= minnorm * s (margin 2^-20 for the rounded
-              // product): no flush to zero is needed.
-              no_small = range.min_abs_nonzero() >=
-                         __uint_as_float(Fp8Fmt<CODEC>::kMinNormBits) * sc * (1.0f + 0x1p-20f);
-            }
-            if (fast) {
-              const float r = (CODEC == kCopy) ? 0.0f : (kTab ? rtab : 1.0f / sc);
-              lds_put_column<ELT_C, ELT_L, CODEC, LDT, PITCH, CODEC != kCopy>(tile, lq[j] * RPL, lc[j], in[j], sc, r,
-                                                                              no_small);
-            } else {
-              lds_put_column<ELT_C, ELT_L, CODEC, LDT, PITCH, false>(tile, lq[j] * RPL, lc[j], in[j], sc, 0.0f);
-            }
-          }
-          lds_barrier();
-          const uint32_t* const d = reinterpret_cast<const uint32_t*>(tile + pr * PITCH + pg * 16);
-          const u32x4 w = {d[0], d[1], d[2], d[3]};
-          const uint32_t off = coff(k);
-          const int lo = pg * CG;
-          if (full_run) {
-            buf_st16(cbuf, off, w);
-          } else {
-            // Whole pieces inside the run go as one vector; edge pieces store
-            // only their in-run columns.
-            const bool whole = lo >= c0 && lo + CG <= c1;
-            buf_st16(cbuf, whole ? off : kOffOob, w);
-#pragma unroll
-            for (int cc = 0; cc < CG; ++cc) {
-              const bool mine = !whole && off != kOffOob && lo + cc >= c0 && lo + cc < c1;
-              buf_st_elem<ELT_C>(cbuf, mine ? off + cc * ELT_C : kOffOob, piece_elem<ELT_C>(w, cc));
-            }
-          }
-          lds_barrier();
-        }
-      };
-      if constexpr (CODEC != kCopy) {
-        if (use_tab) scatter_run(std::true_type{});
-        else scatter_run(std::false_type{});
-      } else {
-        scatter_run(std::false_type{});
+        lds_barrier();
       }
     }
   }
@@ -389,7 +217,7 @@ __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs
         const int i = __builtin_ctzll(skipped);
         skipped &= skipped - 1;
         uint8_t* const row = lin + (t0 - 1 + i) * a.lin_token_stride;
-        for (int64_t k = rb * ELT_L + static_cast<int64_t>(tid) * 16; k < re * ELT_L; k += kCoopThreads * 16)
+        for (int64_t k = rb * ELT + static_cast<int64_t>(tid) * 16; k < re * ELT; k += kCoopThreads * 16)
           st16(row + k, zero);
       }
     }
@@ -454,14 +282,14 @@ hipError_t launch_elem(const TileArgs& a, int64_t planes, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS, bool SCATTER>
+template <int ELT, int BS, bool SCATTER>
 hipError_t launch_tile(const TileArgs& a, int64_t planes, hipStream_t stream) {
-  using S = CoopShape<ELT_C, ELT_L, BS>;
+  using S = CoopShape<ELT, BS>;
   const int64_t chunks = (a.nrows + S::kRows * kChunksPerGroup - 1) / (S::kRows * kChunksPerGroup);
   if (chunks > 65535) return hipErrorInvalidValue;
   const int64_t tiles = (a.num_tokens + kTileTokens - 1) / kTileTokens;
   if (tiles > 0x7FFFFFFF) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((paged_tile_kernel<ELT_C, ELT_L, CODEC, LDT, BS, SCATTER>),
+  hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, SCATTER>),
                      dim3(static_cast<uint32_t>(tiles), static_cast<uint32_t>(planes), static_cast<uint32_t>(chunks)),
                      dim3(kCoopThreads), 0, stream, a);
   return hipGetLastError();
@@ -470,20 +298,20 @@ hipError_t launch_tile(const TileArgs& a, int64_t planes, hipStream_t stream) {
 template <int ELT_C, int ELT_L, int CODEC, int LDT, bool SCATTER>
 hipError_t dispatch_bs(const TileArgs& a, int64_t bs, bool fast, int64_t planes, hipStream_t stream) {
   if (fast) {
-    if constexpr (ELT_C != 1) {
-      if (bs == 8) return launch_tile<ELT_C, ELT_L, CODEC, LDT, 8, SCATTER>(a, planes, stream);
-    }
-    if constexpr (ELT_C == 1 && !SCATTER) {
+    if constexpr (CODEC == kCopy) {
+      // 16- and 32-bit copies: workgroup-cooperative kernel.
+      static_assert(ELT_C == ELT_L, "copies keep the element type");
+      if (bs == 8) return launch_tile<ELT_C, 8, SCATTER>(a, planes, stream);
+      if (bs == 16) return launch_tile<ELT_C, 16, SCATTER>(a, planes, stream);
+      if (bs == 32) return launch_tile<ELT_C, 32, SCATTER>(a, planes, stream);
+    } else if constexpr (!SCATTER) {
       // FP8 dequant-gather: per-wave kernel (kv_paged_waves.hip).
       if (bs == 16) return launch_wave_gather<ELT_C, ELT_L, CODEC, LDT, 16>(a, planes, stream);
       if (bs == 32) return launch_wave_gather<ELT_C, ELT_L, CODEC, LDT, 32>(a, planes, stream);
-    } else if constexpr (ELT_C == 1 && SCATTER) {
+    } else {
       // FP8 quant-store: per-wave kernel (kv_paged_waves.hip).
       if (bs == 16) return launch_wave_scatter<ELT_C, ELT_L, CODEC, LDT, 16>(a, planes, stream);
       if (bs == 32) return launch_wave_scatter<ELT_C, ELT_L, CODEC, LDT, 32>(a, planes, stream);
-    } else {
-      if (bs == 16) return launch_tile<ELT_C, ELT_L, CODEC, LDT, 16, SCATTER>(a, planes, stream);
-      if (bs == 32) return launch_tile<ELT_C, ELT_L, CODEC, LDT, 32, SCATTER>(a, planes, stream);
     }
   }
   return launch_elem<ELT_C, ELT_L, CODEC, LDT, SCATTER>(a, planes, stream);
