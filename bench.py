@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""KV-copy throughput on one MI355X: BASELINE.json configs[1] (headline) plus configs 1, 3, 4 and 5.
+"""KV-copy throughput on one MI355X: BASELINE.json configs[1] (headline) plus configs 1, 3, 4, 5 and the dense preload.
 
 Headline workload: 32 layers of Llama-3-8B KV caches
 [8192 blocks, 16, 8 kv-heads, 128] bf16 (paged layout [NB, NH, HD, BS]),
@@ -17,15 +17,17 @@ of K steps / device time of the K steps between HIP events, in GB/s.
 ``roofline`` is reported for the dominant kernel (the direction with the
 larger total time) against the 8 TB/s HBM peak; its ``traffic`` comes from the
 committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes.  ``cpu_baseline`` times the
-numpy oracle (oracle/kv_oracle.py, a port of the reference algorithm) on a
-bounded sample of the same workload on this host and scales by bytes.
+numpy oracle (oracle/kv_oracle.py, a port of the reference algorithm) on the
+headline workload itself, one layer at a time, on this host.
 
-The other configs are reported under ``extra`` with the same byte convention.
-Their launches are short (0.01-0.3 ms), so they are timed in batches of
-back-to-back launches between two events (host launch overhead hidden behind
-device work); each is also checked outside the timed region, by torch
-indexing, by the reference's FP8 steps restated in torch (tests/torch_ref.py)
-or by a round trip.  The numpy oracle runs only in the CPU-baseline leg.
+The other configs are reported under ``extra`` with the same byte convention
+(config 6: the block-table / CSR dense preload for attention and whole-block
+copies, which are not BASELINE configs).  Their launches are short
+(0.01-0.8 ms), so they are timed in batches of back-to-back launches between
+two events (host launch overhead hidden behind device work); each is also
+checked outside the timed region, by torch indexing, by the reference's FP8
+steps restated in torch (tests/torch_ref.py) or by a round trip.  The numpy
+oracle runs only in the CPU-baseline leg.
 """
 
 from __future__ import annotations
@@ -76,7 +78,7 @@ def make_covering_slots(seed: int, tokens: int, lo: int, hi: int, num_blocks: in
     return sequence_slots(rng, lengths, num_blocks=num_blocks, block_size=block_size)
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "paged_tile_kernel_cfg2_traffic.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "paged_kernels_cfg2_cfg3_traffic.md")
 
 
 def profiled_traffic(direction: str) -> int | None:
@@ -577,24 +579,26 @@ def device_copy(mib: int, reps: int = 5) -> dict:
 
 
 def cpu_baseline(slots_np: np.ndarray, kc: torch.Tensor, vc: torch.Tensor) -> dict:
-    """Time the numpy oracle on a bounded sample of configs[1]: all tokens, first 2 layers, both directions."""
+    """Time the numpy oracle on configs[1] itself: the gather and the scatter of every token of all 32 layers,
+    one layer at a time (each layer's K and V caches are copied to the host outside the timed region)."""
     from oracle import kv_oracle as ko
 
-    layers = 2
     t = int(slots_np.shape[0])
-    k_np = kc[:layers].view(torch.int16).cpu().numpy().view(np.uint16)
-    v_np = vc[:layers].view(torch.int16).cpu().numpy().view(np.uint16)
-    start = time.perf_counter()
-    ks = [ko.paged_to_linear(k_np[layer], slots_np) for layer in range(layers)]
-    vs = [ko.paged_to_linear(v_np[layer], slots_np) for layer in range(layers)]
-    for layer in range(layers):
-        ko.linear_to_paged(ks[layer], k_np[layer], slots_np)
-        ko.linear_to_paged(vs[layer], v_np[layer], slots_np)
-    elapsed = time.perf_counter() - start
-    sample_bytes = 2 * (2 * (2 * layers * t * ROW * 2) + 8 * t)
+    elapsed = 0.0
+    for layer in range(NL):
+        k_np = kc[layer].view(torch.int16).cpu().numpy().view(np.uint16)
+        v_np = vc[layer].view(torch.int16).cpu().numpy().view(np.uint16)
+        start = time.perf_counter()
+        k_lin = ko.paged_to_linear(k_np, slots_np)
+        v_lin = ko.paged_to_linear(v_np, slots_np)
+        ko.linear_to_paged(k_lin, k_np, slots_np)
+        ko.linear_to_paged(v_lin, v_np, slots_np)
+        elapsed += time.perf_counter() - start
+    sample_bytes = 2 * (2 * (2 * NL * t * ROW * 2) + 8 * t)
     return {"value": sample_bytes / elapsed / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle (oracle/kv_oracle.py) gather+scatter of {t} tokens x {layers} of {NL} layers "
-                      f"(K and V), {elapsed:.2f} s, scaled by algorithmic bytes; host has {os.cpu_count()} cpus",
+            "sample": f"numpy oracle (oracle/kv_oracle.py) gather + scatter of all {t} tokens x {NL} layers (K and V) "
+                      f"of configs[1], one layer at a time, {elapsed:.1f} s of CPU time; algorithmic bytes as for the "
+                      f"GPU; host has {os.cpu_count()} cpus, 1 used",
             "seconds": elapsed}
 
 
@@ -672,7 +676,7 @@ def main() -> int:
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(c2["dominant"]),
                      "traffic_source": "rocprofv3 FETCH_SIZE x2.000 + WRITE_SIZE x1.000 per dispatch "
-                                       "(profiles/paged_tile_kernel_cfg2_traffic.md)",
+                                       "(profiles/paged_kernels_cfg2_cfg3_traffic.md)",
                      "bytes_per_launch": c2["bytes_per_direction"], "avg_launch_ms": round(c2["dominant_avg_ms"], 4)},
         "cpu_baseline": cpu,
         "extra": extra,
