@@ -88,8 +88,11 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Chunks of one run handled by one workgroup (grid z covers the rest).
-constexpr int kChunksPerGroup = 4;
+// Chunks of one run handled by one workgroup (grid z covers the rest): the
+// gather does best with more, shorter-lived workgroups, the scatter (whose
+// setup includes the claim check) with longer ones (measured).
+template <bool SCATTER>
+constexpr int kChunksPerGroup = SCATTER ? 4 : 2;
 
 template <int ELT, int BS, bool SCATTER>
 __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs a) {
@@ -107,8 +110,9 @@ __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs
   const int layer = plane >> 1;
   const int kv = plane & 1;
   // Rows [rb, re) of the block, in chunks of kRows.
-  const int64_t rb = static_cast<int64_t>(blockIdx.z) * (kRows * kChunksPerGroup);
-  const int64_t re = (rb + kRows * kChunksPerGroup < a.nrows) ? rb + kRows * kChunksPerGroup : a.nrows;
+  constexpr int kGroupRows = kRows * kChunksPerGroup<SCATTER>;
+  const int64_t rb = static_cast<int64_t>(blockIdx.z) * kGroupRows;
+  const int64_t re = (rb + kGroupRows < a.nrows) ? rb + kGroupRows : a.nrows;
   const int nchunks = static_cast<int>((re - rb + kRows - 1) / kRows);
   uint8_t* const cache = a.cache[kv] + static_cast<int64_t>(layer) * a.cache_layer_stride;
   uint8_t* const lin = a.lin[kv] + static_cast<int64_t>(layer) * a.lin_layer_stride;
@@ -285,7 +289,8 @@ hipError_t launch_elem(const TileArgs& a, int64_t planes, hipStream_t stream) {
 template <int ELT, int BS, bool SCATTER>
 hipError_t launch_tile(const TileArgs& a, int64_t planes, hipStream_t stream) {
   using S = CoopShape<ELT, BS>;
-  const int64_t chunks = (a.nrows + S::kRows * kChunksPerGroup - 1) / (S::kRows * kChunksPerGroup);
+  constexpr int kGroupRows = S::kRows * kChunksPerGroup<SCATTER>;
+  const int64_t chunks = (a.nrows + kGroupRows - 1) / kGroupRows;
   if (chunks > 65535) return hipErrorInvalidValue;
   const int64_t tiles = (a.num_tokens + kTileTokens - 1) / kTileTokens;
   if (tiles > 0x7FFFFFFF) return hipErrorInvalidValue;
