@@ -80,6 +80,16 @@ int musa_aiter_hip_copy_rows(const uint64_t* src_planes, const uint64_t* dst_pla
                              const int64_t* dst_idx, int64_t num_tokens, int64_t num_rows_out, int64_t src_offset,
                              int64_t dst_offset, int64_t src_rows, int64_t dst_rows, int64_t row_bytes,
                              int64_t src_stride, int64_t dst_stride, int zero_invalid, int dedupe, void* stream);
+/* Row copies between two index-addressed plane sets (host arrays of plane bases).  A side
+ * with page_rows > 0 is paged: row r sits at (r / page_rows) * page_stride + (r % page_rows) *
+ * stride of its plane (the page-first [pages, layers, page, item] tensors of SGLang's direct
+ * HiCache transfers).  Tokens with an index outside [0, rows) are skipped; dedupe keeps the
+ * last token of a repeated destination. */
+int musa_aiter_hip_copy_rows_paged(const uint64_t* src_planes, const uint64_t* dst_planes, int64_t num_planes,
+                                   const int64_t* src_idx, const int64_t* dst_idx, int64_t num_tokens,
+                                   int64_t src_rows, int64_t dst_rows, int64_t row_bytes, int64_t src_stride,
+                                   int64_t dst_stride, int64_t src_page_rows, int64_t src_page_stride,
+                                   int64_t dst_page_rows, int64_t dst_page_stride, int dedupe, void* stream);
 
 /* ---- Paged-A [NB,NH,HD,BS] <-> linear [T,NH,HD] -------------------------------------------------
  * binding kv_transfer.py:350-376 (gather), :410-436 (scatter), :480-508 / :542-570 (multi-layer),
@@ -363,6 +373,21 @@ int lmcache_kv_strided_block_transfer(void* staging, const uint64_t* paged_ptrs,
                                       int64_t offset_in_object, int64_t staging_tokens, int64_t block_size,
                                       int64_t row_bytes, int64_t paged_block_stride, int64_t mode,
                                       int64_t value_bytes, int64_t scale_bytes, void* stream);
+
+/* ---- SGLang HiCache layer-first / page-first transfers (binding hicache_transfer.py:57-83,
+ * :196-258; replaces hicache_transfer.mu:4-98).  For each item whose two page indices are both
+ * non-negative and each layer in [start_layer, start_layer + num_layers), item_size_bytes
+ * (rounded down to whole 64-bit words) move from src + page * src_page_stride + layer *
+ * src_layer_stride to the matching destination offset, for K and, when both V pointers are
+ * non-null, for V.  Indices are int64 device arrays and are not range-checked; a destination
+ * page named by several items receives one of them (the Python layer validates indices and
+ * keeps the last item through musa_aiter_hip_copy_rows_paged). ---- */
+int musa_aiter_hicache_transfer_abi_version(void);
+int musa_aiter_hicache_transfer_bytes(const void* src_k, void* dst_k, const void* src_v, void* dst_v,
+                                      const int64_t* src_indices, const int64_t* dst_indices, int64_t num_items,
+                                      int64_t start_layer, int64_t num_layers, int64_t item_size_bytes,
+                                      int64_t src_page_stride_bytes, int64_t src_layer_stride_bytes,
+                                      int64_t dst_page_stride_bytes, int64_t dst_layer_stride_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -941,4 +941,76 @@ int lmcache_kv_strided_block_transfer(void* staging, const uint64_t* paged_ptrs,
   return kvhip::launch_strided_blocks(p, as_stream(stream));
 }
 
+// ----- SGLang HiCache transfers (hicache_transfer.mu:53-98, hicache_transfer.py:196-258) ---------
+
+int musa_aiter_hicache_transfer_abi_version() { return 1; }
+
+// Rows copied between two index-addressed sides whose planes are listed on
+// the host; either side may use paged row addressing.  Tokens whose source or
+// destination index lies outside [0, rows) are skipped; with `dedupe` a
+// destination row named by several tokens keeps the last one.
+int musa_aiter_hip_copy_rows_paged(const uint64_t* src_planes, const uint64_t* dst_planes, int64_t num_planes,
+                                   const int64_t* src_idx, const int64_t* dst_idx, int64_t num_tokens,
+                                   int64_t src_rows, int64_t dst_rows, int64_t row_bytes, int64_t src_stride,
+                                   int64_t dst_stride, int64_t src_page_rows, int64_t src_page_stride,
+                                   int64_t dst_page_rows, int64_t dst_page_stride, int dedupe, void* stream) {
+  if (num_tokens <= 0 || num_planes <= 0 || row_bytes <= 0) return hipSuccess;
+  if (src_idx == nullptr || dst_idx == nullptr) return hipErrorInvalidValue;
+  RowCopyParams p{};
+  p.src_planes = src_planes;
+  p.dst_planes = dst_planes;
+  p.num_planes = num_planes;
+  p.src_idx = src_idx;
+  p.dst_idx = dst_idx;
+  p.num_tokens = num_tokens;
+  p.num_rows_out = num_tokens;
+  p.src_rows = src_rows;
+  p.dst_rows = dst_rows;
+  p.row_bytes = row_bytes;
+  p.src_stride = src_stride;
+  p.dst_stride = dst_stride;
+  p.src_page_rows = src_page_rows;
+  p.src_page_stride = src_page_stride;
+  p.dst_page_rows = dst_page_rows;
+  p.dst_page_stride = dst_page_stride;
+  if (dedupe) {
+    kvhip::ClaimSource claims;
+    claims.idx = dst_idx;
+    claims.src_idx = src_idx;
+    claims.src_rows = src_rows;
+    hipError_t err = prepare_claims(claims, num_tokens, dst_rows, as_stream(stream), &p.owner, &p.epoch);
+    if (err != hipSuccess) return err;
+  }
+  return kvhip::launch_row_copy(p, as_stream(stream));
+}
+
+// The reference kernel's contract: for every item whose two page indices are
+// both non-negative and every layer in [start_layer, start_layer + num_layers),
+// item_size_bytes (whole 64-bit words) move from
+// src + page * src_page_stride + layer * src_layer_stride to the matching
+// destination offset, for K and, when both V pointers are set, for V.  Page
+// indices are not range-checked (the caller validates them) and a destination
+// page named by several items receives one of them.
+int musa_aiter_hicache_transfer_bytes(const void* src_k, void* dst_k, const void* src_v, void* dst_v,
+                                      const int64_t* src_indices, const int64_t* dst_indices, int64_t num_items,
+                                      int64_t start_layer, int64_t num_layers, int64_t item_size_bytes,
+                                      int64_t src_page_stride_bytes, int64_t src_layer_stride_bytes,
+                                      int64_t dst_page_stride_bytes, int64_t dst_layer_stride_bytes, void* stream) {
+  const int64_t row = item_size_bytes / 8 * 8;
+  if (num_items <= 0 || num_layers <= 0 || row <= 0) return hipSuccess;
+  if (src_k == nullptr || dst_k == nullptr || src_indices == nullptr || dst_indices == nullptr)
+    return hipErrorInvalidValue;
+  const bool with_v = src_v != nullptr && dst_v != nullptr;
+  std::vector<uint64_t> s, d;
+  for (int kv = 0; kv < (with_v ? 2 : 1); ++kv)
+    for (int64_t l = 0; l < num_layers; ++l) {
+      s.push_back(addr(kv == 0 ? src_k : src_v, (start_layer + l) * src_layer_stride_bytes));
+      d.push_back(addr(kv == 0 ? dst_k : dst_v, (start_layer + l) * dst_layer_stride_bytes));
+    }
+  const int64_t unbounded = INT64_MAX;
+  return musa_aiter_hip_copy_rows_paged(s.data(), d.data(), static_cast<int64_t>(s.size()), src_indices,
+                                        dst_indices, num_items, unbounded, unbounded, row, src_page_stride_bytes,
+                                        dst_page_stride_bytes, 0, 0, 0, 0, 0, stream);
+}
+
 }  // extern "C"

@@ -69,6 +69,13 @@ struct RowCopyParams {
   int64_t dense_len;
   int64_t index_count;
   int64_t idx_stride;           // elements between index entries (0 or 1: packed vectors)
+  // Paged row addressing (page_rows > 0): row r of a side sits at byte
+  // (r / page_rows) * page_stride + (r % page_rows) * stride of its plane;
+  // 0 keeps the plain r * stride.
+  int64_t src_page_rows;
+  int64_t src_page_stride;
+  int64_t dst_page_rows;
+  int64_t dst_page_stride;
 };
 
 hipError_t launch_row_copy(const RowCopyParams& p, hipStream_t stream);

@@ -3,9 +3,11 @@
 // Every token-major layout of the path reduces to "copy one row of R bytes
 // per (plane, token)": SGLang-MP split caches [NB, BS, NH, HS] <-> LMCache
 // [2, NL, T, NH*HS] buffers, the per-layer list and legacy 6-D caches, the
-// MLA latent rows [NB, BS, D] and the opaque DSV4 byte rows.  One side of the
-// copy is indexed by a slot/row vector (or both, for byte rows); slot < 0
-// skips the token.
+// MLA latent rows [NB, BS, D], the opaque DSV4 byte rows, whole paged blocks
+// and SGLang HiCache items (one (page, layer) row of a layer-first or
+// page-first pool).  One side of the copy is indexed by a slot/row vector (or
+// both); slot < 0 skips the token.  A side may also be paged: row r then sits
+// at (r / page_rows) * page_stride + (r % page_rows) * stride.
 //
 // Rows are cut into VEC-byte pieces (VEC = the widest power of two dividing
 // the row size, strides and plane bases); one block moves 512 consecutive
@@ -47,6 +49,10 @@ struct RowArgs {
   uint32_t dense_len;
   int64_t index_count;
   int64_t idx_stride;         // elements between consecutive entries of src_idx / dst_idx
+  int64_t src_page_rows;      // > 0: paged row addressing of the source side
+  int64_t src_page_stride;
+  int64_t dst_page_rows;
+  int64_t dst_page_stride;
 };
 
 // Work of one block: kBlockPieces consecutive VEC-byte pieces of the
@@ -59,6 +65,14 @@ constexpr int kBlockPieces = 2 * kBlockThreads;
 constexpr int kBlockRows = kBlockPieces + 2;
 constexpr int64_t kSkipRow = -1;  // destination offset: the token writes nothing
 constexpr int64_t kZeroRow = -1;  // source offset: the destination row is zero filled
+
+// Byte offset of row r inside its plane: r * stride, or for a paged side
+// (page_rows > 0) page r / page_rows at page_stride plus row r % page_rows.
+__device__ __forceinline__ int64_t row_offset(int64_t r, int64_t page_rows, int64_t page_stride, int64_t stride) {
+  if (page_rows <= 0) return r * stride;
+  const int64_t pg = r / page_rows;
+  return pg * page_stride + (r - pg * page_rows) * stride;
+}
 
 // Byte offsets of token u's source and destination rows, with the skip and
 // zero-fill marks above.
@@ -76,11 +90,11 @@ __device__ __forceinline__ void resolve_row(const RowArgs& a, int64_t u, int64_t
     if (valid && a.owner != nullptr) valid = (a.owner[drow] == claim_tag(a.epoch, u));
   }
   if (valid) {
-    *so = srow * a.src_stride;
-    *dof = drow * a.dst_stride;
+    *so = row_offset(srow, a.src_page_rows, a.src_page_stride, a.src_stride);
+    *dof = row_offset(drow, a.dst_page_rows, a.dst_page_stride, a.dst_stride);
   } else if (a.zero_invalid && a.dst_idx == nullptr && drow >= 0 && drow < a.dst_rows) {
     // Only a directly addressed destination row inside its extent is cleared.
-    *dof = drow * a.dst_stride;
+    *dof = row_offset(drow, a.dst_page_rows, a.dst_page_stride, a.dst_stride);
   }
 }
 
@@ -273,8 +287,11 @@ hipError_t launch_row_copy(const RowCopyParams& p, hipStream_t stream) {
 
   // Vector width: the largest power of two dividing the row size, both
   // strides and every plane base known on the host.
+  if (p.src_page_rows < 0 || p.dst_page_rows < 0) return hipErrorInvalidValue;
   uint64_t bits = static_cast<uint64_t>(p.row_bytes) | static_cast<uint64_t>(p.src_stride) |
                   static_cast<uint64_t>(p.dst_stride);
+  if (p.src_page_rows > 0) bits |= static_cast<uint64_t>(p.src_page_stride);
+  if (p.dst_page_rows > 0) bits |= static_cast<uint64_t>(p.dst_page_stride);
   for (int64_t i = 0; i < p.num_planes; ++i) {
     if (src_host) bits |= p.src_planes[i];
     if (dst_host) bits |= p.dst_planes[i];
@@ -311,6 +328,10 @@ hipError_t launch_row_copy(const RowCopyParams& p, hipStream_t stream) {
     a.dense_len = static_cast<uint32_t>(p.dense_len);
     a.index_count = p.index_count;
     a.idx_stride = p.idx_stride > 0 ? p.idx_stride : 1;
+    a.src_page_rows = p.src_page_rows;
+    a.src_page_stride = p.src_page_stride;
+    a.dst_page_rows = p.dst_page_rows;
+    a.dst_page_stride = p.dst_page_stride;
     hipError_t err;
     switch (vec) {
       case 16: err = launch_rows_vec<16>(a, n, stream); break;

@@ -2,8 +2,9 @@
 
 Importing this package gives the reference's KV transfer names (paged <->
 linear, merged, FP8 quant-store / dequant-gather, MLA flat rows, DSV4 byte
-rows, LMCache / SGLang-MP converters, layout descriptors) backed by
-hand-written gfx950 HIP kernels in ``_lib/libmusa_aiter_kv_hip.so``.
+rows, LMCache / SGLang-MP converters, SGLang HiCache transfers, layout
+descriptors) backed by hand-written gfx950 HIP kernels in
+``_lib/libmusa_aiter_kv_hip.so``.
 """
 
 from musa_aiter.version import __version__, REFERENCE_API_VERSION
@@ -96,6 +97,22 @@ from musa_aiter.ops.lmcache_kv_transfer import (
     lmcache_paged_to_kv_buffer,
     lmcache_paged_to_kv_buffer_mla,
     native_lmcache_kv_transfer_abi_version,
+)
+from musa_aiter.ops.hicache_transfer import (
+    build_native_hicache_transfer,
+    hicache_transfer_kv_all_layer,
+    hicache_transfer_kv_all_layer_direct_lf_pf,
+    hicache_transfer_kv_all_layer_lf_pf,
+    hicache_transfer_kv_all_layer_mla,
+    hicache_transfer_kv_all_layer_mla_lf_pf,
+    hicache_transfer_kv_direct,
+    hicache_transfer_kv_per_layer,
+    hicache_transfer_kv_per_layer_direct_pf_lf,
+    hicache_transfer_kv_per_layer_mla,
+    hicache_transfer_kv_per_layer_mla_pf_lf,
+    hicache_transfer_kv_per_layer_pf_lf,
+    is_native_hicache_transfer_available,
+    native_hicache_transfer_abi_version,
 )
 
 list_capabilities = registry.list_capabilities

@@ -51,6 +51,16 @@ _SIGNATURES: dict[str, list] = {
         _i64, _i64, _i64,                        # row_bytes, src_stride, dst_stride
         _i32, _i32, _c_void_p,                   # zero_invalid, dedupe, stream
     ],
+    "musa_aiter_hip_copy_rows_paged": [
+        _u64p, _u64p, _i64,                      # host planes, planes
+        _c_void_p, _c_void_p, _i64,              # src_idx, dst_idx, tokens
+        _i64, _i64, _i64, _i64, _i64,            # src_rows, dst_rows, row_bytes, src_stride, dst_stride
+        _i64, _i64, _i64, _i64,                  # src page rows / stride, dst page rows / stride
+        _i32, _c_void_p,                         # dedupe, stream
+    ],
+    # (src_k, dst_k, src_v, dst_v, src_indices, dst_indices, items, start_layer, layers, item_bytes,
+    #  src_page_stride, src_layer_stride, dst_page_stride, dst_layer_stride, stream)
+    "musa_aiter_hicache_transfer_bytes": [_c_void_p] * 6 + [_i64] * 8 + [_c_void_p],
     "lmcache_kv_strided_block_transfer": [
         _c_void_p, _u64p, _c_void_p,
         _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
@@ -68,6 +78,7 @@ _SIGNATURES: dict[str, list] = {
     "native_lmcache_kv_transfer_abi_version": [],
     "musa_aiter_fp8_kv_cache_abi_version": [],
     "musa_aiter_dsv4_kv_copy_abi_version": [],
+    "musa_aiter_hicache_transfer_abi_version": [],
 }
 
 _lock = threading.Lock()
@@ -283,6 +294,43 @@ def csr_dense_rows(
             ptr(key_cache), ptr(value_cache), ptr(kv_indptr), ptr(kv_indices), ptr(out_k), ptr(out_v),
             int(batch), int(dense_len), int(kv_indices.numel()), int(num_tokens), int(row_bytes),
             stream_ptr(device),
+        )
+    check(rc, op)
+
+
+def copy_rows_paged(
+    *,
+    op: str,
+    device: torch.device,
+    src_planes,
+    dst_planes,
+    src_idx: torch.Tensor,
+    dst_idx: torch.Tensor,
+    src_rows: int,
+    dst_rows: int,
+    row_bytes: int,
+    src_stride: int,
+    dst_stride: int,
+    src_page_rows: int = 0,
+    src_page_stride: int = 0,
+    dst_page_rows: int = 0,
+    dst_page_stride: int = 0,
+    dedupe: bool = True,
+) -> None:
+    """Rows between two index-addressed plane sets; `src_idx` / `dst_idx` are contiguous int64
+    device tensors of one length, the plane lists hold device base addresses."""
+    tokens = int(src_idx.numel())
+    planes = len(src_planes)
+    if tokens <= 0 or planes <= 0 or row_bytes <= 0:
+        return
+    if len(dst_planes) != planes:
+        raise ValueError(f"{op}: source and destination plane lists differ in length")
+    with torch.cuda.device(device):
+        rc = fn("musa_aiter_hip_copy_rows_paged")(
+            u64_array(src_planes), u64_array(dst_planes), planes, ptr(src_idx), ptr(dst_idx), tokens,
+            int(src_rows), int(dst_rows), int(row_bytes), int(src_stride), int(dst_stride),
+            int(src_page_rows), int(src_page_stride), int(dst_page_rows), int(dst_page_stride),
+            int(bool(dedupe)), stream_ptr(device),
         )
     check(rc, op)
 

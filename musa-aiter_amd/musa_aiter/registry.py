@@ -128,3 +128,24 @@ _kv("lmcache_mla_buffer_to_paged", "hip-native", _FLOAT, "LMCache [1, NL, T, D] 
 _kv("lmcache_mla_paged_to_buffer", "hip-native", _FLOAT, "Per-layer MLA list caches -> LMCache [1, NL, T, D] buffer.")
 _kv("lmcache_kv_strided_block_transfer", "hip-native", ("uint8",),
     "Block-granular byte copy between an LMCache staging object and padded per-layer pages (modes 0 and 1).")
+# SGLang HiCache layer-first / page-first transfers (any element type: items are byte rows).
+_HICACHE = ("float32", "float16", "bfloat16", "uint8")
+_kv("hicache_transfer_kv_per_layer", "hip-native", _HICACHE,
+    "SGLang HiCache per-layer layer-first transfer with two index tables.")
+_kv("hicache_transfer_kv_per_layer_pf_lf", "hip-native", _HICACHE,
+    "SGLang HiCache per-layer page-first -> layer-first transfer.")
+_kv("hicache_transfer_kv_all_layer", "hip-native", _HICACHE, "SGLang HiCache all-layer layer-first transfer, one launch.")
+_kv("hicache_transfer_kv_all_layer_lf_pf", "hip-native", _HICACHE,
+    "SGLang HiCache all-layer layer-first -> page-first transfer, one launch.")
+_kv("hicache_transfer_kv_per_layer_mla", "hip-native", _HICACHE, "SGLang HiCache per-layer MLA layer-first transfer.")
+_kv("hicache_transfer_kv_per_layer_mla_pf_lf", "hip-native", _HICACHE,
+    "SGLang HiCache per-layer MLA page-first -> layer-first transfer.")
+_kv("hicache_transfer_kv_all_layer_mla", "hip-native", _HICACHE, "SGLang HiCache all-layer MLA layer-first transfer.")
+_kv("hicache_transfer_kv_all_layer_mla_lf_pf", "hip-native", _HICACHE,
+    "SGLang HiCache all-layer MLA layer-first -> page-first transfer.")
+_kv("hicache_transfer_kv_direct", "hip-native", _HICACHE,
+    "SGLang direct HiCache token-range copy over per-layer tensors, one launch.")
+_kv("hicache_transfer_kv_per_layer_direct_pf_lf", "hip-native", _HICACHE,
+    "SGLang direct HiCache page-first pages -> one layer-first layer.")
+_kv("hicache_transfer_kv_all_layer_direct_lf_pf", "hip-native", _HICACHE,
+    "SGLang direct HiCache layer-first rows -> all-layer page-first pages, one launch.")

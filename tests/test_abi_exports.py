@@ -37,13 +37,15 @@ def _declared_symbols() -> set[str]:
 
 def test_header_declares_expected_families():
     names = _declared_symbols()
-    assert len(names) == 103
+    assert len(names) == 106
     for required in ("musa_aiter_kv_load_and_reshape_flash_half", "musa_aiter_kv_triton_indexed_to_dense_bfloat16",
                      "musa_aiter_kv_reshape_and_cache_back_flash_float", "musa_aiter_kv_copy_paged_blocks_fp8_vec8",
                      "musa_aiter_hip_paged_dense_tiles","musa_aiter_kv_paged_to_linear_bfloat16", "musa_aiter_kv_linear_to_paged_multi_layer_half",
                      "musa_aiter_kv_paged_fp8_to_linear_vec4_e5m2", "lmcache_paged_to_kv_buffer_two_x_nl_coalesced_u16",
                      "lmcache_mla_paged_to_buffer_list_bfloat16", "musa_aiter_kv_copy_paged_rows_layer_table_u8",
-                     "lmcache_kv_strided_block_transfer", "musa_aiter_hip_paged_tiles"):
+                     "lmcache_kv_strided_block_transfer", "musa_aiter_hip_paged_tiles",
+                     "musa_aiter_hicache_transfer_bytes", "musa_aiter_hicache_transfer_abi_version",
+                     "musa_aiter_hip_copy_rows_paged"):
         assert required in names
 
 
@@ -56,7 +58,8 @@ def test_library_exports_every_declared_symbol():
 def test_probes_callable_without_gpu():
     lib = ctypes.CDLL(str(_hip.LIB_PATH))
     for name in ("musa_aiter_kv_transfer_abi_version", "native_lmcache_kv_transfer_abi_version",
-                 "musa_aiter_fp8_kv_cache_abi_version", "musa_aiter_dsv4_kv_copy_abi_version"):
+                 "musa_aiter_fp8_kv_cache_abi_version", "musa_aiter_dsv4_kv_copy_abi_version",
+                 "musa_aiter_hicache_transfer_abi_version"):
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int
         assert fn() == 1

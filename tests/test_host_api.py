@@ -140,6 +140,11 @@ def test_kvcache_registry_rows_and_backend():
         "lmcache_kv_buffer_to_paged_two_x_nl", "lmcache_kv_paged_to_buffer", "lmcache_kv_buffer_to_paged",
         "lmcache_paged_to_kv_buffer", "lmcache_kv_buffer_to_paged_mla", "lmcache_paged_to_kv_buffer_mla",
         "lmcache_mla_buffer_to_paged", "lmcache_mla_paged_to_buffer", "lmcache_kv_strided_block_transfer",
+        "hicache_transfer_kv_per_layer", "hicache_transfer_kv_per_layer_pf_lf", "hicache_transfer_kv_all_layer",
+        "hicache_transfer_kv_all_layer_lf_pf", "hicache_transfer_kv_per_layer_mla",
+        "hicache_transfer_kv_per_layer_mla_pf_lf", "hicache_transfer_kv_all_layer_mla",
+        "hicache_transfer_kv_all_layer_mla_lf_pf", "hicache_transfer_kv_direct",
+        "hicache_transfer_kv_per_layer_direct_pf_lf", "hicache_transfer_kv_all_layer_direct_lf_pf",
     }
     for cap in caps:
         assert cap.backends == ("rocm-hip",)
@@ -206,6 +211,8 @@ def test_abi_version_probes():
     assert musa_aiter.native_lmcache_kv_transfer_abi_version() == 1
     assert musa_aiter.native_kv_transfer_abi_version() == 1
     assert musa_aiter.native_fp8_kv_cache_abi_version() == 1
+    assert musa_aiter.native_hicache_transfer_abi_version() == 1
+    assert musa_aiter.is_native_hicache_transfer_available() is True
 
 
 def test_dense_preload_validation_contract():
