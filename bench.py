@@ -1,5 +1,6 @@
 #!/usr/bin/env python3
-"""KV-copy throughput on one MI355X: BASELINE.json configs[1] (headline) plus configs 1, 3, 4, 5 and the dense preload.
+"""KV-copy throughput on one MI355X: BASELINE.json configs[1] (headline) plus configs 1, 3, 4, 5, the dense preload
+and the SGLang HiCache transfers.
 
 Headline workload: 32 layers of Llama-3-8B KV caches
 [8192 blocks, 16, 8 kv-heads, 128] bf16 (paged layout [NB, NH, HD, BS]),
@@ -22,7 +23,8 @@ headline workload itself, one layer at a time, on this host.
 
 The other configs are reported under ``extra`` with the same byte convention
 (config 6: the block-table / CSR dense preload for attention and whole-block
-copies, which are not BASELINE configs).  Their launches are short
+copies; config 7: SGLang HiCache layer-first / page-first transfers; neither
+is a BASELINE config).  Their launches are short
 (0.01-0.8 ms), so they are timed in batches of back-to-back launches between
 two events (host launch overhead hidden behind device work); each is also
 checked outside the timed region, by torch indexing, by the reference's FP8
@@ -559,6 +561,113 @@ def bench_dense() -> dict:
     return out
 
 
+def bench_hicache() -> dict:
+    """SGLang HiCache transfers (the next row after the dense preload), Llama-3-8B and DeepSeek shapes.
+
+    Pools of 65536 tokens: the device pool is layer-first [32, tokens, 8*128] bf16 per K and V,
+    the second-tier pool page-first [tokens, 32, 8*128] (both resident in HBM: the reference's path
+    takes device tensors only).  One transfer moves 512 random pages of 64 tokens (32768 token
+    items of 2 KiB) between random page slots of the two pools.  Backup = one all-layer
+    layer-first -> page-first call; load = 32 per-layer page-first -> layer-first calls, as SGLang
+    loads layer by layer.  Both go through the reference-named C symbol
+    musa_aiter_hicache_transfer_bytes.  MLA: 61 layers of 1152-byte latent rows, all-layer
+    layer-first -> page-first.  Direct: the public all-layer direct API (page_size 64) end to end,
+    host validation of the index tables included.  Bytes = items x layers x planes x (read +
+    write) + 16 B of indices per item and launch.
+    """
+    from musa_aiter.ops import _hip
+    import musa_aiter
+
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(1007)
+    layers, pool, page = NL, 65536, 64
+    pages_moved = 512
+    n = pages_moved * page
+    item = ROW * 2
+    j = np.arange(page)
+    dev_tok = (rng.permutation(pool // page)[:pages_moved][:, None] * page + j).reshape(-1)
+    host_tok = (rng.permutation(pool // page)[:pages_moved][:, None] * page + j).reshape(-1)
+    dev_idx = torch.from_numpy(dev_tok.astype(np.int64)).to(dev)
+    host_idx = torch.from_numpy(host_tok.astype(np.int64)).to(dev)
+    gen = torch.Generator(device=dev).manual_seed(7)
+    dk = torch.randn((layers, pool, ROW), generator=gen, device=dev, dtype=torch.bfloat16)
+    dv = torch.randn((layers, pool, ROW), generator=gen, device=dev, dtype=torch.bfloat16)
+    hk = torch.zeros((pool, layers, ROW), device=dev, dtype=torch.bfloat16)
+    hv = torch.zeros_like(hk)
+    lib = _hip.library()
+    xfer = _bind(lib, "musa_aiter_hicache_transfer_bytes", 6, 8)
+    out = {"pool_tokens": pool, "layers": layers, "page_size": page, "items": n, "item_bytes": item}
+
+    lf_stride, lf_layer = item, pool * item          # layer_first [layers, pool, item]
+    pf_stride, pf_layer = layers * item, item        # page_first [pool, layers, item]
+    backup = (dk.data_ptr(), hk.data_ptr(), dv.data_ptr(), hv.data_ptr(), dev_idx.data_ptr(), host_idx.data_ptr(),
+              n, 0, layers, item, lf_stride, lf_layer, pf_stride, pf_layer)
+    _check(xfer(*backup, _stream()), "hicache backup")
+    torch.cuda.synchronize()
+    ok = bool(torch.equal(hk[host_idx].view(torch.int16), dk[:, dev_idx].transpose(0, 1).view(torch.int16))
+              and torch.equal(hv[host_idx].view(torch.int16), dv[:, dev_idx].transpose(0, 1).view(torch.int16)))
+    mb = batched_ms(lambda: _check(xfer(*backup, _stream()), "hicache backup"), launches=5, reps=5)
+    nbytes = 2 * 2 * layers * n * item + 16 * n
+    out["all_layer_lf_pf_backup"] = {**rate(nbytes, mb, n), "bytes_per_call": nbytes, "parity": ok}
+
+    dk2, dv2 = torch.zeros_like(dk), torch.zeros_like(dv)
+
+    def load_all_layers():
+        for layer in range(layers):
+            _check(xfer(hk.data_ptr(), dk2.data_ptr(), hv.data_ptr(), dv2.data_ptr(), host_idx.data_ptr(),
+                        dev_idx.data_ptr(), n, layer, 1, item, pf_stride, pf_layer, lf_stride, lf_layer, _stream()),
+                   "hicache load")
+
+    load_all_layers()
+    torch.cuda.synchronize()
+    okl = bool(torch.equal(dk2[:, dev_idx].view(torch.int16), dk[:, dev_idx].view(torch.int16))
+               and torch.equal(dv2[:, dev_idx].view(torch.int16), dv[:, dev_idx].view(torch.int16)))
+    ml = batched_ms(load_all_layers, launches=2, reps=5)
+    nbytes = 2 * 2 * layers * n * item + 16 * n * layers
+    out["per_layer_pf_lf_load_x32"] = {**rate(nbytes, ml, n), "bytes_per_call": nbytes, "launches": layers,
+                                       "parity": okl, "parity_check": "backup then load restores every moved item"}
+    del dk2, dv2
+
+    # Public direct API: all layers, layer-first per-layer tensors -> page-first [pages, layers, 64, item].
+    src_layers = [dk[layer] for layer in range(layers)] + [dv[layer] for layer in range(layers)]
+    pk = torch.zeros((pool // page, layers, page, ROW), device=dev, dtype=torch.bfloat16)
+    pv = torch.zeros_like(pk)
+
+    def direct():
+        musa_aiter.hicache_transfer_kv_all_layer_direct_lf_pf(src_layers, [pk, pv], dev_idx, host_idx, page)
+
+    direct()
+    torch.cuda.synchronize()
+    okd = bool(torch.equal(pk[host_idx // page, :, host_idx % page].view(torch.int16),
+                           dk[:, dev_idx].transpose(0, 1).view(torch.int16))
+               and torch.equal(pv[host_idx // page, :, host_idx % page].view(torch.int16),
+                               dv[:, dev_idx].transpose(0, 1).view(torch.int16)))
+    md = batched_ms(direct, launches=5, reps=5)
+    nbytes = 2 * 2 * layers * n * item + 16 * n
+    out["all_layer_direct_lf_pf_api"] = {**rate(nbytes, md, n), "bytes_per_call": nbytes, "parity": okd,
+                                         "timed": "public API incl. host-side index validation"}
+    del src_layers, pk, pv, dk, dv, hk, hv
+    torch.cuda.empty_cache()
+
+    # MLA: DeepSeek latent rows (512 + 64 bf16), 61 layers, no value plane.
+    mla_layers, mla_item = 61, 576 * 2
+    mk = torch.randn((mla_layers, pool, 576), generator=gen, device=dev, dtype=torch.bfloat16)
+    mh = torch.zeros((pool, mla_layers, 576), device=dev, dtype=torch.bfloat16)
+    mla = (mk.data_ptr(), mh.data_ptr(), None, None, dev_idx.data_ptr(), host_idx.data_ptr(), n, 0, mla_layers,
+           mla_item, mla_item, pool * mla_item, mla_layers * mla_item, mla_item)
+    _check(xfer(*mla, _stream()), "hicache mla backup")
+    torch.cuda.synchronize()
+    okm = bool(torch.equal(mh[host_idx].view(torch.int16), mk[:, dev_idx].transpose(0, 1).view(torch.int16)))
+    mm = batched_ms(lambda: _check(xfer(*mla, _stream()), "hicache mla backup"), launches=5, reps=5)
+    nbytes = 2 * mla_layers * n * mla_item + 16 * n
+    out["mla_all_layer_lf_pf_backup_61_layers"] = {**rate(nbytes, mm, n), "bytes_per_call": nbytes, "parity": okm}
+    del mk, mh
+    torch.cuda.empty_cache()
+    log("hicache: " + ", ".join(f"{k} {v['gbs']:.0f} GB/s parity {v['parity']}" for k, v in out.items()
+                                if isinstance(v, dict)))
+    return out
+
+
 def device_copy(mib: int, reps: int = 5) -> dict:
     """Plain device-to-device copy of a known size (torch ``copy_``): the achievable copy rate of this
     GPU and the calibration kernel for the FETCH_SIZE / WRITE_SIZE traffic counters."""
@@ -607,9 +716,9 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--configs", default="1,2,3,4,5,6",
+    parser.add_argument("--configs", default="1,2,3,4,5,6,7",
                         help="comma list of BASELINE configs to run (2, the headline, always runs; 6 = dense "
-                             "preload and block copies)")
+                             "preload and block copies; 7 = SGLang HiCache transfers)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--copy-mib", type=int, default=1024,
                         help="size of the plain device copy timed first (0 = skip)")
@@ -640,7 +749,7 @@ def main() -> int:
     torch.cuda.empty_cache()
     runners = {1: ("config1_fp16_single_layer_gather", bench_config1), 3: ("config3_fp8", bench_config3),
                4: ("config4_lmcache_two_x_nl", bench_config4), 5: ("config5_mla_rows", bench_config5),
-               6: ("dense_preload_and_block_copies", bench_dense)}
+               6: ("dense_preload_and_block_copies", bench_dense), 7: ("sglang_hicache_transfers", bench_hicache)}
     for cfg in sorted(configs - {2}):
         if cfg not in runners:
             continue

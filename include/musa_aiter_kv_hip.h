@@ -374,8 +374,8 @@ int lmcache_kv_strided_block_transfer(void* staging, const uint64_t* paged_ptrs,
                                       int64_t row_bytes, int64_t paged_block_stride, int64_t mode,
                                       int64_t value_bytes, int64_t scale_bytes, void* stream);
 
-/* ---- SGLang HiCache layer-first / page-first transfers (binding hicache_transfer.py:57-83,
- * :196-258; replaces hicache_transfer.mu:4-98).  For each item whose two page indices are both
+/* ---- SGLang HiCache layer-first / page-first transfers (binding hicache_transfer.py:59-82,
+ * :190-258; replaces hicache_transfer.mu:4-98).  For each item whose two page indices are both
  * non-negative and each layer in [start_layer, start_layer + num_layers), item_size_bytes
  * (rounded down to whole 64-bit words) move from src + page * src_page_stride + layer *
  * src_layer_stride to the matching destination offset, for K and, when both V pointers are

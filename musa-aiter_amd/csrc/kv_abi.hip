@@ -941,7 +941,7 @@ int lmcache_kv_strided_block_transfer(void* staging, const uint64_t* paged_ptrs,
   return kvhip::launch_strided_blocks(p, as_stream(stream));
 }
 
-// ----- SGLang HiCache transfers (hicache_transfer.mu:53-98, hicache_transfer.py:196-258) ---------
+// ----- SGLang HiCache transfers (hicache_transfer.mu:53-98, hicache_transfer.py:190-258) ---------
 
 int musa_aiter_hicache_transfer_abi_version() { return 1; }
 
