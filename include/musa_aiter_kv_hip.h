@@ -389,6 +389,20 @@ int musa_aiter_hicache_transfer_bytes(const void* src_k, void* dst_k, const void
                                       int64_t src_page_stride_bytes, int64_t src_layer_stride_bytes,
                                       int64_t dst_page_stride_bytes, int64_t dst_layer_stride_bytes, void* stream);
 
+/* ---- LMCache host <-> device batch copies (binding lmcache_musa_batch_copy.py:121-215 through
+ * the extension object of lmcache_musa_batch_copy_ext.py:19-43; replaces
+ * lmcache_musa_batch_copy_ext.cpp:41-277, which wraps musaMemcpyBatchAsync / musaMemcpyAsync).
+ * Copies count byte ranges srcs[i] -> dsts[i] (sizes[i] bytes), all host -> device (direction 0)
+ * or all device -> host (direction 1), on `stream`.  A range whose host side is pinned host memory
+ * mapped for the device goes through one batch-copy kernel launch per 96 ranges; pageable ranges,
+ * and all ranges when use_copy_engines is non-zero (the reference's prefer_overlap_with_compute
+ * hint), go through hipMemcpyAsync on the DMA engines.  Destination ranges must not overlap. The
+ * version probe returns hipRuntimeGetVersion / hipDriverGetVersion. ---- */
+int musa_aiter_hip_batch_copy_abi_version(void);
+int musa_aiter_hip_runtime_versions(int* runtime_version, int* driver_version);
+int musa_aiter_hip_batch_copy(void* const* dsts, const void* const* srcs, const uint64_t* sizes, int64_t count,
+                              int direction, int use_copy_engines, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1013,4 +1013,58 @@ int musa_aiter_hicache_transfer_bytes(const void* src_k, void* dst_k, const void
                                         dst_page_stride_bytes, 0, 0, 0, 0, 0, stream);
 }
 
+// ----- LMCache host <-> device batch copies (lmcache_musa_batch_copy_ext.cpp:41-277) -------------
+
+int musa_aiter_hip_batch_copy_abi_version() { return 1; }
+
+int musa_aiter_hip_runtime_versions(int* runtime_version, int* driver_version) {
+  if (runtime_version == nullptr || driver_version == nullptr) return hipErrorInvalidValue;
+  const hipError_t err = hipRuntimeGetVersion(runtime_version);
+  if (err != hipSuccess) return err;
+  return hipDriverGetVersion(driver_version);
+}
+
+// Byte ranges between pinned or pageable host memory and device memory of the
+// current device, all in one direction (0: host -> device, 1: device -> host),
+// submitted on `stream`.  Ranges whose host side is pinned host memory with a
+// device mapping go through one batch-copy kernel launch per 96 ranges; the
+// others, and every range when use_copy_engines is set (the DMA engines leave
+// the compute units to concurrent kernels), go through hipMemcpyAsync.
+int musa_aiter_hip_batch_copy(void* const* dsts, const void* const* srcs, const uint64_t* sizes, int64_t count,
+                              int direction, int use_copy_engines, void* stream) {
+  if (count <= 0) return hipSuccess;
+  if (dsts == nullptr || srcs == nullptr || sizes == nullptr || (direction != 0 && direction != 1))
+    return hipErrorInvalidValue;
+  const hipMemcpyKind kind = direction == 0 ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
+  std::vector<uint64_t> ks, kd, kn;
+  for (int64_t i = 0; i < count; ++i) {
+    if (sizes[i] == 0) continue;
+    if (dsts[i] == nullptr || srcs[i] == nullptr) return hipErrorInvalidValue;
+    const void* host = direction == 0 ? srcs[i] : dsts[i];
+    uint64_t mapped = 0;
+    bool kernel = false;
+    if (!use_copy_engines) {
+      hipPointerAttribute_t attr{};
+      if (hipPointerGetAttributes(&attr, host) == hipSuccess) {
+        kernel = attr.type == hipMemoryTypeHost && attr.devicePointer != nullptr && attr.hostPointer != nullptr;
+        if (kernel)
+          mapped = reinterpret_cast<uint64_t>(attr.devicePointer) +
+                   (reinterpret_cast<uint64_t>(host) - reinterpret_cast<uint64_t>(attr.hostPointer));
+      } else {
+        (void)hipGetLastError();  // pageable memory: clear the query's error
+      }
+    }
+    if (kernel) {
+      ks.push_back(direction == 0 ? mapped : reinterpret_cast<uint64_t>(srcs[i]));
+      kd.push_back(direction == 0 ? reinterpret_cast<uint64_t>(dsts[i]) : mapped);
+      kn.push_back(sizes[i]);
+    } else {
+      const hipError_t err = hipMemcpyAsync(dsts[i], srcs[i], sizes[i], kind, as_stream(stream));
+      if (err != hipSuccess) return err;
+    }
+  }
+  return kvhip::launch_batch_copy(ks.data(), kd.data(), kn.data(), static_cast<int64_t>(ks.size()),
+                                  as_stream(stream));
+}
+
 }  // extern "C"

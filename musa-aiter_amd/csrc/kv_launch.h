@@ -119,4 +119,12 @@ struct StridedBlockParams {
 
 hipError_t launch_strided_blocks(const StridedBlockParams& p, hipStream_t stream);
 
+// Byte ranges copied by one launch each (count may exceed it: several launches).
+constexpr int kBatchCopyMax = 96;
+
+// Copies `count` byte ranges src[i] -> dst[i] of size[i] bytes, all addresses
+// device-visible (device memory or the device mapping of pinned host memory).
+hipError_t launch_batch_copy(const uint64_t* src, const uint64_t* dst, const uint64_t* size, int64_t count,
+                             hipStream_t stream);
+
 }  // namespace kvhip

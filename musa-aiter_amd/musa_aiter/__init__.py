@@ -2,9 +2,9 @@
 
 Importing this package gives the reference's KV transfer names (paged <->
 linear, merged, FP8 quant-store / dequant-gather, MLA flat rows, DSV4 byte
-rows, LMCache / SGLang-MP converters, SGLang HiCache transfers, layout
-descriptors) backed by hand-written gfx950 HIP kernels in
-``_lib/libmusa_aiter_kv_hip.so``.
+rows, LMCache / SGLang-MP converters, LMCache host <-> device copy batches,
+SGLang HiCache transfers, layout descriptors) backed by hand-written gfx950 HIP
+kernels in ``_lib/libmusa_aiter_kv_hip.so``.
 """
 
 from musa_aiter.version import __version__, REFERENCE_API_VERSION
@@ -97,6 +97,12 @@ from musa_aiter.ops.lmcache_kv_transfer import (
     lmcache_paged_to_kv_buffer,
     lmcache_paged_to_kv_buffer_mla,
     native_lmcache_kv_transfer_abi_version,
+)
+from musa_aiter.ops.lmcache_musa_batch_copy import (
+    is_native_lmcache_musa_batch_copy_available,
+    lmcache_musa_memcpy_batch_async,
+    native_lmcache_musa_batch_copy_abi_version,
+    native_lmcache_musa_batch_copy_runtime_versions,
 )
 from musa_aiter.ops.hicache_transfer import (
     build_native_hicache_transfer,

@@ -3,7 +3,9 @@
 Priority: a specialized native kernel, then a fused native kernel, then a
 direct batch copy for direct-eligible plans, then (unless native is
 required) the reference fallback.  ``hip_capabilities`` reports what this
-package provides: the gfx950 kernels are the specialized native backend.
+package provides: the gfx950 kernels are the specialized native backend and
+the batch-copy kernel (``lmcache_musa_memcpy_batch_async``) the direct batch
+backend.
 """
 
 from __future__ import annotations
@@ -43,7 +45,7 @@ def hip_capabilities() -> KVBackendCapabilities:
     from . import _hip
 
     available = _hip.is_available()
-    return KVBackendCapabilities(specialized_native=available, fused_native=available, direct_batch=False,
+    return KVBackendCapabilities(specialized_native=available, fused_native=available, direct_batch=available,
                                  reference=False)
 
 

@@ -128,6 +128,9 @@ _kv("lmcache_mla_buffer_to_paged", "hip-native", _FLOAT, "LMCache [1, NL, T, D] 
 _kv("lmcache_mla_paged_to_buffer", "hip-native", _FLOAT, "Per-layer MLA list caches -> LMCache [1, NL, T, D] buffer.")
 _kv("lmcache_kv_strided_block_transfer", "hip-native", ("uint8",),
     "Block-granular byte copy between an LMCache staging object and padded per-layer pages (modes 0 and 1).")
+_kv("lmcache_musa_memcpy_batch_async", "hip-native", ("uint8",),
+    "Opt-in asynchronous host/device byte-copy batch for LMCache direct transfer: one batch-copy kernel launch "
+    "over pinned host memory, or the DMA engines.")
 # SGLang HiCache layer-first / page-first transfers (any element type: items are byte rows).
 _HICACHE = ("float32", "float16", "bfloat16", "uint8")
 _kv("hicache_transfer_kv_per_layer", "hip-native", _HICACHE,
