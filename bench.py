@@ -1,6 +1,6 @@
 #!/usr/bin/env python3
-"""KV-copy throughput on one MI355X: BASELINE.json configs[1] (headline) plus configs 1, 3, 4, 5, the dense preload
-and the SGLang HiCache transfers.
+"""KV-copy throughput on one MI355X: BASELINE.json configs[1] (headline) plus configs 1, 3, 4, 5, the dense preload,
+the SGLang HiCache transfers and the LMCache host <-> device copy batches.
 
 Headline workload: 32 layers of Llama-3-8B KV caches
 [8192 blocks, 16, 8 kv-heads, 128] bf16 (paged layout [NB, NH, HD, BS]),
@@ -23,8 +23,9 @@ headline workload itself, one layer at a time, on this host.
 
 The other configs are reported under ``extra`` with the same byte convention
 (config 6: the block-table / CSR dense preload for attention and whole-block
-copies; config 7: SGLang HiCache layer-first / page-first transfers; neither
-is a BASELINE config).  Their launches are short
+copies; config 7: SGLang HiCache layer-first / page-first transfers; config 8:
+LMCache host <-> device copy batches, rated against the 64 GB/s PCIe 5.0 x16
+link instead of HBM; none is a BASELINE config).  Their launches are short
 (0.01-0.8 ms), so they are timed in batches of back-to-back launches between
 two events (host launch overhead hidden behind device work); each is also
 checked outside the timed region, by torch indexing, by the reference's FP8
@@ -50,6 +51,7 @@ sys.path.insert(0, os.path.join(ROOT, "musa-aiter_amd"))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+HOST_LINK_GBS = 64.0  # PCIe 5.0 x16, per direction
 METRIC = "KV copy HBM GB/s & % of 8 TB/s peak, paged↔linear/FP8, 1 MI355X"
 NL, NB, BS, NH, HD = 32, 8192, 16, 8, 128
 ROW = NH * HD  # elements per K or V token row
@@ -668,6 +670,79 @@ def bench_hicache() -> dict:
     return out
 
 
+def bench_batch_copy() -> dict:
+    """LMCache host <-> device copy batches (the staging step), through the C entry musa_aiter_hip_batch_copy.
+
+    Offload-sized batch: 16 chunks of 256 tokens x 32 layers x K/V, one 512 KiB range (256 x 2 KiB rows)
+    per (chunk, layer, K/V): 1024 ranges, 512 MiB, between pinned host memory and HBM.  Small-range
+    batch: 4096 ranges of 4 KiB.  Each direction runs through the batch-copy kernel (pinned host
+    memory read or written by the GPU over the host link) on at most 64 workgroups and on at most 16
+    (the prefer_overlap_with_compute form), and through one hipMemcpyAsync per range;
+    a single torch copy of one contiguous pinned buffer of the same total size gives the runtime's
+    own rate.  Bytes = bytes moved across the host link (each byte once).
+    """
+    from musa_aiter.ops import _hip
+
+    dev = torch.device("cuda", 0)
+    out = {}
+    fn = _hip.fn("musa_aiter_hip_batch_copy")
+
+    def link_rate(total: int, ms: np.ndarray) -> dict:
+        r = rate(total, ms)
+        r.pop("pct_of_peak")
+        r["pct_of_host_link"] = round(100.0 * r["gbs"] / HOST_LINK_GBS, 2)
+        return r
+
+    def run(ranges: int, size: int, label: str) -> None:
+        total = ranges * size
+        ref = torch.randint(0, 256, (total,), dtype=torch.uint8, generator=torch.Generator().manual_seed(8))
+        host = torch.empty(total, dtype=torch.uint8).pin_memory()
+        gpu = torch.empty(total, dtype=torch.uint8, device=dev)
+        # Host range i <-> device range perm[i]: the device side is shuffled.
+        perm = np.random.default_rng(1008).permutation(ranges)
+        perm_d = torch.from_numpy(perm).to(dev)
+        shuffled = torch.empty_like(gpu)
+        shuffled.view(ranges, size)[perm_d] = ref.to(dev).view(ranges, size)
+        hp = [host.data_ptr() + i * size for i in range(ranges)]
+        gp = [gpu.data_ptr() + int(perm[i]) * size for i in range(ranges)]
+        sizes = (ctypes.c_uint64 * ranges)(*([size] * ranges))
+        arrays = {"h2d": ((ctypes.c_void_p * ranges)(*gp), (ctypes.c_void_p * ranges)(*hp), 0),
+                  "d2h": ((ctypes.c_void_p * ranges)(*hp), (ctypes.c_void_p * ranges)(*gp), 1)}
+        res = {"ranges": ranges, "range_bytes": size, "bytes": total}
+        for direction, (dsts, srcs, code) in arrays.items():
+            for path, mode in (("kernel", 0), ("kernel_16_workgroups", 1), ("hip_memcpy_per_range", 2)):
+                def call(dsts=dsts, srcs=srcs, code=code, mode=mode):
+                    _check(fn(dsts, srcs, sizes, ranges, code, mode, _stream()), "batch copy")
+
+                if direction == "h2d":
+                    host.copy_(ref)
+                    gpu.zero_()
+                else:
+                    gpu.copy_(shuffled)
+                    host.zero_()
+                torch.cuda.synchronize()
+                call()
+                torch.cuda.synchronize()
+                if direction == "h2d":
+                    ok = bool(torch.equal(gpu, shuffled))
+                else:
+                    ok = bool(torch.equal(host, ref))
+                ms = batched_ms(call, launches=3, reps=3)
+                res[f"{direction}_{path}"] = {**link_rate(total, ms), "parity": ok}
+            dst_t, src_t = (gpu, host) if direction == "h2d" else (host, gpu)
+            ms = batched_ms(lambda: dst_t.copy_(src_t, non_blocking=True), launches=3, reps=3)
+            res[f"{direction}_torch_contiguous_copy"] = link_rate(total, ms)
+        out[label] = res
+        del host, gpu, shuffled
+
+    run(1024, 512 << 10, "offload_1024_x_512KiB")
+    run(4096, 4096, "small_4096_x_4KiB")
+    torch.cuda.empty_cache()
+    log("batch copy: " + ", ".join(f"{k}.{d} {v[d]['gbs']:.1f} GB/s" for k, v in out.items() for d in v
+                                   if isinstance(v[d], dict)))
+    return out
+
+
 def device_copy(mib: int, reps: int = 5) -> dict:
     """Plain device-to-device copy of a known size (torch ``copy_``): the achievable copy rate of this
     GPU and the calibration kernel for the FETCH_SIZE / WRITE_SIZE traffic counters."""
@@ -716,9 +791,10 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--configs", default="1,2,3,4,5,6,7",
+    parser.add_argument("--configs", default="1,2,3,4,5,6,7,8",
                         help="comma list of BASELINE configs to run (2, the headline, always runs; 6 = dense "
-                             "preload and block copies; 7 = SGLang HiCache transfers)")
+                             "preload and block copies; 7 = SGLang HiCache transfers; 8 = LMCache host <-> "
+                             "device copy batches)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--copy-mib", type=int, default=1024,
                         help="size of the plain device copy timed first (0 = skip)")
@@ -749,7 +825,8 @@ def main() -> int:
     torch.cuda.empty_cache()
     runners = {1: ("config1_fp16_single_layer_gather", bench_config1), 3: ("config3_fp8", bench_config3),
                4: ("config4_lmcache_two_x_nl", bench_config4), 5: ("config5_mla_rows", bench_config5),
-               6: ("dense_preload_and_block_copies", bench_dense), 7: ("sglang_hicache_transfers", bench_hicache)}
+               6: ("dense_preload_and_block_copies", bench_dense), 7: ("sglang_hicache_transfers", bench_hicache),
+               8: ("lmcache_host_device_batches", bench_batch_copy)}
     for cfg in sorted(configs - {2}):
         if cfg not in runners:
             continue

@@ -393,15 +393,17 @@ int musa_aiter_hicache_transfer_bytes(const void* src_k, void* dst_k, const void
  * the extension object of lmcache_musa_batch_copy_ext.py:19-43; replaces
  * lmcache_musa_batch_copy_ext.cpp:41-277, which wraps musaMemcpyBatchAsync / musaMemcpyAsync).
  * Copies count byte ranges srcs[i] -> dsts[i] (sizes[i] bytes), all host -> device (direction 0)
- * or all device -> host (direction 1), on `stream`.  A range whose host side is pinned host memory
- * mapped for the device goes through one batch-copy kernel launch per 96 ranges; pageable ranges,
- * and all ranges when use_copy_engines is non-zero (the reference's prefer_overlap_with_compute
- * hint), go through hipMemcpyAsync on the DMA engines.  Destination ranges must not overlap. The
- * version probe returns hipRuntimeGetVersion / hipDriverGetVersion. ---- */
+ * or all device -> host (direction 1), on `stream`.  mode 0: a range whose host side is pinned host
+ * memory mapped for the device goes through one batch-copy kernel launch per 96 ranges on at most
+ * 64 workgroups; mode 1 (the reference's prefer_overlap_with_compute hint): the same kernel on at
+ * most 16 workgroups, leaving the other compute units to concurrent kernels; pageable
+ * ranges in modes 0 and 1, and every range in mode 2 (the reference's execute_copy_loop), go through
+ * hipMemcpyAsync.  Destination ranges must not overlap.  The version probe returns
+ * hipRuntimeGetVersion / hipDriverGetVersion. ---- */
 int musa_aiter_hip_batch_copy_abi_version(void);
 int musa_aiter_hip_runtime_versions(int* runtime_version, int* driver_version);
 int musa_aiter_hip_batch_copy(void* const* dsts, const void* const* srcs, const uint64_t* sizes, int64_t count,
-                              int direction, int use_copy_engines, void* stream);
+                              int direction, int mode, void* stream);
 
 #ifdef __cplusplus
 }

@@ -2,9 +2,12 @@
 // step on the far side of the KV buffers.
 //
 // One launch moves up to kBatchCopyMax byte ranges.  Every range is cut into
-// 64 KiB tiles, one workgroup per tile (the block finds its range from the
-// tile prefix in the kernel arguments), so a batch of many small chunks costs
-// one launch instead of one runtime call per chunk.  The host side of every
+// 64 KiB tiles; workgroups stride over the tiles (a workgroup finds a tile's
+// range from the tile prefix in the kernel arguments), so a batch of many
+// small chunks costs one launch instead of one runtime call per chunk.  The
+// grid holds at most `max_groups` workgroups: the host link needs far fewer
+// requests in flight than the chip can issue, and a small grid also leaves
+// the other compute units to concurrent kernels.  The host side of every
 // range is pinned host memory addressed through its device mapping, so the
 // loads or stores of that side travel over the host link; the access width is
 // the widest power of two (<= 16 bytes) to which source and destination are
@@ -51,32 +54,34 @@ __device__ __forceinline__ void copy_tile(const uint8_t* s, uint8_t* d, uint32_t
 }
 
 __global__ __launch_bounds__(kBlockThreads) void batch_copy_kernel(const BatchCopyArgs a) {
-  const uint32_t tile = blockIdx.x;
-  // Range of this tile: the first whose inclusive tile prefix exceeds it (uniform per block).
-  int lo = 0, hi = a.count - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    if (a.tile_end[mid] > tile) hi = mid;
-    else lo = mid + 1;
+  const uint32_t tiles = a.tile_end[a.count - 1];
+  for (uint32_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    // Range of this tile: the first whose inclusive tile prefix exceeds it (uniform per block).
+    int lo = 0, hi = a.count - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (a.tile_end[mid] > tile) hi = mid;
+      else lo = mid + 1;
+    }
+    const uint32_t first = lo == 0 ? 0u : a.tile_end[lo - 1];
+    const uint64_t off = static_cast<uint64_t>(tile - first) * kTileBytes;
+    const uint64_t left = a.size[lo] - off;
+    const uint32_t n = static_cast<uint32_t>(left < kTileBytes ? left : kTileBytes);
+    const uint8_t* s = reinterpret_cast<const uint8_t*>(a.src[lo]) + off;
+    uint8_t* d = reinterpret_cast<uint8_t*>(a.dst[lo]) + off;
+    const uint32_t rel = static_cast<uint32_t>((a.src[lo] ^ a.dst[lo]) & 15u);
+    if (rel == 0) copy_tile<16>(s, d, n);
+    else if ((rel & 7u) == 0) copy_tile<8>(s, d, n);
+    else if ((rel & 3u) == 0) copy_tile<4>(s, d, n);
+    else if ((rel & 1u) == 0) copy_tile<2>(s, d, n);
+    else copy_tile<1>(s, d, n);
   }
-  const uint32_t first = lo == 0 ? 0u : a.tile_end[lo - 1];
-  const uint64_t off = static_cast<uint64_t>(tile - first) * kTileBytes;
-  const uint64_t left = a.size[lo] - off;
-  const uint32_t n = static_cast<uint32_t>(left < kTileBytes ? left : kTileBytes);
-  const uint8_t* s = reinterpret_cast<const uint8_t*>(a.src[lo]) + off;
-  uint8_t* d = reinterpret_cast<uint8_t*>(a.dst[lo]) + off;
-  const uint32_t rel = static_cast<uint32_t>((a.src[lo] ^ a.dst[lo]) & 15u);
-  if (rel == 0) copy_tile<16>(s, d, n);
-  else if ((rel & 7u) == 0) copy_tile<8>(s, d, n);
-  else if ((rel & 3u) == 0) copy_tile<4>(s, d, n);
-  else if ((rel & 1u) == 0) copy_tile<2>(s, d, n);
-  else copy_tile<1>(s, d, n);
 }
 
 }  // namespace
 
 hipError_t launch_batch_copy(const uint64_t* src, const uint64_t* dst, const uint64_t* size, int64_t count,
-                             hipStream_t stream) {
+                             uint32_t max_groups, hipStream_t stream) {
   for (int64_t base = 0; base < count; base += kBatchCopyMax) {
     const int64_t n = (count - base) < kBatchCopyMax ? (count - base) : kBatchCopyMax;
     BatchCopyArgs a{};
@@ -95,7 +100,8 @@ hipError_t launch_batch_copy(const uint64_t* src, const uint64_t* dst, const uin
     }
     if (m == 0) continue;
     a.count = m;
-    hipLaunchKernelGGL(batch_copy_kernel, dim3(static_cast<uint32_t>(tiles)), dim3(kBlockThreads), 0, stream, a);
+    const uint32_t groups = (max_groups != 0 && tiles > max_groups) ? max_groups : static_cast<uint32_t>(tiles);
+    hipLaunchKernelGGL(batch_copy_kernel, dim3(groups), dim3(kBlockThreads), 0, stream, a);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }

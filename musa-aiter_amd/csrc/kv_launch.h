@@ -123,8 +123,9 @@ hipError_t launch_strided_blocks(const StridedBlockParams& p, hipStream_t stream
 constexpr int kBatchCopyMax = 96;
 
 // Copies `count` byte ranges src[i] -> dst[i] of size[i] bytes, all addresses
-// device-visible (device memory or the device mapping of pinned host memory).
+// device-visible (device memory or the device mapping of pinned host memory),
+// on at most `max_groups` workgroups per launch (0: one per 64 KiB tile).
 hipError_t launch_batch_copy(const uint64_t* src, const uint64_t* dst, const uint64_t* size, int64_t count,
-                             hipStream_t stream);
+                             uint32_t max_groups, hipStream_t stream);
 
 }  // namespace kvhip

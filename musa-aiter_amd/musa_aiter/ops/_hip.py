@@ -79,7 +79,7 @@ _SIGNATURES: dict[str, list] = {
     "musa_aiter_fp8_kv_cache_abi_version": [],
     "musa_aiter_dsv4_kv_copy_abi_version": [],
     "musa_aiter_hicache_transfer_abi_version": [],
-    # (dsts, srcs, sizes, count, direction 0 h2d / 1 d2h, use_copy_engines, stream)
+    # (dsts, srcs, sizes, count, direction 0 h2d / 1 d2h, mode 0 kernel / 1 kernel on 32 groups / 2 memcpy, stream)
     "musa_aiter_hip_batch_copy": [ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p), _u64p, _i64,
                                   _i32, _i32, _c_void_p],
     "musa_aiter_hip_batch_copy_abi_version": [],

@@ -5,11 +5,14 @@ whose module functions are ``abi_version``, ``runtime_version``, ``driver_versio
 ``batch_memcpy_supported``, ``execute_batch_copy`` and ``execute_copy_loop``
 (``lmcache_musa_batch_copy_ext.cpp:268-277``).  Here the same object is a thin Python layer over
 ``libmusa_aiter_kv_hip.so``: ``execute_batch_copy`` submits the whole batch through the
-batch-copy kernel (pinned host memory) or, with ``prefer_overlap_with_compute``, through the DMA
-engines; ``execute_copy_loop`` always uses the DMA engines.  Both check their arguments like
-the reference's ``prepare_copy`` (``:80-170``, ``RuntimeError``), run on the current stream of
-the GPU endpoint's device and keep every tensor of a batch alive until the stream has passed
-it, which is what the reference's allocator ``record_event`` / ``recordStream`` calls ensure.
+batch-copy kernel (pinned host memory; with ``prefer_overlap_with_compute`` on at most 16
+workgroups instead of 64, so concurrent kernels keep the other compute units);
+``execute_copy_loop`` issues one ``hipMemcpyAsync`` per range, as the reference's loop does
+with ``musaMemcpyAsync``.  Both
+check their arguments like the reference's ``prepare_copy`` (``:80-170``, ``RuntimeError``),
+run on the current stream of the GPU endpoint's device and keep every tensor of a batch alive
+until the stream has passed it, which is what the reference's allocator ``record_event`` /
+``recordStream`` calls ensure.
 
 The extension is opt-in exactly like the reference's: it is returned only when
 ``MUSA_AITER_LMCACHE_BATCH_COPY=1`` or ``LMCACHE_MUSA_DIRECT_COPY=1``.
@@ -147,7 +150,7 @@ class HipBatchCopyExtension:
                 raise RuntimeError("overlapping destination ranges are invalid in an unordered batch")
         return dsts, srcs, lens, bool(to_gpu), device, gpu_tensors, host_tensors
 
-    def _submit(self, destinations, sources, destination_offsets, source_offsets, sizes, engines: bool) -> bool:
+    def _submit(self, destinations, sources, destination_offsets, source_offsets, sizes, mode: int) -> bool:
         dsts, srcs, lens, to_gpu, device, gpu_tensors, host_tensors = self._prepare(
             destinations, sources, destination_offsets, source_offsets, sizes)
         if not lens:
@@ -157,7 +160,7 @@ class HipBatchCopyExtension:
             stream = torch.cuda.current_stream(device)
             rc = _hip.fn("musa_aiter_hip_batch_copy")(
                 (ctypes.c_void_p * n)(*dsts), (ctypes.c_void_p * n)(*srcs), (ctypes.c_uint64 * n)(*lens), n,
-                0 if to_gpu else 1, int(bool(engines)), ctypes.c_void_p(stream.cuda_stream))
+                0 if to_gpu else 1, int(mode), ctypes.c_void_p(stream.cuda_stream))
             _hip.check(int(rc), "lmcache_musa_memcpy_batch_async")
             for t in {id(t): t for t in gpu_tensors}.values():
                 t.record_stream(stream)
@@ -167,10 +170,10 @@ class HipBatchCopyExtension:
     def execute_batch_copy(self, destinations, sources, destination_offsets, source_offsets, sizes,
                            prefer_overlap_with_compute: bool) -> bool:
         return self._submit(destinations, sources, destination_offsets, source_offsets, sizes,
-                            engines=bool(prefer_overlap_with_compute))
+                            mode=1 if prefer_overlap_with_compute else 0)
 
     def execute_copy_loop(self, destinations, sources, destination_offsets, source_offsets, sizes) -> bool:
-        return self._submit(destinations, sources, destination_offsets, source_offsets, sizes, engines=True)
+        return self._submit(destinations, sources, destination_offsets, source_offsets, sizes, mode=2)
 
 
 def load_lmcache_musa_batch_copy_ext() -> Any | None:

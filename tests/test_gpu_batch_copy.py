@@ -1,10 +1,10 @@
 """GPU parity: LMCache host/device copy batches vs oracle/batch_copy_oracle.py, bit-exact.
 
 Restates the reference's native tests (op_tests/test_lmcache_musa_batch_copy_musa.py:21-160) on
-ROCm and adds random batches through both submission paths (the batch-copy kernel over pinned
-host memory and the DMA engines), pageable host memory, every relative alignment of source and
-destination, ranges crossing the kernel's 64 KiB tiles, more ranges than one launch holds, and
-the C-ABI entry called directly.
+ROCm and adds random batches through every submission path (the batch-copy kernel over pinned
+host memory on its normal and its bounded grid, one hipMemcpyAsync per range), pageable host
+memory, every relative alignment of source and destination, ranges crossing the kernel's 64 KiB
+tiles, more ranges than one launch holds, and the C-ABI entry called directly.
 """
 
 from __future__ import annotations
@@ -172,7 +172,34 @@ def test_c_abi_batch_copy_direct_call():
     assert torch.equal(device[4096:34096].cpu(), host[:30000])
     assert not device[34096:].any()
     assert _hip.fn("musa_aiter_hip_batch_copy")(dsts, srcs, sizes, 3, 2, 0, None) != 0
+    assert _hip.fn("musa_aiter_hip_batch_copy")(dsts, srcs, sizes, 3, 0, 3, None) != 0
     assert _hip.fn("musa_aiter_hip_batch_copy_abi_version")() == 1
+
+
+@pytest.mark.parametrize("direction", ["h2d", "d2h"])
+def test_copy_loop_and_bounded_grid_paths(direction):
+    from musa_aiter.ops import lmcache_musa_batch_copy_ext as ext
+
+    extension = ext.load_lmcache_musa_batch_copy_ext()
+    rng = np.random.default_rng(5)
+    count, other = 40, 300_000
+    sizes, dst_off, src_off = _random_batch(rng, count, 200_000, other, count * 200_040)
+    for run in (lambda *a: extension.execute_copy_loop(*a), lambda *a: extension.execute_batch_copy(*a, True)):
+        if direction == "h2d":
+            src = _host(other, seed=6)
+            dst = torch.zeros(count * 200_040, dtype=torch.uint8, device=DEV)
+            src_np = src.numpy()
+        else:
+            src = torch.randint(0, 256, (other,), dtype=torch.uint8, device=DEV)
+            dst = _host(count * 200_040, seed=7)
+            src_np = src.cpu().numpy()
+        want = (dst.cpu().numpy() if direction == "h2d" else dst.numpy()).copy()
+        torch.cuda.synchronize()
+        assert run([dst] * count, [src] * count, dst_off, src_off, sizes)
+        torch.cuda.synchronize()
+        bo.apply_batch([want] * count, [src_np] * count, sizes, dst_off, src_off)
+        got = dst.cpu().numpy() if direction == "h2d" else dst.numpy()
+        assert np.array_equal(got, want)
 
 
 def test_tensors_stay_alive_until_the_stream_passes():
