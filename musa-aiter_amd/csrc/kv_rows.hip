@@ -53,6 +53,7 @@ struct RowArgs {
   int64_t src_page_stride;
   int64_t dst_page_rows;
   int64_t dst_page_stride;
+  int32_t plane_inner;        // 1: one grid over (row, plane, piece), planes inside rows
 };
 
 // Work of one block: kBlockPieces consecutive VEC-byte pieces of the
@@ -98,30 +99,48 @@ __device__ __forceinline__ void resolve_row(const RowArgs& a, int64_t u, int64_t
   }
 }
 
-template <int VEC>
+// INNER = false: plane-major grid (y = plane), rows addressed relative to the
+// plane's bases.  INNER = true: one grid over (row, plane) units with absolute
+// addresses in LDS and both bases 0; its planes always come from the host
+// arrays, whose alignment VEC already covers.
+template <int VEC, bool INNER>
 __global__ __launch_bounds__(kBlockThreads) void row_flat_kernel(const RowArgs a, const int32_t pieces,
                                                                  const float inv_pieces) {
   using V = typename VecType<VEC>::T;
   __shared__ int64_t s_src[kBlockRows];
   __shared__ int64_t s_dst[kBlockRows];
-  const int pp = a.plane_base + static_cast<int>(blockIdx.y);
+  constexpr bool inner = INNER;
+  const int pp = inner ? 0 : a.plane_base + static_cast<int>(blockIdx.y);
   const uint8_t* const sp =
-      reinterpret_cast<const uint8_t*>(a.src_table ? a.src_table[pp] : a.src_planes[pp - a.plane_base]);
-  uint8_t* const dp = reinterpret_cast<uint8_t*>(a.dst_table ? a.dst_table[pp] : a.dst_planes[pp - a.plane_base]);
+      inner ? nullptr
+            : reinterpret_cast<const uint8_t*>(a.src_table ? a.src_table[pp] : a.src_planes[pp - a.plane_base]);
+  uint8_t* const dp =
+      inner ? nullptr : reinterpret_cast<uint8_t*>(a.dst_table ? a.dst_table[pp] : a.dst_planes[pp - a.plane_base]);
   // Plane bases read from device tables may be less aligned than VEC: such a
   // plane is copied byte by byte (uniform branch).
   const bool narrow = VEC > 1 && ((reinterpret_cast<uintptr_t>(sp) | reinterpret_cast<uintptr_t>(dp)) & (VEC - 1));
 
-  // Block range [l0, l0 + kBlockPieces) starts at piece r0 of row u0.
+  // Block range [l0, l0 + kBlockPieces) starts at piece r0 of unit u0 (a row,
+  // or a (row, plane) pair of a plane-inner grid).
   const int64_t l0 = static_cast<int64_t>(blockIdx.x) * kBlockPieces;
   const int64_t u0 = l0 / pieces;
   const int r0 = static_cast<int>(l0 - u0 * pieces);
-  const int64_t total = a.num_rows_out * pieces;
+  const int64_t units = inner ? a.num_rows_out * a.num_planes : a.num_rows_out;
+  const int64_t total = units * pieces;
   const int span = static_cast<int>((total - l0) < kBlockPieces ? (total - l0) : kBlockPieces);
   const int nrows = (r0 + span - 1) / pieces + 1;
   for (int i = static_cast<int>(threadIdx.x); i < nrows; i += kBlockThreads) {
     int64_t so, dof;
-    resolve_row(a, u0 + i, &so, &dof);
+    if constexpr (!inner) {
+      resolve_row(a, u0 + i, &so, &dof);
+    } else {
+      const int64_t unit = u0 + i;
+      const int64_t row = unit / a.num_planes;
+      const int plane = static_cast<int>(unit - row * a.num_planes);
+      resolve_row(a, row, &so, &dof);
+      if (dof != kSkipRow) dof += static_cast<int64_t>(a.dst_planes[plane]);
+      if (so != kZeroRow) so += static_cast<int64_t>(a.src_planes[plane]);
+    }
     s_src[i] = so;
     s_dst[i] = dof;
   }
@@ -264,11 +283,16 @@ template <int VEC>
 hipError_t launch_rows_vec(const RowArgs& a, int64_t planes, hipStream_t stream) {
   const int64_t pieces = a.row_bytes / VEC;
   if (pieces > (int64_t{1} << 22)) return hipErrorInvalidValue;
-  const int64_t blocks = (a.num_rows_out * pieces + kBlockPieces - 1) / kBlockPieces;
+  const int64_t units = a.plane_inner ? a.num_rows_out * planes : a.num_rows_out;
+  const int64_t blocks = (units * pieces + kBlockPieces - 1) / kBlockPieces;
   if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(row_flat_kernel<VEC>, dim3(static_cast<uint32_t>(blocks), static_cast<uint32_t>(planes)),
-                     dim3(kBlockThreads), 0, stream, a, static_cast<int32_t>(pieces),
-                     1.0f / static_cast<float>(pieces));
+  if (a.plane_inner)
+    hipLaunchKernelGGL((row_flat_kernel<VEC, true>), dim3(static_cast<uint32_t>(blocks)), dim3(kBlockThreads), 0,
+                       stream, a, static_cast<int32_t>(pieces), 1.0f / static_cast<float>(pieces));
+  else
+    hipLaunchKernelGGL((row_flat_kernel<VEC, false>),
+                       dim3(static_cast<uint32_t>(blocks), static_cast<uint32_t>(planes)), dim3(kBlockThreads), 0,
+                       stream, a, static_cast<int32_t>(pieces), 1.0f / static_cast<float>(pieces));
   return hipGetLastError();
 }
 
@@ -298,6 +322,23 @@ hipError_t launch_row_copy(const RowCopyParams& p, hipStream_t stream) {
   }
   // Plane bases held in device tables are checked per plane by the kernel.
   const int vec = vec_for(bits);
+
+  // Destination planes closer together than the destination's rows (the
+  // layers of one token in a page-first pool): walk planes inside rows, so a
+  // token's rows of all planes are written together.  Random reads cost less
+  // than random writes on this GPU, so the scattered side moves to the source.
+  bool inner = false;
+  if (!src_host || !dst_host || p.num_planes < 2 || p.dst_page_rows > 0) {
+    inner = false;
+  } else {
+    uint64_t closest = ~uint64_t{0};
+    for (int64_t i = 0; i + 1 < p.num_planes; ++i) {
+      const uint64_t gap = p.dst_planes[i + 1] > p.dst_planes[i] ? p.dst_planes[i + 1] - p.dst_planes[i]
+                                                                  : p.dst_planes[i] - p.dst_planes[i + 1];
+      if (gap < closest) closest = gap;
+    }
+    inner = p.dst_stride > 0 && closest < static_cast<uint64_t>(p.dst_stride);
+  }
 
   for (int64_t base = 0; base < p.num_planes; base += kMaxPlanes) {
     const int64_t n = (p.num_planes - base) < kMaxPlanes ? (p.num_planes - base) : kMaxPlanes;
@@ -332,6 +373,7 @@ hipError_t launch_row_copy(const RowCopyParams& p, hipStream_t stream) {
     a.src_page_stride = p.src_page_stride;
     a.dst_page_rows = p.dst_page_rows;
     a.dst_page_stride = p.dst_page_stride;
+    a.plane_inner = inner ? 1 : 0;
     hipError_t err;
     switch (vec) {
       case 16: err = launch_rows_vec<16>(a, n, stream); break;
