@@ -377,6 +377,17 @@ def _validate_direct_tensor_lists(src_layers: list[torch.Tensor], dst_layers: li
             raise ValueError("HiCache direct tensors must be contiguous")
 
 
+def _require_one_rocm_device(op: str, tensors) -> torch.device:
+    """The one ROCm device every tensor of a direct transfer lives on (all layers and planes go in one
+    launch there, so tensors on other devices are rejected instead of copied across devices)."""
+    tensors = list(tensors)
+    _require_rocm(op, *tensors)
+    devices = {t.device for t in tensors}
+    if len(devices) != 1:
+        raise ValueError(f"{op}: all HiCache direct tensors must be on one device (got {sorted(map(str, devices))})")
+    return tensors[0].device
+
+
 def _emit_direct(operation: str, tensor: torch.Tensor, reason: str) -> None:
     device, dtype = tensor_device_dtype(tensor)
     emit(DispatchRecord(operation, BACKEND, device, dtype, reason))
@@ -495,8 +506,7 @@ def hicache_transfer_kv_direct(
         if src_max >= int(src.shape[0]) or dst_max >= int(dst.shape[0]):
             raise ValueError("HiCache direct token range exceeds source or destination")
     if src_values.shape[0] > 0:
-        _require_rocm(op, *src_layers, *dst_layers)
-        device = dst_layers[0].device
+        device = _require_one_rocm_device(op, [*dst_layers, *src_layers])
         src_idx, dst_idx = _token_tables(src_indices, dst_indices, src_tokens, dst_tokens, device)
         pairs = []
         for src, dst in zip(src_layers, dst_layers):
@@ -560,8 +570,7 @@ def hicache_transfer_kv_per_layer_direct_pf_lf(
         pairs.append((src.data_ptr() + layer_id * page_rows * row, dst.data_ptr(), row, src_side, _Side(row),
                       pages * page_size, int(dst.shape[0])))
     if starts.shape[0] > 0:
-        _require_rocm(op, *src_ptrs, *dst_ptrs)
-        device = dst_ptrs[0].device
+        device = _require_one_rocm_device(op, [*dst_ptrs, *src_ptrs])
         if _page_groups_regular(src_values, dst_values, page_size, src_page * page_size, dst_start):
             src_tokens = dst_tokens = None
         else:
@@ -651,8 +660,7 @@ def hicache_transfer_kv_all_layer_direct_lf_pf(
                     f"{page_size} source rows do not broadcast to")
 
     if starts.shape[0] > 0:
-        _require_rocm(op, *src_ptrs, *dst_ptrs)
-        device = dst_ptrs[0].device
+        device = _require_one_rocm_device(op, [*dst_ptrs, *src_ptrs])
         page_rows = int(dst_ptrs[0].shape[2])
         if not is_mla and int(dst_ptrs[1].shape[2]) != page_rows:
             raise ValueError("HiCache all-layer direct K and V destinations must use one page size")

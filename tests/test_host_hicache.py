@@ -336,3 +336,11 @@ def test_all_layer_direct_host_logic_matches_oracle(emulate, kind, page_size, pa
     ho.all_layer_direct_lf_pf([s.numpy() for s in src], want, src_t, dst_t, page_size)
     for d, w in zip(dst, want):
         assert np.array_equal(d.numpy(), w)
+
+
+def test_direct_tensors_must_share_one_device(monkeypatch):
+    # All layers and planes of a direct transfer go in one launch on one device.
+    monkeypatch.setattr(hc, "_require_rocm", lambda *args, **kwargs: None)
+    with pytest.raises(ValueError, match="one device"):
+        hc._require_one_rocm_device("op", [torch.zeros(2), torch.zeros(2, device="meta")])
+    assert hc._require_one_rocm_device("op", [torch.zeros(2), torch.zeros(3)]) == torch.device("cpu")
