@@ -345,3 +345,13 @@ def test_direct_reference_native_cases():
     assert torch.equal(dst_tokens[:, 2:4], src_tokens[:, 0:2])
     assert torch.equal(dst_lf[1, 2:4], src_pf[0, 1])
     assert torch.equal(dst_pf[1], src_tokens[:, 0:2])
+
+
+@pytest.mark.parametrize("name,layers", [("hicache_transfer_kv_all_layer_lf_pf", 70),
+                                         ("hicache_transfer_kv_all_layer_mla_lf_pf", 131),
+                                         ("hicache_transfer_kv_all_layer", 70)])
+@pytest.mark.parametrize("kind", ["skips", "duplicates"])
+def test_more_planes_than_one_launch_holds(name, layers, kind):
+    # More than 128 (layer, K/V) planes: the row kernel splits the planes over launches (plane-inner
+    # grids for page-first destinations, plane-major otherwise).
+    _run_layout(name, torch.bfloat16, 40, kind, layers=layers, src_pages=13, dst_pages=17, n=11, seed=layers)
