@@ -169,14 +169,17 @@ def _validate_page_indices(
     dst = dst_indices.to(device=device, dtype=torch.long).contiguous()
     if src.numel() == 0:
         return src, dst
+    # Common case in one host read: both tables' extremes inside [-1, pages).
+    (s_lo, s_hi), (d_lo, d_hi) = torch.stack([torch.stack(torch.aminmax(src)), torch.stack(torch.aminmax(dst))]).tolist()
+    if s_lo >= -1 and d_lo >= -1 and s_hi < src_pages and d_hi < dst_pages:
+        return src, dst
+    # Some pair is invalid: the first one in table order decides the message.
     negative = (src < -1) | (dst < -1)
     bad = negative | (src >= src_pages) | (dst >= dst_pages)
-    if bool(bad.any()):
-        first = int(bad.nonzero()[0, 0])
-        if bool(negative[first]):
-            raise ValueError("HiCache page indices must be -1 or non-negative")
-        raise ValueError("HiCache page index is out of range")
-    return src, dst
+    first = int(bad.nonzero()[0, 0])
+    if bool(negative[first]):
+        raise ValueError("HiCache page indices must be -1 or non-negative")
+    raise ValueError("HiCache page index is out of range")
 
 
 def _transfer(
@@ -203,11 +206,12 @@ def _transfer(
     planes = [(src_k, dst_k)] if src_v is None else [(src_k, dst_k), (src_v, dst_v)]
     _require_rocm("hicache_transfer", *(t for pair in planes for t in pair))
     layers = range(start_layer, start_layer + num_layers)
+    bases = [(s.data_ptr(), d.data_ptr()) for s, d in planes]
     _hip.copy_rows_paged(
         op="hicache_transfer",
         device=dst_k.device,
-        src_planes=[s.data_ptr() + layer * src_geometry[4] for s, _ in planes for layer in layers],
-        dst_planes=[d.data_ptr() + layer * dst_geometry[4] for _, d in planes for layer in layers],
+        src_planes=[s + layer * src_geometry[4] for s, _ in bases for layer in layers],
+        dst_planes=[d + layer * dst_geometry[4] for _, d in bases for layer in layers],
         src_idx=src_idx,
         dst_idx=dst_idx,
         src_rows=src_geometry[1],

@@ -166,7 +166,7 @@ def _validate_two_x_nl_contract(memory_tensor: torch.Tensor, kvcaches: list[list
         raise ValueError(f"{name} num_blocks must be positive")
     for kv_axis, layers in enumerate(kvcaches):
         for layer, cache in enumerate(layers):
-            if not isinstance(cache, torch.Tensor) or tuple(cache.shape) != expected:
+            if not isinstance(cache, torch.Tensor) or cache.shape != expected:
                 raise ValueError(f"{name} cache[{kv_axis}][{layer}] must have shape {expected}")
             if cache.dtype != memory_tensor.dtype:
                 raise ValueError(f"{name} cache dtype must match memory_tensor")
@@ -262,10 +262,14 @@ class _Buffer:
         else:
             self.work = t.contiguous()
         self.elt = t.element_size()
+        # Read once: plane() runs for every (axis, layer) of every call.
+        w = self.work
+        self._base = w.data_ptr()
+        self._axis_bytes = w.stride(0) * self.elt
+        self._layer_bytes = w.stride(1) * self.elt
 
     def plane(self, axis: int, layer: int) -> int:
-        w = self.work
-        return w.data_ptr() + (axis * w.stride(0) + layer * w.stride(1)) * self.elt
+        return self._base + axis * self._axis_bytes + layer * self._layer_bytes
 
     @property
     def token_stride_bytes(self) -> int:
@@ -317,10 +321,11 @@ def lmcache_kv_buffer_to_paged_two_x_nl(memory_tensor: torch.Tensor, kvcaches: l
     start = time.perf_counter()
     device = memory_tensor.device
     caches = kvcaches[0] + kvcaches[1]
-    _same_device(op, device, slot_mapping, *caches)
+    # The contract has checked every cache's dtype and device against memory_tensor.
+    _same_device(op, device, slot_mapping)
     num_layers = len(kvcaches[0])
     num_tokens = int(slot_mapping.numel())
-    elt = _elt(op, memory_tensor, *caches)
+    elt = _elt(op, memory_tensor)
     row = num_heads * head_size * elt
     buf = _Buffer(memory_tensor, writable=False, initialise=False)
     planes = [(a, l) for a in range(2) for l in range(num_layers)]
@@ -342,10 +347,11 @@ def lmcache_kv_paged_to_buffer_two_x_nl(kvcaches: list[list[torch.Tensor]], memo
     start = time.perf_counter()
     device = memory_tensor.device
     caches = kvcaches[0] + kvcaches[1]
-    _same_device(op, device, slot_mapping, *caches)
+    # The contract has checked every cache's dtype and device against memory_tensor.
+    _same_device(op, device, slot_mapping)
     num_layers = len(kvcaches[0])
     num_tokens = int(slot_mapping.numel())
-    elt = _elt(op, memory_tensor, *caches)
+    elt = _elt(op, memory_tensor)
     row = num_heads * head_size * elt
     buf = _Buffer(memory_tensor, writable=True, initialise=False)
     planes = [(a, l) for a in range(2) for l in range(num_layers)]
