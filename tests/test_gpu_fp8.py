@@ -243,3 +243,27 @@ def test_quant_store_bf16_tiny_inputs_scale_window_edges(fmt, bs):
     got_k, got_v = kc_d.cpu().numpy(), vc_d.cpu().numpy()
     assert np.array_equal(got_k, want_k), np.argwhere(got_k != want_k)[:5]
     assert np.array_equal(got_v, want_v), np.argwhere(got_v != want_v)[:5]
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("lin", ["bfloat16", "float16"])
+def test_quant_store_matches_reference_golden_codes(fmt, lin):
+    # Every 16-bit pattern under each scale of tests/golden/fp8_codec_golden.npz (the reference's own
+    # encoder outputs): token t, head h, dim d holds flat index k = t*1024 + h*128 + d, i.e. the int16
+    # value k - 32768, whose bit pattern is k ^ 0x8000.
+    import os
+
+    golden = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "fp8_codec_golden.npz"))
+    table = golden[f"encode_{fmt}_{'bf16' if lin == 'bfloat16' else 'fp16'}"]
+    x = _all_patterns(LIN_DTYPES[lin]).to(DEV)
+    tokens = x.shape[0]
+    slots = torch.arange(tokens, dtype=torch.int64, device=DEV)
+    nb = tokens // BS
+    flat = np.arange(tokens * NH * HD)
+    for i, s in enumerate(golden["scales"]):
+        kc = torch.zeros(nb, NH, HD, BS, dtype=torch.uint8, device=DEV)
+        vc = torch.zeros_like(kc)
+        scale = torch.tensor(float(s), dtype=torch.float32, device=DEV)
+        musa_aiter.kv_linear_to_paged_fp8(x, x, kc, vc, slots, scale, scale, fp8_format=fmt)
+        got = kc.permute(0, 3, 1, 2).reshape(-1).cpu().numpy()   # slot-major = token-major rows
+        assert np.array_equal(got, table[i][flat ^ 0x8000]), float(s)

@@ -15,10 +15,15 @@ a set of scales:
    reference uses: log2, floor, pow, round), which pins numpy-vs-torch
    differences in those primitives (log2 rounding near powers of two);
 4. decoding against torch's float8 -> float32 casts for every normal code and
-   known answers for the codes torch treats as NaN/Inf.
+   known answers for the codes torch treats as NaN/Inf;
+5. the reference's own encoder and decoder: tests/golden/fp8_codec_golden.npz holds their
+   outputs for every bf16 and fp16 pattern and every code under eight scales, written in this
+   build container by tests/golden/make_fp8_golden.py.
 """
 
 from __future__ import annotations
+
+import os
 
 import numpy as np
 import pytest
@@ -197,3 +202,33 @@ def test_torch_decode_table_matches_oracle_on_every_code(fmt):
         want = ko.fp8_dequantize_f32(codes, np.float32(scale), fmt)
         assert np.array_equal(mine.view(np.uint32), want.view(np.uint32))
     assert torch_ref.FP8_FORMATS[fmt] == ko.FP8_FORMATS[fmt]
+
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "fp8_codec_golden.npz")
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("source", ["bf16", "fp16"])
+def test_encoder_matches_reference_golden_table(fmt, source):
+    golden = np.load(GOLDEN)
+    x = _all_bf16_as_f32() if source == "bf16" else _all_f16_as_f32()
+    table = golden[f"encode_{fmt}_{source}"]
+    for i, s in enumerate(golden["scales"]):
+        want = table[i]
+        got = ko.fp8_quantize(x, s, fmt)
+        assert np.array_equal(got, want), (float(s), np.flatnonzero(got != want)[:5])
+        via_torch = torch_ref.fp8_quantize(torch.from_numpy(x), torch.tensor(float(s), dtype=torch.float32), fmt)
+        assert np.array_equal(via_torch.numpy(), want), float(s)
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_decoder_matches_reference_golden_table(fmt):
+    golden = np.load(GOLDEN)
+    codes = np.arange(256, dtype=np.uint8)
+    for i, s in enumerate(golden["scales"]):
+        f32 = ko.fp8_dequantize_f32(codes, s, fmt)
+        assert np.array_equal(f32.view(np.uint32), golden[f"decode_{fmt}_f32"][i])
+        assert np.array_equal(ko.f32_to_bf16_bits(f32), golden[f"decode_{fmt}_bf16"][i])
+        with np.errstate(over="ignore"):  # values beyond fp16's range round to +-Inf, as torch's cast does
+            f16 = f32.astype(np.float16)
+        assert np.array_equal(f16.view(np.uint16), golden[f"decode_{fmt}_fp16"][i])
