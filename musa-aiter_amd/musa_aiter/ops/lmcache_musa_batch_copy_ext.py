@@ -9,7 +9,7 @@ batch-copy kernel (pinned host memory; with ``prefer_overlap_with_compute`` on a
 workgroups instead of 64, so concurrent kernels keep the other compute units);
 ``execute_copy_loop`` issues one ``hipMemcpyAsync`` per range, as the reference's loop does
 with ``musaMemcpyAsync``.  Both
-check their arguments like the reference's ``prepare_copy`` (``:80-170``, ``RuntimeError``),
+check their arguments like the reference's ``prepare_copy`` (``:76-170``, ``RuntimeError``),
 run on the current stream of the GPU endpoint's device and keep every tensor of a batch alive
 until the stream has passed it, which is what the reference's allocator ``record_event`` /
 ``recordStream`` calls ensure.
@@ -100,7 +100,7 @@ class HipBatchCopyExtension:
     @staticmethod
     def _prepare(destinations: Sequence[torch.Tensor], sources: Sequence[torch.Tensor],
                  destination_offsets: Sequence[int], source_offsets: Sequence[int], sizes: Sequence[int]):
-        """The reference's prepare_copy checks (lmcache_musa_batch_copy_ext.cpp:80-170)."""
+        """The reference's prepare_copy checks (lmcache_musa_batch_copy_ext.cpp:76-170)."""
         count = len(sizes)
         if len(destinations) != count or len(sources) != count:
             raise RuntimeError("destinations, sources, and sizes must have the same length")

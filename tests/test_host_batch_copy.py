@@ -237,7 +237,7 @@ def test_cpu_only_batches_are_not_taken(monkeypatch):
 
 
 def test_extension_argument_checks(monkeypatch):
-    # The reference extension's prepare_copy (lmcache_musa_batch_copy_ext.cpp:80-170), with the
+    # The reference extension's prepare_copy (lmcache_musa_batch_copy_ext.cpp:76-170), with the
     # GPU endpoint faked by tensor identity.
     gpu_ids = set()
     monkeypatch.setattr(ext, "_gpu", lambda t: id(t) in gpu_ids)
