@@ -280,3 +280,30 @@ def test_strided_block_transfer_matches_oracle(mode, direction):
     assert np.array_equal(staging_d.cpu().numpy(), want_staging)
     for got, exp in zip(pages_d, want_pages):
         assert np.array_equal(got.cpu().numpy(), exp)
+
+
+@pytest.mark.parametrize("row", [48, 7, 2048])
+def test_copy_rows_plane_inner_grid_zero_fills_skipped_and_tail_rows(row):
+    # Destination planes interleaved inside rows (a [rows, planes, row] buffer): the row launcher walks
+    # planes inside rows.  Skipped tokens and rows past num_tokens of this directly addressed
+    # destination must still be zero filled in every plane.
+    from musa_aiter.ops import _hip
+
+    planes, rows_out, tokens, src_rows = 5, 40, 33, 64
+    rng = np.random.default_rng(row)
+    gen = torch.Generator().manual_seed(row)
+    srcs = [random_payload((src_rows, row), torch.uint8, gen) for _ in range(planes)]
+    idx = rng.integers(-1, src_rows + 3, size=tokens).astype(np.int64)   # -1 and out-of-range skip
+    dst = torch.full((rows_out, planes, row), 0xAB, dtype=torch.uint8, device=DEV)
+    srcs_d = [s.to(DEV) for s in srcs]
+    idx_d = torch.from_numpy(idx).to(DEV)
+    _hip.copy_rows(op="plane-inner test", device=dst.device, src_planes=[s.data_ptr() for s in srcs_d],
+                   dst_planes=[dst.data_ptr() + p * row for p in range(planes)], num_planes=planes, src_idx=idx_d,
+                   dst_idx=None, num_tokens=tokens, num_rows_out=rows_out, src_rows=src_rows, dst_rows=rows_out,
+                   row_bytes=row, src_stride=row, dst_stride=planes * row, zero_invalid=True)
+    want = np.zeros((rows_out, planes, row), dtype=np.uint8)
+    for r in range(tokens):
+        if 0 <= idx[r] < src_rows:
+            for p in range(planes):
+                want[r, p] = srcs[p].numpy()[idx[r]]
+    assert np.array_equal(dst.cpu().numpy(), want)
