@@ -405,6 +405,35 @@ int musa_aiter_hip_runtime_versions(int* runtime_version, int* driver_version);
 int musa_aiter_hip_batch_copy(void* const* dsts, const void* const* srcs, const uint64_t* sizes, int64_t count,
                               int direction, int mode, void* stream);
 
+/* ---- CacheGen-style uniform-bin codec (binding kv_transfer.py:1048-1108; replaces
+ * kv_transfer_float.mu:828-898).  The two reference entries keep the reference kernels'
+ * contracts: encode_float writes bin = clamp(trunc(fma(x - min_val, scale, 0.5f)), 0,
+ * num_bins - 1) for `numel` float32 elements (num_bins in [1, 256]); decode_float writes
+ * output[i] = codebook[encoded[i]] reading the float32 codebook from global memory, so every
+ * code must be inside the caller's codebook.
+ *
+ * musa_aiter_hip_cachegen_encode is the whole of kv_transfer.py:1111-1172 on the device, with no
+ * host synchronisation: input_dtype 0 float32, 1 float16, 2 bfloat16, 3 float64 (widened or
+ * rounded to float32 first), num_bins in [2, 256]; encoded[numel] uint8, codebook[num_bins] and
+ * cdf[num_bins + 1] float32 are written; `workspace` is device memory of at least
+ * musa_aiter_hip_cachegen_workspace_bytes() bytes, private to the call until it completes.
+ * native_rounding = 1 (float32 only) selects the reference kernel's rounding above, 0 the torch
+ * path's: bin = clamp(rint((x - min) * ((1 / (max - min)) * (num_bins - 1))), 0, num_bins - 1).
+ * musa_aiter_hip_cachegen_decode gathers entries of elem_bytes (1, 2, 4, 8 or 16; `table`
+ * aligned to it) from a table of table_len entries (1..256); with table_len < 256 the caller
+ * clears *max_code (device int32) beforehand and afterwards finds there the largest code at or
+ * past table_len, or 0 when every code was inside the table. ---- */
+int musa_aiter_kv_cachegen_encode_float(const void* input, void* encoded, float min_val, float scale, int64_t numel,
+                                        int64_t num_bins, void* stream);
+int musa_aiter_kv_cachegen_decode_float(const void* encoded, const void* codebook, void* output, int64_t numel,
+                                        void* stream);
+int64_t musa_aiter_hip_cachegen_workspace_bytes(void);
+int musa_aiter_hip_cachegen_encode(const void* input, int input_dtype, int64_t numel, int64_t num_bins,
+                                   int native_rounding, void* encoded, void* codebook, void* cdf, void* workspace,
+                                   int64_t workspace_bytes, void* stream);
+int musa_aiter_hip_cachegen_decode(const void* encoded, int64_t numel, const void* table, int64_t table_len,
+                                   int elem_bytes, void* output, int32_t* max_code, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

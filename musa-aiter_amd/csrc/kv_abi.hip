@@ -1077,4 +1077,47 @@ int musa_aiter_hip_batch_copy(void* const* dsts, const void* const* srcs, const 
                                   mode == 1 ? kOverlapGroups : kBatchGroups, as_stream(stream));
 }
 
+// ----- CacheGen-style codec (kv_transfer_float.mu:828-898, kv_transfer.py:1048-1215) ----------
+
+int musa_aiter_kv_cachegen_encode_float(const void* input, void* encoded, float min_val, float scale, int64_t numel,
+                                        int64_t num_bins, void* stream) {
+  if (numel <= 0) return hipSuccess;
+  if (input == nullptr || encoded == nullptr || num_bins < 1 || num_bins > 256) return hipErrorInvalidValue;
+  return kvhip::launch_cachegen_bins(static_cast<const float*>(input), static_cast<uint8_t*>(encoded), min_val, scale,
+                                     numel, static_cast<int>(num_bins), as_stream(stream));
+}
+
+int musa_aiter_kv_cachegen_decode_float(const void* encoded, const void* codebook, void* output, int64_t numel,
+                                        void* stream) {
+  if (numel <= 0) return hipSuccess;
+  if (encoded == nullptr || codebook == nullptr || output == nullptr) return hipErrorInvalidValue;
+  return kvhip::launch_cachegen_decode(static_cast<const uint8_t*>(encoded), numel, codebook, -1, 4, output, nullptr,
+                                       as_stream(stream));
+}
+
+int64_t musa_aiter_hip_cachegen_workspace_bytes(void) { return kvhip::kCacheGenWorkspaceBytes; }
+
+int musa_aiter_hip_cachegen_encode(const void* input, int input_dtype, int64_t numel, int64_t num_bins,
+                                   int native_rounding, void* encoded, void* codebook, void* cdf, void* workspace,
+                                   int64_t workspace_bytes, void* stream) {
+  if (numel <= 0) return hipSuccess;
+  if (input == nullptr || encoded == nullptr || codebook == nullptr || cdf == nullptr || workspace == nullptr ||
+      num_bins < 2 || num_bins > 256 || workspace_bytes < kvhip::kCacheGenWorkspaceBytes ||
+      (native_rounding != 0 && input_dtype != kvhip::kCgF32))
+    return hipErrorInvalidValue;
+  return kvhip::launch_cachegen_encode(input, input_dtype, numel, static_cast<int>(num_bins), native_rounding != 0,
+                                       static_cast<uint8_t*>(encoded), static_cast<float*>(codebook),
+                                       static_cast<float*>(cdf), workspace, as_stream(stream));
+}
+
+int musa_aiter_hip_cachegen_decode(const void* encoded, int64_t numel, const void* table, int64_t table_len,
+                                   int elem_bytes, void* output, int32_t* max_code, void* stream) {
+  if (numel <= 0) return hipSuccess;
+  if (encoded == nullptr || table == nullptr || output == nullptr || table_len < 1 || table_len > 256 ||
+      reinterpret_cast<uintptr_t>(table) % static_cast<uintptr_t>(elem_bytes > 0 ? elem_bytes : 1) != 0)
+    return hipErrorInvalidValue;
+  return kvhip::launch_cachegen_decode(static_cast<const uint8_t*>(encoded), numel, table, static_cast<int>(table_len),
+                                       elem_bytes, output, max_code, as_stream(stream));
+}
+
 }  // extern "C"

@@ -1,0 +1,519 @@
+// CacheGen-style uniform-bin KV codec for MI355X (gfx950).
+//
+// Encode turns a floating tensor into one uint8 bin per element over the
+// tensor's own [min, max] range, plus a dequant codebook and the empirical
+// CDF of the bins.  It is three launches and no host synchronisation:
+//
+//   1. cg_minmax_kernel   -- one pass over the input; each workgroup writes its
+//                            (min, max) pair to the workspace; workgroup 0 also
+//                            clears the bin counters.
+//   2. cg_encode_kernel   -- every workgroup folds the pairs into the global
+//                            range (a few KiB from L2), derives the scale,
+//                            writes the bins and counts them in per-wave LDS
+//                            histograms that are added to the 64-bit global
+//                            counters once per workgroup.
+//   3. cg_finalize_kernel -- one workgroup: codebook (torch.linspace's
+//                            arithmetic) and CDF (prefix sums in double).
+//
+// The input is read twice (the range must be known before any bin is), the
+// bins written once: 2 * elem + 1 bytes per element.  Decode is one launch:
+// a gather through a <= 256-entry table staged in LDS, 1 + E bytes per element.
+//
+// Arithmetic follows the reference's torch path step by step, each float32
+// operation rounded on its own (the library is built without contraction):
+// scale = (1 / (max - min)) * (num_bins - 1), bin = rint((x - min) * scale),
+// clamped.  The reference's native kernel rounds differently, with a
+// double-precision scale and trunc((x - min) * scale + 0.5) as one fused
+// multiply-add; `native` selects it.
+#include <math.h>
+
+#include "kv_hip_common.h"
+#include "kv_launch.h"
+
+namespace kvhip {
+
+namespace {
+
+constexpr int kCgMaxGroups = 1024;
+constexpr int kCgUnroll = 4;
+// Workspace layout: (min, max) pairs of up to kCgMaxGroups workgroups, then 256 counters.
+constexpr int64_t kCgPairsBytes = kCgMaxGroups * 8;
+static_assert(kCgPairsBytes + 256 * 8 <= kCacheGenWorkspaceBytes, "workspace too small");
+
+template <int IN>
+struct CgIn;
+template <>
+struct CgIn<kCgF32> { static constexpr int kBytes = 4; };
+template <>
+struct CgIn<kCgF16> { static constexpr int kBytes = 2; };
+template <>
+struct CgIn<kCgBF16> { static constexpr int kBytes = 2; };
+template <>
+struct CgIn<kCgF64> { static constexpr int kBytes = 8; };
+
+// Element j of a 16-byte slot, widened (or for float64 rounded) to float32 as tensor.float() does.
+template <int IN>
+__device__ __forceinline__ float cg_elem(const u32x4& v, int j) {
+  if constexpr (IN == kCgF32) {
+    return __uint_as_float(v[j]);
+  } else if constexpr (IN == kCgF16) {
+    return f16_bits_to_f32(half_of(v[j >> 1], j & 1));
+  } else if constexpr (IN == kCgBF16) {
+    return bf16_bits_to_f32(half_of(v[j >> 1], j & 1));
+  } else {
+    const uint64_t bits = static_cast<uint64_t>(v[2 * j]) | (static_cast<uint64_t>(v[2 * j + 1]) << 32);
+    return static_cast<float>(__longlong_as_double(static_cast<long long>(bits)));
+  }
+}
+
+template <int IN>
+__device__ __forceinline__ float cg_load1(const uint8_t* x, int64_t i) {
+  if constexpr (IN == kCgF32) {
+    return reinterpret_cast<const float*>(x)[i];
+  } else if constexpr (IN == kCgF16) {
+    return f16_bits_to_f32(reinterpret_cast<const uint16_t*>(x)[i]);
+  } else if constexpr (IN == kCgBF16) {
+    return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(x)[i]);
+  } else {
+    return static_cast<float>(reinterpret_cast<const double*>(x)[i]);
+  }
+}
+
+// Running (min, max) with NaN propagation (torch's min / max return NaN if any element is).
+struct MinMax {
+  float mn = INFINITY;
+  float mx = -INFINITY;
+  bool nan = false;
+  __device__ __forceinline__ void fold(float f) {
+    nan |= f != f;
+    mn = fminf(mn, f);
+    mx = fmaxf(mx, f);
+  }
+};
+
+// Folds a MinMax over the workgroup; every thread returns the result.
+__device__ __forceinline__ MinMax block_minmax(MinMax m) {
+  __shared__ float s_mn[kWavesPerBlock], s_mx[kWavesPerBlock];
+  __shared__ int s_nan[kWavesPerBlock];
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    m.mn = fminf(m.mn, __shfl_xor(m.mn, off));
+    m.mx = fmaxf(m.mx, __shfl_xor(m.mx, off));
+  }
+  const bool any_nan = ballot(m.nan) != 0;
+  const int w = wave_in_block();
+  if (lane_id() == 0) {
+    s_mn[w] = m.mn;
+    s_mx[w] = m.mx;
+    s_nan[w] = any_nan ? 1 : 0;
+  }
+  __syncthreads();
+  MinMax r;
+  for (int i = 0; i < kWavesPerBlock; ++i) {
+    r.mn = fminf(r.mn, s_mn[i]);
+    r.mx = fmaxf(r.mx, s_mx[i]);
+    r.nan |= s_nan[i] != 0;
+  }
+  __syncthreads();
+  if (r.nan) r.mn = r.mx = __builtin_nanf("");
+  return r;
+}
+
+template <int IN, bool VEC>
+__global__ __launch_bounds__(kBlockThreads) void cg_minmax_kernel(const uint8_t* __restrict__ x, int64_t n,
+                                                                  float2* __restrict__ pairs,
+                                                                  uint64_t* __restrict__ counts) {
+  constexpr int kEps = 16 / CgIn<IN>::kBytes;
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * kBlockThreads + threadIdx.x;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlockThreads;
+  MinMax m;
+  int64_t first_scalar = 0;
+  if constexpr (VEC) {
+    const int64_t slots = n / kEps;
+    int64_t s = tid;
+    for (; s + (kCgUnroll - 1) * stride < slots; s += kCgUnroll * stride) {
+      u32x4 v[kCgUnroll];
+#pragma unroll
+      for (int u = 0; u < kCgUnroll; ++u) v[u] = ld16_cached(x + (s + u * stride) * 16);
+#pragma unroll
+      for (int u = 0; u < kCgUnroll; ++u)
+#pragma unroll
+        for (int j = 0; j < kEps; ++j) m.fold(cg_elem<IN>(v[u], j));
+    }
+    for (; s < slots; s += stride) {
+      const u32x4 v = ld16_cached(x + s * 16);
+#pragma unroll
+      for (int j = 0; j < kEps; ++j) m.fold(cg_elem<IN>(v, j));
+    }
+    first_scalar = slots * kEps;
+  }
+  for (int64_t i = first_scalar + tid; i < n; i += stride) m.fold(cg_load1<IN>(x, i));
+  const MinMax r = block_minmax(m);
+  if (threadIdx.x == 0) pairs[blockIdx.x] = make_float2(r.mn, r.mx);
+  if (blockIdx.x == 0) counts[threadIdx.x] = 0;  // kBlockThreads == 256 counters
+}
+
+struct CgEncodeArgs {
+  const uint8_t* x;
+  uint8_t* enc;
+  int64_t n;
+  const float2* pairs;  // null: min_arg / scale_arg given by the caller
+  int32_t num_pairs;
+  uint64_t* counts;     // null: no histogram
+  int32_t num_bins;
+  float min_arg;
+  float scale_arg;
+};
+
+template <bool NATIVE>
+__device__ __forceinline__ uint32_t cg_bin(float x, float mn, float scale, float top, uint32_t itop) {
+  const float t = x - mn;
+  if constexpr (NATIVE) {
+    const float v = __builtin_fmaf(t, scale, 0.5f);
+    return v >= top ? itop : (v > 0.0f ? static_cast<uint32_t>(v) : 0u);
+  } else {
+    const float r = __builtin_rintf(t * scale);
+    return r >= top ? itop : (r > 0.0f ? static_cast<uint32_t>(r) : 0u);
+  }
+}
+
+template <int IN, bool NATIVE, bool HIST, bool VEC>
+__global__ __launch_bounds__(kBlockThreads) void cg_encode_kernel(CgEncodeArgs a) {
+  constexpr int kEps = 16 / CgIn<IN>::kBytes;
+  __shared__ uint32_t hist[kWavesPerBlock][256];
+  const int nb = a.num_bins;
+  float mn = a.min_arg, scale = a.scale_arg;
+  if constexpr (HIST) {
+    MinMax m;
+    for (int i = threadIdx.x; i < a.num_pairs; i += kBlockThreads) {
+      const float2 p = a.pairs[i];
+      m.fold(p.x);
+      m.fold(p.y);
+    }
+    const MinMax r = block_minmax(m);
+    mn = r.mn;
+    if constexpr (NATIVE) {
+      scale = static_cast<float>(static_cast<double>(nb - 1) /
+                                 (static_cast<double>(r.mx) - static_cast<double>(r.mn)));
+    } else {
+      const float recip = 1.0f / (r.mx - r.mn);
+      scale = recip * static_cast<float>(nb - 1);
+    }
+    if (r.mx == r.mn) scale = 0.0f;  // constant tensor: every bin is 0
+    for (int i = threadIdx.x; i < kWavesPerBlock * 256; i += kBlockThreads) (&hist[0][0])[i] = 0;
+    __syncthreads();
+  }
+  const float top = static_cast<float>(nb - 1);
+  const uint32_t itop = static_cast<uint32_t>(nb - 1);
+  uint32_t* my_hist = hist[wave_in_block()];
+  auto count = [&](uint32_t b) {
+    if constexpr (HIST) atomicAdd(&my_hist[b], 1u);
+  };
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * kBlockThreads + threadIdx.x;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlockThreads;
+  int64_t first_scalar = 0;
+  if constexpr (VEC) {
+    const int64_t slots = a.n / kEps;
+    auto emit = [&](int64_t s, const u32x4& v) {
+      uint32_t b[kEps];
+#pragma unroll
+      for (int j = 0; j < kEps; ++j) {
+        b[j] = cg_bin<NATIVE>(cg_elem<IN>(v, j), mn, scale, top, itop);
+        count(b[j]);
+      }
+      uint8_t* d = a.enc + s * kEps;
+      if constexpr (kEps == 8) {
+        u32x2 w;
+        w[0] = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+        w[1] = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+        stv<8>(d, w);
+      } else if constexpr (kEps == 4) {
+        stv<4>(d, b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24));
+      } else {
+        stv<2>(d, static_cast<uint16_t>(b[0] | (b[1] << 8)));
+      }
+    };
+    int64_t s = tid;
+    for (; s + (kCgUnroll - 1) * stride < slots; s += kCgUnroll * stride) {
+      u32x4 v[kCgUnroll];
+#pragma unroll
+      for (int u = 0; u < kCgUnroll; ++u) v[u] = ld16(a.x + (s + u * stride) * 16);
+#pragma unroll
+      for (int u = 0; u < kCgUnroll; ++u) emit(s + u * stride, v[u]);
+    }
+    for (; s < slots; s += stride) emit(s, ld16(a.x + s * 16));
+    first_scalar = slots * kEps;
+  }
+  for (int64_t i = first_scalar + tid; i < a.n; i += stride) {
+    const uint32_t b = cg_bin<NATIVE>(cg_load1<IN>(a.x, i), mn, scale, top, itop);
+    count(b);
+    a.enc[i] = static_cast<uint8_t>(b);
+  }
+  if constexpr (HIST) {
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t < nb) {
+      uint32_t sum = 0;
+#pragma unroll
+      for (int w = 0; w < kWavesPerBlock; ++w) sum += hist[w][t];
+      if (sum != 0) atomicAdd(reinterpret_cast<unsigned long long*>(&a.counts[t]), static_cast<unsigned long long>(sum));
+    }
+  }
+}
+
+// One workgroup: codebook[num_bins] and cdf[num_bins + 1].
+__global__ __launch_bounds__(kBlockThreads) void cg_finalize_kernel(const float2* __restrict__ pairs, int32_t num_pairs,
+                                                                    const uint64_t* __restrict__ counts, int32_t nb,
+                                                                    int64_t numel, float* __restrict__ codebook,
+                                                                    float* __restrict__ cdf) {
+  __shared__ double scan[2][256];
+  MinMax m;
+  for (int i = threadIdx.x; i < num_pairs; i += kBlockThreads) {
+    const float2 p = pairs[i];
+    m.fold(p.x);
+    m.fold(p.y);
+  }
+  const MinMax r = block_minmax(m);
+  const int t = threadIdx.x;
+  if (t < nb) {
+    float v;
+    if (r.mx == r.mn) {
+      v = r.mn;
+    } else {
+      // torch.linspace: step in float32, the first half counted up from start and the
+      // second half down from end, one fused multiply-add each.
+      const float step = (r.mx - r.mn) / static_cast<float>(nb - 1);
+      v = t < nb / 2 ? __builtin_fmaf(step, static_cast<float>(t), r.mn)
+                     : __builtin_fmaf(-step, static_cast<float>(nb - 1 - t), r.mx);
+    }
+    codebook[t] = v;
+  }
+  // CDF: each count rounded to float32, prefix sums in double (exact: integers below 2**53),
+  // rounded to float32, divided by numel in float32.
+  scan[0][t] = t < nb ? static_cast<double>(static_cast<float>(counts[t])) : 0.0;
+  __syncthreads();
+  int cur = 0;
+  for (int off = 1; off < 256; off <<= 1) {
+    const double v = scan[cur][t] + (t >= off ? scan[cur][t - off] : 0.0);
+    scan[cur ^ 1][t] = v;
+    cur ^= 1;
+    __syncthreads();
+  }
+  if (t == 0) cdf[0] = 0.0f;
+  if (t < nb) cdf[t + 1] = static_cast<float>(scan[cur][t]) / static_cast<float>(numel);
+}
+
+struct CgDecodeArgs {
+  const uint8_t* codes;
+  uint8_t* out;
+  int64_t n;
+  const uint8_t* table;  // table_len entries of E bytes, aligned to E
+  int32_t table_len;
+  int32_t* max_code;     // CHECK: largest code seen (atomic max)
+};
+
+template <int E>
+struct Entry;
+template <>
+struct Entry<1> { using T = uint8_t; };
+template <>
+struct Entry<2> { using T = uint16_t; };
+template <>
+struct Entry<4> { using T = uint32_t; };
+template <>
+struct Entry<8> { using T = uint64_t; };
+template <>
+struct Entry<16> { using T = u32x4; };
+
+// Decode through a table staged in LDS (GLOBAL_TABLE: read from global memory, the reference
+// kernel's access, for callers that do not pass the table length).
+template <int E, bool VEC, bool CHECK, bool GLOBAL_TABLE>
+__global__ __launch_bounds__(kBlockThreads) void cg_decode_kernel(CgDecodeArgs a) {
+  using T = typename Entry<E>::T;
+  constexpr int kCodes = 16 / E;  // codes per 16-byte output slot
+  __shared__ T tab[GLOBAL_TABLE ? 1 : 256];
+  const T* table;
+  if constexpr (GLOBAL_TABLE) {
+    table = reinterpret_cast<const T*>(a.table);
+  } else {
+    const T* g = reinterpret_cast<const T*>(a.table);
+    for (int i = threadIdx.x; i < 256; i += kBlockThreads) tab[i] = i < a.table_len ? g[i] : T{};
+    __syncthreads();
+    table = tab;
+  }
+  uint32_t top = 0;
+  auto look = [&](uint32_t c) -> T {
+    if constexpr (CHECK) top = top > c ? top : c;
+    return table[c];
+  };
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * kBlockThreads + threadIdx.x;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlockThreads;
+  int64_t first_scalar = 0;
+  if constexpr (VEC) {
+    const int64_t slots = a.n / kCodes;
+    using C = typename VecType<kCodes>::T;
+    auto emit = [&](int64_t s, C cw) {
+      u32x4 o;
+      if constexpr (E == 16) {
+        o = look(static_cast<uint32_t>(cw));
+      } else if constexpr (E == 8) {
+        const uint32_t w = cw;
+        const uint64_t lo = look(w & 0xFFu), hi = look((w >> 8) & 0xFFu);
+        o[0] = static_cast<uint32_t>(lo);
+        o[1] = static_cast<uint32_t>(lo >> 32);
+        o[2] = static_cast<uint32_t>(hi);
+        o[3] = static_cast<uint32_t>(hi >> 32);
+      } else if constexpr (E == 4) {
+        const uint32_t w = cw;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = look((w >> (8 * j)) & 0xFFu);
+      } else if constexpr (E == 2) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const uint32_t w = cw[k];
+            o[2 * k + j] = static_cast<uint32_t>(look((w >> (16 * j)) & 0xFFu)) |
+                           (static_cast<uint32_t>(look((w >> (16 * j + 8)) & 0xFFu)) << 16);
+          }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t w = cw[k];
+          o[k] = static_cast<uint32_t>(look(w & 0xFFu)) | (static_cast<uint32_t>(look((w >> 8) & 0xFFu)) << 8) |
+                 (static_cast<uint32_t>(look((w >> 16) & 0xFFu)) << 16) |
+                 (static_cast<uint32_t>(look(w >> 24)) << 24);
+        }
+      }
+      stv<16>(a.out + s * 16, o);
+    };
+    int64_t s = tid;
+    for (; s + (kCgUnroll - 1) * stride < slots; s += kCgUnroll * stride) {
+      C cw[kCgUnroll];
+#pragma unroll
+      for (int u = 0; u < kCgUnroll; ++u) cw[u] = ldv<kCodes>(a.codes + (s + u * stride) * kCodes);
+#pragma unroll
+      for (int u = 0; u < kCgUnroll; ++u) emit(s + u * stride, cw[u]);
+    }
+    for (; s < slots; s += stride) emit(s, ldv<kCodes>(a.codes + s * kCodes));
+    first_scalar = slots * kCodes;
+  }
+  for (int64_t i = first_scalar + tid; i < a.n; i += stride)
+    reinterpret_cast<T*>(a.out)[i] = look(a.codes[i]);
+  if constexpr (CHECK) {
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+      const uint32_t o = __shfl_xor(top, off);
+      top = top > o ? top : o;
+    }
+    if (lane_id() == 0 && static_cast<int32_t>(top) >= a.table_len) atomicMax(a.max_code, static_cast<int>(top));
+  }
+}
+
+int cg_groups(int64_t units) {
+  const int64_t per_group = static_cast<int64_t>(kBlockThreads) * kCgUnroll;
+  int64_t g = (units + per_group - 1) / per_group;
+  if (g < 1) g = 1;
+  if (g > kCgMaxGroups) g = kCgMaxGroups;
+  return static_cast<int>(g);
+}
+
+template <int IN>
+hipError_t encode_typed(const uint8_t* x, int64_t n, int nb, bool native, uint8_t* enc, float* codebook, float* cdf,
+                        uint8_t* ws, hipStream_t stream) {
+  constexpr int kEps = 16 / CgIn<IN>::kBytes;
+  const bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(enc) % kEps) == 0;
+  const int groups = cg_groups(vec ? n / kEps : n);
+  float2* pairs = reinterpret_cast<float2*>(ws);
+  uint64_t* counts = reinterpret_cast<uint64_t*>(ws + kCgPairsBytes);
+  if (vec)
+    hipLaunchKernelGGL((cg_minmax_kernel<IN, true>), dim3(groups), dim3(kBlockThreads), 0, stream, x, n, pairs, counts);
+  else
+    hipLaunchKernelGGL((cg_minmax_kernel<IN, false>), dim3(groups), dim3(kBlockThreads), 0, stream, x, n, pairs, counts);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  CgEncodeArgs a{x, enc, n, pairs, groups, counts, nb, 0.0f, 0.0f};
+  if (native) {
+    if (vec) hipLaunchKernelGGL((cg_encode_kernel<IN, true, true, true>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
+    else hipLaunchKernelGGL((cg_encode_kernel<IN, true, true, false>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
+  } else {
+    if (vec) hipLaunchKernelGGL((cg_encode_kernel<IN, false, true, true>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
+    else hipLaunchKernelGGL((cg_encode_kernel<IN, false, true, false>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
+  }
+  err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL(cg_finalize_kernel, dim3(1), dim3(kBlockThreads), 0, stream, pairs, groups, counts, nb, n,
+                     codebook, cdf);
+  return hipGetLastError();
+}
+
+template <int E>
+hipError_t decode_typed(const uint8_t* codes, int64_t n, const uint8_t* table, int table_len, uint8_t* out,
+                        int32_t* max_code, hipStream_t stream) {
+  constexpr int kCodes = 16 / E;
+  const bool vec = (reinterpret_cast<uintptr_t>(codes) % kCodes) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  const bool check = table_len < 256;
+  const int groups = cg_groups(vec ? n / kCodes : n);
+  CgDecodeArgs a{codes, out, n, table, table_len, max_code};
+  if (vec) {
+    if (check) hipLaunchKernelGGL((cg_decode_kernel<E, true, true, false>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
+    else hipLaunchKernelGGL((cg_decode_kernel<E, true, false, false>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
+  } else {
+    if (check) hipLaunchKernelGGL((cg_decode_kernel<E, false, true, false>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
+    else hipLaunchKernelGGL((cg_decode_kernel<E, false, false, false>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_cachegen_encode(const void* x, int in_dtype, int64_t n, int num_bins, bool native, uint8_t* enc,
+                                  float* codebook, float* cdf, void* workspace, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  const uint8_t* xs = static_cast<const uint8_t*>(x);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  switch (in_dtype) {
+    case kCgF32: return encode_typed<kCgF32>(xs, n, num_bins, native, enc, codebook, cdf, ws, stream);
+    case kCgF16: return encode_typed<kCgF16>(xs, n, num_bins, false, enc, codebook, cdf, ws, stream);
+    case kCgBF16: return encode_typed<kCgBF16>(xs, n, num_bins, false, enc, codebook, cdf, ws, stream);
+    case kCgF64: return encode_typed<kCgF64>(xs, n, num_bins, false, enc, codebook, cdf, ws, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_cachegen_bins(const float* x, uint8_t* enc, float min_val, float scale, int64_t n, int num_bins,
+                                hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  const uint8_t* xs = reinterpret_cast<const uint8_t*>(x);
+  const bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(enc) & 3) == 0;
+  CgEncodeArgs a{xs, enc, n, nullptr, 0, nullptr, num_bins, min_val, scale};
+  const int groups = cg_groups(vec ? n / 4 : n);
+  if (vec) hipLaunchKernelGGL((cg_encode_kernel<kCgF32, true, false, true>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
+  else hipLaunchKernelGGL((cg_encode_kernel<kCgF32, true, false, false>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_cachegen_decode(const uint8_t* codes, int64_t n, const void* table, int table_len, int elem_bytes,
+                                  void* out, int32_t* max_code, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  const uint8_t* tb = static_cast<const uint8_t*>(table);
+  uint8_t* o = static_cast<uint8_t*>(out);
+  if (table_len < 0) {  // reference entry: float32 table of unknown length, read from global memory
+    if (elem_bytes != 4) return hipErrorInvalidValue;
+    const bool vec = (reinterpret_cast<uintptr_t>(codes) & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+    CgDecodeArgs a{codes, o, n, tb, 256, nullptr};
+    const int groups = cg_groups(vec ? n / 4 : n);
+    if (vec) hipLaunchKernelGGL((cg_decode_kernel<4, true, false, true>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
+    else hipLaunchKernelGGL((cg_decode_kernel<4, false, false, true>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
+    return hipGetLastError();
+  }
+  if (table_len < 1 || table_len > 256 || (table_len < 256 && max_code == nullptr)) return hipErrorInvalidValue;
+  switch (elem_bytes) {
+    case 1: return decode_typed<1>(codes, n, tb, table_len, o, max_code, stream);
+    case 2: return decode_typed<2>(codes, n, tb, table_len, o, max_code, stream);
+    case 4: return decode_typed<4>(codes, n, tb, table_len, o, max_code, stream);
+    case 8: return decode_typed<8>(codes, n, tb, table_len, o, max_code, stream);
+    case 16: return decode_typed<16>(codes, n, tb, table_len, o, max_code, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace kvhip

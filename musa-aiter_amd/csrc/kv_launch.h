@@ -128,4 +128,29 @@ constexpr int kBatchCopyMax = 96;
 hipError_t launch_batch_copy(const uint64_t* src, const uint64_t* dst, const uint64_t* size, int64_t count,
                              uint32_t max_groups, hipStream_t stream);
 
+// ----- CacheGen-style uniform-bin codec ------------------------------------------------
+
+// Input element types of the encoder.
+enum CacheGenInput : int { kCgF32 = 0, kCgF16 = 1, kCgBF16 = 2, kCgF64 = 3 };
+
+// Device workspace the encoder needs (per-workgroup ranges and the bin counters).
+constexpr int64_t kCacheGenWorkspaceBytes = 16384;
+
+// Bins of the `n` elements of `x` over their own [min, max] (torch-path rounding, or the
+// reference kernel's when `native`; float32 input only), the codebook[num_bins] and the
+// cdf[num_bins + 1]; three launches, no host synchronisation.
+hipError_t launch_cachegen_encode(const void* x, int in_dtype, int64_t n, int num_bins, bool native, uint8_t* enc,
+                                  float* codebook, float* cdf, void* workspace, hipStream_t stream);
+
+// Bins of float32 `x` with a caller-given minimum and scale, the reference kernel's rounding.
+hipError_t launch_cachegen_bins(const float* x, uint8_t* enc, float min_val, float scale, int64_t n, int num_bins,
+                                hipStream_t stream);
+
+// out[i] = table[codes[i]] for entries of `elem_bytes` (1, 2, 4, 8 or 16) bytes.  With
+// table_len in [1, 255] codes at or past the end read zeros and the largest such code is
+// stored to *max_code (atomic max; the caller clears it); table_len < 0 reads a float32
+// table of unknown length straight from global memory (no check).
+hipError_t launch_cachegen_decode(const uint8_t* codes, int64_t n, const void* table, int table_len, int elem_bytes,
+                                  void* out, int32_t* max_code, hipStream_t stream);
+
 }  // namespace kvhip

@@ -48,6 +48,8 @@ from musa_aiter.ops.kv_transfer import (
     is_native_fp8_kv_cache_available,
     is_native_fp8_kv_vectorized_available,
     is_native_kv_transfer_available,
+    kv_cachegen_decode,
+    kv_cachegen_encode,
     kv_copy_paged_blocks,
     kv_copy_paged_blocks_fp8,
     kv_copy_paged_rows,

@@ -84,6 +84,24 @@ _SIGNATURES: dict[str, list] = {
                                   _i32, _i32, _c_void_p],
     "musa_aiter_hip_batch_copy_abi_version": [],
     "musa_aiter_hip_runtime_versions": [ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)],
+    # CacheGen codec.  Reference entries: (input, encoded, min_val, scale, numel, num_bins, stream) and
+    # (encoded, codebook, output, numel, stream).
+    "musa_aiter_kv_cachegen_encode_float": [_c_void_p, _c_void_p, ctypes.c_float, ctypes.c_float, _i64, _i64,
+                                            _c_void_p],
+    "musa_aiter_kv_cachegen_decode_float": [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p],
+    "musa_aiter_hip_cachegen_workspace_bytes": [],
+    # (input, input_dtype, numel, num_bins, native_rounding, encoded, codebook, cdf, workspace,
+    #  workspace_bytes, stream)
+    "musa_aiter_hip_cachegen_encode": [_c_void_p, _i32, _i64, _i64, _i32, _c_void_p, _c_void_p, _c_void_p,
+                                       _c_void_p, _i64, _c_void_p],
+    # (encoded, numel, table, table_len, elem_bytes, output, max_code, stream)
+    "musa_aiter_hip_cachegen_decode": [_c_void_p, _i64, _c_void_p, _i64, _i32, _c_void_p, _c_void_p, _c_void_p],
+}
+
+_RESTYPES = {
+    "musa_aiter_hip_error_string": ctypes.c_char_p,
+    "musa_aiter_hip_backend_name": ctypes.c_char_p,
+    "musa_aiter_hip_cachegen_workspace_bytes": ctypes.c_int64,
 }
 
 _lock = threading.Lock()
@@ -111,10 +129,7 @@ def library() -> ctypes.CDLL:
             for name, argtypes in _SIGNATURES.items():
                 fn = getattr(lib, name)
                 fn.argtypes = argtypes
-                if name == "musa_aiter_hip_error_string" or name == "musa_aiter_hip_backend_name":
-                    fn.restype = ctypes.c_char_p
-                else:
-                    fn.restype = ctypes.c_int
+                fn.restype = _RESTYPES.get(name, ctypes.c_int)
                 _fns[name] = fn
             _lib = lib
     return _lib
@@ -366,5 +381,31 @@ def copy_blocks(
         rc = fn("musa_aiter_kv_copy_paged_blocks_fp8_vec8")(
             ptr(src_k), ptr(src_v), ptr(dst_k), ptr(dst_v), ptr(block_mapping), pairs, int(num_layers),
             int(src_blocks), int(dst_blocks), 1, int(block_bytes), 1, stream_ptr(device),
+        )
+    check(rc, op)
+
+
+def cachegen_encode(*, op: str, x: torch.Tensor, input_dtype: int, num_bins: int, native_rounding: bool,
+                    encoded: torch.Tensor, codebook: torch.Tensor, cdf: torch.Tensor) -> None:
+    """Bins, codebook and CDF of contiguous ``x`` in three launches on the current stream."""
+    device = x.device
+    ws_bytes = int(fn("musa_aiter_hip_cachegen_workspace_bytes")())
+    with torch.cuda.device(device):
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+        rc = fn("musa_aiter_hip_cachegen_encode")(
+            ptr(x), int(input_dtype), int(x.numel()), int(num_bins), int(bool(native_rounding)),
+            ptr(encoded), ptr(codebook), ptr(cdf), ptr(workspace), ws_bytes, stream_ptr(device),
+        )
+    check(rc, op)
+
+
+def cachegen_decode(*, op: str, codes: torch.Tensor, table: torch.Tensor, out: torch.Tensor,
+                    max_code: torch.Tensor | None) -> None:
+    """out[i] = table[codes[i]] for contiguous ``codes`` / ``out`` and a contiguous table."""
+    device = codes.device
+    with torch.cuda.device(device):
+        rc = fn("musa_aiter_hip_cachegen_decode")(
+            ptr(codes), int(codes.numel()), ptr(table), int(table.numel()), int(table.element_size()),
+            ptr(out), ptr(max_code), stream_ptr(device),
         )
     check(rc, op)

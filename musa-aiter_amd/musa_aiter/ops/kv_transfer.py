@@ -32,6 +32,7 @@ import torch
 from musa_aiter.dispatch import DispatchRecord, emit, tensor_device_dtype
 from musa_aiter.ops import _hip
 from musa_aiter.ops.kv_layout import KVLayoutSpec, KVScaleKind
+from musa_aiter.ops.native_gate import native_requested
 
 BACKEND = _hip.BACKEND
 
@@ -1357,6 +1358,98 @@ def kv_copy_paged_blocks_fp8(
 
 
 # ---------------------------------------------------------------------------
+# CacheGen-style uniform-bin codec (reference :1048-1215)
+# ---------------------------------------------------------------------------
+
+_CACHEGEN_INPUT = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
+
+
+def _cachegen_native_rounding(tensor: torch.Tensor) -> bool:
+    """The reference rounds bins with its native kernel only for float32 input and only when
+    ``MUSA_AITER_NATIVE_KV_TRANSFER=1`` (reference :208-209, :1054); otherwise with torch ops."""
+    return tensor.dtype == torch.float32 and native_requested("MUSA_AITER_NATIVE_KV_TRANSFER")
+
+
+def kv_cachegen_encode(
+    tensor: torch.Tensor,
+    *,
+    num_bins: int = 256,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Encode a KV tensor into uint8 bins plus a dequant codebook and the bins' empirical CDF
+    (reference :1111-1172).
+
+    Bins are uniform over the tensor's own [min, max] in float32: ``rint((x - min) * scale)``
+    clamped to [0, num_bins - 1] with ``scale = (1 / (max - min)) * (num_bins - 1)``, or, for
+    float32 input with ``MUSA_AITER_NATIVE_KV_TRANSFER=1``, the reference kernel's
+    ``trunc((x - min) * scale + 0.5)`` with the scale computed in double.  The codebook is
+    ``torch.linspace(min, max, num_bins)`` (all ``min`` for a constant tensor) and the CDF is
+    ``[0, cumsum(counts) / numel]``, as float32.  Range, bins, histogram, codebook and CDF are
+    computed on the device in three launches without a host synchronisation (the reference
+    reads min and max back to the host and counts the bins on the CPU).
+    """
+    op = "kv_cachegen_encode"
+    if num_bins < 2 or num_bins > 256:
+        raise ValueError("kv_cachegen_encode: num_bins must be in [2, 256]")
+    if not tensor.is_floating_point():
+        raise ValueError("kv_cachegen_encode: tensor must use a floating dtype")
+    if tensor.numel() == 0:
+        codebook = torch.zeros(num_bins, dtype=torch.float32, device=tensor.device)
+        cdf = torch.zeros(num_bins + 1, dtype=torch.float32, device=tensor.device)
+        return torch.empty_like(tensor, dtype=torch.uint8), codebook, cdf
+    _require_rocm(op, tensor)
+    native = _cachegen_native_rounding(tensor)
+    input_code = _CACHEGEN_INPUT.get(tensor.dtype)
+    work = tensor if input_code is not None else tensor.float()  # float8 inputs: widened first, as the reference
+    work = work.contiguous()
+    encoded = torch.empty(tensor.shape, dtype=torch.uint8, device=tensor.device)
+    codebook = torch.empty(num_bins, dtype=torch.float32, device=tensor.device)
+    cdf = torch.empty(num_bins + 1, dtype=torch.float32, device=tensor.device)
+    _hip.cachegen_encode(op=op, x=work, input_dtype=input_code if input_code is not None else 0,
+                         num_bins=num_bins, native_rounding=native, encoded=encoded, codebook=codebook, cdf=cdf)
+    _emit(op, tensor, "gfx950 CacheGen encode: range, bins and histogram on device" +
+          (" (native-kernel rounding)" if native else ""))
+    return encoded, codebook, cdf
+
+
+def kv_cachegen_decode(
+    encoded: torch.Tensor,
+    codebook: torch.Tensor,
+    *,
+    dtype: torch.dtype | None = None,
+) -> torch.Tensor:
+    """Decode uint8 CacheGen-style bins through a dequant codebook: ``codebook[encoded]``, cast to
+    ``dtype`` when given (reference :1175-1215).
+
+    The gather runs through the (cast) codebook staged in LDS.  A bin past the end of a codebook
+    of fewer than 256 entries raises ``ValueError`` as in the reference; it is detected by the
+    decode launch itself, which costs one synchronisation for such codebooks and none for
+    256-entry ones.
+    """
+    op = "kv_cachegen_decode"
+    if encoded.dtype != torch.uint8:
+        raise ValueError("kv_cachegen_decode: encoded must be uint8")
+    if codebook.dim() != 1 or codebook.numel() < 2 or codebook.numel() > 256:
+        raise ValueError("kv_cachegen_decode: codebook must be 1-D with 2..256 bins")
+    if codebook.device != encoded.device:
+        raise ValueError("kv_cachegen_decode: encoded and codebook must be on same device")
+    if not codebook.is_floating_point():
+        raise ValueError("kv_cachegen_decode: codebook must use a floating dtype")
+    out_dtype = codebook.dtype if dtype is None else dtype
+    if encoded.numel() == 0:
+        return torch.empty(encoded.shape, dtype=out_dtype, device=encoded.device)
+    _require_rocm(op, encoded)
+    table = (codebook if out_dtype == codebook.dtype else codebook.to(out_dtype)).contiguous()
+    codes = encoded.contiguous()
+    out = torch.empty(encoded.shape, dtype=out_dtype, device=encoded.device)
+    max_code = torch.zeros(1, dtype=torch.int32, device=encoded.device) if table.numel() < 256 else None
+    _hip.cachegen_decode(op=op, codes=codes, table=table, out=out, max_code=max_code)
+    if max_code is not None and int(max_code.item()) >= table.numel():
+        raise ValueError("kv_cachegen_decode: encoded bin exceeds codebook size")
+    _emit(op, encoded, "gfx950 CacheGen decode: LDS codebook gather")
+    return out
+
+
+# ---------------------------------------------------------------------------
 # MLA / DSA flat caches [NB, BS, D] (reference :3769-4118)
 # ---------------------------------------------------------------------------
 
@@ -1805,6 +1898,14 @@ __all__ = [
     "kv_copy_paged_rows",
     "kv_copy_paged_rows_layer_table",
     "kv_copy_paged_rows_multi_pool",
+    "kv_load_and_reshape_flash",
+    "kv_reshape_and_cache_back_flash",
+    "kv_load_and_dequantize_fp8_flash",
+    "kv_triton_indexed_to_dense",
+    "kv_copy_paged_blocks",
+    "kv_copy_paged_blocks_fp8",
+    "kv_cachegen_encode",
+    "kv_cachegen_decode",
     "InterleavedFp8Layout",
     "PoolSpec",
     "clear_dsv4_ptr_table_cache",

@@ -110,6 +110,9 @@ _kv("kv_reshape_and_cache_back_flash", "hip-native", _FLOAT,
 _kv("kv_copy_paged_blocks", "hip-native", _FLOAT, "Copy selected paged KV blocks between same-layout caches.")
 _kv("kv_copy_paged_blocks_fp8", "hip-native", ("uint8", "float8_e4m3fn", "float8_e5m2"),
     "Raw FP8 paged KV block copy between same-layout caches.")
+_kv("kv_cachegen_encode", "hip-native", ("float32", "float16", "bfloat16", "float64"),
+    "CacheGen-style uniform-bin uint8 KV encode with dequant codebook and empirical CDF, on device.")
+_kv("kv_cachegen_decode", "hip-native", ("uint8",), "CacheGen-style uint8 codebook decode through an LDS table.")
 # DSV4 opaque byte rows.
 _kv("kv_copy_paged_rows", "hip-native", ("uint8",), "Opaque byte-row gather/scatter between row pools (per layer).")
 _kv("kv_copy_paged_rows_layer_table", "hip-native", ("uint8",), "Opaque byte-row copy across a layer table, one launch.")

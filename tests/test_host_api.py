@@ -145,7 +145,7 @@ def test_kvcache_registry_rows_and_backend():
         "hicache_transfer_kv_per_layer_mla_pf_lf", "hicache_transfer_kv_all_layer_mla",
         "hicache_transfer_kv_all_layer_mla_lf_pf", "hicache_transfer_kv_direct",
         "hicache_transfer_kv_per_layer_direct_pf_lf", "hicache_transfer_kv_all_layer_direct_lf_pf",
-        "lmcache_musa_memcpy_batch_async",
+        "lmcache_musa_memcpy_batch_async", "kv_cachegen_encode", "kv_cachegen_decode",
     }
     for cap in caps:
         assert cap.backends == ("rocm-hip",)
