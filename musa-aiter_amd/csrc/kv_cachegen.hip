@@ -4,20 +4,23 @@
 // tensor's own [min, max] range, plus a dequant codebook and the empirical
 // CDF of the bins.  It is three launches and no host synchronisation:
 //
-//   1. cg_minmax_kernel   -- one pass over the input; each workgroup writes its
-//                            (min, max) pair to the workspace; workgroup 0 also
-//                            clears the bin counters.
-//   2. cg_encode_kernel   -- every workgroup folds the pairs into the global
-//                            range (a few KiB from L2), derives the scale,
-//                            writes the bins and counts them in per-wave LDS
-//                            histograms that are added to the 64-bit global
-//                            counters once per workgroup.
-//   3. cg_finalize_kernel -- one workgroup: codebook (torch.linspace's
-//                            arithmetic) and CDF (prefix sums in double).
+//   1. cg_minmax_kernel -- one pass over the input; each workgroup writes its
+//                          (min, max) pair to the workspace; workgroup 0 also
+//                          clears the bin counters.
+//   2. cg_encode_kernel -- every workgroup folds the pairs into the range (a
+//                          few KiB from L2) and derives the scale; workgroup 0
+//                          writes the codebook (torch.linspace's arithmetic);
+//                          all write the bins and count them in per-wave LDS
+//                          histograms, added to 64-bit global counters once
+//                          per workgroup.
+//   3. cg_cdf_kernel    -- one workgroup: the counters into the CDF.
 //
 // The input is read twice (the range must be known before any bin is), the
 // bins written once: 2 * elem + 1 bytes per element.  Decode is one launch:
 // a gather through a <= 256-entry table staged in LDS, 1 + E bytes per element.
+// The streaming kernels run grid-stride loops; decode uses up to 8192
+// workgroups (fewer leave part of the chip idle), encode 1024, which keeps
+// the per-workgroup range fold and the global counter updates small.
 //
 // Arithmetic follows the reference's torch path step by step, each float32
 // operation rounded on its own (the library is built without contraction):
@@ -34,11 +37,22 @@ namespace kvhip {
 
 namespace {
 
-constexpr int kCgMaxGroups = 1024;
+// Grid caps of the streaming kernels (grid-stride loops below the cap).
+#ifndef KVHIP_CG_ENCODE_GROUPS
+#define KVHIP_CG_ENCODE_GROUPS 1024
+#endif
+#ifndef KVHIP_CG_DECODE_GROUPS
+#define KVHIP_CG_DECODE_GROUPS 8192
+#endif
+constexpr int kCgEncodeGroups = KVHIP_CG_ENCODE_GROUPS;
+constexpr int kCgDecodeGroups = KVHIP_CG_DECODE_GROUPS;
 constexpr int kCgUnroll = 4;
-// Workspace layout: (min, max) pairs of up to kCgMaxGroups workgroups, then 256 counters.
-constexpr int64_t kCgPairsBytes = kCgMaxGroups * 8;
-static_assert(kCgPairsBytes + 256 * 8 <= kCacheGenWorkspaceBytes, "workspace too small");
+
+// Workspace layout: the 256 bin counters, the per-workgroup (min, max) pairs.
+constexpr int64_t kCgCountsOffset = 0;
+constexpr int64_t kCgPairsOffset = 4096;
+static_assert(kCgCountsOffset + 256 * 8 <= kCgPairsOffset, "workspace layout");
+static_assert(kCgPairsOffset + int64_t{kCgEncodeGroups} * 8 <= kCacheGenWorkspaceBytes, "workspace too small");
 
 template <int IN>
 struct CgIn;
@@ -156,13 +170,24 @@ struct CgEncodeArgs {
   const uint8_t* x;
   uint8_t* enc;
   int64_t n;
-  const float2* pairs;  // null: min_arg / scale_arg given by the caller
+  const float2* pairs;  // null: min_arg / scale_arg given by the caller, no histogram
   int32_t num_pairs;
-  uint64_t* counts;     // null: no histogram
+  uint64_t* counts;
+  float* codebook;
   int32_t num_bins;
   float min_arg;
   float scale_arg;
 };
+
+// codebook[t]: torch.full(min) for a constant range, else torch.linspace(min, max, nb) -- step in
+// float32, the first half counted up from start and the second half down from end, one fused
+// multiply-add each.
+__device__ __forceinline__ float cg_codebook(float mn, float mx, int nb, int t) {
+  if (mx == mn) return mn;
+  const float step = (mx - mn) / static_cast<float>(nb - 1);
+  return t < nb / 2 ? __builtin_fmaf(step, static_cast<float>(t), mn)
+                    : __builtin_fmaf(-step, static_cast<float>(nb - 1 - t), mx);
+}
 
 template <bool NATIVE>
 __device__ __forceinline__ uint32_t cg_bin(float x, float mn, float scale, float top, uint32_t itop) {
@@ -174,6 +199,25 @@ __device__ __forceinline__ uint32_t cg_bin(float x, float mn, float scale, float
     const float r = __builtin_rintf(t * scale);
     return r >= top ? itop : (r > 0.0f ? static_cast<uint32_t>(r) : 0u);
   }
+}
+
+// cdf[0] = 0, cdf[t + 1] = (prefix of float32(count)) / numel, for the workgroup's 256 threads
+// holding counts[t]: each count rounded to float32, prefix sums in double (exact: integers below
+// 2**53), rounded to float32, divided by numel in float32.
+__device__ __forceinline__ void cg_write_cdf(uint64_t count, int nb, int64_t numel, float* cdf) {
+  __shared__ double scan[2][256];
+  const int t = threadIdx.x;
+  scan[0][t] = t < nb ? static_cast<double>(static_cast<float>(count)) : 0.0;
+  __syncthreads();
+  int cur = 0;
+  for (int off = 1; off < 256; off <<= 1) {
+    const double v = scan[cur][t] + (t >= off ? scan[cur][t - off] : 0.0);
+    scan[cur ^ 1][t] = v;
+    cur ^= 1;
+    __syncthreads();
+  }
+  if (t == 0) cdf[0] = 0.0f;
+  if (t < nb) cdf[t + 1] = static_cast<float>(scan[cur][t]) / static_cast<float>(numel);
 }
 
 template <int IN, bool NATIVE, bool HIST, bool VEC>
@@ -199,6 +243,8 @@ __global__ __launch_bounds__(kBlockThreads) void cg_encode_kernel(CgEncodeArgs a
       scale = recip * static_cast<float>(nb - 1);
     }
     if (r.mx == r.mn) scale = 0.0f;  // constant tensor: every bin is 0
+    if (blockIdx.x == 0 && static_cast<int>(threadIdx.x) < nb)
+      a.codebook[threadIdx.x] = cg_codebook(r.mn, r.mx, nb, threadIdx.x);
     for (int i = threadIdx.x; i < kWavesPerBlock * 256; i += kBlockThreads) (&hist[0][0])[i] = 0;
     __syncthreads();
   }
@@ -255,51 +301,19 @@ __global__ __launch_bounds__(kBlockThreads) void cg_encode_kernel(CgEncodeArgs a
       uint32_t sum = 0;
 #pragma unroll
       for (int w = 0; w < kWavesPerBlock; ++w) sum += hist[w][t];
-      if (sum != 0) atomicAdd(reinterpret_cast<unsigned long long*>(&a.counts[t]), static_cast<unsigned long long>(sum));
+      if (sum != 0)
+        atomicAdd(reinterpret_cast<unsigned long long*>(&a.counts[t]), static_cast<unsigned long long>(sum));
     }
   }
 }
 
-// One workgroup: codebook[num_bins] and cdf[num_bins + 1].
-__global__ __launch_bounds__(kBlockThreads) void cg_finalize_kernel(const float2* __restrict__ pairs, int32_t num_pairs,
-                                                                    const uint64_t* __restrict__ counts, int32_t nb,
-                                                                    int64_t numel, float* __restrict__ codebook,
-                                                                    float* __restrict__ cdf) {
-  __shared__ double scan[2][256];
-  MinMax m;
-  for (int i = threadIdx.x; i < num_pairs; i += kBlockThreads) {
-    const float2 p = pairs[i];
-    m.fold(p.x);
-    m.fold(p.y);
-  }
-  const MinMax r = block_minmax(m);
+// One workgroup, after cg_encode_kernel: the counters into cdf[num_bins + 1].  (Finishing in the
+// encode kernel's last workgroup would need a device-scope release fence in every workgroup,
+// which writes back L2 and costs far more than this launch.)
+__global__ __launch_bounds__(kBlockThreads) void cg_cdf_kernel(const uint64_t* __restrict__ counts, int32_t nb,
+                                                               int64_t numel, float* __restrict__ cdf) {
   const int t = threadIdx.x;
-  if (t < nb) {
-    float v;
-    if (r.mx == r.mn) {
-      v = r.mn;
-    } else {
-      // torch.linspace: step in float32, the first half counted up from start and the
-      // second half down from end, one fused multiply-add each.
-      const float step = (r.mx - r.mn) / static_cast<float>(nb - 1);
-      v = t < nb / 2 ? __builtin_fmaf(step, static_cast<float>(t), r.mn)
-                     : __builtin_fmaf(-step, static_cast<float>(nb - 1 - t), r.mx);
-    }
-    codebook[t] = v;
-  }
-  // CDF: each count rounded to float32, prefix sums in double (exact: integers below 2**53),
-  // rounded to float32, divided by numel in float32.
-  scan[0][t] = t < nb ? static_cast<double>(static_cast<float>(counts[t])) : 0.0;
-  __syncthreads();
-  int cur = 0;
-  for (int off = 1; off < 256; off <<= 1) {
-    const double v = scan[cur][t] + (t >= off ? scan[cur][t - off] : 0.0);
-    scan[cur ^ 1][t] = v;
-    cur ^= 1;
-    __syncthreads();
-  }
-  if (t == 0) cdf[0] = 0.0f;
-  if (t < nb) cdf[t + 1] = static_cast<float>(scan[cur][t]) / static_cast<float>(numel);
+  cg_write_cdf(t < nb ? counts[t] : 0, nb, numel, cdf);
 }
 
 struct CgDecodeArgs {
@@ -408,11 +422,11 @@ __global__ __launch_bounds__(kBlockThreads) void cg_decode_kernel(CgDecodeArgs a
   }
 }
 
-int cg_groups(int64_t units) {
+int cg_groups(int64_t units, int cap) {
   const int64_t per_group = static_cast<int64_t>(kBlockThreads) * kCgUnroll;
   int64_t g = (units + per_group - 1) / per_group;
   if (g < 1) g = 1;
-  if (g > kCgMaxGroups) g = kCgMaxGroups;
+  if (g > cap) g = cap;
   return static_cast<int>(g);
 }
 
@@ -421,16 +435,17 @@ hipError_t encode_typed(const uint8_t* x, int64_t n, int nb, bool native, uint8_
                         uint8_t* ws, hipStream_t stream) {
   constexpr int kEps = 16 / CgIn<IN>::kBytes;
   const bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(enc) % kEps) == 0;
-  const int groups = cg_groups(vec ? n / kEps : n);
-  float2* pairs = reinterpret_cast<float2*>(ws);
-  uint64_t* counts = reinterpret_cast<uint64_t*>(ws + kCgPairsBytes);
+  const int groups = cg_groups(vec ? n / kEps : n, kCgEncodeGroups);
+  uint64_t* counts = reinterpret_cast<uint64_t*>(ws + kCgCountsOffset);
+  float2* pairs = reinterpret_cast<float2*>(ws + kCgPairsOffset);
   if (vec)
     hipLaunchKernelGGL((cg_minmax_kernel<IN, true>), dim3(groups), dim3(kBlockThreads), 0, stream, x, n, pairs, counts);
   else
-    hipLaunchKernelGGL((cg_minmax_kernel<IN, false>), dim3(groups), dim3(kBlockThreads), 0, stream, x, n, pairs, counts);
+    hipLaunchKernelGGL((cg_minmax_kernel<IN, false>), dim3(groups), dim3(kBlockThreads), 0, stream, x, n, pairs,
+                       counts);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  CgEncodeArgs a{x, enc, n, pairs, groups, counts, nb, 0.0f, 0.0f};
+  CgEncodeArgs a{x, enc, n, pairs, groups, counts, codebook, nb, 0.0f, 0.0f};
   if (native) {
     if (vec) hipLaunchKernelGGL((cg_encode_kernel<IN, true, true, true>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
     else hipLaunchKernelGGL((cg_encode_kernel<IN, true, true, false>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
@@ -440,8 +455,7 @@ hipError_t encode_typed(const uint8_t* x, int64_t n, int nb, bool native, uint8_
   }
   err = hipGetLastError();
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL(cg_finalize_kernel, dim3(1), dim3(kBlockThreads), 0, stream, pairs, groups, counts, nb, n,
-                     codebook, cdf);
+  hipLaunchKernelGGL(cg_cdf_kernel, dim3(1), dim3(kBlockThreads), 0, stream, counts, nb, n, cdf);
   return hipGetLastError();
 }
 
@@ -451,7 +465,7 @@ hipError_t decode_typed(const uint8_t* codes, int64_t n, const uint8_t* table, i
   constexpr int kCodes = 16 / E;
   const bool vec = (reinterpret_cast<uintptr_t>(codes) % kCodes) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
   const bool check = table_len < 256;
-  const int groups = cg_groups(vec ? n / kCodes : n);
+  const int groups = cg_groups(vec ? n / kCodes : n, kCgDecodeGroups);
   CgDecodeArgs a{codes, out, n, table, table_len, max_code};
   if (vec) {
     if (check) hipLaunchKernelGGL((cg_decode_kernel<E, true, true, false>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
@@ -484,8 +498,8 @@ hipError_t launch_cachegen_bins(const float* x, uint8_t* enc, float min_val, flo
   if (n <= 0) return hipSuccess;
   const uint8_t* xs = reinterpret_cast<const uint8_t*>(x);
   const bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(enc) & 3) == 0;
-  CgEncodeArgs a{xs, enc, n, nullptr, 0, nullptr, num_bins, min_val, scale};
-  const int groups = cg_groups(vec ? n / 4 : n);
+  CgEncodeArgs a{xs, enc, n, nullptr, 0, nullptr, nullptr, num_bins, min_val, scale};
+  const int groups = cg_groups(vec ? n / 4 : n, kCgEncodeGroups);
   if (vec) hipLaunchKernelGGL((cg_encode_kernel<kCgF32, true, false, true>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
   else hipLaunchKernelGGL((cg_encode_kernel<kCgF32, true, false, false>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
   return hipGetLastError();
@@ -500,7 +514,7 @@ hipError_t launch_cachegen_decode(const uint8_t* codes, int64_t n, const void* t
     if (elem_bytes != 4) return hipErrorInvalidValue;
     const bool vec = (reinterpret_cast<uintptr_t>(codes) & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
     CgDecodeArgs a{codes, o, n, tb, 256, nullptr};
-    const int groups = cg_groups(vec ? n / 4 : n);
+    const int groups = cg_groups(vec ? n / 4 : n, kCgDecodeGroups);
     if (vec) hipLaunchKernelGGL((cg_decode_kernel<4, true, false, true>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
     else hipLaunchKernelGGL((cg_decode_kernel<4, false, false, true>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
     return hipGetLastError();
