@@ -18,9 +18,10 @@
 // The input is read twice (the range must be known before any bin is), the
 // bins written once: 2 * elem + 1 bytes per element.  Decode is one launch:
 // a gather through a <= 256-entry table staged in LDS, 1 + E bytes per element.
-// The streaming kernels run grid-stride loops; decode uses up to 8192
-// workgroups (fewer leave part of the chip idle), encode 1024, which keeps
-// the per-workgroup range fold and the global counter updates small.
+// The streaming kernels walk contiguous chunks (layout below): the range and
+// bin passes on 1024 persistent workgroups, which keeps the per-workgroup
+// range fold and the global counter updates small (the bin pass prefetches
+// its next chunk), decode on one chunk per workgroup.
 //
 // Arithmetic follows the reference's torch path step by step, each float32
 // operation rounded on its own (the library is built without contraction):
@@ -37,22 +38,40 @@ namespace kvhip {
 
 namespace {
 
-// Grid caps of the streaming kernels (grid-stride loops below the cap).
+// The streaming kernels visit the 16-byte vectors of their wide side in chunks of
+// kWavesPerBlock * kWave * V vectors: inside a chunk, lane l of wave w takes vectors
+// base + w * kWave * V + k * kWave + l (k < V), so each of a wave's V loads or stores covers
+// 1 KiB contiguously and the wave's V KiB are contiguous too; workgroup g takes chunks g,
+// g + grid, ...  Measured on MI355X over 1 GiB, this shape reads at 7.0 TB/s where a grid-stride
+// loop with four loads per thread spread a grid apart reads at 5.3 TB/s.  Grid caps and V per
+// kernel come from a sweep over 1024-8192 workgroups and 2-8 vectors.
+#ifndef KVHIP_CG_MINMAX_GROUPS
+#define KVHIP_CG_MINMAX_GROUPS 1024
+#endif
 #ifndef KVHIP_CG_ENCODE_GROUPS
 #define KVHIP_CG_ENCODE_GROUPS 1024
 #endif
 #ifndef KVHIP_CG_DECODE_GROUPS
-#define KVHIP_CG_DECODE_GROUPS 8192
+#define KVHIP_CG_DECODE_GROUPS (1 << 22)
 #endif
+constexpr int kCgMinmaxGroups = KVHIP_CG_MINMAX_GROUPS;
 constexpr int kCgEncodeGroups = KVHIP_CG_ENCODE_GROUPS;
 constexpr int kCgDecodeGroups = KVHIP_CG_DECODE_GROUPS;
-constexpr int kCgUnroll = 4;
+#ifndef KVHIP_CG_ENCODE_VECS
+#define KVHIP_CG_ENCODE_VECS 4
+#endif
+constexpr int kCgMinmaxVecs = 4;
+constexpr int kCgEncodeVecs = KVHIP_CG_ENCODE_VECS;
+constexpr int kCgDecodeVecs = 4;
+// Histogram copies per wave: lane l counts into copy l % kCgHistCopies, so lanes of one
+// instruction that hit the same bin use different LDS banks.
+constexpr int kCgHistCopies = 4;
 
 // Workspace layout: the 256 bin counters, the per-workgroup (min, max) pairs.
 constexpr int64_t kCgCountsOffset = 0;
 constexpr int64_t kCgPairsOffset = 4096;
 static_assert(kCgCountsOffset + 256 * 8 <= kCgPairsOffset, "workspace layout");
-static_assert(kCgPairsOffset + int64_t{kCgEncodeGroups} * 8 <= kCacheGenWorkspaceBytes, "workspace too small");
+static_assert(kCgPairsOffset + int64_t{kCgMinmaxGroups} * 8 <= kCacheGenWorkspaceBytes, "workspace too small");
 
 template <int IN>
 struct CgIn;
@@ -142,21 +161,22 @@ __global__ __launch_bounds__(kBlockThreads) void cg_minmax_kernel(const uint8_t*
   MinMax m;
   int64_t first_scalar = 0;
   if constexpr (VEC) {
+    constexpr int V = kCgMinmaxVecs;
     const int64_t slots = n / kEps;
-    int64_t s = tid;
-    for (; s + (kCgUnroll - 1) * stride < slots; s += kCgUnroll * stride) {
-      u32x4 v[kCgUnroll];
+    const int64_t per_chunk = int64_t{kBlockThreads} * V;
+    const int64_t lane_off = int64_t{wave_in_block()} * kWave * V + lane_id();
+    for (int64_t c = blockIdx.x; c * per_chunk < slots; c += gridDim.x) {
+      const int64_t base = c * per_chunk + lane_off;
+      const bool full = (c + 1) * per_chunk <= slots;
+      u32x4 v[V];
 #pragma unroll
-      for (int u = 0; u < kCgUnroll; ++u) v[u] = ld16_cached(x + (s + u * stride) * 16);
+      for (int k = 0; k < V; ++k)
+        if (full || base + k * kWave < slots) v[k] = ld16(x + (base + k * kWave) * 16);
 #pragma unroll
-      for (int u = 0; u < kCgUnroll; ++u)
+      for (int k = 0; k < V; ++k)
+        if (full || base + k * kWave < slots)
 #pragma unroll
-        for (int j = 0; j < kEps; ++j) m.fold(cg_elem<IN>(v[u], j));
-    }
-    for (; s < slots; s += stride) {
-      const u32x4 v = ld16_cached(x + s * 16);
-#pragma unroll
-      for (int j = 0; j < kEps; ++j) m.fold(cg_elem<IN>(v, j));
+          for (int j = 0; j < kEps; ++j) m.fold(cg_elem<IN>(v[k], j));
     }
     first_scalar = slots * kEps;
   }
@@ -223,7 +243,7 @@ __device__ __forceinline__ void cg_write_cdf(uint64_t count, int nb, int64_t num
 template <int IN, bool NATIVE, bool HIST, bool VEC>
 __global__ __launch_bounds__(kBlockThreads) void cg_encode_kernel(CgEncodeArgs a) {
   constexpr int kEps = 16 / CgIn<IN>::kBytes;
-  __shared__ uint32_t hist[kWavesPerBlock][256];
+  __shared__ uint32_t hist[kWavesPerBlock][256 * kCgHistCopies];
   const int nb = a.num_bins;
   float mn = a.min_arg, scale = a.scale_arg;
   if constexpr (HIST) {
@@ -245,14 +265,14 @@ __global__ __launch_bounds__(kBlockThreads) void cg_encode_kernel(CgEncodeArgs a
     if (r.mx == r.mn) scale = 0.0f;  // constant tensor: every bin is 0
     if (blockIdx.x == 0 && static_cast<int>(threadIdx.x) < nb)
       a.codebook[threadIdx.x] = cg_codebook(r.mn, r.mx, nb, threadIdx.x);
-    for (int i = threadIdx.x; i < kWavesPerBlock * 256; i += kBlockThreads) (&hist[0][0])[i] = 0;
+    for (int i = threadIdx.x; i < kWavesPerBlock * 256 * kCgHistCopies; i += kBlockThreads) (&hist[0][0])[i] = 0;
     __syncthreads();
   }
   const float top = static_cast<float>(nb - 1);
   const uint32_t itop = static_cast<uint32_t>(nb - 1);
-  uint32_t* my_hist = hist[wave_in_block()];
-  auto count = [&](uint32_t b) {
-    if constexpr (HIST) atomicAdd(&my_hist[b], 1u);
+  uint32_t* my_hist = hist[wave_in_block()] + (lane_id() & (kCgHistCopies - 1));
+  auto count = [&](uint32_t b, uint32_t inc) {
+    if constexpr (HIST) atomicAdd(&my_hist[b * kCgHistCopies], inc);
   };
   const int64_t tid = static_cast<int64_t>(blockIdx.x) * kBlockThreads + threadIdx.x;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlockThreads;
@@ -261,10 +281,18 @@ __global__ __launch_bounds__(kBlockThreads) void cg_encode_kernel(CgEncodeArgs a
     const int64_t slots = a.n / kEps;
     auto emit = [&](int64_t s, const u32x4& v) {
       uint32_t b[kEps];
+      bool same = true;
 #pragma unroll
       for (int j = 0; j < kEps; ++j) {
         b[j] = cg_bin<NATIVE>(cg_elem<IN>(v, j), mn, scale, top, itop);
-        count(b[j]);
+        same &= b[j] == b[0];
+      }
+      // A run of equal bins (constant regions, zero padding) is one LDS update, not kEps.
+      if (same) {
+        count(b[0], kEps);
+      } else {
+#pragma unroll
+        for (int j = 0; j < kEps; ++j) count(b[j], 1u);
       }
       uint8_t* d = a.enc + s * kEps;
       if constexpr (kEps == 8) {
@@ -278,20 +306,37 @@ __global__ __launch_bounds__(kBlockThreads) void cg_encode_kernel(CgEncodeArgs a
         stv<2>(d, static_cast<uint16_t>(b[0] | (b[1] << 8)));
       }
     };
-    int64_t s = tid;
-    for (; s + (kCgUnroll - 1) * stride < slots; s += kCgUnroll * stride) {
-      u32x4 v[kCgUnroll];
+    // Software-pipelined: the next chunk's vectors are loaded before this chunk's bins are
+    // computed and stored, so each wave keeps 2 * V vectors in flight.
+    constexpr int V = kCgEncodeVecs;
+    const int64_t per_chunk = int64_t{kBlockThreads} * V;
+    const int64_t lane_off = int64_t{wave_in_block()} * kWave * V + lane_id();
+    auto load = [&](int64_t c, u32x4* v) {
+      const int64_t base = c * per_chunk + lane_off;
+      const bool full = (c + 1) * per_chunk <= slots;
 #pragma unroll
-      for (int u = 0; u < kCgUnroll; ++u) v[u] = ld16(a.x + (s + u * stride) * 16);
+      for (int k = 0; k < V; ++k)
+        if (full || base + k * kWave < slots) v[k] = ld16(a.x + (base + k * kWave) * 16);
+    };
+    u32x4 cur[V], nxt[V];
+    int64_t c = blockIdx.x;
+    if (c * per_chunk < slots) load(c, cur);
+    for (; c * per_chunk < slots; c += gridDim.x) {
+      const int64_t cn = c + gridDim.x;
+      if (cn * per_chunk < slots) load(cn, nxt);
+      const int64_t base = c * per_chunk + lane_off;
+      const bool full = (c + 1) * per_chunk <= slots;
 #pragma unroll
-      for (int u = 0; u < kCgUnroll; ++u) emit(s + u * stride, v[u]);
+      for (int k = 0; k < V; ++k)
+        if (full || base + k * kWave < slots) emit(base + k * kWave, cur[k]);
+#pragma unroll
+      for (int k = 0; k < V; ++k) cur[k] = nxt[k];
     }
-    for (; s < slots; s += stride) emit(s, ld16(a.x + s * 16));
     first_scalar = slots * kEps;
   }
   for (int64_t i = first_scalar + tid; i < a.n; i += stride) {
     const uint32_t b = cg_bin<NATIVE>(cg_load1<IN>(a.x, i), mn, scale, top, itop);
-    count(b);
+    count(b, 1u);
     a.enc[i] = static_cast<uint8_t>(b);
   }
   if constexpr (HIST) {
@@ -300,7 +345,9 @@ __global__ __launch_bounds__(kBlockThreads) void cg_encode_kernel(CgEncodeArgs a
     if (t < nb) {
       uint32_t sum = 0;
 #pragma unroll
-      for (int w = 0; w < kWavesPerBlock; ++w) sum += hist[w][t];
+      for (int w = 0; w < kWavesPerBlock; ++w)
+#pragma unroll
+        for (int c = 0; c < kCgHistCopies; ++c) sum += hist[w][t * kCgHistCopies + c];
       if (sum != 0)
         atomicAdd(reinterpret_cast<unsigned long long*>(&a.counts[t]), static_cast<unsigned long long>(sum));
     }
@@ -400,15 +447,20 @@ __global__ __launch_bounds__(kBlockThreads) void cg_decode_kernel(CgDecodeArgs a
       }
       stv<16>(a.out + s * 16, o);
     };
-    int64_t s = tid;
-    for (; s + (kCgUnroll - 1) * stride < slots; s += kCgUnroll * stride) {
-      C cw[kCgUnroll];
+    constexpr int V = kCgDecodeVecs;
+    const int64_t per_chunk = int64_t{kBlockThreads} * V;
+    const int64_t lane_off = int64_t{wave_in_block()} * kWave * V + lane_id();
+    for (int64_t ch = blockIdx.x; ch * per_chunk < slots; ch += gridDim.x) {
+      const int64_t base = ch * per_chunk + lane_off;
+      const bool full = (ch + 1) * per_chunk <= slots;
+      C cw[V];
 #pragma unroll
-      for (int u = 0; u < kCgUnroll; ++u) cw[u] = ldv<kCodes>(a.codes + (s + u * stride) * kCodes);
+      for (int k = 0; k < V; ++k)
+        if (full || base + k * kWave < slots) cw[k] = ldv<kCodes>(a.codes + (base + k * kWave) * kCodes);
 #pragma unroll
-      for (int u = 0; u < kCgUnroll; ++u) emit(s + u * stride, cw[u]);
+      for (int k = 0; k < V; ++k)
+        if (full || base + k * kWave < slots) emit(base + k * kWave, cw[k]);
     }
-    for (; s < slots; s += stride) emit(s, ldv<kCodes>(a.codes + s * kCodes));
     first_scalar = slots * kCodes;
   }
   for (int64_t i = first_scalar + tid; i < a.n; i += stride)
@@ -422,8 +474,9 @@ __global__ __launch_bounds__(kBlockThreads) void cg_decode_kernel(CgDecodeArgs a
   }
 }
 
-int cg_groups(int64_t units, int cap) {
-  const int64_t per_group = static_cast<int64_t>(kBlockThreads) * kCgUnroll;
+// Workgroups for `units` vectors (or scalar elements) at `vecs` per thread, at most `cap`.
+int cg_groups(int64_t units, int vecs, int cap) {
+  const int64_t per_group = static_cast<int64_t>(kBlockThreads) * vecs;
   int64_t g = (units + per_group - 1) / per_group;
   if (g < 1) g = 1;
   if (g > cap) g = cap;
@@ -435,17 +488,19 @@ hipError_t encode_typed(const uint8_t* x, int64_t n, int nb, bool native, uint8_
                         uint8_t* ws, hipStream_t stream) {
   constexpr int kEps = 16 / CgIn<IN>::kBytes;
   const bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(enc) % kEps) == 0;
-  const int groups = cg_groups(vec ? n / kEps : n, kCgEncodeGroups);
+  const int64_t units = vec ? n / kEps : n;
+  const int mgroups = cg_groups(units, kCgMinmaxVecs, kCgMinmaxGroups);
+  const int groups = cg_groups(units, kCgEncodeVecs, kCgEncodeGroups);
   uint64_t* counts = reinterpret_cast<uint64_t*>(ws + kCgCountsOffset);
   float2* pairs = reinterpret_cast<float2*>(ws + kCgPairsOffset);
   if (vec)
-    hipLaunchKernelGGL((cg_minmax_kernel<IN, true>), dim3(groups), dim3(kBlockThreads), 0, stream, x, n, pairs, counts);
+    hipLaunchKernelGGL((cg_minmax_kernel<IN, true>), dim3(mgroups), dim3(kBlockThreads), 0, stream, x, n, pairs, counts);
   else
-    hipLaunchKernelGGL((cg_minmax_kernel<IN, false>), dim3(groups), dim3(kBlockThreads), 0, stream, x, n, pairs,
+    hipLaunchKernelGGL((cg_minmax_kernel<IN, false>), dim3(mgroups), dim3(kBlockThreads), 0, stream, x, n, pairs,
                        counts);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  CgEncodeArgs a{x, enc, n, pairs, groups, counts, codebook, nb, 0.0f, 0.0f};
+  CgEncodeArgs a{x, enc, n, pairs, mgroups, counts, codebook, nb, 0.0f, 0.0f};
   if (native) {
     if (vec) hipLaunchKernelGGL((cg_encode_kernel<IN, true, true, true>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
     else hipLaunchKernelGGL((cg_encode_kernel<IN, true, true, false>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
@@ -465,7 +520,7 @@ hipError_t decode_typed(const uint8_t* codes, int64_t n, const uint8_t* table, i
   constexpr int kCodes = 16 / E;
   const bool vec = (reinterpret_cast<uintptr_t>(codes) % kCodes) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
   const bool check = table_len < 256;
-  const int groups = cg_groups(vec ? n / kCodes : n, kCgDecodeGroups);
+  const int groups = cg_groups(vec ? n / kCodes : n, kCgDecodeVecs, kCgDecodeGroups);
   CgDecodeArgs a{codes, out, n, table, table_len, max_code};
   if (vec) {
     if (check) hipLaunchKernelGGL((cg_decode_kernel<E, true, true, false>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
@@ -499,7 +554,7 @@ hipError_t launch_cachegen_bins(const float* x, uint8_t* enc, float min_val, flo
   const uint8_t* xs = reinterpret_cast<const uint8_t*>(x);
   const bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(enc) & 3) == 0;
   CgEncodeArgs a{xs, enc, n, nullptr, 0, nullptr, nullptr, num_bins, min_val, scale};
-  const int groups = cg_groups(vec ? n / 4 : n, kCgEncodeGroups);
+  const int groups = cg_groups(vec ? n / 4 : n, kCgEncodeVecs, kCgEncodeGroups);
   if (vec) hipLaunchKernelGGL((cg_encode_kernel<kCgF32, true, false, true>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
   else hipLaunchKernelGGL((cg_encode_kernel<kCgF32, true, false, false>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
   return hipGetLastError();
@@ -514,7 +569,7 @@ hipError_t launch_cachegen_decode(const uint8_t* codes, int64_t n, const void* t
     if (elem_bytes != 4) return hipErrorInvalidValue;
     const bool vec = (reinterpret_cast<uintptr_t>(codes) & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
     CgDecodeArgs a{codes, o, n, tb, 256, nullptr};
-    const int groups = cg_groups(vec ? n / 4 : n, kCgDecodeGroups);
+    const int groups = cg_groups(vec ? n / 4 : n, kCgDecodeVecs, kCgDecodeGroups);
     if (vec) hipLaunchKernelGGL((cg_decode_kernel<4, true, false, true>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
     else hipLaunchKernelGGL((cg_decode_kernel<4, false, false, true>), dim3(groups), dim3(kBlockThreads), 0, stream, a);
     return hipGetLastError();
