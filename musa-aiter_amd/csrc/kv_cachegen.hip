@@ -67,6 +67,21 @@ constexpr int kCgDecodeVecs = 4;
 // instruction that hit the same bin use different LDS banks.
 constexpr int kCgHistCopies = 4;
 
+// Calls f(k, vector) for the vectors of chunk c below `slots`; a full chunk (all but the last)
+// takes no per-lane bounds test.
+template <int V, class F>
+__device__ __forceinline__ void for_chunk(int64_t c, int64_t per_chunk, int64_t lane_off, int64_t slots, F&& f) {
+  const int64_t base = c * per_chunk + lane_off;
+  if ((c + 1) * per_chunk <= slots) {
+#pragma unroll
+    for (int k = 0; k < V; ++k) f(k, base + k * kWave);
+  } else {
+#pragma unroll
+    for (int k = 0; k < V; ++k)
+      if (base + k * kWave < slots) f(k, base + k * kWave);
+  }
+}
+
 // Workspace layout: the 256 bin counters, the per-workgroup (min, max) pairs.
 constexpr int64_t kCgCountsOffset = 0;
 constexpr int64_t kCgPairsOffset = 4096;
@@ -166,17 +181,12 @@ __global__ __launch_bounds__(kBlockThreads) void cg_minmax_kernel(const uint8_t*
     const int64_t per_chunk = int64_t{kBlockThreads} * V;
     const int64_t lane_off = int64_t{wave_in_block()} * kWave * V + lane_id();
     for (int64_t c = blockIdx.x; c * per_chunk < slots; c += gridDim.x) {
-      const int64_t base = c * per_chunk + lane_off;
-      const bool full = (c + 1) * per_chunk <= slots;
       u32x4 v[V];
+      for_chunk<V>(c, per_chunk, lane_off, slots, [&](int k, int64_t s) { v[k] = ld16(x + s * 16); });
+      for_chunk<V>(c, per_chunk, lane_off, slots, [&](int k, int64_t) {
 #pragma unroll
-      for (int k = 0; k < V; ++k)
-        if (full || base + k * kWave < slots) v[k] = ld16(x + (base + k * kWave) * 16);
-#pragma unroll
-      for (int k = 0; k < V; ++k)
-        if (full || base + k * kWave < slots)
-#pragma unroll
-          for (int j = 0; j < kEps; ++j) m.fold(cg_elem<IN>(v[k], j));
+        for (int j = 0; j < kEps; ++j) m.fold(cg_elem<IN>(v[k], j));
+      });
     }
     first_scalar = slots * kEps;
   }
@@ -209,15 +219,16 @@ __device__ __forceinline__ float cg_codebook(float mn, float mx, int nb, int t) 
                     : __builtin_fmaf(-step, static_cast<float>(nb - 1 - t), mx);
 }
 
+// Clamping is fminf(fmaxf(v, 0), top): fmaxf returns the non-NaN operand, so NaN gives bin 0, and
+// the float -> uint conversion truncates (exact for the rounded torch-path value).
 template <bool NATIVE>
-__device__ __forceinline__ uint32_t cg_bin(float x, float mn, float scale, float top, uint32_t itop) {
+__device__ __forceinline__ uint32_t cg_bin(float x, float mn, float scale, float top) {
   const float t = x - mn;
   if constexpr (NATIVE) {
     const float v = __builtin_fmaf(t, scale, 0.5f);
-    return v >= top ? itop : (v > 0.0f ? static_cast<uint32_t>(v) : 0u);
+    return static_cast<uint32_t>(fminf(fmaxf(v, 0.0f), top));
   } else {
-    const float r = __builtin_rintf(t * scale);
-    return r >= top ? itop : (r > 0.0f ? static_cast<uint32_t>(r) : 0u);
+    return static_cast<uint32_t>(fminf(fmaxf(__builtin_rintf(t * scale), 0.0f), top));
   }
 }
 
@@ -269,7 +280,6 @@ __global__ __launch_bounds__(kBlockThreads) void cg_encode_kernel(CgEncodeArgs a
     __syncthreads();
   }
   const float top = static_cast<float>(nb - 1);
-  const uint32_t itop = static_cast<uint32_t>(nb - 1);
   uint32_t* my_hist = hist[wave_in_block()] + (lane_id() & (kCgHistCopies - 1));
   auto count = [&](uint32_t b, uint32_t inc) {
     if constexpr (HIST) atomicAdd(&my_hist[b * kCgHistCopies], inc);
@@ -284,7 +294,7 @@ __global__ __launch_bounds__(kBlockThreads) void cg_encode_kernel(CgEncodeArgs a
       bool same = true;
 #pragma unroll
       for (int j = 0; j < kEps; ++j) {
-        b[j] = cg_bin<NATIVE>(cg_elem<IN>(v, j), mn, scale, top, itop);
+        b[j] = cg_bin<NATIVE>(cg_elem<IN>(v, j), mn, scale, top);
         same &= b[j] == b[0];
       }
       // A run of equal bins (constant regions, zero padding) is one LDS update, not kEps.
@@ -312,11 +322,7 @@ __global__ __launch_bounds__(kBlockThreads) void cg_encode_kernel(CgEncodeArgs a
     const int64_t per_chunk = int64_t{kBlockThreads} * V;
     const int64_t lane_off = int64_t{wave_in_block()} * kWave * V + lane_id();
     auto load = [&](int64_t c, u32x4* v) {
-      const int64_t base = c * per_chunk + lane_off;
-      const bool full = (c + 1) * per_chunk <= slots;
-#pragma unroll
-      for (int k = 0; k < V; ++k)
-        if (full || base + k * kWave < slots) v[k] = ld16(a.x + (base + k * kWave) * 16);
+      for_chunk<V>(c, per_chunk, lane_off, slots, [&](int k, int64_t s) { v[k] = ld16(a.x + s * 16); });
     };
     u32x4 cur[V], nxt[V];
     int64_t c = blockIdx.x;
@@ -324,18 +330,14 @@ __global__ __launch_bounds__(kBlockThreads) void cg_encode_kernel(CgEncodeArgs a
     for (; c * per_chunk < slots; c += gridDim.x) {
       const int64_t cn = c + gridDim.x;
       if (cn * per_chunk < slots) load(cn, nxt);
-      const int64_t base = c * per_chunk + lane_off;
-      const bool full = (c + 1) * per_chunk <= slots;
-#pragma unroll
-      for (int k = 0; k < V; ++k)
-        if (full || base + k * kWave < slots) emit(base + k * kWave, cur[k]);
+      for_chunk<V>(c, per_chunk, lane_off, slots, [&](int k, int64_t s) { emit(s, cur[k]); });
 #pragma unroll
       for (int k = 0; k < V; ++k) cur[k] = nxt[k];
     }
     first_scalar = slots * kEps;
   }
   for (int64_t i = first_scalar + tid; i < a.n; i += stride) {
-    const uint32_t b = cg_bin<NATIVE>(cg_load1<IN>(a.x, i), mn, scale, top, itop);
+    const uint32_t b = cg_bin<NATIVE>(cg_load1<IN>(a.x, i), mn, scale, top);
     count(b, 1u);
     a.enc[i] = static_cast<uint8_t>(b);
   }
@@ -450,6 +452,7 @@ __global__ __launch_bounds__(kBlockThreads) void cg_decode_kernel(CgDecodeArgs a
     constexpr int V = kCgDecodeVecs;
     const int64_t per_chunk = int64_t{kBlockThreads} * V;
     const int64_t lane_off = int64_t{wave_in_block()} * kWave * V + lane_id();
+    // (A per-lane bounds test on every vector measures faster here than separate full-chunk code.)
     for (int64_t ch = blockIdx.x; ch * per_chunk < slots; ch += gridDim.x) {
       const int64_t base = ch * per_chunk + lane_off;
       const bool full = (ch + 1) * per_chunk <= slots;
