@@ -84,6 +84,11 @@ _SIGNATURES: dict[str, list] = {
                                   _i32, _i32, _c_void_p],
     "musa_aiter_hip_batch_copy_abi_version": [],
     "musa_aiter_hip_runtime_versions": [ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)],
+    # LMCache extension entries (memory, [kvcache0, kvcache1 | host cache pointer array], slots, sizes..., stream)
+    "lmcache_kv_buffer_to_paged_list2_u16": [_c_void_p] * 4 + [_i64] * 7 + [_c_void_p],
+    "lmcache_paged_to_kv_buffer_list2_u16": [_c_void_p] * 4 + [_i64] * 7 + [_c_void_p],
+    "lmcache_kv_buffer_to_paged_two_x_nl_coalesced_u16": [_c_void_p, _u64p, _c_void_p] + [_i64] * 8 + [_c_void_p],
+    "lmcache_paged_to_kv_buffer_two_x_nl_coalesced_u16": [_c_void_p, _u64p, _c_void_p] + [_i64] * 7 + [_c_void_p],
     # CacheGen codec.  Reference entries: (input, encoded, min_val, scale, numel, num_bins, stream) and
     # (encoded, codebook, output, numel, stream).
     "musa_aiter_kv_cachegen_encode_float": [_c_void_p, _c_void_p, ctypes.c_float, ctypes.c_float, _i64, _i64,

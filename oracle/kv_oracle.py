@@ -426,6 +426,25 @@ def buffer_to_two_x_nl(memory: np.ndarray, caches: list[list[np.ndarray]], slots
             cache[block[keep], offset[keep]] = values[keep]
 
 
+def native_gather_rows(cache_rows: np.ndarray, slots: np.ndarray, out_rows: np.ndarray, skip: int = 0) -> None:
+    """The reference's native token-row gathers for one buffer plane (kv_transfer_float.mu:2233-2308,
+    :2518-2560): row ``skip + i`` (when inside the plane) gets slot row ``slots[i]``, or zeros for a
+    negative slot; the plane's other rows are untouched.  ``cache_rows`` is the cache as
+    [num_slots, row]; callers map slots past the cache to -1, as the kernels skip them."""
+    for i, s in enumerate(np.asarray(slots, dtype=np.int64).tolist()):
+        if 0 <= skip + i < out_rows.shape[0]:
+            out_rows[skip + i] = cache_rows[s] if s >= 0 else 0
+
+
+def native_scatter_rows(in_rows: np.ndarray, slots: np.ndarray, cache_rows: np.ndarray, skip: int = 0) -> None:
+    """The native token-row scatters for one plane: slot row ``slots[i]`` gets buffer row
+    ``skip + i``; negative slots are skipped and a repeated slot keeps the last token."""
+    slots = np.asarray(slots, dtype=np.int64)
+    keep = last_writer_mask(slots)
+    for i in np.nonzero(keep)[0]:
+        cache_rows[slots[i]] = in_rows[skip + i]
+
+
 def list_to_buffer(kvcaches: list[np.ndarray], memory: np.ndarray, slots: np.ndarray) -> None:
     """_lmcache_kv_paged_to_buffer_list reference path (lmcache_kv_transfer.py:451-460)."""
     memory[...] = 0

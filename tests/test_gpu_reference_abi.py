@@ -339,18 +339,8 @@ def test_lmcache_six_d_and_mla_entries(suffix, dtype):
 
 # ---- LMCache token-row planes: 2 x NL, coalesced, list, list2, MLA list (lmcache_kv_transfer.py:699-993) --
 
-def _gather_rows(cache_rows: np.ndarray, slots: np.ndarray, out_rows: np.ndarray, skip: int) -> None:
-    """The native gathers: rows [skip, skip + T) of one buffer plane get the slot rows (zeros for a
-    skipped slot); the plane's other rows are untouched."""
-    for i, s in enumerate(slots.tolist()):
-        if 0 <= skip + i < out_rows.shape[0]:
-            out_rows[skip + i] = cache_rows[s] if s >= 0 else 0
-
-
-def _scatter_rows(in_rows: np.ndarray, slots: np.ndarray, cache_rows: np.ndarray, skip: int) -> None:
-    keep = ko.last_writer_mask(slots)
-    for i in np.nonzero(keep)[0]:
-        cache_rows[slots[i]] = in_rows[skip + i]
+_gather_rows = ko.native_gather_rows
+_scatter_rows = ko.native_scatter_rows
 
 
 @pytest.mark.parametrize("suffix,dtype", [("float", torch.float32), ("u16", torch.float16)])

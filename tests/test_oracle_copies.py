@@ -216,3 +216,37 @@ def test_strided_blocks_closed_forms():
     for layer in range(nl):
         s0 = (layer * staging_tokens + offset) * row
         assert np.array_equal(back[s0:s0 + 3 * bs * row], staging[s0:s0 + 3 * bs * row])
+
+
+@pytest.mark.parametrize("kind", ["skips", "duplicates"])
+def test_native_row_functions_agree_with_the_python_paths(kind):
+    """With no prefix skip and a buffer of exactly T rows, the native row gather / scatter equal the
+    reference's Python-path restatements (which zero the whole buffer first); with a skip, rows
+    outside [skip, skip + T) stay untouched and row skip + i is token i."""
+    rng = np.random.default_rng(3)
+    nl, bs, nh, hs, t = 2, 4, 2, 3, 29
+    slots, nb = make_slots(kind, rng, block_size=bs, tokens=t)
+    caches = [[_rand(rng, (nb, bs, nh, hs)) for _ in range(nl)] for _ in range(2)]
+    want = np.empty((2, nl, t, nh * hs), np.uint16)
+    ko.two_x_nl_to_buffer(caches, want, slots)
+    got = _rand(rng, (2, nl, t, nh * hs))
+    for a in range(2):
+        for layer in range(nl):
+            ko.native_gather_rows(caches[a][layer].reshape(nb * bs, -1), slots, got[a, layer])
+    assert np.array_equal(got, want)
+    mem = _rand(rng, (2, nl, t + 5, nh * hs))
+    want_c = [[c.copy() for c in g] for g in caches]
+    ko.buffer_to_two_x_nl(mem, want_c, slots, 5)
+    got_c = [[c.copy() for c in g] for g in caches]
+    for a in range(2):
+        for layer in range(nl):
+            ko.native_scatter_rows(mem[a, layer], slots, got_c[a][layer].reshape(nb * bs, -1), 5)
+            assert np.array_equal(got_c[a][layer], want_c[a][layer])
+    # prefix skip: only rows [skip, skip + T) of the plane change, clipped at the plane's end
+    plane = _rand(rng, (t + 3, nh * hs))
+    before = plane.copy()
+    rows = caches[0][0].reshape(nb * bs, -1)
+    ko.native_gather_rows(rows, slots, plane, 6)
+    assert np.array_equal(plane[:6], before[:6])
+    for i in range(t + 3 - 6):
+        assert np.array_equal(plane[6 + i], rows[slots[i]] if slots[i] >= 0 else np.zeros(nh * hs, np.uint16))
