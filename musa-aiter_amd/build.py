@@ -1,7 +1,9 @@
-"""Build libmusa_aiter_kv_hip.so for gfx950 with hipcc (in-tree).
+"""Build libmusa_aiter_kv_hip.so for gfx950 with hipcc, and the host helper module, in-tree.
 
-The library is written to ``musa_aiter/_lib/`` next to the Python host layer
-so that it travels with the source tree.  Usage::
+Both are written to ``musa_aiter/_lib/`` next to the Python host layer so that
+they travel with the source tree: the HIP kernel library (C ABI) and
+``_kv_host``, a small CPython extension built with g++ against torch's headers
+that checks lists of cache tensors and packs their addresses.  Usage::
 
     python musa-aiter_amd/build.py            # build (always recompiles)
     python musa-aiter_amd/build.py --check    # print the hipcc command only
@@ -15,6 +17,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
@@ -64,15 +67,46 @@ def _compile(src: Path, obj: Path) -> None:
         sys.stderr.write("\n".join(noise) + "\n")
 
 
+HOST_SOURCE = "kv_host.cpp"
+HOST_MODULE = "_kv_host"
+
+
+def host_module_path() -> Path:
+    return OUT_DIR / (HOST_MODULE + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def _build_host() -> Path:
+    """The host helper extension: g++ against the installed torch's headers and libraries."""
+    from torch.utils import cpp_extension
+
+    import torch
+
+    out = host_module_path()
+    tmp = out.with_name(out.name + ".tmp")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-shared", "-fPIC", "-std=c++17", "-Wall",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}", f"-DTORCH_EXTENSION_NAME={HOST_MODULE}",
+           f"-I{sysconfig.get_paths()['include']}", *[f"-I{p}" for p in cpp_extension.include_paths()],
+           str(CSRC / HOST_SOURCE), "-o", str(tmp),
+           *[f"-L{p}" for p in cpp_extension.library_paths()], "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"host module build failed:\n{' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 def build(verbose: bool = False) -> Path:
     OUT_DIR.mkdir(parents=True, exist_ok=True)
     obj_dir = ROOT / "_build"
     obj_dir.mkdir(exist_ok=True)
     objs = [obj_dir / (Path(s).stem + ".o") for s in SOURCES]
-    with concurrent.futures.ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
+    with concurrent.futures.ThreadPoolExecutor(max_workers=len(SOURCES) + 1) as pool:
+        host = pool.submit(_build_host)
         futures = [pool.submit(_compile, CSRC / s, o) for s, o in zip(SOURCES, objs)]
         for fut in futures:
             fut.result()
+        host_path = host.result()
     out = OUT_DIR / LIB_NAME
     tmp = out.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
@@ -82,6 +116,7 @@ def build(verbose: bool = False) -> Path:
     os.replace(tmp, out)
     if verbose:
         print(f"built {out}")
+        print(f"built {host_path}")
     return out
 
 

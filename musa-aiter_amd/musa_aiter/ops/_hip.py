@@ -10,6 +10,8 @@ which keeps torch's stream handles and allocations valid in the kernels.
 from __future__ import annotations
 
 import ctypes
+import importlib.util
+import sysconfig
 import threading
 from pathlib import Path
 
@@ -17,6 +19,7 @@ import torch
 
 LIB_NAME = "libmusa_aiter_kv_hip.so"
 LIB_PATH = Path(__file__).resolve().parent.parent / "_lib" / LIB_NAME
+HOST_PATH = LIB_PATH.parent / ("_kv_host" + sysconfig.get_config_var("EXT_SUFFIX"))
 BACKEND = "rocm-hip"
 
 _c_void_p = ctypes.c_void_p
@@ -112,6 +115,7 @@ _RESTYPES = {
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
 _fns: dict[str, object] = {}
+_host = None
 
 
 class HipBackendError(RuntimeError):
@@ -145,6 +149,33 @@ def fn(name: str):
     return _fns[name]
 
 
+def host():
+    """The ``_kv_host`` helper module (tensor-list checks and address tables); raise if not built."""
+    global _host
+    if _host is not None:
+        return _host
+    with _lock:
+        if _host is None:
+            if not HOST_PATH.exists():
+                raise HipBackendError(
+                    f"{HOST_PATH.name} is not built (expected at {HOST_PATH}); "
+                    "run `python musa-aiter_amd/build.py`"
+                )
+            spec = importlib.util.spec_from_file_location("_kv_host", HOST_PATH)
+            mod = importlib.util.module_from_spec(spec)
+            spec.loader.exec_module(mod)
+            _host = mod
+    return _host
+
+
+def u64_packed(packed: bytes) -> ctypes.Array:
+    """A ctypes uint64 array over addresses packed by the host module."""
+    n = len(packed) // 8
+    if n == 0:
+        return (ctypes.c_uint64 * 1)()
+    return (ctypes.c_uint64 * n).from_buffer_copy(packed)
+
+
 def is_available() -> bool:
     try:
         library()
@@ -171,6 +202,13 @@ def ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
 def u64_array(values) -> ctypes.Array:
     vals = [int(v) for v in values]
     return (ctypes.c_uint64 * max(1, len(vals)))(*vals)
+
+
+def _as_u64(values) -> ctypes.Array | None:
+    """Addresses as a ctypes uint64 array: None, a ready array, or a sequence of ints."""
+    if values is None or isinstance(values, ctypes.Array):
+        return values
+    return u64_array(values)
 
 
 def paged_tiles(
@@ -240,8 +278,8 @@ def copy_rows(
 ) -> None:
     if num_rows_out <= 0 or num_planes <= 0 or row_bytes <= 0:
         return
-    src_arr = u64_array(src_planes) if src_planes is not None else None
-    dst_arr = u64_array(dst_planes) if dst_planes is not None else None
+    src_arr = _as_u64(src_planes)
+    dst_arr = _as_u64(dst_planes)
     with torch.cuda.device(device):
         rc = fn("musa_aiter_hip_copy_rows")(
             src_arr, dst_arr, ptr(src_table), ptr(dst_table), int(num_planes),

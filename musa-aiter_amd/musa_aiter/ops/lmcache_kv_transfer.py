@@ -134,7 +134,10 @@ def _contains_nested_cache_list(kvcaches: list[Any]) -> bool:
 
 def _validate_two_x_nl_contract(memory_tensor: torch.Tensor, kvcaches: list[list[torch.Tensor]],
                                 slot_mapping: torch.Tensor, skip_prefix_n_tokens: int, block_size: int,
-                                num_heads: int, head_size: int) -> None:
+                                num_heads: int, head_size: int) -> tuple[int, bytes]:
+    """The reference's 2 x NL contract (lmcache_kv_transfer.py:323-413).  Returns, for the caches in
+    [K layers, V layers] order, the index of the first non-contiguous one (-1 if none) and their
+    addresses packed as uint64, from one pass of the host module over the 2 x NL tensors."""
     name = "LMCache TWO_X_NL_X_NB_BS_NH_HS"
     if memory_tensor.dim() != 4 or int(memory_tensor.shape[0]) != 2:
         raise ValueError(f"{name} memory_tensor must be [2, NL, T, NH*HS]")
@@ -164,17 +167,20 @@ def _validate_two_x_nl_contract(memory_tensor: torch.Tensor, kvcaches: list[list
     expected = (num_blocks, block_size, num_heads, head_size)
     if num_blocks <= 0:
         raise ValueError(f"{name} num_blocks must be positive")
-    for kv_axis, layers in enumerate(kvcaches):
-        for layer, cache in enumerate(layers):
-            if not isinstance(cache, torch.Tensor) or cache.shape != expected:
-                raise ValueError(f"{name} cache[{kv_axis}][{layer}] must have shape {expected}")
-            if cache.dtype != memory_tensor.dtype:
-                raise ValueError(f"{name} cache dtype must match memory_tensor")
-            if cache.device != memory_tensor.device:
-                raise ValueError(f"{name} caches and memory_tensor must share a device")
+    # Per cache, in [K layers, V layers] order: type and shape, then dtype, then device.
+    h = _hip.host()
+    status, index, noncontig, packed = h.check_tensors(kvcaches[0] + kvcaches[1], expected, memory_tensor)
+    if status != h.OK:
+        kv_axis, layer = divmod(index, num_layers)
+        if status == h.SHAPE:
+            raise ValueError(f"{name} cache[{kv_axis}][{layer}] must have shape {expected}")
+        if status == h.DTYPE:
+            raise ValueError(f"{name} cache dtype must match memory_tensor")
+        raise ValueError(f"{name} caches and memory_tensor must share a device")
     if slot_mapping.device != memory_tensor.device:
         raise ValueError(f"{name} slot_mapping and data tensors must share a device")
     _validate_slots(slot_mapping, num_tokens=int(slot_mapping.numel()), num_blocks=num_blocks, block_size=block_size)
+    return noncontig, packed
 
 
 def _validate_non_mla_list_contract(memory_tensor: torch.Tensor, kvcaches: list[torch.Tensor],
@@ -271,6 +277,11 @@ class _Buffer:
     def plane(self, axis: int, layer: int) -> int:
         return self._base + axis * self._axis_bytes + layer * self._layer_bytes
 
+    def all_planes(self, axes: int, layers: int):
+        """Every (axis, layer) plane in row-major order, as a ctypes uint64 array."""
+        return _hip.u64_packed(_hip.host().strided_table(self._base, self._axis_bytes, axes, self._layer_bytes,
+                                                           layers))
+
     @property
     def token_stride_bytes(self) -> int:
         w = self.work
@@ -281,19 +292,26 @@ class _Buffer:
             self.user.copy_(self.work)
 
 
-def _rows_gather(op: str, *, device: torch.device, cache_planes: list[int], buf: _Buffer,
-                 buf_planes: list[tuple[int, int]], slots: torch.Tensor, num_tokens: int, memory_tokens: int,
+def _buf_planes(buf: _Buffer, buf_planes):
+    """Plane addresses of ``buf``: a list of (axis, layer) pairs, or a ready ctypes array."""
+    if isinstance(buf_planes, list):
+        return [buf.plane(a, l) for a, l in buf_planes]
+    return buf_planes
+
+
+def _rows_gather(op: str, *, device: torch.device, cache_planes, buf: _Buffer,
+                 buf_planes, slots: torch.Tensor, num_tokens: int, memory_tokens: int,
                  slot_rows: int, row_bytes: int, cache_stride: int) -> None:
-    _hip.copy_rows(op=op, device=device, src_planes=cache_planes, dst_planes=[buf.plane(a, l) for a, l in buf_planes],
+    _hip.copy_rows(op=op, device=device, src_planes=cache_planes, dst_planes=_buf_planes(buf, buf_planes),
                    num_planes=len(cache_planes), src_idx=slots, dst_idx=None, num_tokens=num_tokens,
                    num_rows_out=memory_tokens, src_rows=slot_rows, dst_rows=memory_tokens, row_bytes=row_bytes,
                    src_stride=cache_stride, dst_stride=buf.token_stride_bytes, zero_invalid=True)
 
 
-def _rows_scatter(op: str, *, device: torch.device, cache_planes: list[int], buf: _Buffer,
-                  buf_planes: list[tuple[int, int]], slots: torch.Tensor, num_tokens: int, memory_tokens: int,
+def _rows_scatter(op: str, *, device: torch.device, cache_planes, buf: _Buffer,
+                  buf_planes, slots: torch.Tensor, num_tokens: int, memory_tokens: int,
                   skip: int, slot_rows: int, row_bytes: int, cache_stride: int) -> None:
-    _hip.copy_rows(op=op, device=device, src_planes=[buf.plane(a, l) for a, l in buf_planes], dst_planes=cache_planes,
+    _hip.copy_rows(op=op, device=device, src_planes=_buf_planes(buf, buf_planes), dst_planes=cache_planes,
                    num_planes=len(cache_planes), src_idx=None, dst_idx=slots, num_tokens=num_tokens,
                    num_rows_out=num_tokens, src_offset=skip, src_rows=memory_tokens, dst_rows=slot_rows,
                    row_bytes=row_bytes, src_stride=buf.token_stride_bytes, dst_stride=cache_stride,
@@ -316,11 +334,10 @@ def lmcache_kv_buffer_to_paged_two_x_nl(memory_tensor: torch.Tensor, kvcaches: l
                                         num_heads: int, head_size: int) -> bool:
     """Scatter ``memory[:, :, skip:skip+T]`` into SGLang-MP ``2 x NL x [NB, BS, NH, HS]`` caches, one launch."""
     op = "lmcache_kv_buffer_to_paged_two_x_nl"
-    _validate_two_x_nl_contract(memory_tensor, kvcaches, slot_mapping, skip_prefix_n_tokens, block_size, num_heads,
-                                head_size)
+    noncontig, packed = _validate_two_x_nl_contract(memory_tensor, kvcaches, slot_mapping, skip_prefix_n_tokens,
+                                                    block_size, num_heads, head_size)
     start = time.perf_counter()
     device = memory_tensor.device
-    caches = kvcaches[0] + kvcaches[1]
     # The contract has checked every cache's dtype and device against memory_tensor.
     _same_device(op, device, slot_mapping)
     num_layers = len(kvcaches[0])
@@ -328,11 +345,12 @@ def lmcache_kv_buffer_to_paged_two_x_nl(memory_tensor: torch.Tensor, kvcaches: l
     elt = _elt(op, memory_tensor)
     row = num_heads * head_size * elt
     buf = _Buffer(memory_tensor, writable=False, initialise=False)
-    planes = [(a, l) for a in range(2) for l in range(num_layers)]
-    _rows_scatter(op, device=device, cache_planes=[_contig_cache(op, c).data_ptr() for c in caches], buf=buf,
-                  buf_planes=planes, slots=_device_slots(slot_mapping, device), num_tokens=num_tokens,
-                  memory_tokens=int(memory_tensor.shape[2]), skip=int(skip_prefix_n_tokens),
-                  slot_rows=int(caches[0].shape[0]) * block_size, row_bytes=row, cache_stride=row)
+    if noncontig >= 0:
+        raise ValueError(f"{op}: paged caches must be contiguous tensors")
+    _rows_scatter(op, device=device, cache_planes=_hip.u64_packed(packed), buf=buf,
+                  buf_planes=buf.all_planes(2, num_layers), slots=_device_slots(slot_mapping, device),
+                  num_tokens=num_tokens, memory_tokens=int(memory_tensor.shape[2]), skip=int(skip_prefix_n_tokens),
+                  slot_rows=int(kvcaches[0][0].shape[0]) * block_size, row_bytes=row, cache_stride=row)
     _emit(op, memory_tensor, f"gfx950 row scatter, {2 * num_layers} planes in one launch")
     _log_timing(op, (time.perf_counter() - start) * 1e6, tokens=num_tokens, layers=num_layers)
     return True
@@ -343,10 +361,10 @@ def lmcache_kv_paged_to_buffer_two_x_nl(kvcaches: list[list[torch.Tensor]], memo
                                         head_size: int) -> bool:
     """Gather SGLang-MP caches into ``[2, NL, T, NH*HS]``; the whole buffer is overwritten (zeros where skipped)."""
     op = "lmcache_kv_paged_to_buffer_two_x_nl"
-    _validate_two_x_nl_contract(memory_tensor, kvcaches, slot_mapping, 0, block_size, num_heads, head_size)
+    noncontig, packed = _validate_two_x_nl_contract(memory_tensor, kvcaches, slot_mapping, 0, block_size, num_heads,
+                                                    head_size)
     start = time.perf_counter()
     device = memory_tensor.device
-    caches = kvcaches[0] + kvcaches[1]
     # The contract has checked every cache's dtype and device against memory_tensor.
     _same_device(op, device, slot_mapping)
     num_layers = len(kvcaches[0])
@@ -354,11 +372,12 @@ def lmcache_kv_paged_to_buffer_two_x_nl(kvcaches: list[list[torch.Tensor]], memo
     elt = _elt(op, memory_tensor)
     row = num_heads * head_size * elt
     buf = _Buffer(memory_tensor, writable=True, initialise=False)
-    planes = [(a, l) for a in range(2) for l in range(num_layers)]
-    _rows_gather(op, device=device, cache_planes=[_contig_cache(op, c).data_ptr() for c in caches], buf=buf,
-                 buf_planes=planes, slots=_device_slots(slot_mapping, device), num_tokens=num_tokens,
-                 memory_tokens=int(memory_tensor.shape[2]), slot_rows=int(caches[0].shape[0]) * block_size,
-                 row_bytes=row, cache_stride=row)
+    if noncontig >= 0:
+        raise ValueError(f"{op}: paged caches must be contiguous tensors")
+    _rows_gather(op, device=device, cache_planes=_hip.u64_packed(packed), buf=buf,
+                 buf_planes=buf.all_planes(2, num_layers), slots=_device_slots(slot_mapping, device),
+                 num_tokens=num_tokens, memory_tokens=int(memory_tensor.shape[2]),
+                 slot_rows=int(kvcaches[0][0].shape[0]) * block_size, row_bytes=row, cache_stride=row)
     buf.finish()
     _emit(op, memory_tensor, f"gfx950 row gather, {2 * num_layers} planes in one launch")
     _log_timing(op, (time.perf_counter() - start) * 1e6, tokens=num_tokens, layers=num_layers)
