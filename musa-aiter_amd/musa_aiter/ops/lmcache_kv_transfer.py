@@ -26,6 +26,7 @@ from __future__ import annotations
 import os
 import sys
 import time
+from array import array
 from typing import Any
 
 import torch
@@ -183,9 +184,24 @@ def _validate_two_x_nl_contract(memory_tensor: torch.Tensor, kvcaches: list[list
     return noncontig, packed
 
 
+def _fast_cache_list(kvcaches: list[torch.Tensor], rank: int, nb_dim: int, shape_of, memory_tensor: torch.Tensor):
+    """Packed addresses of a per-layer cache list when every cache has the list's shape
+    (``shape_of(num_blocks)``), memory_tensor's dtype and device and is contiguous, from one pass of
+    the host module; None otherwise, and the caller runs its per-cache checks, which raise the
+    reference's error for the first offending cache."""
+    if not isinstance(kvcaches, list) or not kvcaches:
+        return None
+    first = kvcaches[0]
+    if not isinstance(first, torch.Tensor) or first.dim() != rank:
+        return None
+    h = _hip.host()
+    status, _, noncontig, packed = h.check_tensors(kvcaches, shape_of(int(first.shape[nb_dim])), memory_tensor)
+    return packed if status == h.OK and noncontig < 0 else None
+
+
 def _validate_non_mla_list_contract(memory_tensor: torch.Tensor, kvcaches: list[torch.Tensor],
                                     slot_mapping: torch.Tensor, block_size: int, num_heads: int,
-                                    head_size: int) -> None:
+                                    head_size: int, *, per_cache: bool = True) -> None:
     if memory_tensor.dim() != 4 or int(memory_tensor.shape[0]) != 2:
         raise ValueError("LMCache list non-MLA memory_tensor rank must be 4: [2, NL, T, NH*HS]")
     if len(kvcaches) != int(memory_tensor.shape[1]):
@@ -195,7 +211,7 @@ def _validate_non_mla_list_contract(memory_tensor: torch.Tensor, kvcaches: list[
     if not kvcaches:
         raise ValueError("LMCache list non-MLA kvcaches must not be empty")
     num_blocks = int(kvcaches[0].shape[1])
-    for kvcache in kvcaches:
+    for kvcache in (kvcaches if per_cache else ()):
         if (kvcache.dim() != 5 or int(kvcache.shape[0]) != 2 or int(kvcache.shape[2]) != block_size
                 or int(kvcache.shape[3]) != num_heads or int(kvcache.shape[4]) != head_size):
             raise ValueError("LMCache list non-MLA kvcache rank must be 5: [2, NB, BS, NH, HS]")
@@ -205,7 +221,7 @@ def _validate_non_mla_list_contract(memory_tensor: torch.Tensor, kvcaches: list[
 
 
 def _validate_mla_list_contract(memory_tensor: torch.Tensor, kvcaches: list[torch.Tensor], slot_mapping: torch.Tensor,
-                                block_size: int, head_size: int) -> None:
+                                block_size: int, head_size: int, *, per_cache: bool = True) -> None:
     if memory_tensor.dim() != 4 or int(memory_tensor.shape[0]) != 1:
         raise ValueError("LMCache list MLA memory_tensor rank must be 4: [1, NL, T, HS]")
     if len(kvcaches) != int(memory_tensor.shape[1]):
@@ -213,7 +229,7 @@ def _validate_mla_list_contract(memory_tensor: torch.Tensor, kvcaches: list[torc
     if not kvcaches:
         raise ValueError("LMCache list MLA kvcaches must not be empty")
     num_blocks = int(kvcaches[0].shape[0])
-    for kvcache in kvcaches:
+    for kvcache in (kvcaches if per_cache else ()):
         if kvcache.dim() != 3 or int(kvcache.shape[1]) != block_size or int(kvcache.shape[2]) != head_size:
             raise ValueError("LMCache list MLA kvcache rank must be 3: [NB, BS, HS]")
         if int(kvcache.shape[0]) != num_blocks:
@@ -399,17 +415,38 @@ def _list_planes(kvcaches: list[torch.Tensor], op: str) -> tuple[list[int], list
     return cache_planes, buf_planes
 
 
+def _list_cache_planes(op: str, kvcaches: list[torch.Tensor], packed, memory_tensor: torch.Tensor,
+                       slot_mapping: torch.Tensor, buf: "_Buffer"):
+    """(cache planes, buffer planes, element bytes) of a [2, NB, BS, NH, HS] cache list: K planes of
+    every layer, then V planes.  With ``packed`` (every cache already checked by the host module)
+    the planes come from the packed addresses; otherwise the reference's device, dtype and
+    contiguity checks run cache by cache."""
+    device = memory_tensor.device
+    if packed is None:
+        _same_device(op, device, slot_mapping, *kvcaches)
+        elt = _elt(op, memory_tensor, *kvcaches)
+        cache_planes, buf_planes = _list_planes(kvcaches, op)
+        return cache_planes, buf_planes, elt
+    _same_device(op, device, slot_mapping)
+    elt = _elt(op, memory_tensor)
+    plane_bytes = kvcaches[0][0].numel() * elt
+    ptrs = array("Q", packed)
+    planes = array("Q", ptrs)
+    planes.extend(p + plane_bytes for p in ptrs)
+    return _hip.u64_packed(planes.tobytes()), buf.all_planes(2, len(kvcaches)), elt
+
+
 def _lmcache_kv_buffer_to_paged_list(memory_tensor: torch.Tensor, kvcaches: list[torch.Tensor],
                                      slot_mapping: torch.Tensor, skip_prefix_n_tokens: int, block_size: int,
                                      num_heads: int, head_size: int) -> bool:
     op = "lmcache_kv_buffer_to_paged"
-    _validate_non_mla_list_contract(memory_tensor, kvcaches, slot_mapping, block_size, num_heads, head_size)
+    packed = _fast_cache_list(kvcaches, 5, 1, lambda nb: (2, nb, block_size, num_heads, head_size), memory_tensor)
+    _validate_non_mla_list_contract(memory_tensor, kvcaches, slot_mapping, block_size, num_heads, head_size,
+                                    per_cache=packed is None)
     device = memory_tensor.device
-    _same_device(op, device, slot_mapping, *kvcaches)
-    elt = _elt(op, memory_tensor, *kvcaches)
-    row = num_heads * head_size * elt
-    cache_planes, buf_planes = _list_planes(kvcaches, op)
     buf = _Buffer(memory_tensor, writable=False, initialise=False)
+    cache_planes, buf_planes, elt = _list_cache_planes(op, kvcaches, packed, memory_tensor, slot_mapping, buf)
+    row = num_heads * head_size * elt
     _rows_scatter(op, device=device, cache_planes=cache_planes, buf=buf, buf_planes=buf_planes,
                   slots=_device_slots(slot_mapping, device), num_tokens=int(slot_mapping.numel()),
                   memory_tokens=int(memory_tensor.shape[2]), skip=int(skip_prefix_n_tokens),
@@ -422,13 +459,13 @@ def _lmcache_kv_paged_to_buffer_list(kvcaches: list[torch.Tensor], memory_tensor
                                      slot_mapping: torch.Tensor, block_size: int, num_heads: int,
                                      head_size: int) -> bool:
     op = "lmcache_kv_paged_to_buffer"
-    _validate_non_mla_list_contract(memory_tensor, kvcaches, slot_mapping, block_size, num_heads, head_size)
+    packed = _fast_cache_list(kvcaches, 5, 1, lambda nb: (2, nb, block_size, num_heads, head_size), memory_tensor)
+    _validate_non_mla_list_contract(memory_tensor, kvcaches, slot_mapping, block_size, num_heads, head_size,
+                                    per_cache=packed is None)
     device = memory_tensor.device
-    _same_device(op, device, slot_mapping, *kvcaches)
-    elt = _elt(op, memory_tensor, *kvcaches)
-    row = num_heads * head_size * elt
-    cache_planes, buf_planes = _list_planes(kvcaches, op)
     buf = _Buffer(memory_tensor, writable=True, initialise=False)
+    cache_planes, buf_planes, elt = _list_cache_planes(op, kvcaches, packed, memory_tensor, slot_mapping, buf)
+    row = num_heads * head_size * elt
     _rows_gather(op, device=device, cache_planes=cache_planes, buf=buf, buf_planes=buf_planes,
                  slots=_device_slots(slot_mapping, device), num_tokens=int(slot_mapping.numel()),
                  memory_tokens=int(memory_tensor.shape[2]), slot_rows=int(kvcaches[0].shape[1]) * block_size,
@@ -576,14 +613,23 @@ def _lmcache_mla_buffer_to_paged_list(memory_tensor: torch.Tensor, kvcaches: lis
                                       slot_mapping: torch.Tensor, skip_prefix_n_tokens: int, block_size: int,
                                       head_size: int) -> bool:
     op = "lmcache_mla_buffer_to_paged"
-    _validate_mla_list_contract(memory_tensor, kvcaches, slot_mapping, block_size, head_size)
+    packed = _fast_cache_list(kvcaches, 3, 0, lambda nb: (nb, block_size, head_size), memory_tensor)
+    _validate_mla_list_contract(memory_tensor, kvcaches, slot_mapping, block_size, head_size,
+                                per_cache=packed is None)
     device = memory_tensor.device
-    _same_device(op, device, slot_mapping, *kvcaches)
-    elt = _elt(op, memory_tensor, *kvcaches)
-    row = head_size * elt
     buf = _Buffer(memory_tensor, writable=False, initialise=False)
-    _rows_scatter(op, device=device, cache_planes=[_contig_cache(op, c).data_ptr() for c in kvcaches], buf=buf,
-                  buf_planes=[(0, l) for l in range(len(kvcaches))], slots=_device_slots(slot_mapping, device),
+    if packed is None:
+        _same_device(op, device, slot_mapping, *kvcaches)
+        elt = _elt(op, memory_tensor, *kvcaches)
+        cache_planes = [_contig_cache(op, c).data_ptr() for c in kvcaches]
+        buf_planes = [(0, l) for l in range(len(kvcaches))]
+    else:
+        _same_device(op, device, slot_mapping)
+        elt = _elt(op, memory_tensor)
+        cache_planes, buf_planes = _hip.u64_packed(packed), buf.all_planes(1, len(kvcaches))
+    row = head_size * elt
+    _rows_scatter(op, device=device, cache_planes=cache_planes, buf=buf,
+                  buf_planes=buf_planes, slots=_device_slots(slot_mapping, device),
                   num_tokens=int(slot_mapping.numel()), memory_tokens=int(memory_tensor.shape[2]),
                   skip=int(skip_prefix_n_tokens), slot_rows=int(kvcaches[0].shape[0]) * block_size, row_bytes=row,
                   cache_stride=row)
@@ -594,15 +640,25 @@ def _lmcache_mla_buffer_to_paged_list(memory_tensor: torch.Tensor, kvcaches: lis
 def _lmcache_mla_paged_to_buffer_list(kvcaches: list[torch.Tensor], memory_tensor: torch.Tensor,
                                       slot_mapping: torch.Tensor, block_size: int, head_size: int) -> bool:
     op = "lmcache_mla_paged_to_buffer"
-    _validate_mla_list_contract(memory_tensor, kvcaches, slot_mapping, block_size, head_size)
+    packed = _fast_cache_list(kvcaches, 3, 0, lambda nb: (nb, block_size, head_size), memory_tensor)
+    _validate_mla_list_contract(memory_tensor, kvcaches, slot_mapping, block_size, head_size,
+                                per_cache=packed is None)
     device = memory_tensor.device
-    _same_device(op, device, slot_mapping, *kvcaches)
-    elt = _elt(op, memory_tensor, *kvcaches)
-    row = head_size * elt
     buf = _Buffer(memory_tensor, writable=True, initialise=False)
-    caches = [c if c.is_contiguous() else c.contiguous() for c in kvcaches]
-    _rows_gather(op, device=device, cache_planes=[c.data_ptr() for c in caches], buf=buf,
-                 buf_planes=[(0, l) for l in range(len(kvcaches))], slots=_device_slots(slot_mapping, device),
+    caches = kvcaches  # keeps contiguous copies alive until the launch
+    if packed is None:
+        _same_device(op, device, slot_mapping, *kvcaches)
+        elt = _elt(op, memory_tensor, *kvcaches)
+        caches = [c if c.is_contiguous() else c.contiguous() for c in kvcaches]
+        cache_planes = [c.data_ptr() for c in caches]
+        buf_planes = [(0, l) for l in range(len(kvcaches))]
+    else:
+        _same_device(op, device, slot_mapping)
+        elt = _elt(op, memory_tensor)
+        cache_planes, buf_planes = _hip.u64_packed(packed), buf.all_planes(1, len(kvcaches))
+    row = head_size * elt
+    _rows_gather(op, device=device, cache_planes=cache_planes, buf=buf,
+                 buf_planes=buf_planes, slots=_device_slots(slot_mapping, device),
                  num_tokens=int(slot_mapping.numel()), memory_tokens=int(memory_tensor.shape[2]),
                  slot_rows=int(kvcaches[0].shape[0]) * block_size, row_bytes=row, cache_stride=row)
     buf.finish()

@@ -100,6 +100,33 @@ def test_lmcache_contracts():
         musa_aiter.lmcache_kv_buffer_to_paged(memory, [torch.zeros(2, 1, 2, 1, 4)], torch.tensor([0, 1]), 0, 2)
 
 
+def test_cache_list_checks_keep_the_reference_order():
+    """The per-cache checks of the list paths run in the reference's order (every shape, then
+    devices, then dtypes, then contiguity) whichever cache fails first; the host module's single
+    pass only decides whether they need to run."""
+    nb, bs, nh, hs = 3, 2, 1, 4
+    mem = torch.zeros(2, 3, 5, nh * hs)
+    good = torch.zeros(2, nb, bs, nh, hs)
+    wrong_dtype = torch.zeros(2, nb, bs, nh, hs, dtype=torch.float16)
+    wrong_shape = torch.zeros(2, nb, bs + 1, nh, hs)
+    slots = torch.tensor([0, 1])
+    with pytest.raises(ValueError, match="rank must be 5"):  # the shape error of cache 2 wins over cache 1's dtype
+        musa_aiter.lmcache_kv_paged_to_buffer([good, wrong_dtype, wrong_shape], mem, slots, bs, nh, hs)
+    with pytest.raises(RuntimeError, match="ROCm GPU device"):  # all caches valid: the CPU device is rejected
+        musa_aiter.lmcache_kv_paged_to_buffer([good, good, good], mem, slots, bs, nh, hs)
+    mla_mem = torch.zeros(1, 2, 5, hs)
+    mla_good, mla_bad = torch.zeros(nb, bs, hs), torch.zeros(nb, bs, hs + 1)
+    with pytest.raises(ValueError, match="rank must be 3"):
+        musa_aiter.lmcache_mla_paged_to_buffer([mla_good.half(), mla_bad], mla_mem, slots, bs, hs)
+    k = [torch.zeros(nb, bs, nh, hs) for _ in range(2)]
+    v = [torch.zeros(nb, bs, nh, hs), torch.zeros(nb, bs, nh, hs + 1)]
+    with pytest.raises(ValueError, match=r"cache\[1\]\[1\] must have shape"):
+        musa_aiter.lmcache_kv_paged_to_buffer_two_x_nl([k, v], torch.zeros(2, 2, 5, nh * hs), slots, bs, nh, hs)
+    v[1] = torch.zeros(nb, bs, nh, hs, dtype=torch.float16)
+    with pytest.raises(ValueError, match="cache dtype must match memory_tensor"):
+        musa_aiter.lmcache_kv_paged_to_buffer_two_x_nl([k, v], torch.zeros(2, 2, 5, nh * hs), slots, bs, nh, hs)
+
+
 def test_byte_row_contracts():
     src = torch.zeros(4, 8, dtype=torch.uint8)
     with pytest.raises(TypeError):
