@@ -1,6 +1,6 @@
 #!/usr/bin/env python3
 """KV-copy throughput on one MI355X: BASELINE.json configs[1] (headline) plus configs 1, 3, 4, 5, the dense preload,
-the SGLang HiCache transfers and the LMCache host <-> device copy batches.
+the SGLang HiCache transfers, the LMCache host <-> device copy batches and the CacheGen codec.
 
 Headline workload: 32 layers of Llama-3-8B KV caches
 [8192 blocks, 16, 8 kv-heads, 128] bf16 (paged layout [NB, NH, HD, BS]),
@@ -25,7 +25,8 @@ The other configs are reported under ``extra`` with the same byte convention
 (config 6: the block-table / CSR dense preload for attention and whole-block
 copies; config 7: SGLang HiCache layer-first / page-first transfers; config 8:
 LMCache host <-> device copy batches, rated against the 64 GB/s PCIe 5.0 x16
-link instead of HBM; none is a BASELINE config).  Their launches are short
+link instead of HBM; config 9: the CacheGen-style codec; none is a BASELINE
+config).  Their launches are short
 (0.01-0.8 ms), so they are timed in batches of back-to-back launches between
 two events (host launch overhead hidden behind device work); each is also
 checked outside the timed region, by torch indexing, by the reference's FP8
@@ -743,6 +744,55 @@ def bench_batch_copy() -> dict:
     return out
 
 
+def bench_cachegen() -> dict:
+    """CacheGen-style codec (kv_cachegen_encode / kv_cachegen_decode, 256 bins) on a 32-layer K/V tensor of
+    4096 tokens x 8 heads x 128 ([32, 2, 4096, 8, 128], 268,435,456 elements), in bf16 and float32.
+
+    Bytes: encode reads the input twice (range pass, bin pass) and writes one byte per element; decode reads
+    one byte and writes one output element per element (float32 codebook; bf16 output for the bf16 line).
+    Parity, outside the timed region: the bins and the codebook against the reference's torch expressions
+    (kv_transfer.py:1155-1158) evaluated by torch on this GPU, the CDF against cumsum(bincount) / numel
+    within one float32 ulp (torch accumulates and divides differently on the GPU), and decode against
+    ``codebook[encoded]``."""
+    import musa_aiter
+
+    dev = torch.device("cuda", 0)
+    shape = (NL, 2, 4096, NH, HD)
+    n = int(np.prod(shape))
+    out = {"shape": list(shape), "elements": n, "num_bins": 256}
+    g = torch.Generator(device=dev).manual_seed(9)
+    base = torch.randn(shape, generator=g, device=dev)
+    for dtype, label, dec_dtype in ((torch.bfloat16, "bf16", torch.bfloat16), (torch.float32, "float32", None)):
+        x = base.to(dtype)
+        enc, book, cdf = musa_aiter.kv_cachegen_encode(x, num_bins=256)
+        work = x.float()
+        mn, mx = work.min(), work.max()
+        ref = torch.round((work - mn) * ((256 - 1) / (mx - mn))).clamp_(0, 255).to(torch.uint8)
+        ref_book = torch.linspace(mn.item(), mx.item(), 256, dtype=torch.float32, device=dev)
+        counts = torch.bincount(ref.reshape(-1).long(), minlength=256).double()
+        ref_cdf = torch.cat([torch.zeros(1, dtype=torch.float64, device=dev), torch.cumsum(counts, 0) / n]).float()
+        ulp = torch.finfo(torch.float32).eps
+        dec = musa_aiter.kv_cachegen_decode(enc, book, dtype=dec_dtype)
+        ref_dec = book[enc.long()] if dec_dtype is None else book.to(dec_dtype)[enc.long()]
+        parity = {"bins": bool(torch.equal(enc, ref)), "codebook_vs_torch_linspace": bool(torch.equal(book, ref_book)),
+                  "cdf_within_1ulp": bool(((cdf - ref_cdf).abs() <= ulp * ref_cdf.abs()).all()),
+                  "decode": bool(torch.equal(dec, ref_dec))}
+        del work, ref, ref_dec, dec
+        eb = x.element_size()
+        enc_ms = batched_ms(lambda: musa_aiter.kv_cachegen_encode(x, num_bins=256), launches=10, reps=5)
+        dec_ms = batched_ms(lambda: musa_aiter.kv_cachegen_decode(enc, book, dtype=dec_dtype), launches=10, reps=5)
+        ob = 4 if dec_dtype is None else torch.tensor([], dtype=dec_dtype).element_size()
+        out[label] = {"encode": {**rate(n * (2 * eb + 1), enc_ms), "bytes": n * (2 * eb + 1)},
+                      "decode": {**rate(n * (1 + ob), dec_ms), "bytes": n * (1 + ob),
+                                 "output_dtype": "float32" if dec_dtype is None else "bfloat16"},
+                      "parity": parity}
+        del x, enc, book, cdf
+        torch.cuda.empty_cache()
+    log("cachegen: " + ", ".join(f"{d} {k} {out[d][k]['gbs']:.0f} GB/s" for d in ("bf16", "float32")
+                                 for k in ("encode", "decode")))
+    return out
+
+
 def device_copy(mib: int, reps: int = 5) -> dict:
     """Plain device-to-device copy of a known size (torch ``copy_``): the achievable copy rate of this
     GPU and the calibration kernel for the FETCH_SIZE / WRITE_SIZE traffic counters."""
@@ -791,10 +841,10 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--configs", default="1,2,3,4,5,6,7,8",
+    parser.add_argument("--configs", default="1,2,3,4,5,6,7,8,9",
                         help="comma list of BASELINE configs to run (2, the headline, always runs; 6 = dense "
                              "preload and block copies; 7 = SGLang HiCache transfers; 8 = LMCache host <-> "
-                             "device copy batches)")
+                             "device copy batches; 9 = CacheGen codec)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--copy-mib", type=int, default=1024,
                         help="size of the plain device copy timed first (0 = skip)")
@@ -826,7 +876,7 @@ def main() -> int:
     runners = {1: ("config1_fp16_single_layer_gather", bench_config1), 3: ("config3_fp8", bench_config3),
                4: ("config4_lmcache_two_x_nl", bench_config4), 5: ("config5_mla_rows", bench_config5),
                6: ("dense_preload_and_block_copies", bench_dense), 7: ("sglang_hicache_transfers", bench_hicache),
-               8: ("lmcache_host_device_batches", bench_batch_copy)}
+               8: ("lmcache_host_device_batches", bench_batch_copy), 9: ("cachegen_codec", bench_cachegen)}
     for cfg in sorted(configs - {2}):
         if cfg not in runners:
             continue
