@@ -36,10 +36,50 @@ struct ClaimScratch {
 
 std::mutex g_claim_mu;
 std::map<std::pair<int, uintptr_t>, ClaimScratch>* g_claims = nullptr;
+// Arrays of calls captured into HIP graphs, per (device, capturing stream).
+// A graph keeps the address it was captured with, so an array that is
+// outgrown is left allocated rather than freed.
+std::map<std::pair<int, uintptr_t>, ClaimScratch>* g_graph_claims = nullptr;
+
+// Claim pass of a call being captured into a graph.  The epoch scheme of the
+// eager path would freeze the capture-time epoch into every replay, where
+// claims left by earlier replays carry the same epoch and can win.  Captured
+// calls instead zero the entries they compete for and then claim with epoch 1,
+// which is correct whatever the array held before; growing the array neither
+// synchronises nor is recorded (allocation runs in relaxed capture mode).
+hipError_t prepare_graph_claims(const kvhip::ClaimSource& src, int64_t n, int64_t rows, hipStream_t stream, int dev,
+                                const uint64_t** owner, uint32_t* epoch) {
+  if (g_graph_claims == nullptr) g_graph_claims = new std::map<std::pair<int, uintptr_t>, ClaimScratch>();
+  ClaimScratch& cs = (*g_graph_claims)[{dev, reinterpret_cast<uintptr_t>(stream)}];
+  if (cs.capacity < rows) {
+    int64_t cap = cs.capacity * 2;
+    if (cap < rows) cap = rows;
+    if (cap < (int64_t{1} << 16)) cap = int64_t{1} << 16;
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    hipError_t err = hipThreadExchangeStreamCaptureMode(&mode);
+    if (err != hipSuccess) return err;
+    uint64_t* p = nullptr;
+    const hipError_t merr = hipMalloc(reinterpret_cast<void**>(&p), static_cast<size_t>(cap) * sizeof(uint64_t));
+    err = hipThreadExchangeStreamCaptureMode(&mode);
+    if (merr != hipSuccess) return merr;
+    if (err != hipSuccess) return err;
+    cs.owner = p;
+    cs.capacity = cap;
+  }
+  hipError_t err = kvhip::launch_claim(src, n, rows, cs.owner, 1, stream, true);
+  if (err != hipSuccess) return err;
+  err = kvhip::launch_claim(src, n, rows, cs.owner, 1, stream, false);
+  if (err != hipSuccess) return err;
+  *owner = cs.owner;
+  *epoch = 1;
+  return hipSuccess;
+}
 
 // Runs the claim pass for the `n` destinations of `src` into a destination
 // of `rows` rows and returns the tag array and epoch the copy kernel must
-// check.  A call that cannot collide (n <= 1) skips the pass.
+// check.  A call that cannot collide (n <= 1) skips the pass.  Calls on one
+// stream share that stream's array; graphs captured on one stream share its
+// capture array, so their replays must not overlap one another.
 hipError_t prepare_claims(const kvhip::ClaimSource& src, int64_t n, int64_t rows, hipStream_t stream,
                           const uint64_t** owner, uint32_t* epoch) {
   *owner = nullptr;
@@ -48,7 +88,11 @@ hipError_t prepare_claims(const kvhip::ClaimSource& src, int64_t n, int64_t rows
   int dev = 0;
   hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess) return err;
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  err = hipStreamIsCapturing(stream, &capture);
+  if (err != hipSuccess) return err;
   std::lock_guard<std::mutex> lock(g_claim_mu);
+  if (capture != hipStreamCaptureStatusNone) return prepare_graph_claims(src, n, rows, stream, dev, owner, epoch);
   if (g_claims == nullptr) g_claims = new std::map<std::pair<int, uintptr_t>, ClaimScratch>();
   ClaimScratch& cs = (*g_claims)[{dev, reinterpret_cast<uintptr_t>(stream)}];
   if (cs.capacity < rows) {

@@ -93,9 +93,10 @@ struct ClaimSource {
 };
 
 // Marks, for every destination row, the last token (in token order) that
-// writes it.
+// writes it.  With `reset` it instead zeroes the entries of the rows the
+// tokens write, so that a following claim pass needs no cleared array.
 hipError_t launch_claim(const ClaimSource& src, int64_t n, int64_t rows, uint64_t* owner, uint32_t epoch,
-                        hipStream_t stream);
+                        hipStream_t stream, bool reset = false);
 hipError_t launch_fill_u64(uint64_t* p, int64_t n, uint64_t value, hipStream_t stream);
 
 // Block-granular byte copies between an LMCache staging object and padded pages.

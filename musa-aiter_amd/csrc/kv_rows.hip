@@ -190,7 +190,7 @@ __global__ __launch_bounds__(kBlockThreads) void row_flat_kernel(const RowArgs a
 __global__ __launch_bounds__(kBlockThreads) void claim_kernel(const int64_t* idx, int64_t idx_stride,
                                                               const BlockTableSlots bt, const int64_t* src_idx,
                                                               int64_t src_rows, int64_t n, int64_t rows,
-                                                              uint64_t* owner, uint32_t epoch) {
+                                                              uint64_t* owner, uint32_t epoch, int reset) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
   // A token whose source is skipped never writes, so it claims nothing.
@@ -200,6 +200,11 @@ __global__ __launch_bounds__(kBlockThreads) void claim_kernel(const int64_t* idx
   }
   const int64_t s = bt.block_tables != nullptr ? block_table_slot(bt, i) : idx[i * idx_stride];
   if (s < 0 || s >= rows) return;
+  // The reset pass clears exactly the entries the claim pass will compete for.
+  if (reset) {
+    owner[s] = 0;
+    return;
+  }
   atomicMax(reinterpret_cast<unsigned long long*>(owner + s), static_cast<unsigned long long>(claim_tag(epoch, i)));
 }
 
@@ -388,12 +393,12 @@ hipError_t launch_row_copy(const RowCopyParams& p, hipStream_t stream) {
 }
 
 hipError_t launch_claim(const ClaimSource& src, int64_t n, int64_t rows, uint64_t* owner, uint32_t epoch,
-                        hipStream_t stream) {
+                        hipStream_t stream, bool reset) {
   if (n <= 0) return hipSuccess;
   if ((src.bt.block_tables == nullptr && src.idx == nullptr) || src.idx_stride < 1) return hipErrorInvalidValue;
   const int64_t blocks = (n + kBlockThreads - 1) / kBlockThreads;
   hipLaunchKernelGGL(claim_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kBlockThreads), 0, stream, src.idx,
-                     src.idx_stride, src.bt, src.src_idx, src.src_rows, n, rows, owner, epoch);
+                     src.idx_stride, src.bt, src.src_idx, src.src_rows, n, rows, owner, epoch, reset ? 1 : 0);
   return hipGetLastError();
 }
 
