@@ -1071,8 +1071,8 @@ int musa_aiter_hip_runtime_versions(int* runtime_version, int* driver_version) {
 // Byte ranges between pinned or pageable host memory and device memory of the
 // current device, all in one direction (0: host -> device, 1: device -> host),
 // submitted on `stream`.  mode 0 and 1: ranges whose host side is pinned host
-// memory with a device mapping go through one batch-copy kernel launch per 96
-// ranges on at most kBatchGroups (mode 0) or kOverlapGroups workgroups (mode 1,
+// memory with a device mapping go through the batch-copy kernel (one launch for
+// the whole batch) on at most kBatchGroups (mode 0) or kOverlapGroups workgroups (mode 1,
 // which leaves nearly all compute units to concurrent kernels); the other
 // ranges go through hipMemcpyAsync.  mode 2: every range goes through
 // hipMemcpyAsync.  Measured on MI355X, a few dozen workgroups keep enough
@@ -1081,6 +1081,82 @@ int musa_aiter_hip_runtime_versions(int* runtime_version, int* driver_version) {
 // workgroup per tile, while 4 KiB ranges need at least 32.
 constexpr uint32_t kBatchGroups = 64;
 constexpr uint32_t kOverlapGroups = 16;
+
+// Batches of more than kBatchCopyMax ranges take one launch over per-tile
+// descriptors written into pinned host memory.  Each (device, stream) has a
+// ring of kDescSlots such buffers; a slot is rewritten only after the event
+// recorded behind its last launch has completed, so several batches can be
+// queued on the stream without waiting.
+constexpr int kDescSlots = 4;
+
+struct DescSlot {
+  uint64_t* host = nullptr;
+  size_t capacity = 0;  // uint64 values
+  hipEvent_t done = nullptr;
+  bool pending = false;
+};
+
+struct DescRing {
+  DescSlot slots[kDescSlots];
+  int next = 0;
+};
+
+std::mutex g_desc_mu;
+std::map<std::pair<int, uintptr_t>, DescRing>* g_desc_rings = nullptr;
+
+hipError_t batch_copy_by_descriptors(const std::vector<uint64_t>& src, const std::vector<uint64_t>& dst,
+                                     const std::vector<uint64_t>& size, uint32_t max_groups, hipStream_t stream) {
+  const uint64_t tiles = kvhip::batch_copy_tile_count(size.data(), static_cast<int64_t>(size.size()));
+  if (tiles == 0) return hipSuccess;
+  if (tiles > 0x7FFFFFFFu) return hipErrorInvalidValue;
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  std::lock_guard<std::mutex> lock(g_desc_mu);
+  if (g_desc_rings == nullptr) g_desc_rings = new std::map<std::pair<int, uintptr_t>, DescRing>();
+  DescRing& ring = (*g_desc_rings)[{dev, reinterpret_cast<uintptr_t>(stream)}];
+  DescSlot& slot = ring.slots[ring.next];
+  ring.next = (ring.next + 1) % kDescSlots;
+  if (slot.pending) {
+    err = hipEventSynchronize(slot.done);
+    if (err != hipSuccess) return err;
+    slot.pending = false;
+  }
+  if (slot.done == nullptr) {
+    err = hipEventCreateWithFlags(&slot.done, hipEventDisableTiming);
+    if (err != hipSuccess) {
+      slot.done = nullptr;
+      return err;
+    }
+  }
+  const size_t need = static_cast<size_t>(tiles) * 3;
+  if (slot.capacity < need) {
+    if (slot.host != nullptr) {
+      err = hipHostFree(slot.host);
+      slot.host = nullptr;
+      slot.capacity = 0;
+      if (err != hipSuccess) return err;
+    }
+    size_t cap = need < 8192 ? 8192 : need;
+    err = hipHostMalloc(reinterpret_cast<void**>(&slot.host), cap * sizeof(uint64_t),
+                        hipHostMallocMapped | hipHostMallocCoherent);
+    if (err != hipSuccess) {
+      slot.host = nullptr;
+      return err;
+    }
+    slot.capacity = cap;
+  }
+  kvhip::batch_copy_fill_desc(src.data(), dst.data(), size.data(), static_cast<int64_t>(size.size()), slot.host);
+  void* mapped = nullptr;
+  err = hipHostGetDevicePointer(&mapped, slot.host, 0);
+  if (err != hipSuccess) return err;
+  err = kvhip::launch_batch_copy_desc(static_cast<const uint64_t*>(mapped), tiles, max_groups, stream);
+  if (err != hipSuccess) return err;
+  err = hipEventRecord(slot.done, stream);
+  if (err != hipSuccess) return err;
+  slot.pending = true;
+  return hipSuccess;
+}
 
 int musa_aiter_hip_batch_copy(void* const* dsts, const void* const* srcs, const uint64_t* sizes, int64_t count,
                               int direction, int mode, void* stream) {
@@ -1117,8 +1193,17 @@ int musa_aiter_hip_batch_copy(void* const* dsts, const void* const* srcs, const 
       if (err != hipSuccess) return err;
     }
   }
-  return kvhip::launch_batch_copy(ks.data(), kd.data(), kn.data(), static_cast<int64_t>(ks.size()),
-                                  mode == 1 ? kOverlapGroups : kBatchGroups, as_stream(stream));
+  const uint32_t groups = mode == 1 ? kOverlapGroups : kBatchGroups;
+  if (ks.size() > static_cast<size_t>(kvhip::kBatchCopyMax)) {
+    // A graph capture would keep the descriptor slot's address while the ring
+    // reuses it, so captured batches stay on the kernel-argument launches.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    const hipError_t err = hipStreamIsCapturing(as_stream(stream), &capture);
+    if (err != hipSuccess) return err;
+    if (capture == hipStreamCaptureStatusNone) return batch_copy_by_descriptors(ks, kd, kn, groups, as_stream(stream));
+  }
+  return kvhip::launch_batch_copy(ks.data(), kd.data(), kn.data(), static_cast<int64_t>(ks.size()), groups,
+                                  as_stream(stream));
 }
 
 // ----- CacheGen-style codec (kv_transfer_float.mu:828-898, kv_transfer.py:1048-1215) ----------

@@ -1,10 +1,11 @@
 // Batched host <-> device byte copies for MI355X (gfx950): the LMCache staging
 // step on the far side of the KV buffers.
 //
-// One launch moves up to kBatchCopyMax byte ranges.  Every range is cut into
-// 64 KiB tiles; workgroups stride over the tiles (a workgroup finds a tile's
-// range from the tile prefix in the kernel arguments), so a batch of many
-// small chunks costs one launch instead of one runtime call per chunk.  The
+// Every range is cut into 64 KiB tiles and workgroups stride over the tiles,
+// so a batch of many small chunks costs one launch instead of one runtime
+// call per chunk.  Up to kBatchCopyMax ranges travel in the kernel arguments
+// (a workgroup finds a tile's range from the tile prefix there); larger
+// batches use one descriptor per tile in pinned host memory.  The
 // grid holds at most `max_groups` workgroups: the host link needs far fewer
 // requests in flight than the chip can issue, and a small grid also leaves
 // the other compute units to concurrent kernels.  The host side of every
@@ -53,6 +54,44 @@ __device__ __forceinline__ void copy_tile(const uint8_t* s, uint8_t* d, uint32_t
   for (uint32_t t = head + body * VEC + tid; t < n; t += kBlockThreads) d[t] = s[t];
 }
 
+// Copies n bytes at the widest access to which source and destination are equally aligned.
+__device__ __forceinline__ void copy_range(uint64_t src, uint64_t dst, uint32_t n) {
+  const uint8_t* s = reinterpret_cast<const uint8_t*>(src);
+  uint8_t* d = reinterpret_cast<uint8_t*>(dst);
+  const uint32_t rel = static_cast<uint32_t>((src ^ dst) & 15u);
+  if (rel == 0) copy_tile<16>(s, d, n);
+  else if ((rel & 7u) == 0) copy_tile<8>(s, d, n);
+  else if ((rel & 3u) == 0) copy_tile<4>(s, d, n);
+  else if ((rel & 1u) == 0) copy_tile<2>(s, d, n);
+  else copy_tile<1>(s, d, n);
+}
+
+// One (src, dst, bytes) descriptor per tile, read from pinned host memory
+// through its device mapping.  A workgroup loads the descriptor of its next
+// tile before copying the current one, so the read's link latency overlaps
+// the copy.  The grid never exceeds `tiles`.
+__global__ __launch_bounds__(kBlockThreads) void batch_copy_desc_kernel(const uint64_t* desc, uint32_t tiles) {
+  uint32_t tile = blockIdx.x;
+  uint64_t s = desc[3 * static_cast<uint64_t>(tile)];
+  uint64_t d = desc[3 * static_cast<uint64_t>(tile) + 1];
+  uint64_t n = desc[3 * static_cast<uint64_t>(tile) + 2];
+  while (true) {
+    const uint32_t next = tile + gridDim.x;
+    uint64_t ns = 0, nd = 0, nn = 0;
+    if (next < tiles) {
+      ns = desc[3 * static_cast<uint64_t>(next)];
+      nd = desc[3 * static_cast<uint64_t>(next) + 1];
+      nn = desc[3 * static_cast<uint64_t>(next) + 2];
+    }
+    copy_range(s, d, static_cast<uint32_t>(n));
+    if (next >= tiles) break;
+    tile = next;
+    s = ns;
+    d = nd;
+    n = nn;
+  }
+}
+
 __global__ __launch_bounds__(kBlockThreads) void batch_copy_kernel(const BatchCopyArgs a) {
   const uint32_t tiles = a.tile_end[a.count - 1];
   for (uint32_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
@@ -67,18 +106,39 @@ __global__ __launch_bounds__(kBlockThreads) void batch_copy_kernel(const BatchCo
     const uint64_t off = static_cast<uint64_t>(tile - first) * kTileBytes;
     const uint64_t left = a.size[lo] - off;
     const uint32_t n = static_cast<uint32_t>(left < kTileBytes ? left : kTileBytes);
-    const uint8_t* s = reinterpret_cast<const uint8_t*>(a.src[lo]) + off;
-    uint8_t* d = reinterpret_cast<uint8_t*>(a.dst[lo]) + off;
-    const uint32_t rel = static_cast<uint32_t>((a.src[lo] ^ a.dst[lo]) & 15u);
-    if (rel == 0) copy_tile<16>(s, d, n);
-    else if ((rel & 7u) == 0) copy_tile<8>(s, d, n);
-    else if ((rel & 3u) == 0) copy_tile<4>(s, d, n);
-    else if ((rel & 1u) == 0) copy_tile<2>(s, d, n);
-    else copy_tile<1>(s, d, n);
+    copy_range(a.src[lo] + off, a.dst[lo] + off, n);
   }
 }
 
 }  // namespace
+
+uint64_t batch_copy_tile_count(const uint64_t* size, int64_t count) {
+  uint64_t tiles = 0;
+  for (int64_t i = 0; i < count; ++i) tiles += (size[i] + kTileBytes - 1) / kTileBytes;
+  return tiles;
+}
+
+void batch_copy_fill_desc(const uint64_t* src, const uint64_t* dst, const uint64_t* size, int64_t count,
+                          uint64_t* desc) {
+  for (int64_t i = 0; i < count; ++i) {
+    for (uint64_t off = 0; off < size[i]; off += kTileBytes) {
+      const uint64_t left = size[i] - off;
+      desc[0] = src[i] + off;
+      desc[1] = dst[i] + off;
+      desc[2] = left < kTileBytes ? left : kTileBytes;
+      desc += 3;
+    }
+  }
+}
+
+hipError_t launch_batch_copy_desc(const uint64_t* desc, uint64_t tiles, uint32_t max_groups, hipStream_t stream) {
+  if (tiles == 0) return hipSuccess;
+  if (desc == nullptr || tiles > 0x7FFFFFFFu) return hipErrorInvalidValue;
+  const uint32_t groups = (max_groups != 0 && tiles > max_groups) ? max_groups : static_cast<uint32_t>(tiles);
+  hipLaunchKernelGGL(batch_copy_desc_kernel, dim3(groups), dim3(kBlockThreads), 0, stream, desc,
+                     static_cast<uint32_t>(tiles));
+  return hipGetLastError();
+}
 
 hipError_t launch_batch_copy(const uint64_t* src, const uint64_t* dst, const uint64_t* size, int64_t count,
                              uint32_t max_groups, hipStream_t stream) {

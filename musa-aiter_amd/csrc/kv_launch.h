@@ -128,6 +128,14 @@ constexpr int kBatchCopyMax = 96;
 // on at most `max_groups` workgroups per launch (0: one per 64 KiB tile).
 hipError_t launch_batch_copy(const uint64_t* src, const uint64_t* dst, const uint64_t* size, int64_t count,
                              uint32_t max_groups, hipStream_t stream);
+// Per-tile descriptors for batches larger than kBatchCopyMax ranges: the
+// number of 64 KiB tiles of the ranges, the (src, dst, bytes) triple of each
+// tile written into host memory `desc` (3 values per tile), and one launch
+// over descriptors that the device reads at `desc` (a pinned, mapped copy).
+uint64_t batch_copy_tile_count(const uint64_t* size, int64_t count);
+void batch_copy_fill_desc(const uint64_t* src, const uint64_t* dst, const uint64_t* size, int64_t count,
+                          uint64_t* desc);
+hipError_t launch_batch_copy_desc(const uint64_t* desc, uint64_t tiles, uint32_t max_groups, hipStream_t stream);
 
 // ----- CacheGen-style uniform-bin codec ------------------------------------------------
 

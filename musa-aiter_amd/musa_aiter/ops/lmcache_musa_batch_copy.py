@@ -13,10 +13,9 @@ module ``musa_aiter/ops/lmcache_musa_batch_copy.py`` (0.5.0):
   ``max_batch_entries`` entries (default 1024, ``MUSA_AITER_LMCACHE_BATCH_MAX_ENTRIES``).
 
 Each chunk becomes one ``musa_aiter_hip_batch_copy`` call of ``libmusa_aiter_kv_hip.so``: ranges
-whose host side is pinned memory move in one batch-copy kernel launch per 96 ranges (the GPU
-reads or writes the host memory over its mapping; with ``prefer_overlap_with_compute=True`` the
-kernel runs on at most 16 workgroups instead of 64, so that concurrent kernels keep the other compute
-units),
+whose host side is pinned memory move in one batch-copy kernel launch per chunk (the GPU reads or
+writes the host memory over its mapping; with ``prefer_overlap_with_compute=True`` the kernel runs
+on at most 16 workgroups instead of 64, so that concurrent kernels keep the other compute units);
 pageable ranges go through ``hipMemcpyAsync``.
 """
 

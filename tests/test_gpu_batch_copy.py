@@ -4,7 +4,8 @@ Restates the reference's native tests (op_tests/test_lmcache_musa_batch_copy_mus
 ROCm and adds random batches through every submission path (the batch-copy kernel over pinned
 host memory on its normal and its bounded grid, one hipMemcpyAsync per range), pageable host
 memory, every relative alignment of source and destination, ranges crossing the kernel's 64 KiB
-tiles, more ranges than one launch holds, and the C-ABI entry called directly.
+tiles, more ranges than the kernel arguments hold (one launch over per-tile descriptors in a ring of
+pinned buffers, with batches queued back to back), and the C-ABI entry called directly.
 """
 
 from __future__ import annotations
@@ -212,3 +213,35 @@ def test_tensors_stay_alive_until_the_stream_passes():
     torch.cuda.synchronize()
     assert len(extension.in_flight) == 0
     assert torch.equal(device.cpu(), host)
+
+
+@pytest.mark.parametrize("direction", ["h2d", "d2h"])
+def test_queued_large_batches_reuse_descriptor_slots(direction):
+    # Batches of more than 96 ranges run as one launch over per-tile descriptors in a ring of pinned
+    # buffers; twelve batches queued without a sync cycle the ring three times, each with its own data.
+    rng = np.random.default_rng(21 if direction == "h2d" else 22)
+    calls, count, size = 12, 200, 4096 + 24
+    dev = torch.zeros(calls * count * size, dtype=torch.uint8, device=DEV)
+    hosts = [_host(count * size, seed=100 + c) for c in range(calls)]
+    if direction == "d2h":
+        dev.copy_(torch.randint(0, 256, dev.shape, dtype=torch.uint8, device=DEV))
+        hosts = [torch.zeros(count * size, dtype=torch.uint8).pin_memory() for _ in range(calls)]
+    torch.cuda.synchronize()
+    perms = [rng.permutation(count) for _ in range(calls)]
+    for c in range(calls):
+        dev_off = [int(c * count * size + p * size) for p in perms[c]]
+        host_off = [i * size for i in range(count)]
+        if direction == "h2d":
+            ok = musa_aiter.lmcache_musa_memcpy_batch_async([dev] * count, [hosts[c]] * count, [size] * count,
+                                                            destination_offsets=dev_off, source_offsets=host_off)
+        else:
+            ok = musa_aiter.lmcache_musa_memcpy_batch_async([hosts[c]] * count, [dev] * count, [size] * count,
+                                                            destination_offsets=host_off, source_offsets=dev_off)
+        assert ok
+    torch.cuda.synchronize()
+    got_dev = dev.cpu().numpy()
+    for c in range(calls):
+        h = hosts[c].numpy()
+        for i, p in enumerate(perms[c]):
+            d0 = c * count * size + p * size
+            assert np.array_equal(got_dev[d0:d0 + size], h[i * size:(i + 1) * size]), (c, i)
