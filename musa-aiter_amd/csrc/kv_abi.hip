@@ -1158,6 +1158,52 @@ hipError_t batch_copy_by_descriptors(const std::vector<uint64_t>& src, const std
   return hipSuccess;
 }
 
+// The last pinned host allocation seen in one batch call: host range [lo, hi) and
+// the device address of lo.  Batches usually take many ranges from one staging
+// buffer, so one range lookup replaces a pointer query per range.
+struct PinnedRange {
+  uint64_t lo = 0, hi = 0, dev = 0;
+};
+
+// Device-side address of `host` when it lies in pinned host memory with a
+// device mapping.  A pointer outside the cached range is queried; its
+// allocation's range is then cached, but only when the device address of the
+// range's last byte, queried on its own, lies at the same offset.
+bool map_pinned(const void* host, PinnedRange& cache, uint64_t* mapped) {
+  const uint64_t h = reinterpret_cast<uint64_t>(host);
+  if (h >= cache.lo && h < cache.hi) {
+    *mapped = cache.dev + (h - cache.lo);
+    return true;
+  }
+  auto query = [](const void* p, uint64_t* dev) {
+    hipPointerAttribute_t attr{};
+    if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+      (void)hipGetLastError();  // pageable memory: clear the query's error
+      return false;
+    }
+    if (attr.type != hipMemoryTypeHost || attr.devicePointer == nullptr || attr.hostPointer == nullptr) return false;
+    *dev = reinterpret_cast<uint64_t>(attr.devicePointer) +
+           (reinterpret_cast<uint64_t>(p) - reinterpret_cast<uint64_t>(attr.hostPointer));
+    return true;
+  };
+  if (!query(host, mapped)) return false;
+  void* start = nullptr;
+  size_t size = 0;
+  hipDeviceptr_t hp = const_cast<void*>(host);
+  if (hipPointerGetAttribute(&start, HIP_POINTER_ATTRIBUTE_RANGE_START_ADDR, hp) != hipSuccess ||
+      hipPointerGetAttribute(&size, HIP_POINTER_ATTRIBUTE_RANGE_SIZE, hp) != hipSuccess) {
+    (void)hipGetLastError();
+    return true;
+  }
+  const uint64_t lo = reinterpret_cast<uint64_t>(start);
+  if (size == 0 || h < lo || h - lo >= size) return true;
+  const uint64_t dev_lo = *mapped - (h - lo);
+  uint64_t dev_last = 0;
+  if (query(reinterpret_cast<const void*>(lo + size - 1), &dev_last) && dev_last == dev_lo + (size - 1))
+    cache = PinnedRange{lo, lo + size, dev_lo};
+  return true;
+}
+
 int musa_aiter_hip_batch_copy(void* const* dsts, const void* const* srcs, const uint64_t* sizes, int64_t count,
                               int direction, int mode, void* stream) {
   if (count <= 0) return hipSuccess;
@@ -1167,23 +1213,16 @@ int musa_aiter_hip_batch_copy(void* const* dsts, const void* const* srcs, const 
   const bool use_copy_engines = mode == 2;
   const hipMemcpyKind kind = direction == 0 ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
   std::vector<uint64_t> ks, kd, kn;
+  ks.reserve(static_cast<size_t>(count));
+  kd.reserve(static_cast<size_t>(count));
+  kn.reserve(static_cast<size_t>(count));
+  PinnedRange pinned;
   for (int64_t i = 0; i < count; ++i) {
     if (sizes[i] == 0) continue;
     if (dsts[i] == nullptr || srcs[i] == nullptr) return hipErrorInvalidValue;
     const void* host = direction == 0 ? srcs[i] : dsts[i];
     uint64_t mapped = 0;
-    bool kernel = false;
-    if (!use_copy_engines) {
-      hipPointerAttribute_t attr{};
-      if (hipPointerGetAttributes(&attr, host) == hipSuccess) {
-        kernel = attr.type == hipMemoryTypeHost && attr.devicePointer != nullptr && attr.hostPointer != nullptr;
-        if (kernel)
-          mapped = reinterpret_cast<uint64_t>(attr.devicePointer) +
-                   (reinterpret_cast<uint64_t>(host) - reinterpret_cast<uint64_t>(attr.hostPointer));
-      } else {
-        (void)hipGetLastError();  // pageable memory: clear the query's error
-      }
-    }
+    const bool kernel = !use_copy_engines && map_pinned(host, pinned, &mapped);
     if (kernel) {
       ks.push_back(direction == 0 ? mapped : reinterpret_cast<uint64_t>(srcs[i]));
       kd.push_back(direction == 0 ? reinterpret_cast<uint64_t>(dsts[i]) : mapped);

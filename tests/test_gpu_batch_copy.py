@@ -245,3 +245,42 @@ def test_queued_large_batches_reuse_descriptor_slots(direction):
         for i, p in enumerate(perms[c]):
             d0 = c * count * size + p * size
             assert np.array_equal(got_dev[d0:d0 + size], h[i * size:(i + 1) * size]), (c, i)
+
+
+@pytest.mark.parametrize("direction", ["h2d", "d2h"])
+def test_batch_alternating_between_host_allocations(direction):
+    # One batch whose host side alternates between two pinned buffers and a pageable one: the
+    # library's cached pinned range must switch allocations, and pageable ranges keep hipMemcpyAsync.
+    rng = np.random.default_rng(31 if direction == "h2d" else 32)
+    count, size = 240, 3000
+    hosts = [_host(count * size, seed=40), _host(count * size, seed=41), _host(count * size, pinned=False, seed=42)]
+    dev = torch.randint(0, 256, (count * (size + 16),), dtype=torch.uint8, device=DEV)
+    which = rng.integers(0, 3, size=count)
+    host_off = [int(i * size) for i in range(count)]
+    dev_off = [int(p * (size + 16) + 3) for p in rng.permutation(count)]
+    if direction == "d2h":
+        for h in hosts:
+            h.zero_()
+    want_dev = dev.cpu().numpy().copy()
+    want_hosts = [h.numpy().copy() for h in hosts]
+    torch.cuda.synchronize()
+    for i in range(count):
+        h = want_hosts[which[i]]
+        if direction == "h2d":
+            want_dev[dev_off[i]:dev_off[i] + size] = h[host_off[i]:host_off[i] + size]
+        else:
+            h[host_off[i]:host_off[i] + size] = want_dev[dev_off[i]:dev_off[i] + size]
+    picked = [hosts[k] for k in which]
+    if direction == "h2d":
+        ok = musa_aiter.lmcache_musa_memcpy_batch_async([dev] * count, picked, [size] * count,
+                                                        destination_offsets=dev_off, source_offsets=host_off,
+                                                        require_pinned_host=False)
+    else:
+        ok = musa_aiter.lmcache_musa_memcpy_batch_async(picked, [dev] * count, [size] * count,
+                                                        destination_offsets=host_off, source_offsets=dev_off,
+                                                        require_pinned_host=False)
+    assert ok
+    torch.cuda.synchronize()
+    assert np.array_equal(dev.cpu().numpy(), want_dev)
+    for h, w in zip(hosts, want_hosts):
+        assert np.array_equal(h.numpy(), w)
