@@ -9,6 +9,7 @@ which keeps torch's stream handles and allocations valid in the kernels.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import importlib.util
 import sysconfig
@@ -191,8 +192,21 @@ def check(rc: int, op: str) -> None:
         raise HipBackendError(f"{op}: HIP launch failed with error {rc} ({text})")
 
 
+_SAME_DEVICE = contextlib.nullcontext()
+
+
+def on_device(device: torch.device):
+    """Context making ``device`` the current device; a no-op (no device exchange) when it already is."""
+    if device.index is None or device.index == torch._C._cuda_getDevice():
+        return _SAME_DEVICE
+    return torch.cuda.device(device)
+
+
 def stream_ptr(device: torch.device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    # The raw accessor returns the same handle as current_stream(device).cuda_stream
+    # without building a Stream object (about 2 us less per call).
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(index))
 
 
 def ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
@@ -241,7 +255,7 @@ def paged_tiles(
     if num_tokens <= 0 or num_layers <= 0:
         return
     device = key_cache.device
-    with torch.cuda.device(device):
+    with on_device(device):
         rc = fn("musa_aiter_hip_paged_tiles")(
             int(scatter), int(codec), int(cache_elt), int(lin_elt), int(lin_dtype),
             ptr(key_cache), ptr(value_cache), ptr(key_linear), ptr(value_linear), ptr(slots),
@@ -280,7 +294,7 @@ def copy_rows(
         return
     src_arr = _as_u64(src_planes)
     dst_arr = _as_u64(dst_planes)
-    with torch.cuda.device(device):
+    with on_device(device):
         rc = fn("musa_aiter_hip_copy_rows")(
             src_arr, dst_arr, ptr(src_table), ptr(dst_table), int(num_planes),
             ptr(src_idx), ptr(dst_idx),
@@ -323,7 +337,7 @@ def paged_dense_tiles(
     if batch <= 0 or dense_len <= 0:
         return
     device = key_cache.device
-    with torch.cuda.device(device):
+    with on_device(device):
         rc = fn("musa_aiter_hip_paged_dense_tiles")(
             int(scatter), int(codec), int(cache_elt), int(lin_elt), int(lin_dtype),
             ptr(key_cache), ptr(value_cache), ptr(dense_k), ptr(dense_v), ptr(block_tables), ptr(seq_lens),
@@ -352,7 +366,7 @@ def csr_dense_rows(
     if batch <= 0 or dense_len <= 0 or row_bytes <= 0:
         return
     device = key_cache.device
-    with torch.cuda.device(device):
+    with on_device(device):
         rc = fn("musa_aiter_hip_csr_dense_rows")(
             ptr(key_cache), ptr(value_cache), ptr(kv_indptr), ptr(kv_indices), ptr(out_k), ptr(out_v),
             int(batch), int(dense_len), int(kv_indices.numel()), int(num_tokens), int(row_bytes),
@@ -388,7 +402,7 @@ def copy_rows_paged(
         return
     if len(dst_planes) != planes:
         raise ValueError(f"{op}: source and destination plane lists differ in length")
-    with torch.cuda.device(device):
+    with on_device(device):
         rc = fn("musa_aiter_hip_copy_rows_paged")(
             u64_array(src_planes), u64_array(dst_planes), planes, ptr(src_idx), ptr(dst_idx), tokens,
             int(src_rows), int(dst_rows), int(row_bytes), int(src_stride), int(dst_stride),
@@ -420,7 +434,7 @@ def copy_blocks(
     if pairs <= 0 or num_layers <= 0:
         return
     device = dst_k.device
-    with torch.cuda.device(device):
+    with on_device(device):
         rc = fn("musa_aiter_kv_copy_paged_blocks_fp8_vec8")(
             ptr(src_k), ptr(src_v), ptr(dst_k), ptr(dst_v), ptr(block_mapping), pairs, int(num_layers),
             int(src_blocks), int(dst_blocks), 1, int(block_bytes), 1, stream_ptr(device),
@@ -433,7 +447,7 @@ def cachegen_encode(*, op: str, x: torch.Tensor, input_dtype: int, num_bins: int
     """Bins, codebook and CDF of contiguous ``x`` in three launches on the current stream."""
     device = x.device
     ws_bytes = int(fn("musa_aiter_hip_cachegen_workspace_bytes")())
-    with torch.cuda.device(device):
+    with on_device(device):
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
         rc = fn("musa_aiter_hip_cachegen_encode")(
             ptr(x), int(input_dtype), int(x.numel()), int(num_bins), int(bool(native_rounding)),
@@ -446,7 +460,7 @@ def cachegen_decode(*, op: str, codes: torch.Tensor, table: torch.Tensor, out: t
                     max_code: torch.Tensor | None) -> None:
     """out[i] = table[codes[i]] for contiguous ``codes`` / ``out`` and a contiguous table."""
     device = codes.device
-    with torch.cuda.device(device):
+    with on_device(device):
         rc = fn("musa_aiter_hip_cachegen_decode")(
             ptr(codes), int(codes.numel()), ptr(table), int(table.numel()), int(table.element_size()),
             ptr(out), ptr(max_code), stream_ptr(device),

@@ -29,7 +29,7 @@ from typing import Literal
 import numpy as np
 import torch
 
-from musa_aiter.dispatch import DispatchRecord, emit, tensor_device_dtype
+from musa_aiter.dispatch import DispatchRecord, emit, tensor_device_dtype, trace_enabled
 from musa_aiter.ops import _hip
 from musa_aiter.ops.kv_transfer import BuildResult, _require_rocm, build_native_kv_transfer
 
@@ -393,6 +393,8 @@ def _require_one_rocm_device(op: str, tensors) -> torch.device:
 
 
 def _emit_direct(operation: str, tensor: torch.Tensor, reason: str) -> None:
+    if not trace_enabled():
+        return
     device, dtype = tensor_device_dtype(tensor)
     emit(DispatchRecord(operation, BACKEND, device, dtype, reason))
 

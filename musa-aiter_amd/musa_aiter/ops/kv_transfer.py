@@ -29,7 +29,7 @@ from typing import Literal
 
 import torch
 
-from musa_aiter.dispatch import DispatchRecord, emit, tensor_device_dtype
+from musa_aiter.dispatch import DispatchRecord, emit, tensor_device_dtype, trace_enabled
 from musa_aiter.ops import _hip
 from musa_aiter.ops.kv_layout import KVLayoutSpec, KVScaleKind
 from musa_aiter.ops.native_gate import native_requested
@@ -160,6 +160,8 @@ def _float_elt(name: str, *tensors: torch.Tensor) -> int:
 
 
 def _emit(op: str, tensor: torch.Tensor, reason: str) -> None:
+    if not trace_enabled():
+        return
     device, dtype = tensor_device_dtype(tensor)
     emit(DispatchRecord(op, BACKEND, device, dtype, reason))
 

@@ -31,7 +31,7 @@ from typing import Any
 
 import torch
 
-from musa_aiter.dispatch import DispatchRecord, emit
+from musa_aiter.dispatch import DispatchRecord, emit, trace_enabled
 from musa_aiter.ops import _hip
 from musa_aiter.ops.native_gate import native_requested
 
@@ -73,6 +73,8 @@ def _log_timing(op: str, elapsed_us: float, **fields: Any) -> None:
 
 
 def _emit(op: str, tensor: torch.Tensor, reason: str) -> None:
+    if not trace_enabled():
+        return
     emit(DispatchRecord(op, BACKEND, str(tensor.device), str(tensor.dtype), reason))
 
 
