@@ -17,7 +17,8 @@
  *   the cache are treated as skipped.  Scatters keep last-writer-wins for
  *   duplicate destinations, like the reference's token loop: a claim pass
  *   records the last token per destination in a per-(device, stream) scratch
- *   array owned by the library (allocated on first use, grown on demand).
+ *   array owned by the library (allocated on first use, grown on demand;
+ *   calls captured into a HIP graph get an array per capture and stream).
  *   Element types: "_float" = fp32, "_half" = fp16, "_bfloat16" / "_u16" =
  *   16-bit payloads (bf16 or fp16, copied bit-exactly).
  */
@@ -38,6 +39,9 @@ int musa_aiter_dsv4_kv_copy_abi_version(void);
 /* No reference counterpart: backend label and HIP error text for diagnostics. */
 const char* musa_aiter_hip_backend_name(void);
 const char* musa_aiter_hip_error_string(int code);
+/* No reference counterpart: number of duplicate-slot claim arrays held for scatters captured into
+ * HIP graphs (one per capture and capturing stream; never freed, as graphs keep their addresses). */
+int64_t musa_aiter_hip_graph_claim_arrays(void);
 
 /* ---- Generic entries used by this package's Python host layer (no reference counterpart) ----
  * Paged-A caches [NL, NB, NH, HD, BS] <-> linear rows with explicit strides.

@@ -26,7 +26,7 @@ using kvhip::RowCopyParams;
 
 namespace {
 
-// ----- duplicate-slot claim scratch (one array per device and stream) ------------
+// ----- duplicate-slot claim scratch --------------------------------------------------------
 
 struct ClaimScratch {
   uint64_t* owner = nullptr;
@@ -34,52 +34,91 @@ struct ClaimScratch {
   uint32_t epoch = 0;
 };
 
-std::mutex g_claim_mu;
-std::map<std::pair<int, uintptr_t>, ClaimScratch>* g_claims = nullptr;
-// Arrays of calls captured into HIP graphs, per (device, capturing stream).
-// A graph keeps the address it was captured with, so an array that is
-// outgrown is left allocated rather than freed.
-std::map<std::pair<int, uintptr_t>, ClaimScratch>* g_graph_claims = nullptr;
-
-// Claim pass of a call being captured into a graph.  The epoch scheme of the
-// eager path would freeze the capture-time epoch into every replay, where
-// claims left by earlier replays carry the same epoch and can win.  Captured
-// calls instead zero the entries they compete for and then claim with epoch 1,
-// which is correct whatever the array held before; growing the array neither
-// synchronises nor is recorded (allocation runs in relaxed capture mode).
-hipError_t prepare_graph_claims(const kvhip::ClaimSource& src, int64_t n, int64_t rows, hipStream_t stream, int dev,
-                                const uint64_t** owner, uint32_t* epoch) {
-  if (g_graph_claims == nullptr) g_graph_claims = new std::map<std::pair<int, uintptr_t>, ClaimScratch>();
-  ClaimScratch& cs = (*g_graph_claims)[{dev, reinterpret_cast<uintptr_t>(stream)}];
-  if (cs.capacity < rows) {
-    int64_t cap = cs.capacity * 2;
-    if (cap < rows) cap = rows;
-    if (cap < (int64_t{1} << 16)) cap = int64_t{1} << 16;
-    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
-    hipError_t err = hipThreadExchangeStreamCaptureMode(&mode);
-    if (err != hipSuccess) return err;
-    uint64_t* p = nullptr;
-    const hipError_t merr = hipMalloc(reinterpret_cast<void**>(&p), static_cast<size_t>(cap) * sizeof(uint64_t));
-    err = hipThreadExchangeStreamCaptureMode(&mode);
-    if (merr != hipSuccess) return merr;
-    if (err != hipSuccess) return err;
-    cs.owner = p;
-    cs.capacity = cap;
+// Eager calls: one array per (device, stream).  Captured calls: one array per
+// (device, capture id, capturing stream), so graphs captured one after another
+// on the same stream (torch captures every graph on one process-wide stream)
+// never share an array, and replays of different graphs may overlap.
+using EagerKey = std::pair<int, uintptr_t>;
+struct GraphKey {
+  int dev;
+  unsigned long long capture_id;
+  uintptr_t stream;
+  bool operator<(const GraphKey& o) const {
+    if (dev != o.dev) return dev < o.dev;
+    if (capture_id != o.capture_id) return capture_id < o.capture_id;
+    return stream < o.stream;
   }
-  hipError_t err = kvhip::launch_claim(src, n, rows, cs.owner, 1, stream, true);
+};
+
+std::mutex g_claim_mu;
+std::map<EagerKey, ClaimScratch>* g_claims = nullptr;
+std::map<GraphKey, ClaimScratch>* g_graph_claims = nullptr;
+// Outgrown eager arrays.  Kernels queued before the growth may still read
+// them, and freeing would synchronise the device, so they stay allocated;
+// capacities double, so they add at most the size of the live arrays.
+std::vector<uint64_t*>* g_retired_claims = nullptr;
+
+// hipMalloc in relaxed capture mode: another thread's global-mode capture is
+// not invalidated, and nothing is recorded into a graph being captured.
+hipError_t malloc_relaxed(uint64_t** p, int64_t count) {
+  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+  hipError_t err = hipThreadExchangeStreamCaptureMode(&mode);
   if (err != hipSuccess) return err;
-  err = kvhip::launch_claim(src, n, rows, cs.owner, 1, stream, false);
+  const hipError_t merr = hipMalloc(reinterpret_cast<void**>(p), static_cast<size_t>(count) * sizeof(uint64_t));
+  err = hipThreadExchangeStreamCaptureMode(&mode);
+  if (merr != hipSuccess) {
+    *p = nullptr;
+    return merr;
+  }
+  return err;
+}
+
+int64_t grown_capacity(int64_t have, int64_t rows) {
+  int64_t cap = have * 2;
+  if (cap < rows) cap = rows;
+  if (cap < (int64_t{1} << 16)) cap = int64_t{1} << 16;
+  return cap;
+}
+
+// Claim pass that needs no cleared array: a reset pass zeroes exactly the
+// entries the tokens compete for, then the tokens claim with epoch 1.  Used by
+// calls captured into graphs (an eager epoch would be frozen into every
+// replay, where claims left by earlier replays carry the same epoch and could
+// win) and by the allocation-free entry point.
+hipError_t reset_and_claim(const kvhip::ClaimSource& src, int64_t n, int64_t rows, uint64_t* owner,
+                           hipStream_t stream, const uint64_t** out_owner, uint32_t* epoch) {
+  hipError_t err = kvhip::launch_claim(src, n, rows, owner, 1, stream, true);
   if (err != hipSuccess) return err;
-  *owner = cs.owner;
+  err = kvhip::launch_claim(src, n, rows, owner, 1, stream, false);
+  if (err != hipSuccess) return err;
+  *out_owner = owner;
   *epoch = 1;
   return hipSuccess;
 }
 
+// Claim pass of a call being captured into a graph.  A graph keeps the array
+// address it was captured with, so arrays of captures are never freed.
+hipError_t prepare_graph_claims(const kvhip::ClaimSource& src, int64_t n, int64_t rows, hipStream_t stream, int dev,
+                                unsigned long long capture_id, const uint64_t** owner, uint32_t* epoch) {
+  if (g_graph_claims == nullptr) g_graph_claims = new std::map<GraphKey, ClaimScratch>();
+  ClaimScratch& cs = (*g_graph_claims)[GraphKey{dev, capture_id, reinterpret_cast<uintptr_t>(stream)}];
+  if (cs.capacity < rows) {
+    const int64_t cap = grown_capacity(cs.capacity, rows);
+    uint64_t* p = nullptr;
+    const hipError_t err = malloc_relaxed(&p, cap);
+    if (err != hipSuccess) return err;
+    cs.owner = p;
+    cs.capacity = cap;
+  }
+  return reset_and_claim(src, n, rows, cs.owner, stream, owner, epoch);
+}
+
 // Runs the claim pass for the `n` destinations of `src` into a destination
 // of `rows` rows and returns the tag array and epoch the copy kernel must
-// check.  A call that cannot collide (n <= 1) skips the pass.  Calls on one
-// stream share that stream's array; graphs captured on one stream share its
-// capture array, so their replays must not overlap one another.
+// check.  A call that cannot collide (n <= 1) skips the pass.  Eager calls on
+// one stream share that stream's array (stream order keeps them apart); a
+// captured graph has arrays of its own, so one graph must not replay on two
+// streams at once.
 hipError_t prepare_claims(const kvhip::ClaimSource& src, int64_t n, int64_t rows, hipStream_t stream,
                           const uint64_t** owner, uint32_t* epoch) {
   *owner = nullptr;
@@ -89,29 +128,24 @@ hipError_t prepare_claims(const kvhip::ClaimSource& src, int64_t n, int64_t rows
   hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess) return err;
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-  err = hipStreamIsCapturing(stream, &capture);
+  unsigned long long capture_id = 0;
+  err = hipStreamGetCaptureInfo(stream, &capture, &capture_id);
   if (err != hipSuccess) return err;
   std::lock_guard<std::mutex> lock(g_claim_mu);
-  if (capture != hipStreamCaptureStatusNone) return prepare_graph_claims(src, n, rows, stream, dev, owner, epoch);
-  if (g_claims == nullptr) g_claims = new std::map<std::pair<int, uintptr_t>, ClaimScratch>();
+  if (capture != hipStreamCaptureStatusNone)
+    return prepare_graph_claims(src, n, rows, stream, dev, capture_id, owner, epoch);
+  if (g_claims == nullptr) g_claims = new std::map<EagerKey, ClaimScratch>();
   ClaimScratch& cs = (*g_claims)[{dev, reinterpret_cast<uintptr_t>(stream)}];
   if (cs.capacity < rows) {
-    int64_t cap = cs.capacity * 2;
-    if (cap < rows) cap = rows;
-    if (cap < (int64_t{1} << 16)) cap = int64_t{1} << 16;
+    const int64_t cap = grown_capacity(cs.capacity, rows);
+    uint64_t* p = nullptr;
+    err = malloc_relaxed(&p, cap);
+    if (err != hipSuccess) return err;
     if (cs.owner != nullptr) {
-      err = hipStreamSynchronize(stream);
-      if (err != hipSuccess) return err;
-      err = hipFree(cs.owner);
-      cs.owner = nullptr;
-      cs.capacity = 0;
-      if (err != hipSuccess) return err;
+      if (g_retired_claims == nullptr) g_retired_claims = new std::vector<uint64_t*>();
+      g_retired_claims->push_back(cs.owner);
     }
-    err = hipMalloc(reinterpret_cast<void**>(&cs.owner), static_cast<size_t>(cap) * sizeof(uint64_t));
-    if (err != hipSuccess) {
-      cs.owner = nullptr;
-      return err;
-    }
+    cs.owner = p;
     cs.capacity = cap;
     cs.epoch = 0;
     err = kvhip::launch_fill_u64(cs.owner, cap, 0, stream);
@@ -429,6 +463,11 @@ int musa_aiter_fp8_kv_cache_abi_version() { return 1; }
 int musa_aiter_dsv4_kv_copy_abi_version() { return 1; }
 const char* musa_aiter_hip_backend_name() { return "rocm-hip"; }
 const char* musa_aiter_hip_error_string(int code) { return hipGetErrorString(static_cast<hipError_t>(code)); }
+
+int64_t musa_aiter_hip_graph_claim_arrays() {
+  std::lock_guard<std::mutex> lock(g_claim_mu);
+  return g_graph_claims == nullptr ? 0 : static_cast<int64_t>(g_graph_claims->size());
+}
 
 // ----- generic entries used by the Python host layer ----------------------------------------
 
@@ -1097,12 +1136,18 @@ struct DescSlot {
 };
 
 struct DescRing {
+  std::mutex mu;  // held while a slot is claimed, waited for and refilled
   DescSlot slots[kDescSlots];
   int next = 0;
 };
 
+// g_desc_mu guards only the ring lookup; waits happen under the ring's own
+// mutex, so batches on other streams never queue behind them.
 std::mutex g_desc_mu;
 std::map<std::pair<int, uintptr_t>, DescRing>* g_desc_rings = nullptr;
+// Outgrown descriptor buffers: freeing pinned memory synchronises the device,
+// so they stay allocated (capacities double, bounding them by the live ones).
+std::vector<uint64_t*>* g_retired_desc = nullptr;
 
 hipError_t batch_copy_by_descriptors(const std::vector<uint64_t>& src, const std::vector<uint64_t>& dst,
                                      const std::vector<uint64_t>& size, uint32_t max_groups, hipStream_t stream) {
@@ -1112,9 +1157,14 @@ hipError_t batch_copy_by_descriptors(const std::vector<uint64_t>& src, const std
   int dev = 0;
   hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess) return err;
-  std::lock_guard<std::mutex> lock(g_desc_mu);
-  if (g_desc_rings == nullptr) g_desc_rings = new std::map<std::pair<int, uintptr_t>, DescRing>();
-  DescRing& ring = (*g_desc_rings)[{dev, reinterpret_cast<uintptr_t>(stream)}];
+  DescRing* ring_ptr = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_desc_mu);
+    if (g_desc_rings == nullptr) g_desc_rings = new std::map<std::pair<int, uintptr_t>, DescRing>();
+    ring_ptr = &(*g_desc_rings)[{dev, reinterpret_cast<uintptr_t>(stream)}];  // map nodes never move
+  }
+  DescRing& ring = *ring_ptr;
+  std::lock_guard<std::mutex> ring_lock(ring.mu);
   DescSlot& slot = ring.slots[ring.next];
   ring.next = (ring.next + 1) % kDescSlots;
   if (slot.pending) {
@@ -1131,19 +1181,19 @@ hipError_t batch_copy_by_descriptors(const std::vector<uint64_t>& src, const std
   }
   const size_t need = static_cast<size_t>(tiles) * 3;
   if (slot.capacity < need) {
-    if (slot.host != nullptr) {
-      err = hipHostFree(slot.host);
-      slot.host = nullptr;
-      slot.capacity = 0;
-      if (err != hipSuccess) return err;
-    }
-    size_t cap = need < 8192 ? 8192 : need;
-    err = hipHostMalloc(reinterpret_cast<void**>(&slot.host), cap * sizeof(uint64_t),
+    size_t cap = slot.capacity * 2;
+    if (cap < need) cap = need;
+    if (cap < 8192) cap = 8192;
+    uint64_t* host = nullptr;
+    err = hipHostMalloc(reinterpret_cast<void**>(&host), cap * sizeof(uint64_t),
                         hipHostMallocMapped | hipHostMallocCoherent);
-    if (err != hipSuccess) {
-      slot.host = nullptr;
-      return err;
+    if (err != hipSuccess) return err;
+    if (slot.host != nullptr) {
+      std::lock_guard<std::mutex> lock(g_desc_mu);
+      if (g_retired_desc == nullptr) g_retired_desc = new std::vector<uint64_t*>();
+      g_retired_desc->push_back(slot.host);
     }
+    slot.host = host;
     slot.capacity = cap;
   }
   kvhip::batch_copy_fill_desc(src.data(), dst.data(), size.data(), static_cast<int64_t>(size.size()), slot.host);

@@ -78,6 +78,7 @@ _SIGNATURES: dict[str, list] = {
     "musa_aiter_kv_copy_paged_blocks_fp8_vec8": [_c_void_p] * 5 + [_i64] * 7 + [_c_void_p],
     "musa_aiter_hip_error_string": [_i32],
     "musa_aiter_hip_backend_name": [],
+    "musa_aiter_hip_graph_claim_arrays": [],
     "musa_aiter_kv_transfer_abi_version": [],
     "native_lmcache_kv_transfer_abi_version": [],
     "musa_aiter_fp8_kv_cache_abi_version": [],
@@ -111,6 +112,7 @@ _RESTYPES = {
     "musa_aiter_hip_error_string": ctypes.c_char_p,
     "musa_aiter_hip_backend_name": ctypes.c_char_p,
     "musa_aiter_hip_cachegen_workspace_bytes": ctypes.c_int64,
+    "musa_aiter_hip_graph_claim_arrays": ctypes.c_int64,
 }
 
 _lock = threading.Lock()

@@ -115,3 +115,42 @@ def test_triton_indexed_to_dense_replays():
         wk, wv = kv_triton_indexed_to_dense(k, v, indptr, indices, max_seq_len=dense)
         torch.cuda.synchronize()
         assert np.array_equal(bits(ok), bits(wk)) and np.array_equal(bits(ov), bits(wv)), rep
+
+
+def test_graphs_on_the_default_capture_stream_get_their_own_claim_arrays():
+    # torch captures every graph on one process-wide stream; two graphs captured there must not
+    # share a claim array, or replays of both on different streams would clear each other's tags.
+    from musa_aiter.ops import _hip
+
+    nl, nb, bs, nh, hs, t = 2, 16, 16, 2, 64, 96
+    rng = np.random.default_rng(9)
+    gen = torch.Generator().manual_seed(9)
+    count = _hip.fn("musa_aiter_hip_graph_claim_arrays")
+    graphs, cases = [], []
+    before = int(count())
+    for _ in range(2):
+        caches = [[random_payload((nb, bs, nh, hs), torch.bfloat16, gen).to(DEV) for _ in range(nl)]
+                  for _ in range(2)]
+        src = random_payload((2, nl, t, nh * hs), torch.bfloat16, gen).to(DEV)
+        slots = torch.from_numpy(rng.integers(0, nb * bs // 8, size=t)).to(DEV)  # many repeats
+        g, _ = _capture(lambda c=caches, m=src, s=slots: musa_aiter.lmcache_kv_buffer_to_paged_two_x_nl(
+            m, c, s, 0, bs, nh, hs))
+        graphs.append(g)
+        cases.append((caches, src, slots))
+    assert int(count()) - before == 2
+    # both graphs still replay correctly, on two different streams
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    want = []
+    for caches, src, slots in cases:
+        ref = [[c.clone() for c in grp] for grp in caches]
+        musa_aiter.lmcache_kv_buffer_to_paged_two_x_nl(src, ref, slots, 0, bs, nh, hs)
+        want.append(ref)
+    torch.cuda.synchronize()
+    for g, s in zip(graphs, streams):
+        with torch.cuda.stream(s):
+            g.replay()
+    torch.cuda.synchronize()
+    for (caches, _, _), ref in zip(cases, want):
+        for a in range(2):
+            for layer in range(nl):
+                assert np.array_equal(bits(caches[a][layer]), bits(ref[a][layer])), (a, layer)
