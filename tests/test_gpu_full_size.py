@@ -8,9 +8,10 @@ configs these tests check, for every token:
 * configs[1] (32 layers bf16, 8,192 blocks of 16, 64 sequences of 128-4,096 tokens): a scatter
   followed by a gather returns the input bit for bit; every cache row named by a slot equals its
   linear row by torch indexing; every cache row no slot names keeps its previous bits;
-* configs[2] (FP8 E4M3, per-kv-head scales amax/448, one layer of the same shape): every cache byte
-  equals the reference encoder's steps restated in torch (tests/torch_ref.py), every dequantised
-  row equals the reference decoder's steps, untouched cache bytes keep their sentinel;
+* configs[2] (FP8, one layer of the same shape; E4M3 with per-kv-head scales amax/448 or a scalar
+  scale, E5M2 with per-head scales amax/57344): every cache byte equals the reference encoder's
+  steps restated in torch (tests/torch_ref.py, evaluated on CPU copies), every dequantised row
+  equals the reference decoder's steps, untouched cache bytes keep their sentinel;
 * configs[3] (SGLang MP caches 2 x 32 x [4,096, 16, 8, 128] bf16, sixteen 256-token chunks of
   random sequences): each chunk's gather equals torch indexing, and a scatter of the gathered
   buffer into zeroed caches restores exactly the named rows;
@@ -122,11 +123,16 @@ def test_config2_multi_layer_bf16_round_trip_full_size():
             assert torch.equal(rows[unnamed], torch_ref.paged_rows(before[layer]).view(torch.int16)[unnamed]), layer
 
 
-def test_config3_fp8_e4m3_per_head_full_size():
+@pytest.mark.parametrize("fmt,per_head,fmax", [("e4m3", True, 448.0), ("e4m3", False, 448.0),
+                                               ("e5m2", True, 57344.0)])
+def test_config3_fp8_full_size(fmt, per_head, fmax):
+    # per-kv-head scales amax/448 (the headline), a scalar scale (global amax/448), and
+    # E5M2 with per-head scales amax/57344.  The expected codes and dequantised values are computed
+    # from CPU copies, where tests/test_oracle_fp8.py pins tests/torch_ref.py against the oracle.
     nb, bs, nh, hd = 8192, 16, 8, 128
     slots_np = _slots(1003, 64, 128, 4096, nb, bs)
     t = int(slots_np.shape[0])
-    print(f"configs[2] full size: {t} tokens", flush=True)
+    print(f"configs[2] full size: {t} tokens, {fmt}, per_head={per_head}", flush=True)
     slots = torch.from_numpy(slots_np).to(DEV)
     gen = torch.Generator(device=DEV).manual_seed(13)
     lin = []
@@ -135,21 +141,27 @@ def test_config3_fp8_e4m3_per_head_full_size():
         x.mul_(torch.where(torch.rand(x.shape, generator=gen, device=DEV) < 0.01, 50.0, 1.0))
         lin.append(x.to(torch.bfloat16))
     kl, vl = lin
-    ks = (kl.float().abs().amax(dim=(0, 2)) / 448.0).contiguous()
-    vs = (vl.float().abs().amax(dim=(0, 2)) / 448.0).contiguous()
+    if per_head:
+        ks = (kl.float().abs().amax(dim=(0, 2)) / fmax).contiguous()
+        vs = (vl.float().abs().amax(dim=(0, 2)) / fmax).contiguous()
+    else:
+        ks = (kl.float().abs().amax() / fmax).reshape(1).contiguous()
+        vs = (vl.float().abs().amax() / fmax).reshape(1).contiguous()
     kc = torch.full((nb, nh, hd, bs), 0x5A, dtype=torch.uint8, device=DEV)
     vc = torch.full_like(kc, 0x5A)
-    musa_aiter.kv_linear_to_paged_fp8(kl, vl, kc, vc, slots, ks, vs, fp8_format="e4m3")
-    ok, ov = musa_aiter.kv_paged_fp8_to_linear(kc, vc, slots, ks, vs, out_dtype=torch.bfloat16, fp8_format="e4m3")
+    musa_aiter.kv_linear_to_paged_fp8(kl, vl, kc, vc, slots, ks, vs, fp8_format=fmt)
+    ok, ov = musa_aiter.kv_paged_fp8_to_linear(kc, vc, slots, ks, vs, out_dtype=torch.bfloat16, fp8_format=fmt)
     torch.cuda.synchronize()
     unnamed = _unnamed(slots, nb * bs)
     for cache, x, scale, out in ((kc, kl, ks, ok), (vc, vl, vs, ov)):
         rows = torch_ref.paged_rows(cache)
-        want = torch_ref.fp8_quantize(x, scale.reshape(-1, 1), "e4m3")
-        assert torch.equal(rows[slots], want)
-        want_deq = torch_ref.fp8_dequantize(want, scale.reshape(-1, 1), "e4m3", torch.bfloat16)
-        assert torch.equal(out.view(torch.int16), want_deq.view(torch.int16))
+        scale_cpu = scale.cpu().reshape(-1, 1)
+        want = torch_ref.fp8_quantize(x.cpu(), scale_cpu, fmt)
+        assert torch.equal(rows[slots].cpu(), want)
+        want_deq = torch_ref.fp8_dequantize(want, scale_cpu, fmt, torch.bfloat16)
+        assert torch.equal(out.cpu().view(torch.int16), want_deq.view(torch.int16))
         assert bool((rows[unnamed] == 0x5A).all())
+        del want, want_deq
 
 
 def test_config5_mla_rows_full_size():
