@@ -56,6 +56,22 @@ int musa_aiter_hip_paged_tiles(int scatter, int codec, int cache_elt, int lin_el
                                int64_t head_dim, int64_t block_size, int64_t lin_token_stride,
                                int64_t lin_layer_stride, const float* k_scale, const float* v_scale, int scale_mode,
                                int fill_zeros, int dedupe, void* stream);
+/* No reference counterpart.  For callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): musa_aiter_hip_paged_tiles with the
+ * same arguments and results, allocating nothing.  A scatter with dedupe keeps its last-writer claim
+ * tags in a static device array of MUSA_AITER_HIP_NOALLOC_MAX_SLOTS uint64 entries (16 MiB per
+ * device, held until the process ends), cleared and claimed by every call; a scatter with dedupe
+ * whose num_blocks * block_size exceeds that maximum returns hipErrorInvalidValue (1) and launches
+ * nothing.  All calls on one device share the array: calls that overlap in time on one device
+ * (concurrent streams, or graphs replaying at once) race and must not be issued. */
+#define MUSA_AITER_HIP_NOALLOC_MAX_SLOTS 2097152
+int musa_aiter_hip_paged_tiles_noalloc(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtype,
+                                       void* key_cache, void* value_cache, void* key_linear, void* value_linear,
+                                       const int64_t* slot_mapping, int64_t num_layers, int64_t num_tokens,
+                                       int64_t num_blocks, int64_t num_heads, int64_t head_dim, int64_t block_size,
+                                       int64_t lin_token_stride, int64_t lin_layer_stride, const float* k_scale,
+                                       const float* v_scale, int scale_mode, int fill_zeros, int dedupe,
+                                       void* stream);
 /* Paged-A caches [NB, NH, HD, BS] <-> dense [batch, dense_len, NH, HD] tensors addressed through
  * block tables: dense token (b, pos) uses slot block_tables[b, pos / BS] * BS + pos % BS while
  * pos < seq_lens[b], the logical block is below max_blocks and the block id lies in [0, num_blocks).

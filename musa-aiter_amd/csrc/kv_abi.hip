@@ -24,6 +24,14 @@
 using kvhip::PagedTileParams;
 using kvhip::RowCopyParams;
 
+// Claim tags of musa_aiter_hip_paged_tiles_noalloc: one uint64 per destination
+// slot of the caches (16 MiB on every device the library runs on, held until
+// the process ends).  In host code `scratch` names a host-side stand-in, not a
+// device address: only the per-device address returned by
+// hipGetSymbolAddress (noalloc_scratch below) is passed to kernels.
+constexpr int64_t kNoAllocMaxSlots = MUSA_AITER_HIP_NOALLOC_MAX_SLOTS;
+static __device__ __align__(256) uint64_t scratch[kNoAllocMaxSlots];
+
 namespace {
 
 // ----- duplicate-slot claim scratch --------------------------------------------------------
@@ -174,13 +182,36 @@ hipError_t prepare_claims(const int64_t* idx, int64_t n, int64_t rows, hipStream
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Device address of `scratch` on the current device, looked up once per
+// device (each device holds its own copy of the array at its own address).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint64_t* g_scratch_ptr[kMaxDevices] = {};
+
+hipError_t noalloc_scratch(uint64_t** out) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return err;
+    if (ptr == nullptr) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = static_cast<uint64_t*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
+}
+
 // ----- paged-A helpers -------------------------------------------------------------------
 
 int paged_tiles(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtype, void* kc, void* vc, void* kl,
                 void* vl, const int64_t* slots, int64_t nl, int64_t t, int64_t nb, int64_t nh, int64_t hd, int64_t bs,
                 int64_t tok_stride_elems, int64_t layer_stride_elems, const float* ks, const float* vs,
                 int scale_mode, int fill_zeros, int dedupe, hipStream_t stream,
-                const kvhip::BlockTableSlots* bt = nullptr) {
+                const kvhip::BlockTableSlots* bt = nullptr, uint64_t* fixed_owner = nullptr) {
   if (t <= 0 || nl <= 0) return hipSuccess;
   PagedTileParams p{};
   p.scatter = scatter;
@@ -210,7 +241,11 @@ int paged_tiles(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtyp
     kvhip::ClaimSource src;
     src.idx = slots;
     if (bt != nullptr) src.bt = *bt;
-    hipError_t err = prepare_claims(src, t, nb * bs, stream, &p.owner, &p.epoch);
+    // A caller-provided tag array (the allocation-free entry) is cleared and
+    // claimed per call; otherwise the library's per-stream array is used.
+    hipError_t err = hipSuccess;
+    if (fixed_owner == nullptr) err = prepare_claims(src, t, nb * bs, stream, &p.owner, &p.epoch);
+    else if (t > 1) err = reset_and_claim(src, t, nb * bs, fixed_owner, stream, &p.owner, &p.epoch);
     if (err != hipSuccess) return err;
   }
   return kvhip::launch_paged_tiles(p, stream);
@@ -481,6 +516,25 @@ int musa_aiter_hip_paged_tiles(int scatter, int codec, int cache_elt, int lin_el
                      slot_mapping, num_layers, num_tokens, num_blocks, num_heads, head_dim, block_size,
                      lin_token_stride, lin_layer_stride, k_scale, v_scale, scale_mode, fill_zeros, dedupe,
                      as_stream(stream));
+}
+
+int musa_aiter_hip_paged_tiles_noalloc(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtype,
+                                       void* key_cache, void* value_cache, void* key_linear, void* value_linear,
+                                       const int64_t* slot_mapping, int64_t num_layers, int64_t num_tokens,
+                                       int64_t num_blocks, int64_t num_heads, int64_t head_dim, int64_t block_size,
+                                       int64_t lin_token_stride, int64_t lin_layer_stride, const float* k_scale,
+                                       const float* v_scale, int scale_mode, int fill_zeros, int dedupe,
+                                       void* stream) {
+  uint64_t* owner = nullptr;
+  if (scatter && dedupe) {
+    if (num_blocks < 0 || block_size <= 0 || num_blocks > kNoAllocMaxSlots / block_size) return hipErrorInvalidValue;
+    const hipError_t err = noalloc_scratch(&owner);
+    if (err != hipSuccess) return err;
+  }
+  return paged_tiles(scatter, codec, cache_elt, lin_elt, lin_dtype, key_cache, value_cache, key_linear, value_linear,
+                     slot_mapping, num_layers, num_tokens, num_blocks, num_heads, head_dim, block_size,
+                     lin_token_stride, lin_layer_stride, k_scale, v_scale, scale_mode, fill_zeros, dedupe,
+                     as_stream(stream), nullptr, owner);
 }
 
 int musa_aiter_hip_paged_dense_tiles(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtype,

@@ -37,7 +37,7 @@ def _declared_symbols() -> set[str]:
 
 def test_header_declares_expected_families():
     names = _declared_symbols()
-    assert len(names) == 115
+    assert len(names) == 116
     for required in ("musa_aiter_kv_load_and_reshape_flash_half", "musa_aiter_kv_triton_indexed_to_dense_bfloat16",
                      "musa_aiter_kv_reshape_and_cache_back_flash_float", "musa_aiter_kv_copy_paged_blocks_fp8_vec8",
                      "musa_aiter_hip_paged_dense_tiles","musa_aiter_kv_paged_to_linear_bfloat16", "musa_aiter_kv_linear_to_paged_multi_layer_half",
@@ -66,3 +66,20 @@ def test_probes_callable_without_gpu():
     name = lib.musa_aiter_hip_backend_name
     name.restype = ctypes.c_char_p
     assert name() == b"rocm-hip"
+
+
+def test_noalloc_entry_rejects_caches_beyond_its_scratch_without_a_gpu():
+    # The size check runs before any HIP call, so it is observable on the CPU: a deduplicating
+    # scatter into more than MUSA_AITER_HIP_NOALLOC_MAX_SLOTS slots returns hipErrorInvalidValue.
+    lib = ctypes.CDLL(str(_hip.LIB_PATH))
+    f = lib.musa_aiter_hip_paged_tiles_noalloc
+    f.argtypes = _hip._SIGNATURES["musa_aiter_hip_paged_tiles"]
+    f.restype = ctypes.c_int
+    text = HEADER.read_text()
+    max_slots = int(re.search(r"#define MUSA_AITER_HIP_NOALLOC_MAX_SLOTS (\d+)", text).group(1))
+    assert max_slots == 1 << 21
+    bs = 16
+    for nb in (max_slots // bs + 1, 1 << 40):
+        rc = f(1, 0, 2, 2, 2, None, None, None, None, None, 1, 10, nb, 8, 128, bs, 1024, 10240,
+               None, None, 0, 0, 1, None)
+        assert rc == 1, nb
