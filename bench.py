@@ -17,9 +17,17 @@ once, outside the timed region.
 of K steps / device time of the K steps between HIP events, in GB/s.
 ``roofline`` is reported for the dominant kernel (the direction with the
 larger total time) against the 8 TB/s HBM peak; its ``traffic`` comes from the
-committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes.  ``cpu_baseline`` times the
-numpy oracle (oracle/kv_oracle.py, a port of the reference algorithm) on the
-headline workload itself, one layer at a time, on this host.
+committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes.  ``ceilings`` times, on the
+same caches and linear buffers, a plain whole-block copy in the block order of
+the slot mapping (random cache blocks read with the linear side written in
+order, and the reverse): the rate that access pattern allows a copy with no
+index work, which the two kernels are measured against.  ``placements``
+re-allocates the caches several times in this process and times the step on
+each, because where the caches land moves the rate by several percent.
+``cpu_baseline`` times the reference's own torch operations
+(oracle/torch_cpu_port.py, a port of kv_transfer.py:3047-3112) on this host's
+cores: configs[1] on a prefix of its tokens, configs[0] at full shape, and a
+vectorised torch line.
 
 The other configs are reported under ``extra`` with the same byte convention
 (config 6: the block-table / CSR dense preload for attention and whole-block
@@ -158,6 +166,123 @@ def _check(rc: int, name: str) -> None:
         raise RuntimeError(f"{name} returned HIP error {rc}")
 
 
+def run_blocks(slots_np: np.ndarray, block_size: int) -> np.ndarray:
+    """Cache blocks in the order a slot mapping first visits them (skipped tokens ignored)."""
+    blk = slots_np[slots_np >= 0] // block_size
+    first = np.unique(blk, return_index=True)[1]
+    return blk[np.sort(first)].astype(np.int32)
+
+
+def pattern_copy_fn(src: torch.Tensor, dst: torch.Tensor, *, src_blocks, dst_blocks, num_blocks: int,
+                    src_region_blocks: int, dst_region_blocks: int, src_block_bytes: int, dst_block_bytes: int,
+                    planes: int, src_plane_stride: int, dst_plane_stride: int):
+    """A launcher of the library's block-pattern copy (musa_aiter_hip_block_pattern_copy): whole blocks in the
+    given order, no index resolution or transpose, on the caller's own buffers -- the access-pattern ceiling."""
+    from musa_aiter.ops import _hip
+
+    fn = getattr(_hip.library(), "musa_aiter_hip_block_pattern_copy")
+    fn.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 8 + [ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+    sb = src_blocks.data_ptr() if src_blocks is not None else None
+    db = dst_blocks.data_ptr() if dst_blocks is not None else None
+    args = (src.data_ptr(), dst.data_ptr(), sb, db, num_blocks, src_region_blocks, dst_region_blocks,
+            src_block_bytes, dst_block_bytes, planes, src_plane_stride, dst_plane_stride)
+    return lambda: _check(fn(*args, _stream()), "block pattern copy")
+
+
+def config2_ceilings(slots_np: np.ndarray, kc: torch.Tensor, vc: torch.Tensor, kl: torch.Tensor,
+                     vl: torch.Tensor) -> dict:
+    """Access-pattern ceilings of the configs[1] copies, on the same caches and linear buffers: whole 32 KiB
+    blocks of all 64 planes, cache blocks in the order the slot mapping visits them (random) and linear
+    blocks in order -- read random / write in order (the gather's pattern), the reverse (the scatter's),
+    and both in order (a plain copy of the same bytes)."""
+    dev = kc.device
+    t = int(slots_np.shape[0])
+    order_np = run_blocks(slots_np, BS)
+    nblk = min(order_np.size, t // BS)
+    order = torch.from_numpy(order_np[:nblk].copy()).to(dev)
+    blk_bytes = ROW * BS * 2
+    cache_stride, lin_stride = NB * blk_bytes, t * ROW * 2
+    legs = {
+        "gather_pattern": dict(src=(kc, vc), dst=(kl, vl), src_blocks=order, dst_blocks=None,
+                               src_region_blocks=NB, dst_region_blocks=t // BS, src_plane_stride=cache_stride,
+                               dst_plane_stride=lin_stride),
+        "scatter_pattern": dict(src=(kl, vl), dst=(kc, vc), src_blocks=None, dst_blocks=order,
+                                src_region_blocks=t // BS, dst_region_blocks=NB, src_plane_stride=lin_stride,
+                                dst_plane_stride=cache_stride),
+        "sequential": dict(src=(kc, vc), dst=(kl, vl), src_blocks=None, dst_blocks=None, src_region_blocks=NB,
+                           dst_region_blocks=t // BS, src_plane_stride=cache_stride, dst_plane_stride=lin_stride),
+    }
+    nbytes = 2 * NL * nblk * blk_bytes * 2
+    out = {"blocks_per_plane": nblk, "planes": 2 * NL, "bytes_per_launch_pair": nbytes,
+           "shape": "one wave per 1 KiB (16 B per lane), whole 32 KiB blocks, K and V caches one launch each"}
+    for name, leg in legs.items():
+        fns = [pattern_copy_fn(src, dst, src_blocks=leg["src_blocks"], dst_blocks=leg["dst_blocks"],
+                               num_blocks=nblk, src_region_blocks=leg["src_region_blocks"],
+                               dst_region_blocks=leg["dst_region_blocks"], src_block_bytes=blk_bytes,
+                               dst_block_bytes=blk_bytes, planes=NL, src_plane_stride=leg["src_plane_stride"],
+                               dst_plane_stride=leg["dst_plane_stride"]) for src, dst in zip(leg["src"], leg["dst"])]
+
+        def both(fns=fns):
+            for f in fns:
+                f()
+
+        both()
+        out[name] = rate(nbytes, batched_ms(both, launches=5, reps=5))
+    g, sc = out["gather_pattern"]["gbs"], out["scatter_pattern"]["gbs"]
+    out["step_ceiling_gbs"] = 2.0 / (1.0 / g + 1.0 / sc)
+    log(f"config 2 ceilings: gather pattern {g:.0f}, scatter pattern {sc:.0f}, sequential "
+        f"{out['sequential']['gbs']:.0f}, step {out['step_ceiling_gbs']:.0f} GB/s")
+    return out
+
+
+def config2_placements(slots: torch.Tensor, kl: torch.Tensor, vl: torch.Tensor, ok: torch.Tensor,
+                       ov: torch.Tensor, placements: int, steps: int) -> dict:
+    """The configs[1] step on freshly allocated caches, ``placements`` times in this process, each behind a
+    pad allocation of a different size (the caches land at different device addresses), all other buffers
+    unchanged: the spread of the step rate with where the caches land."""
+    from musa_aiter.ops import _hip
+
+    dev = kl.device
+    t = int(slots.shape[0])
+    scatter = _bind(_hip.library(), "musa_aiter_kv_linear_to_paged_multi_layer_bfloat16", 5, 6)
+    gather = _bind(_hip.library(), "musa_aiter_kv_paged_to_linear_multi_layer_bfloat16", 5, 6)
+    per_dir = 2 * (2 * NL * t * ROW * 2) + 8 * t
+    runs = []
+    for i in range(placements):
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        pad = torch.empty(((i * 7 + 1) % 16) * (200 << 20) + (i << 20), dtype=torch.uint8, device=dev)
+        kc = torch.empty((NL, NB, NH, HD, BS), device=dev, dtype=torch.bfloat16).normal_()
+        vc = torch.empty((NL, NB, NH, HD, BS), device=dev, dtype=torch.bfloat16).normal_()
+        sa = (kl.data_ptr(), vl.data_ptr(), slots.data_ptr(), kc.data_ptr(), vc.data_ptr(), NL, t, NB, NH, HD, BS)
+        ga = (kc.data_ptr(), vc.data_ptr(), slots.data_ptr(), ok.data_ptr(), ov.data_ptr(), NL, t, NB, NH, HD, BS)
+        for _ in range(2):
+            _check(scatter(*sa, _stream()), "scatter")
+            _check(gather(*ga, _stream()), "gather")
+        torch.cuda.synchronize()
+        ts, tg = EventTimer(), EventTimer()
+        for _ in range(steps):
+            e = ts.start()
+            _check(scatter(*sa, _stream()), "scatter")
+            ts.stop(e)
+            e = tg.start()
+            _check(gather(*ga, _stream()), "gather")
+            tg.stop(e)
+        torch.cuda.synchronize()
+        ms_s, ms_g = float(np.mean(ts.ms())), float(np.mean(tg.ms()))
+        runs.append({"pad_bytes": int(pad.numel()), "cache_address": hex(kc.data_ptr()), "scatter_ms": ms_s,
+                     "gather_ms": ms_g, "step_gbs": 2 * per_dir / ((ms_s + ms_g) * 1e-3) / 1e9})
+        del kc, vc, pad
+    torch.cuda.empty_cache()
+    vals = np.array([r["step_gbs"] for r in runs])
+    out = {"placements": placements, "steps_each": steps, "step_gbs_min": float(vals.min()),
+           "step_gbs_median": float(np.median(vals)), "step_gbs_max": float(vals.max()), "runs": runs}
+    log(f"config 2 placements: step {out['step_gbs_min']:.0f} / {out['step_gbs_median']:.0f} / "
+        f"{out['step_gbs_max']:.0f} GB/s (min / median / max of {placements})")
+    return out
+
+
 def bench_config2(steps: int, warmup: int) -> dict:
     """Multi-layer bf16 paged<->linear scatter + gather."""
     import musa_aiter
@@ -229,7 +354,7 @@ def bench_config2(steps: int, warmup: int) -> dict:
         "dominant": dominant[0],
         "dominant_avg_ms": avg_dom,
         "parity_roundtrip": parity,
-        "_tensors": (slots_np, kc, vc),
+        "_tensors": (slots_np, slots, kc, vc, kl, vl, ok, ov),
     }
 
 
@@ -324,6 +449,29 @@ def bench_config3() -> dict:
                                      "encode/decode steps in torch (tests/torch_ref.py)"}
         log(f"config 3 {name}: quant {out[name]['quant_store']['gbs']:.0f} GB/s, "
             f"dequant {out[name]['dequant_gather']['gbs']:.0f} GB/s, parity {parity}")
+    # Access-pattern ceilings on the same buffers: 32 KiB of bf16 rows (16 tokens) per 16 KiB FP8 block,
+    # cache blocks in the order the slot mapping visits them.
+    order_np = run_blocks(slots_np, BS)
+    nblk = min(order_np.size, t // BS)
+    order = torch.from_numpy(order_np[:nblk].copy()).to(dev)
+    lin_blk, cache_blk = ROW * BS * 2, ROW * BS
+    ceil_bytes = 2 * nblk * (lin_blk + cache_blk)
+    out["ceilings"] = {"blocks": nblk, "bytes_per_launch_pair": ceil_bytes}
+    for name, src_pair, dst_pair, sbytes, dbytes, sblocks, dblocks, sreg, dreg in (
+            ("quant_store_pattern", (kl, vl), (kc, vc), lin_blk, cache_blk, None, order, t // BS, NB),
+            ("dequant_gather_pattern", (kc, vc), (ok, ov), cache_blk, lin_blk, order, None, NB, t // BS)):
+        fns = [pattern_copy_fn(a, b, src_blocks=sblocks, dst_blocks=dblocks, num_blocks=nblk, src_region_blocks=sreg,
+                               dst_region_blocks=dreg, src_block_bytes=sbytes, dst_block_bytes=dbytes, planes=1,
+                               src_plane_stride=0, dst_plane_stride=0) for a, b in zip(src_pair, dst_pair)]
+
+        def both(fns=fns):
+            for f in fns:
+                f()
+
+        both()
+        out["ceilings"][name] = rate(ceil_bytes, batched_ms(both))
+    log(f"config 3 ceilings: quant pattern {out['ceilings']['quant_store_pattern']['gbs']:.0f}, dequant pattern "
+        f"{out['ceilings']['dequant_gather_pattern']['gbs']:.0f} GB/s")
     return out
 
 
@@ -812,28 +960,114 @@ def device_copy(mib: int, reps: int = 5) -> dict:
     return {"bytes_read_plus_written": nbytes, "avg_ms": float(ms.mean()), "gbs": nbytes / (ms.mean() * 1e-3) / 1e9}
 
 
-def cpu_baseline(slots_np: np.ndarray, kc: torch.Tensor, vc: torch.Tensor) -> dict:
-    """Time the numpy oracle on configs[1] itself: the gather and the scatter of every token of all 32 layers,
-    one layer at a time (each layer's K and V caches are copied to the host outside the timed region)."""
-    from oracle import kv_oracle as ko
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    t = int(slots_np.shape[0])
-    elapsed = 0.0
-    for layer in range(NL):
-        k_np = kc[layer].view(torch.int16).cpu().numpy().view(np.uint16)
-        v_np = vc[layer].view(torch.int16).cpu().numpy().view(np.uint16)
-        start = time.perf_counter()
-        k_lin = ko.paged_to_linear(k_np, slots_np)
-        v_lin = ko.paged_to_linear(v_np, slots_np)
-        ko.linear_to_paged(k_lin, k_np, slots_np)
-        ko.linear_to_paged(v_lin, v_np, slots_np)
-        elapsed += time.perf_counter() - start
-    sample_bytes = 2 * (2 * (2 * NL * t * ROW * 2) + 8 * t)
-    return {"value": sample_bytes / elapsed / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle (oracle/kv_oracle.py) gather + scatter of all {t} tokens x {NL} layers (K and V) "
-                      f"of configs[1], one layer at a time, {elapsed:.1f} s of CPU time; algorithmic bytes as for the "
-                      f"GPU; host has {os.cpu_count()} cpus, 1 used",
-            "seconds": elapsed}
+
+def _timed(fn, min_s: float) -> tuple[float, int]:
+    """Seconds per call of ``fn`` over at least ``min_s`` seconds (one untimed call first)."""
+    fn()
+    calls, start = 0, time.perf_counter()
+    while True:
+        fn()
+        calls += 1
+        elapsed = time.perf_counter() - start
+        if elapsed >= min_s:
+            return elapsed / calls, calls
+
+
+def cpu_baseline(slots_np: np.ndarray, kc: torch.Tensor, vc: torch.Tensor, sample_tokens: int = 8192,
+                 vector_layers: int = 8) -> dict:
+    """The reference's CPU algorithm on this host's cores, in the torch operations it uses
+    (oracle/torch_cpu_port.py: advanced-index gather + torch.where, kv_transfer.py:3047-3089; per-token
+    loop scatter, :3092-3112), with torch's thread count at the host's CPU share.
+
+    value: configs[1]'s step (gather + scatter of K and V in all 32 layers) on its first ``sample_tokens``
+    tokens -- the loop scatter of all 128k tokens would take minutes.  Legs: configs[0] at full shape with
+    the same ops; configs[1]'s whole token set, first ``vector_layers`` layers, with whole-tensor index ops
+    (the vectorised torch-CPU line).  Caches are copied to the host one layer at a time, outside the timed
+    regions; algorithmic bytes as for the GPU."""
+    from oracle import torch_cpu_port as tp
+
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    prev_threads = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        t = int(slots_np.shape[0])
+        n = min(sample_tokens, t)
+        s_cpu = torch.from_numpy(slots_np)
+        s_sample = s_cpu[:n].clone()
+        gather_s = scatter_s = 0.0
+        for layer in range(NL):
+            for cache in (kc, vc):
+                host = cache[layer].cpu()
+                start = time.perf_counter()
+                lin = tp.paged_to_linear_reference_ops(host, s_sample)
+                mid = time.perf_counter()
+                tp.linear_to_paged_reference_ops(lin, host, s_sample)
+                gather_s += mid - start
+                scatter_s += time.perf_counter() - mid
+        per_dir = 2 * (2 * NL * n * ROW * 2) + 8 * n
+        value = 2 * per_dir / (gather_s + scatter_s) / 1e9
+
+        # configs[0] at full shape: fp16 [1024, 8, 128, 16] caches, 32 sequences of 1-512 tokens.
+        s1 = torch.from_numpy(make_slots(1001, 32, 1, 512, 1024, BS))
+        t1 = int(s1.shape[0])
+        gen = torch.Generator().manual_seed(1)
+        k1 = torch.randn((1024, NH, HD, BS), generator=gen).to(torch.float16)
+        v1 = torch.randn((1024, NH, HD, BS), generator=gen).to(torch.float16)
+        b1 = 2 * (2 * t1 * ROW * 2) + 8 * t1
+        g1, gcalls = _timed(lambda: (tp.paged_to_linear_reference_ops(k1, s1),
+                                     tp.paged_to_linear_reference_ops(v1, s1)), 1.5)
+        l1 = (tp.paged_to_linear_reference_ops(k1, s1), tp.paged_to_linear_reference_ops(v1, s1))
+        sc1, scalls = _timed(lambda: (tp.linear_to_paged_reference_ops(l1[0], k1, s1),
+                                      tp.linear_to_paged_reference_ops(l1[1], v1, s1)), 1.5)
+
+        # Vectorised torch on configs[1]'s whole token set, first layers.
+        vec_g = vec_s = 0.0
+        for layer in range(min(vector_layers, NL)):
+            for cache in (kc, vc):
+                host = cache[layer].cpu()
+                start = time.perf_counter()
+                lin = tp.paged_to_linear_vectorised(host, s_cpu)
+                mid = time.perf_counter()
+                tp.linear_to_paged_vectorised(lin, host, s_cpu)
+                vec_g += mid - start
+                vec_s += time.perf_counter() - mid
+        vec_dir = 2 * (2 * min(vector_layers, NL) * t * ROW * 2) + 8 * t
+    finally:
+        torch.set_num_threads(prev_threads)
+    return {
+        "value": value, "unit": "GB/s", "cores": threads, "kind": "port", "config": "configs[1]",
+        "algorithm": "the reference's torch ops: advanced-index gather + torch.where (kv_transfer.py:3047-3089), "
+                     "per-token .item()/copy_ loop scatter (:3092-3112); oracle/torch_cpu_port.py",
+        "sample": f"configs[1] gather + scatter of K and V in all {NL} layers for the first {n} of {t} tokens "
+                  f"({gather_s + scatter_s:.1f} s: gather {gather_s:.2f} s, scatter loop {scatter_s:.1f} s); "
+                  f"torch threads {threads} (the scatter loop runs on one); host cpus {os.cpu_count()}",
+        "cpu_model": _cpu_model(),
+        "legs": {
+            "configs[1]_gather_reference_ops": {"gbs": per_dir / gather_s / 1e9, "seconds": gather_s,
+                                               "tokens": n},
+            "configs[1]_scatter_reference_ops": {"gbs": per_dir / scatter_s / 1e9, "seconds": scatter_s,
+                                                "tokens": n},
+            "configs[0]_gather_reference_ops": {"gbs": b1 / g1 / 1e9, "ms_per_call": g1 * 1e3, "calls": gcalls,
+                                               "tokens": t1, "tokens_per_ms": t1 / (g1 * 1e3),
+                                               "shape": "full: fp16 caches [1024, 8, 128, 16], 32 seqs U[1,512]"},
+            "configs[0]_scatter_reference_ops": {"gbs": b1 / sc1 / 1e9, "ms_per_call": sc1 * 1e3, "calls": scalls,
+                                                "tokens": t1},
+            "configs[1]_vectorised_torch": {"gbs_gather": vec_dir / vec_g / 1e9, "gbs_scatter": vec_dir / vec_s / 1e9,
+                                            "layers": min(vector_layers, NL), "tokens": t,
+                                            "ops": "index on the [NB, BS, NH, HD] view; index_put_ after a "
+                                                   "last-writer pass"},
+        },
+    }
 
 
 def main() -> int:
@@ -846,6 +1080,9 @@ def main() -> int:
                              "preload and block copies; 7 = SGLang HiCache transfers; 8 = LMCache host <-> "
                              "device copy batches; 9 = CacheGen codec)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--placements", type=int, default=5,
+                        help="re-allocate the configs[1] caches this many times and time the step on each "
+                             "(0 = skip)")
     parser.add_argument("--copy-mib", type=int, default=1024,
                         help="size of the plain device copy timed first (0 = skip)")
     args = parser.parse_args()
@@ -864,14 +1101,18 @@ def main() -> int:
         log(f"device copy of {args.copy_mib} MiB: {extra['device_copy']['gbs']:.0f} GB/s (read+write)")
         torch.cuda.empty_cache()
     c2 = bench_config2(args.steps, args.warmup)
-    slots_np, kc, vc = c2.pop("_tensors")
+    slots_np, slots, kc, vc, kl, vl, ok, ov = c2.pop("_tensors")
     log(f"config 2: scatter {c2['scatter']['gbs']:.0f} GB/s, gather {c2['gather']['gbs']:.0f} GB/s")
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(slots_np, kc, vc)
-        cpu.pop("seconds")
-        log(f"cpu baseline {cpu['value']:.2f} GB/s")
+        log(f"cpu baseline {cpu['value']:.2f} GB/s ({cpu['cores']} threads)")
+    ceilings = config2_ceilings(slots_np, kc, vc, kl, vl)
     del kc, vc
+    placements = None
+    if args.placements > 0:
+        placements = config2_placements(slots, kl, vl, ok, ov, args.placements, 5)
+    del kl, vl, ok, ov, slots
     torch.cuda.empty_cache()
     runners = {1: ("config1_fp16_single_layer_gather", bench_config1), 3: ("config3_fp8", bench_config3),
                4: ("config4_lmcache_two_x_nl", bench_config4), 5: ("config5_mla_rows", bench_config5),
@@ -884,7 +1125,6 @@ def main() -> int:
         extra[key] = fn()
         log(f"config {cfg}: {json.dumps(extra[key])}")
         torch.cuda.empty_cache()
-    dom = c2[c2["dominant"]]
     achieved = c2["bytes_per_direction"] / (c2["dominant_avg_ms"] * 1e-3) / 1e9
     line = {
         "metric": METRIC,
@@ -915,9 +1155,12 @@ def main() -> int:
                                        "(profiles/paged_kernels_cfg2_cfg3_traffic.md)",
                      "bytes_per_launch": c2["bytes_per_direction"], "avg_launch_ms": round(c2["dominant_avg_ms"], 4)},
         "cpu_baseline": cpu,
+        "ceilings": {**ceilings, "gather_frac_of_pattern": c2["gather"]["gbs"] / ceilings["gather_pattern"]["gbs"],
+                     "scatter_frac_of_pattern": c2["scatter"]["gbs"] / ceilings["scatter_pattern"]["gbs"],
+                     "step_frac_of_ceiling": c2["value_gbs"] / ceilings["step_ceiling_gbs"]},
+        "placements": placements,
         "extra": extra,
     }
-    _ = dom
     print(json.dumps(line), flush=True)
     return 0
 

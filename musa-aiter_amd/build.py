@@ -25,7 +25,7 @@ CSRC = ROOT / "csrc"
 OUT_DIR = ROOT / "musa_aiter" / "_lib"
 LIB_NAME = "libmusa_aiter_kv_hip.so"
 SOURCES = ("kv_paged_tiles.hip", "kv_paged_waves.hip", "kv_rows.hip", "kv_batch_copy.hip", "kv_cachegen.hip",
-           "kv_abi.hip")
+           "kv_pattern.hip", "kv_abi.hip")
 ARCH = os.environ.get("MUSA_AITER_HIP_ARCH", "gfx950")
 
 # Packed fp32 VALU forms are disabled for the whole library; fp32 division

@@ -499,6 +499,27 @@ int musa_aiter_dsv4_kv_copy_abi_version() { return 1; }
 const char* musa_aiter_hip_backend_name() { return "rocm-hip"; }
 const char* musa_aiter_hip_error_string(int code) { return hipGetErrorString(static_cast<hipError_t>(code)); }
 
+int musa_aiter_hip_block_pattern_copy(const void* src, void* dst, const int32_t* src_blocks,
+                                      const int32_t* dst_blocks, int64_t num_blocks, int64_t src_region_blocks,
+                                      int64_t dst_region_blocks, int64_t src_block_bytes, int64_t dst_block_bytes,
+                                      int64_t planes, int64_t src_plane_stride, int64_t dst_plane_stride,
+                                      void* stream) {
+  kvhip::BlockPatternParams p{};
+  p.src = src;
+  p.dst = dst;
+  p.src_blocks = src_blocks;
+  p.dst_blocks = dst_blocks;
+  p.num_blocks = num_blocks;
+  p.src_region_blocks = src_region_blocks;
+  p.dst_region_blocks = dst_region_blocks;
+  p.src_block_bytes = src_block_bytes;
+  p.dst_block_bytes = dst_block_bytes;
+  p.planes = planes;
+  p.src_plane_stride = src_plane_stride;
+  p.dst_plane_stride = dst_plane_stride;
+  return kvhip::launch_block_pattern(p, as_stream(stream));
+}
+
 int64_t musa_aiter_hip_graph_claim_arrays() {
   std::lock_guard<std::mutex> lock(g_claim_mu);
   return g_graph_claims == nullptr ? 0 : static_cast<int64_t>(g_graph_claims->size());

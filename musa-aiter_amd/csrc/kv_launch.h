@@ -137,6 +137,29 @@ void batch_copy_fill_desc(const uint64_t* src, const uint64_t* dst, const uint64
                           uint64_t* desc);
 hipError_t launch_batch_copy_desc(const uint64_t* desc, uint64_t tiles, uint32_t max_groups, hipStream_t stream);
 
+// Whole blocks copied between two block-addressed regions of `planes` planes
+// in a given block order (the access-pattern ceiling of a paged copy):
+// block i of the copy reads block src_blocks[i] (or i) of the source and
+// writes block dst_blocks[i] (or i) of the destination.  Block sizes are
+// multiples of 1 KiB, equal or in a 2:1 / 1:2 ratio; block ids outside
+// [0, *_region_blocks) are skipped.
+struct BlockPatternParams {
+  const void* src;
+  void* dst;
+  const int32_t* src_blocks;
+  const int32_t* dst_blocks;
+  int64_t num_blocks;
+  int64_t src_region_blocks;
+  int64_t dst_region_blocks;
+  int64_t src_block_bytes;
+  int64_t dst_block_bytes;
+  int64_t planes;
+  int64_t src_plane_stride;  // bytes
+  int64_t dst_plane_stride;
+};
+
+hipError_t launch_block_pattern(const BlockPatternParams& p, hipStream_t stream);
+
 // ----- CacheGen-style uniform-bin codec ------------------------------------------------
 
 // Input element types of the encoder.

@@ -27,6 +27,7 @@ struct TileArgs {
   int32_t block_size;          // used by the generic kernel only
   float inv_head_dim;          // 1 / head_dim, for small-integer division by head_dim
   BlockTableSlots bt;          // block_tables set: slots derived per dense token
+  int32_t row_groups;          // tile kernel: row groups per block (grid x of a gather = tile * row_groups + group)
 };
 
 // Slot of token t: the slot vector's entry, or the block-table slot of the

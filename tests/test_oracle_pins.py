@@ -288,3 +288,29 @@ def test_cachegen_helpers():
     assert all(np.isnan(v) for v in co.minmax(np.array([1.0, np.nan], np.float32)))
     # bincount with minlength
     assert co.histogram(np.array([[0, 2], [2, 2]], np.uint8), 4).tolist() == [1, 0, 3, 0]
+
+
+# ----- the torch-CPU port timed by bench.py's CPU baseline ----------------------------------------
+
+
+@pytest.mark.parametrize("form", ["reference_ops", "vectorised"])
+def test_torch_cpu_port_matches_the_oracle(form):
+    import torch
+
+    from oracle import torch_cpu_port as tp
+
+    rng = np.random.default_rng(19)
+    nb, nh, hd, bs, t = 6, 2, 8, 16, 70
+    slots = _dup_slots(nb * bs, t, rng)
+    cache = rng.integers(0, 1 << 16, size=(nb, nh, hd, bs), dtype=np.uint16)
+    lin = rng.integers(0, 1 << 16, size=(t, nh, hd), dtype=np.uint16)
+    gather = getattr(tp, f"paged_to_linear_{form}")
+    scatter = getattr(tp, f"linear_to_paged_{form}")
+    as_t = lambda a: torch.from_numpy(a.astype(np.int32)).to(torch.int16)  # noqa: E731
+    got = gather(as_t(cache), torch.from_numpy(slots)).numpy().astype(np.uint16)
+    assert np.array_equal(got, ko.paged_to_linear(cache, slots))
+    tc = as_t(cache)
+    scatter(as_t(lin), tc, torch.from_numpy(slots))
+    want = cache.copy()
+    ko.linear_to_paged(lin, want, slots)
+    assert np.array_equal(tc.numpy().astype(np.uint16), want)
