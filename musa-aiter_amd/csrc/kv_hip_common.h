@@ -316,6 +316,12 @@ __device__ __forceinline__ float div_rn(float x, float s) { return x / s; }
 // first correction makes q1 faithful, the second is Markstein's final
 // correction with a correctly rounded reciprocal.  No over- or underflow can
 // occur in that range.  Elements outside it use div_rn.
+//
+// When x has at most 12 significant bits (every bf16 and fp16 value) q1 is
+// already RN(x/s): checked exhaustively over every pair of significands (all
+// 2^11 x all 2^23 for 12-bit x; tests/quotient_check.c), and both sides scale
+// exactly by powers of two inside the range, so those inputs skip the second
+// correction (2 of the ~13 VALU operations per quantised element).
 // ---------------------------------------------------------------------------
 constexpr uint32_t kFastLoBits = 0x21800000u;  // 2^-60
 constexpr uint32_t kFastHiBits = 0x5D800000u;  // 2^60
@@ -324,10 +330,13 @@ __device__ __forceinline__ bool fast_scale_ok(float s) {
   return (__float_as_uint(s) - kFastLoBits) < (kFastHiBits - kFastLoBits);
 }
 
+// NARROW: x is a widened bf16 / fp16 value (at most 12 significant bits).
+template <bool NARROW>
 __device__ __forceinline__ float quot_fast(float x, float s, float r) {
   const float q0 = x * r;
   const float e0 = __builtin_fmaf(-s, q0, x);
   const float q1 = __builtin_fmaf(e0, r, q0);
+  if constexpr (NARROW) return q1;
   const float e1 = __builtin_fmaf(-s, q1, x);
   return __builtin_fmaf(e1, r, q1);
 }

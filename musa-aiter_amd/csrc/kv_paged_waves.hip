@@ -276,17 +276,17 @@ struct TileBound {
   }
 };
 
-template <int CODEC>
+template <int CODEC, int LDT>
 __device__ __forceinline__ uint32_t quant_soft(float x, float sc, float r, bool fast) {
-  return fast ? fp8_encode_fast<CODEC>(quot_fast(x, sc, r)) : fp8_encode<CODEC>(div_rn(x, sc));
+  return fast ? fp8_encode_fast<CODEC>(quot_fast<LDT != kLinF32>(x, sc, r)) : fp8_encode<CODEC>(div_rn(x, sc));
 }
 
 // One element, checked on its own (edge columns of partial runs).
-template <int CODEC>
+template <int CODEC, int LDT>
 __device__ __forceinline__ uint32_t quant_one(float x, float sc, float r, bool scale_ok) {
   const uint32_t ax = __float_as_uint(x) & 0x7FFFFFFFu;
   const bool fast = scale_ok && (ax == 0u || (ax >= kFastLoBits && ax < kFastHiBits));
-  return quant_soft<CODEC>(x, sc, r, fast);
+  return quant_soft<CODEC, LDT>(x, sc, r, fast);
 }
 
 template <int ELT_L, int LDT, int RPL>
@@ -397,7 +397,8 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const
             for (int g = 0; g < 2; ++g) {
               float w[4];
 #pragma unroll
-              for (int k = 0; k < 4; ++k) w[k] = quot_fast(tile_elem<ELT_L, LDT, RPL>(in[4 * g + k], q), sc, r);
+              for (int k = 0; k < 4; ++k)
+                w[k] = quot_fast<LDT != kLinF32>(tile_elem<ELT_L, LDT, RPL>(in[4 * g + k], q), sc, r);
               word[g] = fp8_pack4_hw<CODEC>(w[0], w[1], w[2], w[3]);
             }
             lds_half[2 * lds_slot<RPL, NCG>((rg * RPL + q) * NCG + ct)] = u32x2{word[0], word[1]};
@@ -427,7 +428,7 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const
 #pragma unroll
         for (int q = 0; q < RPL; ++q)
           crow[q * BS + c] =
-              static_cast<uint8_t>(quant_one<CODEC>(tile_elem<ELT_L, LDT, RPL>(piece, q), sc, r, scale_ok));
+              static_cast<uint8_t>(quant_one<CODEC, LDT>(tile_elem<ELT_L, LDT, RPL>(piece, q), sc, r, scale_ok));
       }
     }
   }
