@@ -1,28 +1,30 @@
 """Opt-in host/device byte-copy batches for LMCache on MI355X (ROCm HIP backend).
 
-Public names, signatures, defaults, return values and exception messages follow the reference
-module ``musa_aiter/ops/lmcache_musa_batch_copy.py`` (0.5.0):
+Contract (the reference's ``musa_aiter/ops/lmcache_musa_batch_copy.py``, 0.5.0; public names,
+keyword arguments, defaults, return values, gate variables and messages, :1-263):
 
 - ``lmcache_musa_memcpy_batch_async`` submits one unordered batch of byte copies, all host ->
   device or all device -> host, on the current stream of the GPU endpoints' device.  ``True``
   means submitted (or empty); ``False`` means the feature is not requested
-  (``MUSA_AITER_LMCACHE_BATCH_COPY=1`` / ``LMCACHE_MUSA_DIRECT_COPY=1``) or the backend is
-  unavailable, so the caller keeps its own path (reference :121-215);
+  (``MUSA_AITER_LMCACHE_BATCH_COPY=1`` / ``LMCACHE_MUSA_DIRECT_COPY=1``), the backend is
+  unavailable or an entry is not a host <-> GPU pair, so the caller keeps its own path;
 - the batch is validated and split at host registration boundaries by
-  ``lmcache_musa_batch_copy_plan``, then submitted in stream-ordered chunks of at most
-  ``max_batch_entries`` entries (default 1024, ``MUSA_AITER_LMCACHE_BATCH_MAX_ENTRIES``).
+  ``lmcache_musa_batch_copy_plan`` and submitted in stream-ordered groups of at most
+  ``max_batch_entries`` entries (default 1024, ``MUSA_AITER_LMCACHE_BATCH_MAX_ENTRIES``); a group
+  that fails after an earlier one went out raises instead of falling back.
 
-Each chunk becomes one ``musa_aiter_hip_batch_copy`` call of ``libmusa_aiter_kv_hip.so``: ranges
-whose host side is pinned memory move in one batch-copy kernel launch per chunk (the GPU reads or
-writes the host memory over its mapping; with ``prefer_overlap_with_compute=True`` the kernel runs
-on at most 16 workgroups instead of 64, so that concurrent kernels keep the other compute units);
-pageable ranges go through ``hipMemcpyAsync``.
+Each group becomes one ``execute_batch_copy`` call of the extension object
+(``lmcache_musa_batch_copy_ext``), i.e. one ``musa_aiter_hip_batch_copy`` call of
+``libmusa_aiter_kv_hip.so``: pinned host ranges move in one batch-copy kernel launch (the GPU
+reads or writes the host memory over its mapping; ``prefer_overlap_with_compute=True`` keeps the
+kernel to 16 workgroups), pageable ranges go through ``hipMemcpyAsync``.
 """
 
 from __future__ import annotations
 
 import os
-from typing import Protocol, Sequence, cast
+from dataclasses import dataclass
+from typing import Protocol, Sequence
 
 import torch
 
@@ -34,6 +36,10 @@ from .lmcache_musa_batch_copy_plan import chunk_batch_copy_plan as _chunk_batch_
 
 _ABI_VERSION = 1
 _DEFAULT_MAX_BATCH_ENTRIES = 1024
+_MAX_ENTRIES_ENV = "MUSA_AITER_LMCACHE_BATCH_MAX_ENTRIES"
+
+# (source kind, destination kind) -> (direction, index of the host tensor in (source, destination)).
+_ROUTES = {("cpu", "gpu"): ("h2d", 0), ("gpu", "cpu"): ("d2h", 1)}
 
 
 class _BatchCopyExtension(Protocol):
@@ -54,61 +60,82 @@ def native_lmcache_musa_batch_copy_abi_version() -> int:
     return _ABI_VERSION
 
 
-def native_lmcache_musa_batch_copy_runtime_versions() -> tuple[int, int] | None:
-    """(runtime, driver) versions of the HIP runtime when the feature is requested (reference :42-56)."""
+def _extension_if_requested(*, need_batch: bool) -> _BatchCopyExtension | None:
+    """The extension object when the feature is requested and its ABI matches (and, with ``need_batch``,
+    it supports batched copies); ``None`` otherwise.  Any error the extension raises counts as absent."""
     if not lmcache_musa_batch_copy_requested():
         return None
     extension = load_lmcache_musa_batch_copy_ext()
     if extension is None:
         return None
     try:
-        if extension.abi_version() != _ABI_VERSION:
-            return None
+        usable = extension.abi_version() == _ABI_VERSION and (not need_batch or extension.batch_memcpy_supported())
+    except Exception:
+        return None
+    return extension if usable else None
+
+
+def native_lmcache_musa_batch_copy_runtime_versions() -> tuple[int, int] | None:
+    """(HIP runtime, driver) versions reported by the extension, or ``None`` when the feature is off."""
+    extension = _extension_if_requested(need_batch=False)
+    if extension is None:
+        return None
+    try:
         return extension.runtime_version(), extension.driver_version()
     except Exception:
         return None
 
 
-def _compatible_extension(extension: object | None) -> _BatchCopyExtension | None:
-    if extension is None:
-        return None
-    candidate = cast(_BatchCopyExtension, extension)
-    try:
-        if candidate.abi_version() != _ABI_VERSION or not candidate.batch_memcpy_supported():
-            return None
-    except Exception:
-        return None
-    return candidate
-
-
 def is_native_lmcache_musa_batch_copy_available() -> bool:
-    if not lmcache_musa_batch_copy_requested():
-        return False
-    return _compatible_extension(load_lmcache_musa_batch_copy_ext()) is not None
+    return _extension_if_requested(need_batch=True) is not None
 
 
 def select_lmcache_batch_copy_backend(plan: KVTransferPlan, *, native_available: bool | None = None,
                                       require_native: bool = False) -> KVBackendDecision:
-    """Classify an LMCache plan before submitting byte copies (reference :65-87)."""
+    """Backend decision for an LMCache transfer plan before any copy is submitted (the batch path counts
+    as the direct-batch capability; the caller's own copies are the reference path)."""
     if native_available is None:
         native_available = is_native_lmcache_musa_batch_copy_available()
-    return select_kv_backend(plan, capabilities=KVBackendCapabilities(direct_batch=bool(native_available),
-                                                                      reference=True),
-                             require_native=require_native)
+    capabilities = KVBackendCapabilities(direct_batch=bool(native_available), reference=True)
+    return select_kv_backend(plan, capabilities=capabilities, require_native=require_native)
 
 
 def _tensor_device_kind(tensor: torch.Tensor) -> str:
-    """"cpu", "gpu" (a ROCm device) or "unsupported"."""
-    kind = tensor.device.type.lower()
-    if kind == "cpu":
-        return "cpu"
-    if kind == "cuda":
-        return "gpu"
-    return "unsupported"
+    """"cpu", "gpu" (a ROCm device: torch's "cuda" type) or "unsupported"."""
+    return {"cpu": "cpu", "cuda": "gpu"}.get(tensor.device.type.lower(), "unsupported")
 
 
-def _tensor_capacity_bytes(tensor: torch.Tensor) -> int:
-    return tensor.numel() * tensor.element_size()
+@dataclass(frozen=True)
+class _Endpoints:
+    """What a batch's tensors say about it: its direction and its one GPU device."""
+
+    direction: str
+    device: tuple[str, int | None]
+
+
+def _classify(destinations: tuple, sources: tuple, require_pinned_host: bool) -> _Endpoints | None:
+    """Check every pair in order; ``None`` as soon as a pair is not host <-> GPU (not this backend's)."""
+    directions, devices = set(), set()
+    for index, (destination, source) in enumerate(zip(destinations, sources)):
+        if not isinstance(destination, torch.Tensor) or not isinstance(source, torch.Tensor):
+            raise TypeError("destinations and sources must contain torch.Tensor values")
+        if not (destination.is_contiguous() and source.is_contiguous()):
+            raise ValueError("batch-copy tensors must be contiguous")
+        route = _ROUTES.get((_tensor_device_kind(source), _tensor_device_kind(destination)))
+        if route is None:
+            return None
+        direction, host_side = route
+        pair = (source, destination)
+        if require_pinned_host and not pair[host_side].is_pinned():
+            raise ValueError(f"host tensor at index {index} must use pinned memory")
+        gpu = pair[1 - host_side]
+        directions.add(direction)
+        devices.add((gpu.device.type, gpu.device.index))
+    if len(directions) != 1:
+        raise ValueError("one batch cannot mix h2d and d2h copies")
+    if len(devices) != 1:
+        raise ValueError("all batch entries must use the same GPU device")
+    return _Endpoints(directions.pop(), devices.pop())
 
 
 def lmcache_musa_memcpy_batch_async(
@@ -126,72 +153,38 @@ def lmcache_musa_memcpy_batch_async(
 ) -> bool:
     """Submit an opt-in host/device byte-copy batch on the current stream.
 
-    ``True`` means the batch was submitted (or was empty). ``False`` means the
-    backend is not requested or unavailable, allowing the caller to use its
-    existing transfer path. Oversized plans are submitted as ordered chunks of
-    at most ``max_batch_entries`` entries on the same current stream.
+    ``True`` means the batch was submitted (or was empty); ``False`` means the backend was not
+    requested or is unavailable, so the caller uses its existing transfer path.  A plan longer than
+    ``max_batch_entries`` goes out as ordered groups on the same current stream.
     """
     destinations, sources, sizes = tuple(destinations), tuple(sources), tuple(sizes)
-    count = len(sizes)
-    if not destinations and not sources and not sizes:
+    if not (destinations or sources or sizes):
         return True
-    if len(destinations) != count or len(sources) != count:
+    if not len(destinations) == len(sources) == len(sizes):
         raise ValueError("destinations, sources, and sizes must have the same length")
-
-    directions: list[str] = []
-    gpu_devices: set[tuple[str, int | None]] = set()
-    for index, (destination, source) in enumerate(zip(destinations, sources)):
-        if not isinstance(destination, torch.Tensor) or not isinstance(source, torch.Tensor):
-            raise TypeError("destinations and sources must contain torch.Tensor values")
-        if not destination.is_contiguous() or not source.is_contiguous():
-            raise ValueError("batch-copy tensors must be contiguous")
-        kinds = (_tensor_device_kind(source), _tensor_device_kind(destination))
-        if kinds == ("cpu", "gpu"):
-            direction, host_tensor, gpu_tensor = "h2d", source, destination
-        elif kinds == ("gpu", "cpu"):
-            direction, host_tensor, gpu_tensor = "d2h", destination, source
-        else:
-            return False
-        if require_pinned_host and not host_tensor.is_pinned():
-            raise ValueError(f"host tensor at index {index} must use pinned memory")
-        directions.append(direction)
-        gpu_devices.add((gpu_tensor.device.type, gpu_tensor.device.index))
-    if len(set(directions)) != 1:
-        raise ValueError("one batch cannot mix h2d and d2h copies")
-    if len(gpu_devices) != 1:
-        raise ValueError("all batch entries must use the same GPU device")
-
-    plan = _build_batch_copy_plan(
-        direction=directions[0],
-        sizes=sizes,
-        source_capacities=[_tensor_capacity_bytes(t) for t in sources],
-        destination_capacities=[_tensor_capacity_bytes(t) for t in destinations],
-        source_offsets=source_offsets,
-        destination_offsets=destination_offsets,
-        host_registration_offsets=host_registration_offsets,
-        pin_chunk_size=pin_chunk_size,
-        destination_keys=[id(t) for t in destinations],
-    )
-
-    if not lmcache_musa_batch_copy_requested():
+    endpoints = _classify(destinations, sources, require_pinned_host)
+    if endpoints is None:
         return False
-    extension = _compatible_extension(load_lmcache_musa_batch_copy_ext())
+    nbytes = [t.numel() * t.element_size() for t in (*sources, *destinations)]
+    plan = _build_batch_copy_plan(
+        direction=endpoints.direction, sizes=sizes, source_capacities=nbytes[:len(sources)],
+        destination_capacities=nbytes[len(sources):], source_offsets=source_offsets,
+        destination_offsets=destination_offsets, host_registration_offsets=host_registration_offsets,
+        pin_chunk_size=pin_chunk_size, destination_keys=[id(t) for t in destinations])
+    extension = _extension_if_requested(need_batch=True)
     if extension is None:
         return False
-
-    for chunk_index, entries in enumerate(_chunk_batch_copy_plan(plan, _resolve_max_batch_entries(max_batch_entries))):
-        submitted = extension.execute_batch_copy(
-            [destinations[e.input_index] for e in entries],
-            [sources[e.input_index] for e in entries],
-            [e.destination_offset for e in entries],
-            [e.source_offset for e in entries],
-            [e.size for e in entries],
-            prefer_overlap_with_compute,
-        )
-        if not submitted:
-            if chunk_index:
-                raise RuntimeError("batch-copy chunk failed after an earlier chunk was submitted")
+    groups = _chunk_batch_copy_plan(plan, _resolve_max_batch_entries(max_batch_entries))
+    for number, group in enumerate(groups):
+        ok = extension.execute_batch_copy([destinations[e.input_index] for e in group],
+                                          [sources[e.input_index] for e in group],
+                                          [e.destination_offset for e in group], [e.source_offset for e in group],
+                                          [e.size for e in group], prefer_overlap_with_compute)
+        if ok:
+            continue
+        if number == 0:
             return False
+        raise RuntimeError("batch-copy chunk failed after an earlier chunk was submitted")
     return True
 
 
@@ -208,7 +201,7 @@ def lmcache_musa_memcpy_batch_async_internal(
     prefer_overlap_with_compute: bool = False,
     max_batch_entries: int | None = None,
 ) -> bool:
-    """LMCache-only facade requiring an explicit host registration boundary (reference :218-244)."""
+    """The LMCache entry: the same submission, with the host registration boundary mandatory."""
     if host_registration_offsets is None or pin_chunk_size is None:
         raise ValueError("LMCache internal API requires a host registration boundary")
     return lmcache_musa_memcpy_batch_async(
@@ -219,15 +212,18 @@ def lmcache_musa_memcpy_batch_async_internal(
 
 
 def _resolve_max_batch_entries(value: int | None) -> int:
+    """The explicit limit, else the environment's, else 1024."""
     if value is not None:
         if isinstance(value, bool) or not isinstance(value, int) or value <= 0:
             raise ValueError("max_batch_entries must be a positive integer")
         return value
-    configured = os.environ.get("MUSA_AITER_LMCACHE_BATCH_MAX_ENTRIES", str(_DEFAULT_MAX_BATCH_ENTRIES))
+    text = os.environ.get(_MAX_ENTRIES_ENV)
+    if text is None:
+        return _DEFAULT_MAX_BATCH_ENTRIES
     try:
-        configured_value = int(configured)
+        limit = int(text)
     except ValueError as exc:
-        raise ValueError("MUSA_AITER_LMCACHE_BATCH_MAX_ENTRIES must be an integer") from exc
-    if configured_value <= 0:
-        raise ValueError("MUSA_AITER_LMCACHE_BATCH_MAX_ENTRIES must be positive")
-    return configured_value
+        raise ValueError(f"{_MAX_ENTRIES_ENV} must be an integer") from exc
+    if limit <= 0:
+        raise ValueError(f"{_MAX_ENTRIES_ENV} must be positive")
+    return limit
