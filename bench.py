@@ -501,6 +501,27 @@ def bench_config4() -> dict:
             musa_aiter.lmcache_kv_paged_to_buffer_two_x_nl(kvcaches, m, s_c, BS, NH, HD)
 
     mg = batched_ms(per_chunk_gather, launches=5, reps=5) / nchunks
+    # The same per-chunk gathers through the reference-named C entry (host work of a ctypes call only), so
+    # consecutive launches are bound by the kernel rather than by the Python API's per-call host time.
+    from musa_aiter.ops import _hip
+
+    centry = getattr(_hip.library(), "lmcache_paged_to_kv_buffer_two_x_nl_coalesced_u16")
+    centry.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint64), ctypes.c_void_p] + [ctypes.c_int64] * 7 + \
+        [ctypes.c_void_p]
+    centry.restype = ctypes.c_int
+    cache_ptrs = (ctypes.c_uint64 * (2 * nl))(*[c.data_ptr() for axis in kvcaches for c in axis])
+    c_chunks = [(s_c, m.contiguous()) for s_c, m in chunks]
+
+    def per_chunk_gather_c():
+        for s_c, m in c_chunks:
+            _check(centry(m.data_ptr(), cache_ptrs, s_c.data_ptr(), nl, chunk, chunk, nb, BS, NH, HD, _stream()),
+                   "cfg4 chunk")
+
+    per_chunk_gather_c()
+    torch.cuda.synchronize()
+    flat = cache.reshape(2, nl, nb * BS, ROW)
+    parity = parity and all(bool(torch.equal(m, flat[:, :, s_c])) for s_c, m in c_chunks)
+    mc = batched_ms(per_chunk_gather_c, launches=5, reps=5) / nchunks
     mb = batched_ms(lambda: musa_aiter.lmcache_kv_paged_to_buffer_two_x_nl(kvcaches, memory, slots, BS, NH, HD),
                     launches=10)
     ms = batched_ms(lambda: musa_aiter.lmcache_kv_buffer_to_paged_two_x_nl(memory, kvcaches, slots, 0, BS, NH, HD),
@@ -508,10 +529,12 @@ def bench_config4() -> dict:
     per_chunk = 2 * (2 * nl * chunk * ROW * 2) + 8 * chunk
     return {"chunk_tokens": chunk, "chunks": nchunks, "bytes_per_chunk": per_chunk, "parity": parity,
             "gather_per_chunk_call": rate(per_chunk, mg, chunk),
+            "gather_per_chunk_c_abi": rate(per_chunk, mc, chunk),
             "gather_batched_16": rate(per_chunk * nchunks, mb, chunk * nchunks),
             "scatter_batched_16": rate(per_chunk * nchunks, ms, chunk * nchunks),
-            "note": "per-chunk calls go through the Python API (validation, pointer tables) back to back; "
-                    "batched = one call for all 16 chunks"}
+            "note": "per-chunk calls go through the Python API (validation, pointer tables) back to back, or through "
+                    "the reference-named C entry (lmcache_paged_to_kv_buffer_two_x_nl_coalesced_u16); each of the 16 "
+                    "chunks gathers its own rows into its own buffer slice; batched = one call for all 16 chunks"}
 
 
 def bench_config5() -> dict:
