@@ -91,11 +91,12 @@ def make_covering_slots(seed: int, tokens: int, lo: int, hi: int, num_blocks: in
     return sequence_slots(rng, lengths, num_blocks=num_blocks, block_size=block_size)
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "paged_kernels_cfg2_cfg3_traffic.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "kv_kernels_hbm_traffic.md")
 
 
 def profiled_traffic(direction: str) -> int | None:
-    """HBM bytes per launch of a profiled kernel (cfg 2 scatter/gather, cfg 3 FP8 quant/dequant), from the
+    """HBM bytes per launch of a profiled kernel (cfg 2 scatter/gather, cfg 3 FP8 quant/dequant, cfg 1 gather, one
+    cfg 4 chunk gather), from the
     committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes (scaled by the plain-copy calibration); None if absent."""
     try:
         with open(TRAFFIC_PROFILE) as fh:
@@ -381,6 +382,7 @@ def bench_config1() -> dict:
     ms = batched_ms(lambda: _check(fn(*args, _stream()), "cfg1 gather"), launches=50)
     nbytes = 2 * (2 * t * ROW * 2) + 8 * t
     return {"tokens": t, "bytes_per_call": nbytes, "gather": rate(nbytes, ms, t), "parity": parity,
+            "traffic_per_call": profiled_traffic("cfg1_gather"),
             "parity_check": "every gathered row equals its slot's cache row (torch indexing)",
             "api": "musa_aiter_kv_paged_to_linear_half"}
 
@@ -528,6 +530,7 @@ def bench_config4() -> dict:
                     launches=10)
     per_chunk = 2 * (2 * nl * chunk * ROW * 2) + 8 * chunk
     return {"chunk_tokens": chunk, "chunks": nchunks, "bytes_per_chunk": per_chunk, "parity": parity,
+            "traffic_per_chunk": profiled_traffic("cfg4_chunk_gather"),
             "gather_per_chunk_call": rate(per_chunk, mg, chunk),
             "gather_per_chunk_c_abi": rate(per_chunk, mc, chunk),
             "gather_batched_16": rate(per_chunk * nchunks, mb, chunk * nchunks),
@@ -1006,7 +1009,7 @@ def _timed(fn, min_s: float) -> tuple[float, int]:
             return elapsed / calls, calls
 
 
-def cpu_baseline(slots_np: np.ndarray, kc: torch.Tensor, vc: torch.Tensor, sample_tokens: int = 8192,
+def cpu_baseline(slots_np: np.ndarray, kc: torch.Tensor, vc: torch.Tensor, sample_tokens: int = 32768,
                  vector_layers: int = 8) -> dict:
     """The reference's CPU algorithm on this host's cores, in the torch operations it uses
     (oracle/torch_cpu_port.py: advanced-index gather + torch.where, kv_transfer.py:3047-3089; per-token
@@ -1175,7 +1178,7 @@ def main() -> int:
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(c2["dominant"]),
                      "traffic_source": "rocprofv3 FETCH_SIZE x2.000 + WRITE_SIZE x1.000 per dispatch "
-                                       "(profiles/paged_kernels_cfg2_cfg3_traffic.md)",
+                                       "(profiles/kv_kernels_hbm_traffic.md)",
                      "bytes_per_launch": c2["bytes_per_direction"], "avg_launch_ms": round(c2["dominant_avg_ms"], 4)},
         "cpu_baseline": cpu,
         "ceilings": {**ceilings, "gather_frac_of_pattern": c2["gather"]["gbs"] / ceilings["gather_pattern"]["gbs"],
