@@ -381,10 +381,35 @@ def bench_config1() -> dict:
     parity = bool(torch.equal(ok, paged_rows(kc)[slots]) and torch.equal(ov, paged_rows(vc)[slots]))
     ms = batched_ms(lambda: _check(fn(*args, _stream()), "cfg1 gather"), launches=50)
     nbytes = 2 * (2 * t * ROW * 2) + 8 * t
+    floor = short_launch_floor(slots_np, nb, torch.float16)
     return {"tokens": t, "bytes_per_call": nbytes, "gather": rate(nbytes, ms, t), "parity": parity,
-            "traffic_per_call": profiled_traffic("cfg1_gather"),
+            "traffic_per_call": profiled_traffic("cfg1_gather"), "floor": floor,
             "parity_check": "every gathered row equals its slot's cache row (torch indexing)",
             "api": "musa_aiter_kv_paged_to_linear_half"}
+
+
+def short_launch_floor(slots_np: np.ndarray, nb: int, dtype: torch.dtype) -> dict:
+    """What one launch of configs[0]'s size costs with no index work: the gather's bytes as whole cache blocks
+    (K and V two planes of one launch), copied by the block-pattern kernel back to back like the gather --
+    cache blocks in the order the slots visit them, or both sides in order."""
+    dev = torch.device("cuda", 0)
+    t = int(slots_np.shape[0])
+    nblk = t // BS
+    blk_bytes = NH * HD * BS * torch.tensor([], dtype=dtype).element_size()
+    src = torch.zeros((2, nb, NH, HD, BS), dtype=dtype, device=dev)
+    dst = torch.empty((2, nblk * BS, NH, HD), dtype=dtype, device=dev)
+    order = torch.from_numpy(run_blocks(slots_np, BS)[:nblk].copy()).to(dev)
+    nbytes = 2 * nblk * blk_bytes * 2
+    out = {"bytes_per_launch": nbytes, "blocks_per_plane": nblk, "planes": 2}
+    for name, blocks in (("gather_pattern", order), ("sequential", None)):
+        fn = pattern_copy_fn(src, dst, src_blocks=blocks, dst_blocks=None, num_blocks=nblk, src_region_blocks=nb,
+                             dst_region_blocks=nblk, src_block_bytes=blk_bytes, dst_block_bytes=blk_bytes, planes=2,
+                             src_plane_stride=nb * blk_bytes, dst_plane_stride=nblk * blk_bytes)
+        fn()
+        out[name] = rate(nbytes, batched_ms(fn, launches=50))
+    log(f"config 1 floor: gather pattern {out['gather_pattern']['p50_ms'] * 1e3:.2f} us, sequential "
+        f"{out['sequential']['p50_ms'] * 1e3:.2f} us per launch")
+    return out
 
 
 def bench_config3() -> dict:
@@ -524,6 +549,26 @@ def bench_config4() -> dict:
     flat = cache.reshape(2, nl, nb * BS, ROW)
     parity = parity and all(bool(torch.equal(m, flat[:, :, s_c])) for s_c, m in c_chunks)
     mc = batched_ms(per_chunk_gather_c, launches=5, reps=5) / nchunks
+    # The floor of such a launch: each chunk's bytes as whole 32 KiB blocks of all 64 planes (cache blocks in the
+    # order the chunk's slots visit them, buffer blocks in order), by the block-pattern kernel, same rotation.
+    blk_bytes = BS * ROW * 2
+    floor_fns = []
+    for i in range(nchunks):
+        order = torch.from_numpy(run_blocks(slots_np[i * chunk:(i + 1) * chunk], BS)[:chunk // BS].copy()).to(dev)
+        dst_blocks = torch.arange(i * (chunk // BS), (i + 1) * (chunk // BS), dtype=torch.int32, device=dev)
+        floor_fns.append(pattern_copy_fn(cache, memory, src_blocks=order, dst_blocks=dst_blocks,
+                                         num_blocks=int(order.numel()), src_region_blocks=nb,
+                                         dst_region_blocks=chunk * nchunks // BS, src_block_bytes=blk_bytes,
+                                         dst_block_bytes=blk_bytes, planes=2 * nl, src_plane_stride=nb * blk_bytes,
+                                         dst_plane_stride=chunk * nchunks * ROW * 2))
+
+    def per_chunk_floor():
+        for f in floor_fns:
+            f()
+
+    per_chunk_floor()
+    mf = batched_ms(per_chunk_floor, launches=5, reps=5) / nchunks
+    floor_bytes = 2 * nl * (chunk // BS) * blk_bytes * 2
     mb = batched_ms(lambda: musa_aiter.lmcache_kv_paged_to_buffer_two_x_nl(kvcaches, memory, slots, BS, NH, HD),
                     launches=10)
     ms = batched_ms(lambda: musa_aiter.lmcache_kv_buffer_to_paged_two_x_nl(memory, kvcaches, slots, 0, BS, NH, HD),
@@ -533,6 +578,7 @@ def bench_config4() -> dict:
             "traffic_per_chunk": profiled_traffic("cfg4_chunk_gather"),
             "gather_per_chunk_call": rate(per_chunk, mg, chunk),
             "gather_per_chunk_c_abi": rate(per_chunk, mc, chunk),
+            "per_chunk_floor_pattern_copy": rate(floor_bytes, mf),
             "gather_batched_16": rate(per_chunk * nchunks, mb, chunk * nchunks),
             "scatter_batched_16": rate(per_chunk * nchunks, ms, chunk * nchunks),
             "note": "per-chunk calls go through the Python API (validation, pointer tables) back to back, or through "

@@ -27,6 +27,8 @@
 #include "kv_launch.h"
 #include "kv_paged_args.h"
 
+#include <type_traits>
+
 namespace kvhip {
 
 // ----- the cooperative tile kernel (16- and 32-bit copies) ----------------------------
@@ -94,7 +96,7 @@ __device__ __forceinline__ void lds_barrier() {
 template <bool SCATTER>
 constexpr int kChunksPerGroup = SCATTER ? 4 : 2;
 
-template <int ELT, int BS, bool SCATTER>
+template <int ELT, int BS, bool SCATTER, bool FEW>
 __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs a) {
   using S = CoopShape<ELT, BS>;
   constexpr int CG = S::CG, NCG = S::NCG, ROWB = S::ROWB, kRows = S::kRows;
@@ -159,6 +161,7 @@ __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs
   const uint32_t cpiece = static_cast<uint32_t>(tid) * 16u;
   const uint32_t stride32 = static_cast<uint32_t>(a.lin_token_stride);
 
+  [[maybe_unused]] bool tile_used = false;  // wave-uniform: some chunk of this workgroup has filled the LDS tile
   while (heads) {
     const int i = __builtin_ctzll(heads);
     heads &= heads - 1;
@@ -178,20 +181,30 @@ __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs
     auto coff = [&](int k) -> uint32_t { return prow_in(k) ? cpiece + k * kCacheStep : kOffOob; };
     auto loff = [&](int k) -> uint32_t { return (lmine && lrow_in(k)) ? lbase + k * kLinStep : kOffOob; };
 
+    // Every payload load of the run is issued before its first store.  Wave
+    // memory counters retire in issue order, so a wait for a load issued after
+    // a store would also wait for that store's round trip.
+    constexpr int C = kChunksPerGroup<SCATTER>;
     if constexpr (!SCATTER) {
-      u32x4 nxt = buf_ld16(cbuf, coff(0));
-      for (int k = 0; k < nchunks; ++k) {
-        const u32x4 cur = nxt;
-        nxt = buf_ld16(cbuf, (k + 1 < nchunks) ? coff(k + 1) : kOffOob);
+      u32x4 v[C];
+#pragma unroll
+      for (int k = 0; k < C; ++k) v[k] = buf_ld16(cbuf, k < nchunks ? coff(k) : kOffOob);
+#pragma unroll
+      for (int k = 0; k < C; ++k) {
+        if (k >= nchunks) break;
+        if (tile_used) lds_barrier();  // the tile's previous column reads are done
+        tile_used = true;
         if (prow_in(k)) {
           uint32_t* const d = reinterpret_cast<uint32_t*>(tile + pr * PITCH + pg * 16);
-          d[0] = cur[0]; d[1] = cur[1]; d[2] = cur[2]; d[3] = cur[3];
+          d[0] = v[k][0]; d[1] = v[k][1]; d[2] = v[k][2]; d[3] = v[k][3];
         }
         lds_barrier();
         buf_st16(lbuf, loff(k), lds_column_piece<ELT, PITCH>(tile, lq * RPL, lc));
-        lds_barrier();
       }
-    } else {
+    } else if constexpr (!FEW) {
+      // Large scatters: chunk by chunk with the next chunk's load in flight
+      // (2 % faster than the form below when the grid is many rounds of
+      // workgroups, measured; their time is the random cache writes).
       u32x4 nxt = buf_ld16(lbuf, loff(0));
       const bool full_run = (c0 == 0) && (c1 == BS);
       for (int k = 0; k < nchunks; ++k) {
@@ -206,8 +219,6 @@ __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs
         if (full_run) {
           buf_st16(cbuf, off, w);
         } else {
-          // Whole pieces inside the run go as one vector; edge pieces store
-          // only their in-run columns.
           const bool whole = lo >= c0 && lo + CG <= c1;
           buf_st16(cbuf, whole ? off : kOffOob, w);
 #pragma unroll
@@ -218,6 +229,44 @@ __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs
         }
         lds_barrier();
       }
+    } else {
+      // Small scatters (a few rounds of workgroups) are bound by each
+      // workgroup's latency.  Full and partial runs are separate straight-line
+      // paths, so that the compiler's wait counts are exact on each and no
+      // chunk's load wait covers an earlier chunk's stores.
+      auto scatter_run = [&](auto full_tag) {
+        constexpr bool kFull = decltype(full_tag)::value;
+        u32x4 v[C];
+#pragma unroll
+        for (int k = 0; k < C; ++k) v[k] = buf_ld16(lbuf, k < nchunks ? loff(k) : kOffOob);
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+          if (k >= nchunks) break;
+          if (tile_used) lds_barrier();  // the tile's previous row reads are done
+          tile_used = true;
+          if (lmine && lrow_in(k)) lds_put_column<ELT, PITCH>(tile, lq * RPL, lc, v[k]);
+          lds_barrier();
+          const uint32_t* const d = reinterpret_cast<const uint32_t*>(tile + pr * PITCH + pg * 16);
+          const u32x4 w = {d[0], d[1], d[2], d[3]};
+          const uint32_t off = coff(k);
+          if constexpr (kFull) {
+            buf_st16(cbuf, off, w);
+          } else {
+            // Whole pieces inside the run go as one vector; edge pieces store
+            // only their in-run columns.
+            const int lo = pg * CG;
+            const bool whole = lo >= c0 && lo + CG <= c1;
+            buf_st16(cbuf, whole ? off : kOffOob, w);
+#pragma unroll
+            for (int cc = 0; cc < CG; ++cc) {
+              const bool mine = !whole && off != kOffOob && lo + cc >= c0 && lo + cc < c1;
+              buf_st_elem<ELT>(cbuf, mine ? off + cc * ELT : kOffOob, piece_elem<ELT>(w, cc));
+            }
+          }
+        }
+      };
+      if (c0 == 0 && c1 == BS) scatter_run(std::true_type{});
+      else scatter_run(std::false_type{});
     }
   }
 
@@ -294,6 +343,10 @@ hipError_t launch_elem(const TileArgs& a, int64_t planes, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Scatters of at most this many workgroups (about four rounds of resident
+// workgroups on 256 CUs) take the latency form of the kernel.
+constexpr int64_t kFewScatterGroups = 8192;
+
 template <int ELT, int BS, bool SCATTER>
 hipError_t launch_tile(const TileArgs& a0, int64_t planes, hipStream_t stream) {
   using S = CoopShape<ELT, BS>;
@@ -311,7 +364,13 @@ hipError_t launch_tile(const TileArgs& a0, int64_t planes, hipStream_t stream) {
     if (tiles > 0x7FFFFFFF / groups) return hipErrorInvalidValue;
     grid = dim3(static_cast<uint32_t>(tiles * groups), static_cast<uint32_t>(planes), 1);
   }
-  hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, SCATTER>), grid, dim3(kCoopThreads), 0, stream, a);
+  if constexpr (SCATTER) {
+    if (tiles * planes * groups <= kFewScatterGroups) {
+      hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, true, true>), grid, dim3(kCoopThreads), 0, stream, a);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, SCATTER, false>), grid, dim3(kCoopThreads), 0, stream, a);
   return hipGetLastError();
 }
 
