@@ -95,6 +95,39 @@ __device__ __forceinline__ void buf_st_elem(buf_t r, uint32_t off, uint32_t v) {
 }
 
 // ---------------------------------------------------------------------------
+// XCD-aware workgroup order.  MI355X dispatches workgroup i of a launch (in
+// linearised grid order) to XCD i mod 8, and each XCD has its own L2.  With
+// ON, a workgroup takes the coordinates of position w of the grid, where XCD
+// k's workgroups cover one contiguous eighth of the grid in order: tiles that
+// neighbour each other (overlapping slot windows, the row groups of one
+// cache block) then run on the same XCD.  The grid must hold fewer than 2^32
+// workgroups.
+// ---------------------------------------------------------------------------
+struct WgXyz {
+  uint32_t x, y, z;
+};
+
+template <bool ON>
+__device__ __forceinline__ WgXyz xcd_contiguous_wg() {
+  if constexpr (!ON) {
+    return {blockIdx.x, blockIdx.y, blockIdx.z};
+  } else {
+    constexpr uint32_t kXcds = 8;
+    const uint32_t gx = gridDim.x, gy = gridDim.y;
+    const uint32_t total = gx * gy * gridDim.z;
+    const uint32_t lin = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+    const uint32_t xcd = lin % kXcds, idx = lin / kXcds;
+    const uint32_t q = total / kXcds, r = total % kXcds;  // XCDs below r take q + 1 workgroups
+    const uint32_t w = xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
+    const uint32_t gxy = gx * gy;
+    const uint32_t z = w / gxy;
+    const uint32_t rem = w - z * gxy;
+    const uint32_t y = rem / gx;
+    return {rem - y * gx, y, z};
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Wave-level helpers (wave64).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }

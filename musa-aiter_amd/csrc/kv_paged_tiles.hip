@@ -96,6 +96,9 @@ __device__ __forceinline__ void lds_barrier() {
 template <bool SCATTER>
 constexpr int kChunksPerGroup = SCATTER ? 4 : 2;
 
+// FEW selects the form for launches bound by per-workgroup latency rather than
+// by HBM: for a scatter the loads-first chunk loop, for a gather the natural
+// workgroup order (FEW false: the XCD-contiguous order).
 template <int ELT, int BS, bool SCATTER, bool FEW>
 __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs a) {
   using S = CoopShape<ELT, BS>;
@@ -110,13 +113,15 @@ __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs
   // the row groups of one tile next to each other in x, so the pieces of one
   // cache block are read by neighbouring workgroups at the same time (3 %
   // faster on random blocks than visiting each group of all tiles in turn).
-  const int64_t tile_id =
-      SCATTER ? static_cast<int64_t>(blockIdx.x) : static_cast<int64_t>(blockIdx.x) / a.row_groups;
+  // Gathers over many planes give each XCD a contiguous eighth of the grid
+  // (FEW false; chosen by the launcher).
+  const WgXyz wg = xcd_contiguous_wg<!SCATTER && !FEW>();
+  const int64_t tile_id = SCATTER ? static_cast<int64_t>(wg.x) : static_cast<int64_t>(wg.x) / a.row_groups;
   const int64_t group =
-      SCATTER ? static_cast<int64_t>(blockIdx.z) : static_cast<int64_t>(blockIdx.x) - tile_id * a.row_groups;
+      SCATTER ? static_cast<int64_t>(wg.z) : static_cast<int64_t>(wg.x) - tile_id * a.row_groups;
   const int64_t t0 = tile_id * kTileTokens;
   if (t0 >= a.num_tokens) return;
-  const int plane = static_cast<int>(blockIdx.y);
+  const int plane = static_cast<int>(wg.y);
   const int layer = plane >> 1;
   const int kv = plane & 1;
   // Rows [rb, re) of the block, in chunks of kRows.
@@ -344,8 +349,14 @@ hipError_t launch_elem(const TileArgs& a, int64_t planes, hipStream_t stream) {
 }
 
 // Scatters of at most this many workgroups (about four rounds of resident
-// workgroups on 256 CUs) take the latency form of the kernel.
-constexpr int64_t kFewScatterGroups = 8192;
+// workgroups on 256 CUs) take the loads-first chunk loop (FEW true).
+constexpr int64_t kFewGroups = 8192;
+// Gathers over at least this many planes take the XCD-contiguous workgroup
+// order (FEW false).  Measured on 128,708 tokens: the natural order slows
+// from 6.14 TB/s at 2 planes to 5.77 TB/s at 64, the XCD-contiguous order
+// stays at 5.88-5.92 TB/s; they cross between 16 and 32 planes.  Short
+// launches keep the natural order too (cfg 1: 13.0 against 13.9 us).
+constexpr int64_t kXcdOrderPlanes = 32;
 
 template <int ELT, int BS, bool SCATTER>
 hipError_t launch_tile(const TileArgs& a0, int64_t planes, hipStream_t stream) {
@@ -364,13 +375,15 @@ hipError_t launch_tile(const TileArgs& a0, int64_t planes, hipStream_t stream) {
     if (tiles > 0x7FFFFFFF / groups) return hipErrorInvalidValue;
     grid = dim3(static_cast<uint32_t>(tiles * groups), static_cast<uint32_t>(planes), 1);
   }
-  if constexpr (SCATTER) {
-    if (tiles * planes * groups <= kFewScatterGroups) {
-      hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, true, true>), grid, dim3(kCoopThreads), 0, stream, a);
-      return hipGetLastError();
-    }
-  }
-  hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, SCATTER, false>), grid, dim3(kCoopThreads), 0, stream, a);
+  const int64_t workgroups = tiles * planes * groups;
+  // (The XCD order indexes the grid in 32 bits.)
+  const bool few = SCATTER ? workgroups <= kFewGroups
+                           : !(planes >= kXcdOrderPlanes && workgroups > kFewGroups &&
+                               workgroups <= int64_t{0xFFFFFFFF});
+  if (few)
+    hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, SCATTER, true>), grid, dim3(kCoopThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, SCATTER, false>), grid, dim3(kCoopThreads), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -136,15 +136,18 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_gather_kernel(const 
     const int c1 = c0 + len;
     const int64_t tf = t0 - 1 + i;
     uint8_t* const chunk = cache + (blk * a.nrows + r0) * BS * ELT_C;
-    uint8_t* const lrow = lin + tf * a.lin_token_stride + trow * ELT_L;
-
     if (c0 < CG && c1 > BS - CG) {
-      // The run touches every column group: stage the whole chunk.
+      // The run touches every column group: stage the whole chunk.  Loads and
+      // stores go through wave-uniform buffer descriptors with per-lane 32-bit
+      // offsets (kOffOob for masked lanes): no per-lane branches and no shared
+      // 64-bit address registers, so the compiler issues all RPL loads back to
+      // back and never waits on one access before the next address.
+      const buf_t cb = make_buf(chunk);
       u32x4 v[RPL];
 #pragma unroll
       for (int k = 0; k < RPL; ++k) {
         const int pc = k * kWave + lane;
-        if (r0 + pc / NCG < r_end) v[k] = ld16(chunk + pc * 16);
+        v[k] = buf_ld16(cb, r0 + pc / NCG < r_end ? static_cast<uint32_t>(pc) * 16u : kOffOob);
       }
 #pragma unroll
       for (int k = 0; k < RPL; ++k) lds[lds_slot<RPL, NCG>(k * kWave + lane)] = v[k];
@@ -153,14 +156,17 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_gather_kernel(const 
 #pragma unroll
       for (int q = 0; q < RPL; ++q) d[q] = lds[lds_slot<RPL, NCG>((rg * RPL + q) * NCG + ct)];
       wave_lds_sync();
-      if (tile_in) {
+      // The run's first token row at row r0; the lane's rows start rg * RPL
+      // further.  Token offsets stay below 2 GiB (token stride <= 32 MiB).
+      const buf_t lb = make_buf(lin + tf * a.lin_token_stride + r0 * ELT_L);
+      const uint32_t lane_off = static_cast<uint32_t>(rg * RPL * ELT_L);
+      const uint32_t stride32 = static_cast<uint32_t>(a.lin_token_stride);
 #pragma unroll
-        for (int cc = 0; cc < CG; ++cc) {
-          const int c = ct * CG + cc;
-          if (c >= c0 && c < c1)
-            st16(lrow + static_cast<int64_t>(c - c0) * a.lin_token_stride,
+      for (int cc = 0; cc < CG; ++cc) {
+        const int c = ct * CG + cc;
+        const bool mine = tile_in && c >= c0 && c < c1;
+        buf_st16(lb, mine ? lane_off + static_cast<uint32_t>(c - c0) * stride32 : kOffOob,
                  gather_column<ELT_C, ELT_L, CODEC, LDT, RPL>(d, cc, sc));
-        }
       }
       continue;
     }
