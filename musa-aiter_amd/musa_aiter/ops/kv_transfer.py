@@ -318,11 +318,11 @@ def kv_paged_to_linear(
     slots = _ensure_slotmapping_vector(slot_mapping, expected_len=tcount, name=op)
     if key_cache.device != value_cache.device or slots.device != key_cache.device:
         raise ValueError("kv_paged_to_linear: all tensors must be on the same device")
+    _check_slots_in_bounds(slots, nb, bs, op)
     _float_elt(op, key_cache, value_cache)
     _check_gather_out(out_k, (tcount, nh, hd), key_cache.dtype, key_cache.device, op)
     _check_gather_out(out_v, (tcount, nh, hd), value_cache.dtype, value_cache.device, op)
     fill_zeros = _fill_mode(fill_skipped, out_k, out_v, op)
-    _check_slots_in_bounds(slots, nb, bs, op)
     _require_rocm(op, key_cache)
     ok = out_k if out_k is not None else torch.empty((tcount, nh, hd), dtype=key_cache.dtype, device=key_cache.device)
     ov = out_v if out_v is not None else torch.empty((tcount, nh, hd), dtype=value_cache.dtype, device=value_cache.device)
@@ -348,6 +348,7 @@ def kv_paged_to_linear_multi_layer(
     slots = _ensure_slotmapping_vector(slot_mapping, expected_len=tcount, name=op)
     if value_cache.device != key_cache.device or slots.device != key_cache.device:
         raise ValueError("kv_paged_to_linear_multi_layer: all tensors must be on the same device")
+    _check_slots_in_bounds(slots, nb, bs, op)
     if out_k is not None and tuple(out_k.shape) != (nl, tcount, nh, hd):
         raise ValueError(
             f"kv_paged_to_linear_multi_layer: out_k must be [num_layers, T, kv_heads, head_dim], got {tuple(out_k.shape)}")
@@ -360,7 +361,6 @@ def kv_paged_to_linear_multi_layer(
     _check_gather_out(out_k, (nl, tcount, nh, hd), key_cache.dtype, key_cache.device, op)
     _check_gather_out(out_v, (nl, tcount, nh, hd), value_cache.dtype, value_cache.device, op)
     fill_zeros = _fill_mode(fill_skipped, out_k, out_v, op)
-    _check_slots_in_bounds(slots, nb, bs, op)
     _require_rocm(op, key_cache)
     shape = (nl, tcount, nh, hd)
     ok = out_k if out_k is not None else torch.empty(shape, dtype=key_cache.dtype, device=key_cache.device)
@@ -397,8 +397,8 @@ def kv_linear_to_paged(
     dev = key_cache.device
     if any(x.device != dev for x in (key_linear, value_linear, key_cache, value_cache, slots)):
         raise ValueError("kv_linear_to_paged: all tensors must be on same device")
-    _float_elt(op, key_cache, value_cache)
     _check_slots_in_bounds(slots, nb, bs, op)
+    _float_elt(op, key_cache, value_cache)
     _require_rocm(op, key_cache)
     _paged_scatter(op, key_linear, value_linear, key_cache, value_cache, slots, nl=1, tcount=int(tcount), nb=nb,
                    nh=nh, hd=hd, bs=bs, token_dim=0)
@@ -433,8 +433,8 @@ def kv_linear_to_paged_multi_layer(
     dev = key_cache.device
     if any(x.device != dev for x in (key_linear, value_linear, key_cache, value_cache, slots)):
         raise ValueError("kv_linear_to_paged_multi_layer: all tensors must be on same device")
-    _float_elt(op, key_cache, value_cache)
     _check_slots_in_bounds(slots, nb, bs, op)
+    _float_elt(op, key_cache, value_cache)
     _require_rocm(op, key_cache)
     _paged_scatter(op, key_linear, value_linear, key_cache, value_cache, slots, nl=nl, tcount=tcount, nb=nb, nh=nh,
                    hd=hd, bs=bs, token_dim=1)
@@ -468,9 +468,9 @@ def kv_paged_to_merged_linear(
             raise ValueError("kv_paged_to_merged_linear: out dtype/device must match caches")
     if fill_skipped == "preserve" and out is None:
         raise ValueError("kv_paged_to_merged_linear: fill_skipped=preserve requires out")
+    _check_slots_in_bounds(slots, nb, bs, op)
     _float_elt(op, key_cache, value_cache)
     fill_zeros = fill_skipped != "preserve"
-    _check_slots_in_bounds(slots, nb, bs, op)
     _require_rocm(op, key_cache)
     res = out if out is not None else torch.empty((tcount, 2, nh, hd), dtype=key_cache.dtype, device=key_cache.device)
     _paged_gather(op, key_cache, value_cache, slots, nl=1, tcount=tcount, nb=nb, nh=nh, hd=hd, bs=bs,
@@ -496,8 +496,8 @@ def kv_merged_linear_to_paged(
     slots = _ensure_slotmapping_vector(slot_mapping, expected_len=tcount, name=op)
     if any(x.device != key_cache.device for x in (merged_linear, key_cache, value_cache, slots)):
         raise ValueError("kv_merged_linear_to_paged: all tensors must be on same device")
-    _float_elt(op, key_cache, value_cache)
     _check_slots_in_bounds(slots, nb, bs, op)
+    _float_elt(op, key_cache, value_cache)
     _require_rocm(op, key_cache)
     _paged_scatter(op, merged_linear[:, 0], merged_linear[:, 1], key_cache, value_cache, slots, nl=1, tcount=tcount,
                    nb=nb, nh=nh, hd=hd, bs=bs, token_dim=0)
@@ -526,9 +526,9 @@ def kv_paged_to_merged_linear_multi_layer(
             raise ValueError("kv_paged_to_merged_linear_multi_layer: out dtype/device must match caches")
     if fill_skipped == "preserve" and out is None:
         raise ValueError("kv_paged_to_merged_linear_multi_layer: fill_skipped=preserve requires out")
+    _check_slots_in_bounds(slots, nb, bs, op)
     _float_elt(op, key_cache, value_cache)
     fill_zeros = fill_skipped != "preserve"
-    _check_slots_in_bounds(slots, nb, bs, op)
     _require_rocm(op, key_cache)
     res = out if out is not None else torch.empty((nl, tcount, 2, nh, hd), dtype=key_cache.dtype,
                                                   device=key_cache.device)
@@ -557,8 +557,8 @@ def kv_merged_linear_to_paged_multi_layer(
     slots = _ensure_slotmapping_vector(slot_mapping, expected_len=tcount, name=op)
     if any(x.device != key_cache.device for x in (merged_linear, key_cache, value_cache, slots)):
         raise ValueError("kv_merged_linear_to_paged_multi_layer: all tensors must be on same device")
-    _float_elt(op, key_cache, value_cache)
     _check_slots_in_bounds(slots, nb, bs, op)
+    _float_elt(op, key_cache, value_cache)
     _require_rocm(op, key_cache)
     _paged_scatter(op, merged_linear[:, :, 0], merged_linear[:, :, 1], key_cache, value_cache, slots, nl=nl,
                    tcount=tcount, nb=nb, nh=nh, hd=hd, bs=bs, token_dim=1)
@@ -1546,11 +1546,11 @@ def kv_paged_to_mla_linear(
     slots = _ensure_slotmapping_vector(slot_mapping, expected_len=tcount, name=op)
     if k_pe_cache.device != kv_cache.device or slots.device != kv_cache.device:
         raise ValueError("kv_paged_to_mla_linear: all tensors must be on the same device")
+    _check_slots_in_bounds(slots, nb, bs, op)
     if out_kv is not None and tuple(out_kv.shape) != (tcount, kv_dim):
         raise ValueError(f"{op}: first_out shape mismatch {tuple(out_kv.shape)}")
     if out_k_pe is not None and tuple(out_k_pe.shape) != (tcount, pe_dim):
         raise ValueError(f"{op}: second_out shape mismatch {tuple(out_k_pe.shape)}")
-    _check_slots_in_bounds(slots, nb, bs, op)
     _require_rocm(op, kv_cache)
     okv = out_kv if out_kv is not None else torch.empty((tcount, kv_dim), dtype=kv_cache.dtype, device=kv_cache.device)
     ope = out_k_pe if out_k_pe is not None else torch.empty((tcount, pe_dim), dtype=k_pe_cache.dtype,

@@ -80,6 +80,26 @@ def test_slot_bounds_contract():
                                                   torch.tensor([0, 13]))
 
 
+def test_slot_bounds_come_before_output_and_dtype_checks():
+    # The reference checks slot bounds right after the device check
+    # (kv_transfer.py:3153, :3234, :3351, :3858): a call that is wrong in
+    # several ways reports the bad slot first.
+    kc = torch.zeros(2, 1, 4, 4)
+    bad = torch.tensor([0, 8])
+    with pytest.raises(ValueError, match="out of bounds"):
+        musa_aiter.kv_paged_to_linear(kc, kc.clone(), bad, out_k=torch.zeros(5), fill_skipped="preserve")
+    big = torch.zeros(2, 2, 1, 4, 4)
+    with pytest.raises(ValueError, match="out of bounds"):
+        musa_aiter.kv_paged_to_linear_multi_layer(big, big.clone(), bad, out_k=torch.zeros(5), out_v=torch.zeros(5))
+    ints = torch.zeros(2, 1, 4, 4, dtype=torch.int32)
+    with pytest.raises(ValueError, match="out of bounds"):
+        musa_aiter.kv_linear_to_paged(torch.zeros(2, 1, 4, dtype=torch.int32), torch.zeros(2, 1, 4, dtype=torch.int32),
+                                      ints, ints.clone(), bad)
+    flat = torch.zeros(2, 4, 3)
+    with pytest.raises(ValueError, match="out of bounds"):
+        musa_aiter.kv_paged_to_mla_linear(flat, flat.clone(), bad, out_kv=torch.zeros(1))
+
+
 def test_lmcache_contracts():
     # op_tests/test_lmcache_kv_transfer.py:213-241, :276-295
     memory = torch.zeros(2, 2, 2, 4)

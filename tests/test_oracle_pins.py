@@ -293,8 +293,11 @@ def test_cachegen_helpers():
 # ----- the torch-CPU port timed by bench.py's CPU baseline ----------------------------------------
 
 
-@pytest.mark.parametrize("form", ["reference_ops", "vectorised"])
-def test_torch_cpu_port_matches_the_oracle(form):
+@pytest.mark.parametrize("gather_name,scatter_name", [
+    ("paged_to_linear_reference_ops", "linear_to_paged_reference_ops"),
+    ("paged_to_linear_vectorised", "linear_to_paged_vectorised"),
+])
+def test_torch_cpu_port_matches_the_oracle(gather_name, scatter_name):
     import torch
 
     from oracle import torch_cpu_port as tp
@@ -304,8 +307,8 @@ def test_torch_cpu_port_matches_the_oracle(form):
     slots = _dup_slots(nb * bs, t, rng)
     cache = rng.integers(0, 1 << 16, size=(nb, nh, hd, bs), dtype=np.uint16)
     lin = rng.integers(0, 1 << 16, size=(t, nh, hd), dtype=np.uint16)
-    gather = getattr(tp, f"paged_to_linear_{form}")
-    scatter = getattr(tp, f"linear_to_paged_{form}")
+    gather = getattr(tp, gather_name)
+    scatter = getattr(tp, scatter_name)
     as_t = lambda a: torch.from_numpy(a.astype(np.int32)).to(torch.int16)  # noqa: E731
     got = gather(as_t(cache), torch.from_numpy(slots)).numpy().astype(np.uint16)
     assert np.array_equal(got, ko.paged_to_linear(cache, slots))
