@@ -207,3 +207,32 @@ def test_large_roundtrip_properties():
     untouched = ~used.view(nb, bs)
     kc_t = kc.permute(0, 1, 4, 2, 3)  # [L, NB, BS, NH, HD]
     assert bool((kc_t[:, untouched] == 3.0).all())
+
+
+@pytest.mark.parametrize("layers,tokens,kind", [
+    (2, 2500, "duplicates"),    # scatter: 1,256 workgroups, the loads-first form
+    (16, 2500, "duplicates"),   # scatter: 10,048 workgroups, the chunk-by-chunk form
+    (16, 1500, "skips"),        # gather: 32 planes, 12,032 workgroups, the XCD-contiguous order
+    (8, 1500, "sequences"),     # gather: 16 planes, natural order
+])
+def test_kernel_forms_either_side_of_the_launch_thresholds(layers, tokens, kind):
+    # The tile kernels pick a form by launch size (scatters of at most 8,192 workgroups; gathers
+    # over at least 32 planes and more than 8,192 workgroups): every form against the oracle,
+    # with repeated, skipped and partial-block slots.
+    shape = (8, 128, 16)
+    nh, hd, _ = shape
+    slots, kc, vc = _case(torch.bfloat16, shape, kind, tokens=tokens, seed=31 + layers, layers=layers)
+    s_d = torch.from_numpy(slots).to(DEV)
+    ok, ov = musa_aiter.kv_paged_to_linear_multi_layer(kc.to(DEV), vc.to(DEV), s_d)
+    assert np.array_equal(bits(ok), ko.paged_to_linear_multi_layer(bits(kc), slots))
+    assert np.array_equal(bits(ov), ko.paged_to_linear_multi_layer(bits(vc), slots))
+    gen = torch.Generator().manual_seed(7)
+    kl = random_payload((layers, len(slots), nh, hd), torch.bfloat16, gen)
+    vl = random_payload((layers, len(slots), nh, hd), torch.bfloat16, gen)
+    kc_d, vc_d = kc.to(DEV), vc.to(DEV)
+    musa_aiter.kv_linear_to_paged_multi_layer(kl.to(DEV), vl.to(DEV), kc_d, vc_d, s_d)
+    want_k, want_v = bits(kc).copy(), bits(vc).copy()
+    ko.linear_to_paged_multi_layer(bits(kl), want_k, slots)
+    ko.linear_to_paged_multi_layer(bits(vl), want_v, slots)
+    assert np.array_equal(bits(kc_d), want_k)
+    assert np.array_equal(bits(vc_d), want_v)
