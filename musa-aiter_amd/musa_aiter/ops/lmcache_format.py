@@ -34,6 +34,7 @@ _SUPPORTED = (torch.float32, torch.float16, torch.bfloat16, torch.uint8)
 
 
 def _dtype_name(tensor: torch.Tensor) -> str:
+    """The dtype's short name; raises for dtypes LMCache buffers do not use."""
     if tensor.dtype not in _SUPPORTED:
         raise ValueError(f"unsupported LMCache dtype={tensor.dtype}")
     return str(tensor.dtype).removeprefix("torch.")
@@ -53,13 +54,13 @@ def describe_lmcache_format(memory_tensor: torch.Tensor) -> LMCacheFormatFacts:
     if len(shape) == 4:
         if shape[0] != 2:
             raise ValueError("KV_2LTD memory tensor must have leading K/V dimension 2")
-        _dtype_name(memory_tensor)
+        _dtype_name(memory_tensor)  # a bad dtype is reported before the layout is built
         _, layers, tokens, hidden = shape
         spec = _linear(memory_tensor, KVLayoutKind.KV_2LTD, KVOrganization.SEPARATE, layers, tokens, hidden)
         return LMCacheFormatFacts(LMCacheFormat.KV_2LTD, spec)
     if len(shape) != 3:
         raise ValueError("LMCache memory tensor rank must be 3 or 4")
-    _dtype_name(memory_tensor)
+    _dtype_name(memory_tensor)  # a bad dtype is reported before the 3-D shape errors
     first, second, hidden = shape
     if first == 2 and second == 2:
         raise ValueError("3-D LMCache tensor is ambiguous when both leading dimensions are 2")

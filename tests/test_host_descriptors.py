@@ -295,3 +295,19 @@ def test_format_facts_are_exported_from_package():
     # :56-60
     assert musa_aiter.LMCacheFormat is LMCacheFormat
     assert musa_aiter.describe_lmcache_format is describe_lmcache_format
+
+
+def test_format_dtype_errors_come_before_shape_errors():
+    # lmcache_format.py:58 and :77 check the dtype before the 3-D shape rules: an unsupported dtype
+    # is reported even where the shape alone would be ambiguous or unclassifiable.
+    with pytest.raises(ValueError, match="unsupported LMCache dtype"):
+        describe_lmcache_format(torch.zeros(2, 2, 4, dtype=torch.int64))
+    with pytest.raises(ValueError, match="unsupported LMCache dtype"):
+        describe_lmcache_format(torch.zeros(3, 5, 4, dtype=torch.int32))
+    with pytest.raises(ValueError, match="unsupported LMCache dtype"):
+        describe_lmcache_format(torch.zeros(2, 3, 5, 4, dtype=torch.float64))
+    with pytest.raises(ValueError, match="ambiguous"):
+        describe_lmcache_format(torch.zeros(2, 2, 4))
+    with pytest.raises(ValueError, match=r"\[T, 2, H\] or \[2, T, H\]"):
+        describe_lmcache_format(torch.zeros(3, 5, 4))
+    assert describe_lmcache_format(torch.zeros(2, 5, 4, dtype=torch.uint8)).spec.dtype_name == "uint8"
