@@ -626,8 +626,27 @@ def bench_config5() -> dict:
     out["bf16_576"] = {"bytes_per_call": nbytes, "gather": rate(nbytes, mg, t), "scatter": rate(nbytes, ms, t),
                        "parity": parity, "parity_check": "256 sampled tokens x 61 layers equal to their slot rows; "
                                                           "scatter of the gathered rows leaves the cache checksum unchanged"}
+    # Access-pattern ceilings on the same buffers: whole 72 KiB cache blocks (64 rows) in the order the slots visit
+    # them against the buffer in order, by the block-pattern kernel.
+    blk = bs * hs * 2
+    nblk = t // bs
+    order = torch.from_numpy(run_blocks(slots_np, bs)[:nblk].copy()).to(dev)
+    pbytes = 2 * nl * nblk * blk
+    ceil = {"block_bytes": blk, "blocks_per_plane": nblk, "planes": nl}
+    for name, src, dst, sblocks, dblocks, sreg, dreg, sps, dps in (
+            ("gather_pattern", paged, buf, order, None, nb, nblk, nb * blk, t * hs * 2),
+            ("scatter_pattern", buf, paged, None, order, nblk, nb, t * hs * 2, nb * blk)):
+        fn = pattern_copy_fn(src, dst, src_blocks=sblocks, dst_blocks=dblocks, num_blocks=nblk, src_region_blocks=sreg,
+                             dst_region_blocks=dreg, src_block_bytes=blk, dst_block_bytes=blk, planes=nl,
+                             src_plane_stride=sps, dst_plane_stride=dps)
+        fn()
+        ceil[name] = rate(pbytes, batched_ms(fn, launches=3, reps=3))
+    out["bf16_576"]["ceilings"] = ceil
+    out["bf16_576"]["gather_frac_of_pattern"] = out["bf16_576"]["gather"]["gbs"] / ceil["gather_pattern"]["gbs"]
+    out["bf16_576"]["scatter_frac_of_pattern"] = out["bf16_576"]["scatter"]["gbs"] / ceil["scatter_pattern"]["gbs"]
     log(f"config 5 bf16: gather {out['bf16_576']['gather']['gbs']:.0f} GB/s, "
-        f"scatter {out['bf16_576']['scatter']['gbs']:.0f} GB/s, parity {parity}")
+        f"scatter {out['bf16_576']['scatter']['gbs']:.0f} GB/s, parity {parity}; pattern ceilings "
+        f"{ceil['gather_pattern']['gbs']:.0f} / {ceil['scatter_pattern']['gbs']:.0f} GB/s")
     del paged, buf, flat
     torch.cuda.empty_cache()
 
