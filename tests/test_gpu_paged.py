@@ -236,3 +236,15 @@ def test_kernel_forms_either_side_of_the_launch_thresholds(layers, tokens, kind)
     ko.linear_to_paged_multi_layer(bits(vl), want_v, slots)
     assert np.array_equal(bits(kc_d), want_k)
     assert np.array_equal(bits(vc_d), want_v)
+
+
+@pytest.mark.parametrize("dtype,shape,tokens", [
+    (torch.float32, (4, 32, 32), 3000),   # 32 planes x 188 tiles x 2 row groups (12,032 workgroups): XCD order
+    (torch.float16, (2, 64, 8), 5000),    # 32 planes x 313 tiles x 1 row group (10,016 workgroups): XCD order
+])
+def test_xcd_order_gathers_other_shapes(dtype, shape, tokens):
+    slots, kc, vc = _case(dtype, shape, "skips", tokens=tokens, seed=41, layers=16)
+    s_d = torch.from_numpy(slots).to(DEV)
+    ok, ov = musa_aiter.kv_paged_to_linear_multi_layer(kc.to(DEV), vc.to(DEV), s_d)
+    assert np.array_equal(bits(ok), ko.paged_to_linear_multi_layer(bits(kc), slots))
+    assert np.array_equal(bits(ov), ko.paged_to_linear_multi_layer(bits(vc), slots))
