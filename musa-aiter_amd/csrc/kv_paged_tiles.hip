@@ -277,14 +277,22 @@ __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs
 
   if constexpr (!SCATTER) {
     if (a.fill_zeros) {
-      uint64_t skipped = ~vmask & window;
+      // Skipped tokens (the positions past seq_lens of a dense preload, a
+      // negative slot) get zero rows.  All threads share the work: thread tid
+      // writes piece tid % P of the (tid / P)-th skipped token of each pass,
+      // P being the 16-byte pieces of one token's row group.
+      const uint64_t skipped = ~vmask & window;
+      constexpr int P = kRows * kChunksPerGroup<false> * ELT / 16;
+      static_assert(kCoopThreads % P == 0, "a pass covers whole tokens");
+      constexpr int kTokensPerPass = kCoopThreads / P;
+      const int64_t k = rb * ELT + static_cast<int64_t>(tid % P) * 16;
+      const int nskip = __builtin_popcountll(skipped);
       const u32x4 zero = {0u, 0u, 0u, 0u};
-      while (skipped) {
-        const int i = __builtin_ctzll(skipped);
-        skipped &= skipped - 1;
-        uint8_t* const row = lin + (t0 - 1 + i) * a.lin_token_stride;
-        for (int64_t k = rb * ELT + static_cast<int64_t>(tid) * 16; k < re * ELT; k += kCoopThreads * 16)
-          st16(row + k, zero);
+      for (int o = tid / P; o < nskip; o += kTokensPerPass) {
+        uint64_t m = skipped;
+        for (int j = 0; j < o; ++j) m &= m - 1;  // drop the first o skipped tokens
+        const int i = __builtin_ctzll(m);
+        if (k < re * ELT) st16(lin + (t0 - 1 + i) * a.lin_token_stride + k, zero);
       }
     }
   }
