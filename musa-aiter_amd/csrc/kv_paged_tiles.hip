@@ -35,17 +35,17 @@ namespace kvhip {
 
 constexpr int kCoopThreads = 256;
 
-template <int ELT, int BS>
+template <int ELT, int BS, int NT = kCoopThreads>
 struct CoopShape {
   static constexpr int CG = 16 / ELT;                 // block columns per cache piece
   static constexpr int NCG = BS / CG;                 // cache pieces per cache row
   static constexpr int ROWB = BS * ELT;               // bytes per cache row of a block
-  static constexpr int kRows = kCoopThreads * 16 / ROWB;  // cache rows per chunk (4 KiB)
+  static constexpr int kRows = NT * 16 / ROWB;        // cache rows per chunk (NT x 16 bytes)
   static constexpr int RPL = 16 / ELT;                // rows per linear piece
   static constexpr int G = kRows / RPL;               // linear pieces per token per chunk
   static constexpr int PITCH = ROWB + 4;              // LDS bytes per cache row (one pad dword)
   static_assert(BS % CG == 0, "block row must be a whole number of 16-byte pieces");
-  static_assert(BS * G == kCoopThreads, "linear pieces must cover the chunk");
+  static_assert(BS * G == NT, "linear pieces must cover the chunk");
   static_assert(G % 8 == 0, "row groups come in eights");
 
   // Linear piece p of a chunk -> (block column, row group).  Eight
@@ -98,10 +98,11 @@ constexpr int kChunksPerGroup = SCATTER ? 4 : 2;
 
 // FEW selects the form for launches bound by per-workgroup latency rather than
 // by HBM: for a scatter the loads-first chunk loop, for a gather the natural
-// workgroup order (FEW false: the XCD-contiguous order).
-template <int ELT, int BS, bool SCATTER, bool FEW>
-__global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs a) {
-  using S = CoopShape<ELT, BS>;
+// workgroup order (FEW false: the XCD-contiguous order).  NT is the workgroup
+// size; a chunk is NT 16-byte pieces.
+template <int ELT, int BS, bool SCATTER, bool FEW, int NT = kCoopThreads>
+__global__ __launch_bounds__(NT) void paged_tile_kernel(const TileArgs a) {
+  using S = CoopShape<ELT, BS, NT>;
   constexpr int CG = S::CG, NCG = S::NCG, ROWB = S::ROWB, kRows = S::kRows;
   constexpr int RPL = S::RPL, PITCH = S::PITCH;
   static_assert(kTileTokens + BS + 1 <= kWave, "run window must fit one wave");
@@ -283,8 +284,8 @@ __global__ __launch_bounds__(kCoopThreads) void paged_tile_kernel(const TileArgs
       // P being the 16-byte pieces of one token's row group.
       const uint64_t skipped = ~vmask & window;
       constexpr int P = kRows * kChunksPerGroup<false> * ELT / 16;
-      static_assert(kCoopThreads % P == 0, "a pass covers whole tokens");
-      constexpr int kTokensPerPass = kCoopThreads / P;
+      static_assert(NT % P == 0, "a pass covers whole tokens");
+      constexpr int kTokensPerPass = NT / P;
       const int64_t k = rb * ELT + static_cast<int64_t>(tid % P) * 16;
       const int nskip = __builtin_popcountll(skipped);
       const u32x4 zero = {0u, 0u, 0u, 0u};
@@ -366,24 +367,53 @@ constexpr int64_t kFewGroups = 8192;
 // launches keep the natural order too (cfg 1: 13.0 against 13.9 us).
 constexpr int64_t kXcdOrderPlanes = 32;
 
-template <int ELT, int BS, bool SCATTER>
-hipError_t launch_tile(const TileArgs& a0, int64_t planes, hipStream_t stream) {
-  using S = CoopShape<ELT, BS>;
+// 16-bit gathers whose 256-thread grid has at most kFewGroups workgroups use
+// 128-thread workgroups (2 KiB chunks) for block sizes up to 16.  Measured on
+// 1-4 planes of short sequences: 3-4 % faster with skipped slots or several
+// layers (4 bf16 layers: 13.5 -> 12.9 us), unchanged on configs[0] without
+// skips (12.9 us), 1 % slower for fp32 (chunks of only 32 rows).
+constexpr int kShortGatherThreads = 128;
+
+// Tile grid of one launch with NT-thread workgroups: (tile, plane, row group)
+// for a scatter, (tile x row group, plane) for a gather.
+template <int ELT, int BS, bool SCATTER, int NT>
+hipError_t tile_grid(const TileArgs& a0, int64_t planes, TileArgs* a, dim3* grid, int64_t* workgroups) {
+  using S = CoopShape<ELT, BS, NT>;
   constexpr int kGroupRows = S::kRows * kChunksPerGroup<SCATTER>;
   const int64_t groups = (a0.nrows + kGroupRows - 1) / kGroupRows;
   if (groups > 65535) return hipErrorInvalidValue;
   const int64_t tiles = (a0.num_tokens + kTileTokens - 1) / kTileTokens;
-  TileArgs a = a0;
-  a.row_groups = static_cast<int32_t>(groups);
-  dim3 grid;
+  *a = a0;
+  a->row_groups = static_cast<int32_t>(groups);
   if constexpr (SCATTER) {
     if (tiles > 0x7FFFFFFF) return hipErrorInvalidValue;
-    grid = dim3(static_cast<uint32_t>(tiles), static_cast<uint32_t>(planes), static_cast<uint32_t>(groups));
+    *grid = dim3(static_cast<uint32_t>(tiles), static_cast<uint32_t>(planes), static_cast<uint32_t>(groups));
   } else {
     if (tiles > 0x7FFFFFFF / groups) return hipErrorInvalidValue;
-    grid = dim3(static_cast<uint32_t>(tiles * groups), static_cast<uint32_t>(planes), 1);
+    *grid = dim3(static_cast<uint32_t>(tiles * groups), static_cast<uint32_t>(planes), 1);
   }
-  const int64_t workgroups = tiles * planes * groups;
+  *workgroups = tiles * planes * groups;
+  return hipSuccess;
+}
+
+template <int ELT, int BS, bool SCATTER>
+hipError_t launch_tile(const TileArgs& a0, int64_t planes, hipStream_t stream) {
+  TileArgs a;
+  dim3 grid;
+  int64_t workgroups = 0;
+  hipError_t err = tile_grid<ELT, BS, SCATTER, kCoopThreads>(a0, planes, &a, &grid, &workgroups);
+  if (err != hipSuccess) return err;
+  if constexpr (!SCATTER && ELT == 2 && BS <= 16) {
+    if (workgroups <= kFewGroups) {
+      // Short gathers: twice the workgroups, half the size each (on cfg 2's
+      // 64 planes this form is 1 % slower than 256 threads).
+      err = tile_grid<ELT, BS, SCATTER, kShortGatherThreads>(a0, planes, &a, &grid, &workgroups);
+      if (err != hipSuccess) return err;
+      hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, SCATTER, true, kShortGatherThreads>), grid,
+                         dim3(kShortGatherThreads), 0, stream, a);
+      return hipGetLastError();
+    }
+  }
   // (The XCD order indexes the grid in 32 bits.)
   const bool few = SCATTER ? workgroups <= kFewGroups
                            : !(planes >= kXcdOrderPlanes && workgroups > kFewGroups &&
