@@ -1,8 +1,9 @@
 """HIP graph capture of the entry points that never synchronise with the host.
 
-kv_cachegen_encode, kv_cachegen_decode (256-entry codebook), the LMCache 2 x NL gather and scatter
-and kv_triton_indexed_to_dense launch only kernels on the current stream (no host reads, no
-memsets), so a caller can capture them in a graph.  A captured scatter whose slots may repeat
+kv_cachegen_encode, kv_cachegen_decode (256-entry codebook), the LMCache 2 x NL gather and scatter,
+kv_triton_indexed_to_dense and the reference-named C entries (the multi-layer paged scatter and
+gather, the FP8 quant-store and dequant-gather) launch only kernels on the current stream (no host
+reads, no memsets), so a caller can capture them in a graph.  A captured scatter whose slots may repeat
 clears and re-claims its slots on every replay instead of relying on the eager path's per-call
 epoch, which a replay would repeat.  Each case is captured once and replayed several times with
 new inputs copied into the captured tensors and eager calls in between; every replay must equal
@@ -154,3 +155,109 @@ def test_graphs_on_the_default_capture_stream_get_their_own_claim_arrays():
         for a in range(2):
             for layer in range(nl):
                 assert np.array_equal(bits(caches[a][layer]), bits(ref[a][layer])), (a, layer)
+
+
+def _abi(name: str, nptr: int, ni64: int, fp8: bool = False):
+    """A reference-named C entry: pointers, int64 sizes, then the stream; the FP8 entries put an int
+    dtype code before the stream and an int scale mode after it."""
+    import ctypes
+
+    from musa_aiter.ops import _hip
+
+    fn = getattr(_hip.library(), name)
+    tail = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int] if fp8 else [ctypes.c_void_p]
+    fn.argtypes = [ctypes.c_void_p] * nptr + [ctypes.c_longlong] * ni64 + tail
+    fn.restype = ctypes.c_int
+    return fn
+
+
+def _cur_stream():
+    import ctypes
+
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def test_reference_abi_multi_layer_scatter_then_gather_replays():
+    # The headline pair through the reference-named C entries (kv_transfer.py:2446-2480 argument
+    # order): a multi-layer scatter whose slots repeat and skip, then the gather of other slots,
+    # captured as one graph; every replay takes new linear rows, slots and cache contents.
+    nl, nb, nh, hd, bs, t = 3, 64, 4, 64, 16, 300
+    rng = np.random.default_rng(10)
+    gen = torch.Generator().manual_seed(10)
+    scatter = _abi("musa_aiter_kv_linear_to_paged_multi_layer_bfloat16", 5, 6)
+    gather = _abi("musa_aiter_kv_paged_to_linear_multi_layer_bfloat16", 5, 6)
+    kl = torch.empty((nl, t, nh, hd), dtype=torch.bfloat16, device=DEV)
+    vl = torch.empty_like(kl)
+    kc = torch.empty((nl, nb, nh, hd, bs), dtype=torch.bfloat16, device=DEV)
+    vc = torch.empty_like(kc)
+    ss = torch.zeros(t, dtype=torch.long, device=DEV)
+    gs = torch.zeros(t, dtype=torch.long, device=DEV)
+    ok = torch.empty_like(kl)
+    ov = torch.empty_like(vl)
+
+    def step(kl, vl, kc, vc, ss, gs, ok, ov):
+        assert scatter(kl.data_ptr(), vl.data_ptr(), ss.data_ptr(), kc.data_ptr(), vc.data_ptr(), nl, t, nb, nh, hd,
+                       bs, _cur_stream()) == 0
+        assert gather(kc.data_ptr(), vc.data_ptr(), gs.data_ptr(), ok.data_ptr(), ov.data_ptr(), nl, t, nb, nh, hd,
+                      bs, _cur_stream()) == 0
+
+    bufs = (kl, vl, kc, vc, ss, gs, ok, ov)
+    g, _ = _capture(lambda: step(*bufs))
+    for rep in range(3):
+        for x in (kl, vl, kc, vc):
+            x.copy_(random_payload(tuple(x.shape), torch.bfloat16, gen))
+        scat = rng.integers(-1, nb * bs // 4, size=t)  # many repeated destinations
+        gath = rng.permutation(nb * bs)[:t]
+        gath[rng.random(t) < 0.1] = -1
+        ss.copy_(torch.from_numpy(scat))
+        gs.copy_(torch.from_numpy(gath))
+        ref = tuple(x.clone() for x in bufs)
+        step(*ref)  # eager, on other buffers, between the replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for got, want in zip((kc, vc, ok, ov), ref[2:4] + ref[6:8]):
+            assert np.array_equal(bits(got), bits(want)), rep
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_reference_abi_fp8_quant_store_then_dequant_replays(fmt):
+    # FP8 vec4 entries with per-head scales (scale mode 1, kv_transfer.py:2401-2440): the quant-store
+    # with repeated slots and the dequant-gather of the same slots, captured together.
+    nb, nh, hd, bs, t = 64, 4, 64, 16, 256
+    rng = np.random.default_rng(11)
+    gen = torch.Generator(device=DEV).manual_seed(11)
+    quant = _abi(f"musa_aiter_kv_linear_to_paged_fp8_vec4_{fmt}", 7, 5, fp8=True)
+    deq = _abi(f"musa_aiter_kv_paged_fp8_to_linear_vec4_{fmt}", 7, 5, fp8=True)
+    kl = torch.empty((t, nh, hd), dtype=torch.bfloat16, device=DEV)
+    vl = torch.empty_like(kl)
+    kc = torch.zeros((nb, nh, hd, bs), dtype=torch.uint8, device=DEV)
+    vc = torch.zeros_like(kc)
+    ks = torch.empty(nh, dtype=torch.float32, device=DEV)
+    vs = torch.empty_like(ks)
+    slots = torch.zeros(t, dtype=torch.long, device=DEV)
+    ok = torch.empty_like(kl)
+    ov = torch.empty_like(vl)
+
+    def step(kl, vl, kc, vc, ks, vs, slots, ok, ov):
+        assert quant(kl.data_ptr(), vl.data_ptr(), slots.data_ptr(), kc.data_ptr(), vc.data_ptr(), ks.data_ptr(),
+                     vs.data_ptr(), t, nb, nh, hd, bs, 2, _cur_stream(), 1) == 0
+        assert deq(kc.data_ptr(), vc.data_ptr(), slots.data_ptr(), ks.data_ptr(), vs.data_ptr(), ok.data_ptr(),
+                   ov.data_ptr(), t, nb, nh, hd, bs, 2, _cur_stream(), 1) == 0
+
+    bufs = (kl, vl, kc, vc, ks, vs, slots, ok, ov)
+    g, _ = _capture(lambda: step(*bufs))
+    for rep in range(3):
+        for x in (kl, vl):
+            x.copy_((torch.randn(tuple(x.shape), generator=gen, device=DEV) * 3.0).to(torch.bfloat16))
+        for s, x in ((ks, kl), (vs, vl)):
+            s.copy_(x.float().abs().amax(dim=(0, 2)) / (448.0 if fmt == "e4m3" else 57344.0))
+        s_np = rng.integers(-1, nb * bs // 3, size=t)
+        slots.copy_(torch.from_numpy(s_np))
+        ref = tuple(x.clone() for x in bufs)
+        step(*ref)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for got, want in zip((kc, vc, ok, ov), ref[2:4] + ref[7:9]):
+            assert np.array_equal(bits(got), bits(want)), rep
