@@ -21,7 +21,9 @@ committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes.  ``ceilings`` times, on the
 same caches and linear buffers, a plain whole-block copy in the block order of
 the slot mapping (random cache blocks read with the linear side written in
 order, and the reverse): the rate that access pattern allows a copy with no
-index work, which the two kernels are measured against.  ``placements``
+index work, which the two kernels are measured against.  Each ceiling and
+floor is timed with non-temporal and with write-through stores and keeps the
+faster.  ``placements``
 re-allocates the caches several times in this process and times the step on
 each, because where the caches land moves the rate by several percent.
 ``cpu_baseline`` times the reference's own torch operations
@@ -176,19 +178,40 @@ def run_blocks(slots_np: np.ndarray, block_size: int) -> np.ndarray:
 
 def pattern_copy_fn(src: torch.Tensor, dst: torch.Tensor, *, src_blocks, dst_blocks, num_blocks: int,
                     src_region_blocks: int, dst_region_blocks: int, src_block_bytes: int, dst_block_bytes: int,
-                    planes: int, src_plane_stride: int, dst_plane_stride: int):
+                    planes: int, src_plane_stride: int, dst_plane_stride: int, write_through: bool = False):
     """A launcher of the library's block-pattern copy (musa_aiter_hip_block_pattern_copy): whole blocks in the
-    given order, no index resolution or transpose, on the caller's own buffers -- the access-pattern ceiling."""
+    given order, no index resolution or transpose, on the caller's own buffers -- the access-pattern ceiling.
+    ``write_through`` selects agent-scope stores (through the L2) over plain non-temporal ones."""
     from musa_aiter.ops import _hip
 
     fn = getattr(_hip.library(), "musa_aiter_hip_block_pattern_copy")
-    fn.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 8 + [ctypes.c_void_p]
+    fn.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 8 + [ctypes.c_int, ctypes.c_void_p]
     fn.restype = ctypes.c_int
     sb = src_blocks.data_ptr() if src_blocks is not None else None
     db = dst_blocks.data_ptr() if dst_blocks is not None else None
     args = (src.data_ptr(), dst.data_ptr(), sb, db, num_blocks, src_region_blocks, dst_region_blocks,
-            src_block_bytes, dst_block_bytes, planes, src_plane_stride, dst_plane_stride)
+            src_block_bytes, dst_block_bytes, planes, src_plane_stride, dst_plane_stride, int(write_through))
     return lambda: _check(fn(*args, _stream()), "block pattern copy")
+
+
+def _run_all(fns):
+    """One callable that launches ``fns`` in order."""
+    def run():
+        for f in fns:
+            f()
+    return run
+
+
+def pattern_rate(make, nbytes: int, per_call: int = 1, **timing) -> dict:
+    """The faster store policy of a block-pattern copy: ``make(write_through)`` returns the launcher (of
+    ``per_call`` copies, each of ``nbytes``).  The ceiling is the better plain copy; both rates are kept."""
+    by = {}
+    for wt in (False, True):
+        f = make(wt)
+        f()
+        by["write_through" if wt else "non_temporal"] = rate(nbytes, batched_ms(f, **timing) / per_call)
+    best = max(by, key=lambda k: by[k]["gbs"])
+    return {**by[best], "store_policy": best, "gbs_by_store_policy": {k: v["gbs"] for k, v in by.items()}}
 
 
 def config2_ceilings(slots_np: np.ndarray, kc: torch.Tensor, vc: torch.Tensor, kl: torch.Tensor,
@@ -218,18 +241,16 @@ def config2_ceilings(slots_np: np.ndarray, kc: torch.Tensor, vc: torch.Tensor, k
     out = {"blocks_per_plane": nblk, "planes": 2 * NL, "bytes_per_launch_pair": nbytes,
            "shape": "one wave per 1 KiB (16 B per lane), whole 32 KiB blocks, K and V caches one launch each"}
     for name, leg in legs.items():
-        fns = [pattern_copy_fn(src, dst, src_blocks=leg["src_blocks"], dst_blocks=leg["dst_blocks"],
-                               num_blocks=nblk, src_region_blocks=leg["src_region_blocks"],
-                               dst_region_blocks=leg["dst_region_blocks"], src_block_bytes=blk_bytes,
-                               dst_block_bytes=blk_bytes, planes=NL, src_plane_stride=leg["src_plane_stride"],
-                               dst_plane_stride=leg["dst_plane_stride"]) for src, dst in zip(leg["src"], leg["dst"])]
+        def make(wt, leg=leg):
+            return _run_all([pattern_copy_fn(src, dst, src_blocks=leg["src_blocks"], dst_blocks=leg["dst_blocks"],
+                                             num_blocks=nblk, src_region_blocks=leg["src_region_blocks"],
+                                             dst_region_blocks=leg["dst_region_blocks"], src_block_bytes=blk_bytes,
+                                             dst_block_bytes=blk_bytes, planes=NL,
+                                             src_plane_stride=leg["src_plane_stride"],
+                                             dst_plane_stride=leg["dst_plane_stride"], write_through=wt)
+                             for src, dst in zip(leg["src"], leg["dst"])])
 
-        def both(fns=fns):
-            for f in fns:
-                f()
-
-        both()
-        out[name] = rate(nbytes, batched_ms(both, launches=5, reps=5))
+        out[name] = pattern_rate(make, nbytes, launches=5, reps=5)
     g, sc = out["gather_pattern"]["gbs"], out["scatter_pattern"]["gbs"]
     out["step_ceiling_gbs"] = 2.0 / (1.0 / g + 1.0 / sc)
     log(f"config 2 ceilings: gather pattern {g:.0f}, scatter pattern {sc:.0f}, sequential "
@@ -402,11 +423,13 @@ def short_launch_floor(slots_np: np.ndarray, nb: int, dtype: torch.dtype) -> dic
     nbytes = 2 * nblk * blk_bytes * 2
     out = {"bytes_per_launch": nbytes, "blocks_per_plane": nblk, "planes": 2}
     for name, blocks in (("gather_pattern", order), ("sequential", None)):
-        fn = pattern_copy_fn(src, dst, src_blocks=blocks, dst_blocks=None, num_blocks=nblk, src_region_blocks=nb,
-                             dst_region_blocks=nblk, src_block_bytes=blk_bytes, dst_block_bytes=blk_bytes, planes=2,
-                             src_plane_stride=nb * blk_bytes, dst_plane_stride=nblk * blk_bytes)
-        fn()
-        out[name] = rate(nbytes, batched_ms(fn, launches=50))
+        def make(wt, blocks=blocks):
+            return pattern_copy_fn(src, dst, src_blocks=blocks, dst_blocks=None, num_blocks=nblk,
+                                   src_region_blocks=nb, dst_region_blocks=nblk, src_block_bytes=blk_bytes,
+                                   dst_block_bytes=blk_bytes, planes=2, src_plane_stride=nb * blk_bytes,
+                                   dst_plane_stride=nblk * blk_bytes, write_through=wt)
+
+        out[name] = pattern_rate(make, nbytes, launches=50)
     log(f"config 1 floor: gather pattern {out['gather_pattern']['p50_ms'] * 1e3:.2f} us, sequential "
         f"{out['sequential']['p50_ms'] * 1e3:.2f} us per launch")
     return out
@@ -487,16 +510,15 @@ def bench_config3() -> dict:
     for name, src_pair, dst_pair, sbytes, dbytes, sblocks, dblocks, sreg, dreg in (
             ("quant_store_pattern", (kl, vl), (kc, vc), lin_blk, cache_blk, None, order, t // BS, NB),
             ("dequant_gather_pattern", (kc, vc), (ok, ov), cache_blk, lin_blk, order, None, NB, t // BS)):
-        fns = [pattern_copy_fn(a, b, src_blocks=sblocks, dst_blocks=dblocks, num_blocks=nblk, src_region_blocks=sreg,
-                               dst_region_blocks=dreg, src_block_bytes=sbytes, dst_block_bytes=dbytes, planes=1,
-                               src_plane_stride=0, dst_plane_stride=0) for a, b in zip(src_pair, dst_pair)]
+        def make(wt, src_pair=src_pair, dst_pair=dst_pair, sbytes=sbytes, dbytes=dbytes, sblocks=sblocks,
+                 dblocks=dblocks, sreg=sreg, dreg=dreg):
+            return _run_all([pattern_copy_fn(a, b, src_blocks=sblocks, dst_blocks=dblocks, num_blocks=nblk,
+                                             src_region_blocks=sreg, dst_region_blocks=dreg, src_block_bytes=sbytes,
+                                             dst_block_bytes=dbytes, planes=1, src_plane_stride=0,
+                                             dst_plane_stride=0, write_through=wt)
+                             for a, b in zip(src_pair, dst_pair)])
 
-        def both(fns=fns):
-            for f in fns:
-                f()
-
-        both()
-        out["ceilings"][name] = rate(ceil_bytes, batched_ms(both))
+        out["ceilings"][name] = pattern_rate(make, ceil_bytes)
     log(f"config 3 ceilings: quant pattern {out['ceilings']['quant_store_pattern']['gbs']:.0f}, dequant pattern "
         f"{out['ceilings']['dequant_gather_pattern']['gbs']:.0f} GB/s")
     return out
@@ -550,25 +572,23 @@ def bench_config4() -> dict:
     parity = parity and all(bool(torch.equal(m, flat[:, :, s_c])) for s_c, m in c_chunks)
     mc = batched_ms(per_chunk_gather_c, launches=5, reps=5) / nchunks
     # The floor of such a launch: each chunk's bytes as whole 32 KiB blocks of all 64 planes (cache blocks in the
-    # order the chunk's slots visit them, buffer blocks in order), by the block-pattern kernel, same rotation.
+    # order the chunk's slots visit them) copied in order into that chunk's own contiguous buffer, the one the
+    # C-entry timing above writes, by the block-pattern kernel, same rotation.  (The block-id tensors stay
+    # referenced by `orders` while the launchers that read them exist.)
     blk_bytes = BS * ROW * 2
-    floor_fns = []
-    for i in range(nchunks):
-        order = torch.from_numpy(run_blocks(slots_np[i * chunk:(i + 1) * chunk], BS)[:chunk // BS].copy()).to(dev)
-        dst_blocks = torch.arange(i * (chunk // BS), (i + 1) * (chunk // BS), dtype=torch.int32, device=dev)
-        floor_fns.append(pattern_copy_fn(cache, memory, src_blocks=order, dst_blocks=dst_blocks,
-                                         num_blocks=int(order.numel()), src_region_blocks=nb,
-                                         dst_region_blocks=chunk * nchunks // BS, src_block_bytes=blk_bytes,
-                                         dst_block_bytes=blk_bytes, planes=2 * nl, src_plane_stride=nb * blk_bytes,
-                                         dst_plane_stride=chunk * nchunks * ROW * 2))
+    orders = [torch.from_numpy(run_blocks(slots_np[i * chunk:(i + 1) * chunk], BS)[:chunk // BS].copy()).to(dev)
+              for i in range(nchunks)]
 
-    def per_chunk_floor():
-        for f in floor_fns:
-            f()
+    def per_chunk_floor(wt):
+        return _run_all([pattern_copy_fn(cache, m, src_blocks=order, dst_blocks=None, num_blocks=int(order.numel()),
+                                         src_region_blocks=nb, dst_region_blocks=chunk // BS,
+                                         src_block_bytes=blk_bytes, dst_block_bytes=blk_bytes, planes=2 * nl,
+                                         src_plane_stride=nb * blk_bytes, dst_plane_stride=chunk * ROW * 2,
+                                         write_through=wt)
+                         for order, (_, m) in zip(orders, c_chunks)])
 
-    per_chunk_floor()
-    mf = batched_ms(per_chunk_floor, launches=5, reps=5) / nchunks
     floor_bytes = 2 * nl * (chunk // BS) * blk_bytes * 2
+    floor = pattern_rate(per_chunk_floor, floor_bytes, per_call=nchunks, launches=5, reps=5)
     mb = batched_ms(lambda: musa_aiter.lmcache_kv_paged_to_buffer_two_x_nl(kvcaches, memory, slots, BS, NH, HD),
                     launches=10)
     ms = batched_ms(lambda: musa_aiter.lmcache_kv_buffer_to_paged_two_x_nl(memory, kvcaches, slots, 0, BS, NH, HD),
@@ -578,7 +598,7 @@ def bench_config4() -> dict:
             "traffic_per_chunk": profiled_traffic("cfg4_chunk_gather"),
             "gather_per_chunk_call": rate(per_chunk, mg, chunk),
             "gather_per_chunk_c_abi": rate(per_chunk, mc, chunk),
-            "per_chunk_floor_pattern_copy": rate(floor_bytes, mf),
+            "per_chunk_floor_pattern_copy": floor,
             "gather_batched_16": rate(per_chunk * nchunks, mb, chunk * nchunks),
             "scatter_batched_16": rate(per_chunk * nchunks, ms, chunk * nchunks),
             "note": "per-chunk calls go through the Python API (validation, pointer tables) back to back, or through "
@@ -636,11 +656,13 @@ def bench_config5() -> dict:
     for name, src, dst, sblocks, dblocks, sreg, dreg, sps, dps in (
             ("gather_pattern", paged, buf, order, None, nb, nblk, nb * blk, t * hs * 2),
             ("scatter_pattern", buf, paged, None, order, nblk, nb, t * hs * 2, nb * blk)):
-        fn = pattern_copy_fn(src, dst, src_blocks=sblocks, dst_blocks=dblocks, num_blocks=nblk, src_region_blocks=sreg,
-                             dst_region_blocks=dreg, src_block_bytes=blk, dst_block_bytes=blk, planes=nl,
-                             src_plane_stride=sps, dst_plane_stride=dps)
-        fn()
-        ceil[name] = rate(pbytes, batched_ms(fn, launches=3, reps=3))
+        def make(wt, src=src, dst=dst, sblocks=sblocks, dblocks=dblocks, sreg=sreg, dreg=dreg, sps=sps, dps=dps):
+            return pattern_copy_fn(src, dst, src_blocks=sblocks, dst_blocks=dblocks, num_blocks=nblk,
+                                   src_region_blocks=sreg, dst_region_blocks=dreg, src_block_bytes=blk,
+                                   dst_block_bytes=blk, planes=nl, src_plane_stride=sps, dst_plane_stride=dps,
+                                   write_through=wt)
+
+        ceil[name] = pattern_rate(make, pbytes, launches=3, reps=3)
     out["bf16_576"]["ceilings"] = ceil
     out["bf16_576"]["gather_frac_of_pattern"] = out["bf16_576"]["gather"]["gbs"] / ceil["gather_pattern"]["gbs"]
     out["bf16_576"]["scatter_frac_of_pattern"] = out["bf16_576"]["scatter"]["gbs"] / ceil["scatter_pattern"]["gbs"]

@@ -46,12 +46,13 @@ int64_t musa_aiter_hip_graph_claim_arrays(void);
  * num_blocks whole blocks of every plane: block i reads block src_blocks[i] (NULL: i) of the source
  * region and writes block dst_blocks[i] (NULL: i) of the destination; block sizes are multiples of
  * 1 KiB, equal or in a 2:1 / 1:2 ratio (FP8 quant-store / dequant-gather traffic); ids outside
- * [0, *_region_blocks) are skipped.  int32 block ids; strides in bytes. */
+ * [0, *_region_blocks) are skipped.  int32 block ids; strides in bytes.  write_through: 0 non-temporal
+ * stores, 1 also agent-scope (written through the L2, as the paged gathers' linear stores). */
 int musa_aiter_hip_block_pattern_copy(const void* src, void* dst, const int32_t* src_blocks,
                                       const int32_t* dst_blocks, int64_t num_blocks, int64_t src_region_blocks,
                                       int64_t dst_region_blocks, int64_t src_block_bytes, int64_t dst_block_bytes,
                                       int64_t planes, int64_t src_plane_stride, int64_t dst_plane_stride,
-                                      void* stream);
+                                      int write_through, void* stream);
 
 /* ---- Generic entries used by this package's Python host layer (no reference counterpart) ----
  * Paged-A caches [NL, NB, NH, HD, BS] <-> linear rows with explicit strides.

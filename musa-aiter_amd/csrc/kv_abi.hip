@@ -503,7 +503,7 @@ int musa_aiter_hip_block_pattern_copy(const void* src, void* dst, const int32_t*
                                       const int32_t* dst_blocks, int64_t num_blocks, int64_t src_region_blocks,
                                       int64_t dst_region_blocks, int64_t src_block_bytes, int64_t dst_block_bytes,
                                       int64_t planes, int64_t src_plane_stride, int64_t dst_plane_stride,
-                                      void* stream) {
+                                      int write_through, void* stream) {
   kvhip::BlockPatternParams p{};
   p.src = src;
   p.dst = dst;
@@ -517,6 +517,7 @@ int musa_aiter_hip_block_pattern_copy(const void* src, void* dst, const int32_t*
   p.planes = planes;
   p.src_plane_stride = src_plane_stride;
   p.dst_plane_stride = dst_plane_stride;
+  p.write_through = write_through != 0;
   return kvhip::launch_block_pattern(p, as_stream(stream));
 }
 

@@ -73,6 +73,16 @@ __device__ __forceinline__ void st16_cached(uint8_t* p, u32x4 v) { *(KVHIP_GLOBA
 using buf_t = __amdgpu_buffer_rsrc_t;
 constexpr uint32_t kOffOob = 0x80000000u;
 constexpr int kBufNT = 2;  // cache policy bits: non-temporal
+// Non-temporal and agent scope (sc1): the store writes through the L2 of the
+// XCD that issues it.  Each of MI355X's eight XCDs has its own L2, so a kernel
+// ends by writing its dirty L2 lines back; stores that wrote through leave
+// none.  Measured on sequentially written outputs: a 61 MB gather 13.0 ->
+// 12.1 us, a 67 MB 2 x NL chunk 13.0 -> 12.6 us, the 34 GB cfg 2 gather
+// +1.1 %.  Used only for destination rows of whole 128-byte lines (656-byte
+// rows written through were 7 % slower: their shared lines left the L2 once
+// per row); the tile scatter's random blocks and the dense preload's gathers
+// were no faster with it and keep kBufNT.
+constexpr int kBufWT = kBufNT | 16;
 
 __device__ __forceinline__ buf_t make_buf(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7FFFFFFF, 0x00020000);
@@ -86,6 +96,11 @@ __device__ __forceinline__ u32x4 buf_ld16(buf_t r, uint32_t off, uint32_t soff) 
 }
 __device__ __forceinline__ void buf_st16(buf_t r, uint32_t off, u32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kBufNT);
+}
+// The same store with cache-policy bits CP (kBufNT or kBufWT).
+template <int CP>
+__device__ __forceinline__ void buf_st16_p(buf_t r, uint32_t off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, CP);
 }
 template <int ELT>
 __device__ __forceinline__ void buf_st_elem(buf_t r, uint32_t off, uint32_t v) {

@@ -156,6 +156,7 @@ struct BlockPatternParams {
   int64_t planes;
   int64_t src_plane_stride;  // bytes
   int64_t dst_plane_stride;
+  int write_through;         // 1: agent-scope stores (through the L2), 0: non-temporal only
 };
 
 hipError_t launch_block_pattern(const BlockPatternParams& p, hipStream_t stream);

@@ -99,8 +99,9 @@ constexpr int kChunksPerGroup = SCATTER ? 4 : 2;
 // FEW selects the form for launches bound by per-workgroup latency rather than
 // by HBM: for a scatter the loads-first chunk loop, for a gather the natural
 // workgroup order (FEW false: the XCD-contiguous order).  NT is the workgroup
-// size; a chunk is NT 16-byte pieces.
-template <int ELT, int BS, bool SCATTER, bool FEW, int NT = kCoopThreads>
+// size; a chunk is NT 16-byte pieces.  LSTP: cache-policy bits of a gather's
+// linear-side stores.
+template <int ELT, int BS, bool SCATTER, bool FEW, int NT = kCoopThreads, int LSTP = kBufNT>
 __global__ __launch_bounds__(NT) void paged_tile_kernel(const TileArgs a) {
   using S = CoopShape<ELT, BS, NT>;
   constexpr int CG = S::CG, NCG = S::NCG, ROWB = S::ROWB, kRows = S::kRows;
@@ -205,7 +206,7 @@ __global__ __launch_bounds__(NT) void paged_tile_kernel(const TileArgs a) {
           d[0] = v[k][0]; d[1] = v[k][1]; d[2] = v[k][2]; d[3] = v[k][3];
         }
         lds_barrier();
-        buf_st16(lbuf, loff(k), lds_column_piece<ELT, PITCH>(tile, lq * RPL, lc));
+        buf_st16_p<LSTP>(lbuf, loff(k), lds_column_piece<ELT, PITCH>(tile, lq * RPL, lc));
       }
     } else if constexpr (!FEW) {
       // Large scatters: chunk by chunk with the next chunk's load in flight
@@ -396,6 +397,15 @@ hipError_t tile_grid(const TileArgs& a0, int64_t planes, TileArgs* a, dim3* grid
   return hipSuccess;
 }
 
+// True when every linear token row of the launch covers whole 128-byte lines
+// (row size, token and layer strides, both bases): only then do write-through
+// stores leave no line to be written once per token.
+bool linear_rows_whole_lines(const TileArgs& a, int elt) {
+  constexpr int64_t kLine = 128;
+  return (a.nrows * elt) % kLine == 0 && a.lin_token_stride % kLine == 0 && a.lin_layer_stride % kLine == 0 &&
+         reinterpret_cast<uintptr_t>(a.lin[0]) % kLine == 0 && reinterpret_cast<uintptr_t>(a.lin[1]) % kLine == 0;
+}
+
 template <int ELT, int BS, bool SCATTER>
 hipError_t launch_tile(const TileArgs& a0, int64_t planes, hipStream_t stream) {
   TileArgs a;
@@ -403,23 +413,34 @@ hipError_t launch_tile(const TileArgs& a0, int64_t planes, hipStream_t stream) {
   int64_t workgroups = 0;
   hipError_t err = tile_grid<ELT, BS, SCATTER, kCoopThreads>(a0, planes, &a, &grid, &workgroups);
   if (err != hipSuccess) return err;
+  const bool lines = !SCATTER && linear_rows_whole_lines(a0, ELT);
   if constexpr (!SCATTER && ELT == 2 && BS <= 16) {
     if (workgroups <= kFewGroups) {
       // Short gathers: twice the workgroups, half the size each (on cfg 2's
       // 64 planes this form is 1 % slower than 256 threads).
       err = tile_grid<ELT, BS, SCATTER, kShortGatherThreads>(a0, planes, &a, &grid, &workgroups);
       if (err != hipSuccess) return err;
-      hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, SCATTER, true, kShortGatherThreads>), grid,
-                         dim3(kShortGatherThreads), 0, stream, a);
+      if (lines)
+        hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, SCATTER, true, kShortGatherThreads, kBufWT>), grid,
+                           dim3(kShortGatherThreads), 0, stream, a);
+      else
+        hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, SCATTER, true, kShortGatherThreads>), grid,
+                           dim3(kShortGatherThreads), 0, stream, a);
       return hipGetLastError();
     }
   }
-  // (The XCD order indexes the grid in 32 bits.)
+  // (The XCD order indexes the grid in 32 bits.)  Short and XCD-ordered
+  // gathers write linear rows of whole lines through the L2 (kBufWT); the
+  // other gathers (few planes, many workgroups: the dense preload) measured
+  // no faster with it.
   const bool few = SCATTER ? workgroups <= kFewGroups
                            : !(planes >= kXcdOrderPlanes && workgroups > kFewGroups &&
                                workgroups <= int64_t{0xFFFFFFFF});
   if (few)
     hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, SCATTER, true>), grid, dim3(kCoopThreads), 0, stream, a);
+  else if (lines)
+    hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, SCATTER, false, kCoopThreads, kBufWT>), grid, dim3(kCoopThreads),
+                       0, stream, a);
   else
     hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, SCATTER, false>), grid, dim3(kCoopThreads), 0, stream, a);
   return hipGetLastError();

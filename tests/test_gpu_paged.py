@@ -241,6 +241,9 @@ def test_kernel_forms_either_side_of_the_launch_thresholds(layers, tokens, kind)
 @pytest.mark.parametrize("dtype,shape,tokens", [
     (torch.float32, (4, 32, 32), 3000),   # 32 planes x 188 tiles x 2 row groups (12,032 workgroups): XCD order
     (torch.float16, (2, 64, 8), 5000),    # 32 planes x 313 tiles x 1 row group (10,016 workgroups): XCD order
+    # 240-byte token rows (not whole 128-byte lines) keep non-temporal stores in both forms
+    (torch.bfloat16, (3, 40, 16), 5000),  # 10,016 workgroups: XCD order
+    (torch.bfloat16, (3, 40, 16), 600),   # 1,216 workgroups: the short 128-thread form
 ])
 def test_xcd_order_gathers_other_shapes(dtype, shape, tokens):
     slots, kc, vc = _case(dtype, shape, "skips", tokens=tokens, seed=41, layers=16)
