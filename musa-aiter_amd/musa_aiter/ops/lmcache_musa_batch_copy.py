@@ -13,6 +13,10 @@ keyword arguments, defaults, return values, gate variables and messages, :1-263)
   ``max_batch_entries`` entries (default 1024, ``MUSA_AITER_LMCACHE_BATCH_MAX_ENTRIES``); a group
   that fails after an earlier one went out raises instead of falling back.
 
+The host work is sized for batches of thousands of ranges: per-tensor facts are read once per
+distinct tensor, and the plan is built and cut into groups as int64 columns (no per-range Python
+objects on this path).
+
 Each group becomes one ``execute_batch_copy`` call of the extension object
 (``lmcache_musa_batch_copy_ext``), i.e. one ``musa_aiter_hip_batch_copy`` call of
 ``libmusa_aiter_kv_hip.so``: pinned host ranges move in one batch-copy kernel launch (the GPU
@@ -33,6 +37,7 @@ from .kv_transfer_plan import KVTransferPlan
 from .lmcache_musa_batch_copy_ext import lmcache_musa_batch_copy_requested, load_lmcache_musa_batch_copy_ext
 from .lmcache_musa_batch_copy_plan import build_batch_copy_plan as _build_batch_copy_plan
 from .lmcache_musa_batch_copy_plan import chunk_batch_copy_plan as _chunk_batch_copy_plan
+from .lmcache_musa_batch_copy_plan import plan_columns as _plan_columns
 
 _ABI_VERSION = 1
 _DEFAULT_MAX_BATCH_ENTRIES = 1024
@@ -114,9 +119,19 @@ class _Endpoints:
 
 
 def _classify(destinations: tuple, sources: tuple, require_pinned_host: bool) -> _Endpoints | None:
-    """Check every pair in order; ``None`` as soon as a pair is not host <-> GPU (not this backend's)."""
+    """Check every pair in order; ``None`` as soon as a pair is not host <-> GPU (not this backend's).
+
+    A batch names the same few tensors many times (one staging buffer, one cache).  An entry whose
+    (destination, source) pair of objects already appeared passes or fails exactly as its first
+    appearance did, and the first failing entry is always a first appearance, so only the first
+    appearance of each pair is checked, in entry order."""
+    firsts: dict[tuple[int, int], int] = {}
+    for index, key in enumerate(zip(map(id, destinations), map(id, sources))):
+        if key not in firsts:
+            firsts[key] = index
     directions, devices = set(), set()
-    for index, (destination, source) in enumerate(zip(destinations, sources)):
+    for index in firsts.values():
+        destination, source = destinations[index], sources[index]
         if not isinstance(destination, torch.Tensor) or not isinstance(source, torch.Tensor):
             raise TypeError("destinations and sources must contain torch.Tensor values")
         if not (destination.is_contiguous() and source.is_contiguous()):
@@ -165,21 +180,27 @@ def lmcache_musa_memcpy_batch_async(
     endpoints = _classify(destinations, sources, require_pinned_host)
     if endpoints is None:
         return False
-    nbytes = [t.numel() * t.element_size() for t in (*sources, *destinations)]
-    plan = _build_batch_copy_plan(
-        direction=endpoints.direction, sizes=sizes, source_capacities=nbytes[:len(sources)],
-        destination_capacities=nbytes[len(sources):], source_offsets=source_offsets,
+    capacity: dict[int, int] = {}
+    for t in (*sources, *destinations):
+        if id(t) not in capacity:
+            capacity[id(t)] = t.numel() * t.element_size()
+    plan = _plan_columns(
+        direction=endpoints.direction, sizes=sizes, source_capacities=[capacity[id(t)] for t in sources],
+        destination_capacities=[capacity[id(t)] for t in destinations], source_offsets=source_offsets,
         destination_offsets=destination_offsets, host_registration_offsets=host_registration_offsets,
         pin_chunk_size=pin_chunk_size, destination_keys=[id(t) for t in destinations])
     extension = _extension_if_requested(need_batch=True)
     if extension is None:
         return False
-    groups = _chunk_batch_copy_plan(plan, _resolve_max_batch_entries(max_batch_entries))
-    for number, group in enumerate(groups):
-        ok = extension.execute_batch_copy([destinations[e.input_index] for e in group],
-                                          [sources[e.input_index] for e in group],
-                                          [e.destination_offset for e in group], [e.source_offset for e in group],
-                                          [e.size for e in group], prefer_overlap_with_compute)
+    # Groups of max_batch_entries pieces in plan order, each one extension call.
+    limit = _resolve_max_batch_entries(max_batch_entries)
+    total = plan.input_index.shape[0]
+    for number, lo in enumerate(range(0, total, limit)):
+        index = plan.input_index[lo:lo + limit].tolist()
+        ok = extension.execute_batch_copy([destinations[i] for i in index], [sources[i] for i in index],
+                                          plan.destination_offset[lo:lo + limit].tolist(),
+                                          plan.source_offset[lo:lo + limit].tolist(),
+                                          plan.size[lo:lo + limit].tolist(), prefer_overlap_with_compute)
         if ok:
             continue
         if number == 0:

@@ -26,6 +26,7 @@ import threading
 from collections import deque
 from typing import Any, Sequence
 
+import numpy as np
 import torch
 
 from musa_aiter.ops import _hip
@@ -98,73 +99,122 @@ class HipBatchCopyExtension:
         return True
 
     @staticmethod
-    def _prepare(destinations: Sequence[torch.Tensor], sources: Sequence[torch.Tensor],
+    def _prepare_entry(i: int, dst: torch.Tensor, src: torch.Tensor, d_off: int, s_off: int, size: int,
+                       to_gpu: bool | None, device) -> None:
+        """The reference's prepare_copy checks of entry ``i`` (lmcache_musa_batch_copy_ext.cpp:76-170), in its
+        order; ``to_gpu`` / ``device`` are those of the first entry (None while checking the first)."""
+        if not dst.is_contiguous() or not src.is_contiguous():
+            raise RuntimeError("batch-copy tensors must be contiguous")
+        if _gpu(dst) == _gpu(src):
+            raise RuntimeError("each entry must have exactly one GPU endpoint")
+        if to_gpu is not None and _gpu(dst) != to_gpu:
+            raise RuntimeError("one batch cannot mix h2d and d2h copies")
+        gpu_t, host_t = (dst, src) if _gpu(dst) else (src, dst)
+        if host_t.device.type != "cpu":
+            raise RuntimeError("the non-GPU endpoint must be a CPU tensor")
+        if device is not None and gpu_t.device != device:
+            raise RuntimeError("all entries must use the same GPU device")
+        if d_off < 0:
+            raise RuntimeError(f"destination_offsets[{i}] must be non-negative")
+        if s_off < 0:
+            raise RuntimeError(f"source_offsets[{i}] must be non-negative")
+        if size <= 0:
+            raise RuntimeError(f"copy_sizes[{i}] must be positive")
+        if d_off + size > dst.numel() * dst.element_size():
+            raise RuntimeError(f"destination range at index {i} exceeds tensor capacity")
+        if s_off + size > src.numel() * src.element_size():
+            raise RuntimeError(f"source range at index {i} exceeds tensor capacity")
+
+    @classmethod
+    def _prepare(cls, destinations: Sequence[torch.Tensor], sources: Sequence[torch.Tensor],
                  destination_offsets: Sequence[int], source_offsets: Sequence[int], sizes: Sequence[int]):
-        """The reference's prepare_copy checks (lmcache_musa_batch_copy_ext.cpp:76-170)."""
+        """The reference's prepare_copy checks (lmcache_musa_batch_copy_ext.cpp:76-170) for a whole group.
+
+        Each distinct tensor's facts (contiguity, device, address, byte size) are read once; the per-entry
+        checks then run as int64 column operations, and the first entry that fails any of them is checked
+        again on its own (``_prepare_entry``) to raise the reference's error for it."""
         count = len(sizes)
         if len(destinations) != count or len(sources) != count:
             raise RuntimeError("destinations, sources, and sizes must have the same length")
         if len(destination_offsets) != count or len(source_offsets) != count:
             raise RuntimeError("offset vectors must have the same length as sizes")
-        dsts, srcs, lens, gpu_tensors, host_tensors = [], [], [], [], []
-        to_gpu = None
-        device = None
-        spans = []
-        for i in range(count):
-            dst, src = destinations[i], sources[i]
-            if not dst.is_contiguous() or not src.is_contiguous():
-                raise RuntimeError("batch-copy tensors must be contiguous")
-            if _gpu(dst) == _gpu(src):
-                raise RuntimeError("each entry must have exactly one GPU endpoint")
-            if to_gpu is None:
-                to_gpu = _gpu(dst)
-            if _gpu(dst) != to_gpu:
-                raise RuntimeError("one batch cannot mix h2d and d2h copies")
-            gpu_t, host_t = (dst, src) if to_gpu else (src, dst)
-            if host_t.device.type != "cpu":
-                raise RuntimeError("the non-GPU endpoint must be a CPU tensor")
-            if device is None:
-                device = gpu_t.device
-            if gpu_t.device != device:
-                raise RuntimeError("all entries must use the same GPU device")
-            d_off, s_off, size = int(destination_offsets[i]), int(source_offsets[i]), int(sizes[i])
-            if d_off < 0:
-                raise RuntimeError(f"destination_offsets[{i}] must be non-negative")
-            if s_off < 0:
-                raise RuntimeError(f"source_offsets[{i}] must be non-negative")
-            if size <= 0:
-                raise RuntimeError(f"copy_sizes[{i}] must be positive")
-            if d_off + size > dst.numel() * dst.element_size():
-                raise RuntimeError(f"destination range at index {i} exceeds tensor capacity")
-            if s_off + size > src.numel() * src.element_size():
-                raise RuntimeError(f"source range at index {i} exceeds tensor capacity")
-            dsts.append(dst.data_ptr() + d_off)
-            srcs.append(src.data_ptr() + s_off)
-            lens.append(size)
-            spans.append((dsts[-1], dsts[-1] + size))
-            gpu_tensors.append(gpu_t)
-            host_tensors.append(host_t)
-        spans.sort()
-        for (_, prev_end), (start, _) in zip(spans, spans[1:]):
-            if start < prev_end:
-                raise RuntimeError("overlapping destination ranges are invalid in an unordered batch")
-        return dsts, srcs, lens, bool(to_gpu), device, gpu_tensors, host_tensors
+        if count == 0:
+            return np.zeros(0, np.uint64), np.zeros(0, np.uint64), np.zeros(0, np.uint64), True, None, [], []
+        slot: dict[int, int] = {}
+        tensors: list[torch.Tensor] = []
+
+        def index_of(t: torch.Tensor) -> int:
+            k = slot.get(id(t))
+            if k is None:
+                k = slot[id(t)] = len(tensors)
+                tensors.append(t)
+            return k
+
+        di = np.fromiter(map(index_of, destinations), dtype=np.int64, count=count)
+        si = np.fromiter(map(index_of, sources), dtype=np.int64, count=count)
+        contig = np.array([t.is_contiguous() for t in tensors])
+        gpu = np.array([_gpu(t) for t in tensors])
+        cpu = np.array([t.device.type == "cpu" for t in tensors])
+        devices = [t.device for t in tensors]
+        nbytes = np.array([t.numel() * t.element_size() for t in tensors], dtype=np.int64)
+        try:
+            d_off = np.fromiter(map(int, destination_offsets), dtype=np.int64, count=count)
+            s_off = np.fromiter(map(int, source_offsets), dtype=np.int64, count=count)
+            size = np.fromiter(map(int, sizes), dtype=np.int64, count=count)
+            big = any(int(a.max()) >= 1 << 61 for a in (d_off, s_off, size))
+        except OverflowError:
+            big = True
+        first_gpu = bool(gpu[di[0]]) if gpu[di[0]] != gpu[si[0]] else None
+        if big or first_gpu is None:
+            bad_index = 0 if first_gpu is None else None
+        else:
+            gi = np.where(gpu[di], di, si)
+            hi = np.where(gpu[di], si, di)
+            device = devices[gi[0]]
+            same_device = np.array([d == device for d in devices])
+            bad = (~(contig[di] & contig[si]) | (gpu[di] == gpu[si]) | (gpu[di] != first_gpu) | ~cpu[hi]
+                   | ~same_device[gi] | (d_off < 0) | (s_off < 0) | (size <= 0)
+                   | (d_off + size > nbytes[di]) | (s_off + size > nbytes[si]))
+            bad_index = int(np.argmax(bad)) if bad.any() else None
+        if big or bad_index is not None:
+            to_gpu = device = None
+            for i in range(count if big else bad_index + 1):
+                dst, src = destinations[i], sources[i]
+                cls._prepare_entry(i, dst, src, int(destination_offsets[i]), int(source_offsets[i]), int(sizes[i]),
+                                   to_gpu, device)
+                if to_gpu is None:
+                    to_gpu, device = _gpu(dst), (dst if _gpu(dst) else src).device
+            if not big:
+                raise AssertionError("a column check failed where the entry checks pass")
+            raise RuntimeError("batch-copy offsets and sizes must stay below 2**61")
+        ptr = np.array([t.data_ptr() for t in tensors], dtype=np.uint64)
+        dsts = ptr[di] + d_off.astype(np.uint64)
+        srcs = ptr[si] + s_off.astype(np.uint64)
+        lens = size.astype(np.uint64)
+        order = np.lexsort((dsts + lens, dsts))
+        start, stop = dsts[order], (dsts + lens)[order]
+        if np.any(start[1:] < stop[:-1]):
+            raise RuntimeError("overlapping destination ranges are invalid in an unordered batch")
+        gpu_tensors = [t for t, g in zip(tensors, gpu) if g]
+        host_tensors = [t for t, g in zip(tensors, gpu) if not g]
+        return dsts, srcs, lens, bool(first_gpu), device, gpu_tensors, host_tensors
 
     def _submit(self, destinations, sources, destination_offsets, source_offsets, sizes, mode: int) -> bool:
         dsts, srcs, lens, to_gpu, device, gpu_tensors, host_tensors = self._prepare(
             destinations, sources, destination_offsets, source_offsets, sizes)
-        if not lens:
+        n = int(lens.shape[0])
+        if n == 0:
             return True
-        n = len(lens)
         with torch.cuda.device(device):
             stream = torch.cuda.current_stream(device)
             rc = _hip.fn("musa_aiter_hip_batch_copy")(
-                (ctypes.c_void_p * n)(*dsts), (ctypes.c_void_p * n)(*srcs), (ctypes.c_uint64 * n)(*lens), n,
-                0 if to_gpu else 1, int(mode), ctypes.c_void_p(stream.cuda_stream))
+                (ctypes.c_void_p * n).from_buffer_copy(dsts), (ctypes.c_void_p * n).from_buffer_copy(srcs),
+                (ctypes.c_uint64 * n).from_buffer_copy(lens), n, 0 if to_gpu else 1, int(mode),
+                ctypes.c_void_p(stream.cuda_stream))
             _hip.check(int(rc), "lmcache_musa_memcpy_batch_async")
-            for t in {id(t): t for t in gpu_tensors}.values():
+            for t in gpu_tensors:
                 t.record_stream(stream)
-            self.in_flight.add(stream, tuple({id(t): t for t in host_tensors + gpu_tensors}.values()))
+            self.in_flight.add(stream, tuple(host_tensors + gpu_tensors))
         return True
 
     def execute_batch_copy(self, destinations, sources, destination_offsets, source_offsets, sizes,

@@ -1,4 +1,4 @@
-"""Validation and splitting of one unordered host/device byte-copy batch (no torch dependency).
+"""Validation and splitting of one unordered host/device byte-copy batch.
 
 Contract (the reference's ``musa_aiter/ops/lmcache_musa_batch_copy_plan.py``, 0.5.0; its
 dataclasses, keyword arguments and ``ValueError`` messages are the public interface, :7-178):
@@ -8,17 +8,23 @@ destination never overlap, because the batch is unordered.  With ``pin_chunk_siz
 cut wherever its host-side offset reaches a multiple of ``pin_chunk_size`` (a host registration
 boundary, :129-152), so no piece straddles two registrations.
 
-Design: the six integer columns are normalised by one helper, the per-entry rules are a table of
-(predicate, message) pairs evaluated in the reference's order, overlaps are found with one sort of
-(destination group, start, end) triples, and an entry's pieces are the spans between its
-boundary offsets.
+Design: a batch can hold thousands of ranges, so the checks and the split run column-wise on
+int64 arrays.  The per-entry rules are a table of (predicate, message) pairs: all of them are
+evaluated over whole columns, and only the first failing entry is re-checked rule by rule to
+report the reference's message for it (entries in order, rules in order).  Overlaps are found with
+one sort of (destination group, start) pairs; an entry's pieces are the spans between its
+boundary offsets, computed for all entries at once.  Values too large for int64 arithmetic take
+the same rules one entry at a time.  ``build_batch_copy_plan`` returns the reference's dataclasses;
+the submission path reads the columns (``plan_columns``) and never builds per-entry objects.
 """
 
 from __future__ import annotations
 
 from dataclasses import dataclass
 from itertools import islice
-from typing import Callable, Hashable, Iterator, Sequence
+from typing import Callable, Hashable, Iterator, NamedTuple, Sequence
+
+import numpy as np
 
 
 @dataclass(frozen=True)
@@ -38,6 +44,19 @@ class BatchCopyPlan:
     input_entry_count: int
 
 
+class PlanColumns(NamedTuple):
+    """The plan's pieces in submission order, one int64 array per field."""
+
+    direction: str
+    input_index: np.ndarray
+    source_offset: np.ndarray
+    destination_offset: np.ndarray
+    size: np.ndarray
+    host_registration_offset: np.ndarray
+    total_bytes: int
+    input_entry_count: int
+
+
 def _is_int(value: object) -> bool:
     return isinstance(value, int) and not isinstance(value, bool)
 
@@ -46,7 +65,8 @@ def _column(name: str, values: Sequence[int], count: int) -> tuple[int, ...]:
     column = tuple(values)
     if len(column) != count:
         raise ValueError(f"{name} must have the same length as sizes")
-    if not all(_is_int(v) for v in column):
+    # Plain ints pass in one C-level pass over the element types; anything else is checked one by one.
+    if not set(map(type, column)) <= {int} and not all(_is_int(v) for v in column):
         raise ValueError(f"{name} must contain integers")
     return column
 
@@ -64,23 +84,66 @@ def _key_column(values: Sequence[Hashable] | None, count: int) -> tuple[Hashable
 
 
 # Per-entry rules, checked entry by entry in this order: (violated?, message).  The arguments are
-# (index, size, source offset, destination offset, host offset, source capacity, destination capacity).
-_Rule = Callable[[int, int, int, int, int, int, int], bool]
+# (index, size, source offset, destination offset, host offset, source capacity, destination capacity);
+# they hold for Python ints and, element-wise, for int64 arrays.
+_Rule = Callable[..., object]
 _ENTRY_RULES: tuple[tuple[_Rule, Callable[[int], str]], ...] = (
     (lambda i, n, so, do, ho, sc, dc: n <= 0,
      lambda i: f"sizes[{i}] must be positive"),
-    (lambda i, n, so, do, ho, sc, dc: min(so, do, ho) < 0,
+    (lambda i, n, so, do, ho, sc, dc: (so < 0) | (do < 0) | (ho < 0),
      lambda i: "copy offsets must be non-negative"),
-    (lambda i, n, so, do, ho, sc, dc: dc < 0 or do + n > dc,
+    (lambda i, n, so, do, ho, sc, dc: (dc < 0) | (do + n > dc),
      lambda i: f"destination range at index {i} exceeds tensor capacity"),
-    (lambda i, n, so, do, ho, sc, dc: sc < 0 or so + n > sc,
+    (lambda i, n, so, do, ho, sc, dc: (sc < 0) | (so + n > sc),
      lambda i: f"source range at index {i} exceeds tensor capacity"),
 )
 
+# Columns whose values all lie within +-2^61 cannot overflow int64 in the sums the rules and the
+# split form (offset + size, offset + a piece start).
+_LIMIT = 1 << 61
 
-def _reject_overlaps(destination_offsets: Sequence[int], sizes: Sequence[int], keys: Sequence[Hashable]) -> None:
-    """Any two overlapping ranges of one destination put an overlapping pair next to each other once the
-    ranges are sorted by (destination, start), so one pass over the sorted triples finds them."""
+
+def _as_int64(columns: Sequence[tuple[int, ...]]) -> list[np.ndarray] | None:
+    arrays = []
+    for column in columns:
+        if column and (max(column) >= _LIMIT or min(column) <= -_LIMIT):
+            return None
+        arrays.append(np.fromiter(column, dtype=np.int64, count=len(column)))
+    return arrays
+
+
+def _check_rules(columns: Sequence[tuple[int, ...]], arrays: list[np.ndarray] | None) -> None:
+    """Raise the message of the first violated rule of the first entry that violates one."""
+    count = len(columns[0])
+    if arrays is not None:
+        bad = np.zeros(count, dtype=bool)
+        for violated, _ in _ENTRY_RULES:
+            bad |= violated(None, *arrays)
+        if not bad.any():
+            return
+        first = int(np.argmax(bad))
+        rows = [(first, *(c[first] for c in columns))]
+    else:
+        rows = zip(range(count), *columns)
+    for row in rows:
+        for violated, message in _ENTRY_RULES:
+            if violated(*row):
+                raise ValueError(message(row[0]))
+
+
+def _reject_overlaps(destination_offsets: np.ndarray, sizes: np.ndarray, keys: Sequence[Hashable]) -> None:
+    """Sorted by (destination, start), any two overlapping ranges of one destination include an
+    adjacent overlapping pair, so one comparison of neighbours finds them."""
+    group: dict[Hashable, int] = {}
+    groups = np.fromiter((group.setdefault(k, len(group)) for k in keys), dtype=np.int64, count=len(keys))
+    order = np.lexsort((destination_offsets, groups))
+    g, start, end = groups[order], destination_offsets[order], (destination_offsets + sizes)[order]
+    if np.any((g[1:] == g[:-1]) & (start[1:] < end[:-1])):
+        raise ValueError("overlapping destination ranges are invalid in an unordered batch")
+
+
+def _reject_overlaps_scalar(destination_offsets: Sequence[int], sizes: Sequence[int],
+                            keys: Sequence[Hashable]) -> None:
     group: dict[Hashable, int] = {}
     spans = sorted((group.setdefault(k, len(group)), off, off + n) for k, off, n in zip(keys, destination_offsets, sizes))
     for (g0, _, end0), (g1, start1, _) in zip(spans, spans[1:]):
@@ -100,7 +163,25 @@ def _pieces(host_offset: int, size: int, pin_chunk_size: int | None) -> Iterator
         yield start, stop - start
 
 
-def build_batch_copy_plan(
+def _split(sizes: np.ndarray, host_offsets: np.ndarray, pin_chunk_size: int | None):
+    """(entry index, start, length) of every piece, entries in order and pieces in order within each:
+    piece 0 of an entry ends at its first boundary (``pin - host_offset % pin`` bytes in) or at its
+    end, piece j > 0 starts j - 1 chunks after that boundary."""
+    count = sizes.shape[0]
+    if pin_chunk_size is None:
+        return np.arange(count, dtype=np.int64), np.zeros(count, dtype=np.int64), sizes
+    first_cut = pin_chunk_size - host_offsets % pin_chunk_size
+    beyond = np.maximum(sizes - first_cut, 0)
+    pieces = 1 + (beyond + pin_chunk_size - 1) // pin_chunk_size
+    index = np.repeat(np.arange(count, dtype=np.int64), pieces)
+    j = np.arange(index.shape[0], dtype=np.int64) - np.repeat(np.cumsum(pieces) - pieces, pieces)
+    cut = first_cut[index]
+    start = np.where(j == 0, 0, cut + (j - 1) * pin_chunk_size)
+    stop = np.minimum(cut + j * pin_chunk_size, sizes[index])
+    return index, start, stop - start
+
+
+def plan_columns(
     *,
     direction: str,
     sizes: Sequence[int],
@@ -111,8 +192,8 @@ def build_batch_copy_plan(
     host_registration_offsets: Sequence[int] | None = None,
     pin_chunk_size: int | None = None,
     destination_keys: Sequence[Hashable] | None = None,
-) -> BatchCopyPlan:
-    """Validate one unordered batch and split its entries at host registration boundaries."""
+) -> PlanColumns:
+    """``build_batch_copy_plan``'s checks and split, returned as int64 columns."""
     if direction not in ("h2d", "d2h"):
         raise ValueError("direction must be 'h2d' or 'd2h'")
     if pin_chunk_size is not None and not (_is_int(pin_chunk_size) and pin_chunk_size > 0):
@@ -131,18 +212,49 @@ def build_batch_copy_plan(
                        else host_registration_offsets, count)
     keys = _key_column(destination_keys, count)
 
-    for row in zip(range(count), n, src_off, dst_off, host_off, src_cap, dst_cap):
-        for violated, message in _ENTRY_RULES:
-            if violated(*row):
-                raise ValueError(message(row[0]))
-    _reject_overlaps(dst_off, n, keys)
+    columns = (n, src_off, dst_off, host_off, src_cap, dst_cap)
+    arrays = None if pin_chunk_size is not None and pin_chunk_size >= _LIMIT else _as_int64(columns)
+    _check_rules(columns, arrays)
+    if arrays is None:
+        _reject_overlaps_scalar(dst_off, n, keys)
+        pieces = [(i, start, length) for i, ho, size in zip(range(count), host_off, n)
+                  for start, length in _pieces(ho, size, pin_chunk_size)]
+        index = np.array([p[0] for p in pieces], dtype=np.int64)
+        start = [p[1] for p in pieces]
+        so_, do_, ho_ = ([c[i] + s for i, s in zip(index.tolist(), start)] for c in (src_off, dst_off, host_off))
+        length = [p[2] for p in pieces]
+        as_obj = (lambda v: np.array(v, dtype=object))
+        return PlanColumns(direction, index, as_obj(so_), as_obj(do_), as_obj(length), as_obj(ho_), sum(n), count)
+    n_a, so_a, do_a, ho_a = arrays[:4]
+    _reject_overlaps(do_a, n_a, keys)
+    index, start, length = _split(n_a, ho_a, pin_chunk_size)
+    return PlanColumns(direction, index, so_a[index] + start, do_a[index] + start, length, ho_a[index] + start,
+                       sum(n), count)
 
+
+def build_batch_copy_plan(
+    *,
+    direction: str,
+    sizes: Sequence[int],
+    source_capacities: Sequence[int],
+    destination_capacities: Sequence[int],
+    source_offsets: Sequence[int] | None = None,
+    destination_offsets: Sequence[int] | None = None,
+    host_registration_offsets: Sequence[int] | None = None,
+    pin_chunk_size: int | None = None,
+    destination_keys: Sequence[Hashable] | None = None,
+) -> BatchCopyPlan:
+    """Validate one unordered batch and split its entries at host registration boundaries."""
+    c = plan_columns(direction=direction, sizes=sizes, source_capacities=source_capacities,
+                     destination_capacities=destination_capacities, source_offsets=source_offsets,
+                     destination_offsets=destination_offsets, host_registration_offsets=host_registration_offsets,
+                     pin_chunk_size=pin_chunk_size, destination_keys=destination_keys)
     entries = tuple(
-        BatchCopyEntry(input_index=i, source_offset=so + start, destination_offset=do + start, size=length,
-                       host_registration_offset=ho + start)
-        for i, so, do, ho, size in zip(range(count), src_off, dst_off, host_off, n)
-        for start, length in _pieces(ho, size, pin_chunk_size))
-    return BatchCopyPlan(direction=direction, entries=entries, total_bytes=sum(n), input_entry_count=count)
+        BatchCopyEntry(input_index=i, source_offset=so, destination_offset=do, size=n, host_registration_offset=ho)
+        for i, so, do, n, ho in zip(c.input_index.tolist(), c.source_offset.tolist(), c.destination_offset.tolist(),
+                                    c.size.tolist(), c.host_registration_offset.tolist()))
+    return BatchCopyPlan(direction=direction, entries=entries, total_bytes=c.total_bytes,
+                         input_entry_count=c.input_entry_count)
 
 
 def chunk_batch_copy_plan(plan: BatchCopyPlan, max_batch_entries: int) -> tuple[tuple[BatchCopyEntry, ...], ...]:

@@ -141,6 +141,82 @@ def test_batch_limit_environment_override(monkeypatch):
         batch._resolve_max_batch_entries(True)
 
 
+def _plan_by_entry(sizes, src_cap, dst_cap, src_off, dst_off, host_off, pin, keys):
+    """The plan's rules restated one entry at a time (entries in order, rules in order), the overlap
+    check as a pairwise scan, and the split from oracle/batch_copy_oracle.split_sizes."""
+    for i, (n, so, do, ho, sc, dc) in enumerate(zip(sizes, src_off, dst_off, host_off, src_cap, dst_cap)):
+        if n <= 0:
+            return f"sizes[{i}] must be positive"
+        if min(so, do, ho) < 0:
+            return "copy offsets must be non-negative"
+        if dc < 0 or do + n > dc:
+            return f"destination range at index {i} exceeds tensor capacity"
+        if sc < 0 or so + n > sc:
+            return f"source range at index {i} exceeds tensor capacity"
+    for a in range(len(sizes)):
+        for b in range(a + 1, len(sizes)):
+            if keys[a] == keys[b] and dst_off[a] < dst_off[b] + sizes[b] and dst_off[b] < dst_off[a] + sizes[a]:
+                return "overlapping destination ranges are invalid in an unordered batch"
+    out = []
+    for i in range(len(sizes)):
+        s, d, h = src_off[i], dst_off[i], host_off[i]
+        for piece in bo.split_sizes(sizes[i], host_off[i], pin):
+            out.append((i, s, d, piece, h))
+            s, d, h = s + piece, d + piece, h + piece
+    return out
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_column_plan_matches_per_entry_rules(seed):
+    # Larger random batches with planted violations (non-positive sizes, negative offsets, ranges past a
+    # capacity, overlaps within one destination) and, for some seeds, offsets near 2**62 that take the
+    # one-entry-at-a-time path: same pieces or the same first error as the per-entry restatement.
+    rng = np.random.default_rng(1000 + seed)
+    n = int(rng.integers(1, 400))
+    big = (1 << 62) if seed % 7 == 0 else 0
+    sizes = [int(x) for x in rng.integers(1, 5000, size=n)]
+    keys = [int(x) for x in rng.integers(0, 4, size=n)]
+    dst_off = [0] * n
+    cursor = {}
+    for i in range(n):  # disjoint ranges per destination unless an overlap is planted below
+        dst_off[i] = cursor.get(keys[i], big) + int(rng.integers(0, 3))
+        cursor[keys[i]] = dst_off[i] + sizes[i]
+    src_off = [int(x) + big for x in rng.integers(0, 1000, size=n)]
+    host_off = [int(x) for x in rng.integers(0, 1 << 20, size=n)]
+    src_cap = [so + sz + int(rng.integers(0, 10)) for so, sz in zip(src_off, sizes)]
+    dst_cap = [do + sz + int(rng.integers(0, 10)) for do, sz in zip(dst_off, sizes)]
+    pin = int(rng.integers(1, 9000)) if seed % 3 else None
+    kind = seed % 6
+    j = int(rng.integers(0, n))
+    if kind == 1:
+        sizes[j] = -int(rng.integers(0, 3))
+    elif kind == 2:
+        host_off[j] = -1
+    elif kind == 3:
+        dst_cap[j] = dst_off[j] + sizes[j] - 1
+    elif kind == 4:
+        src_cap[j] = -5
+    elif kind == 5 and n > 1:
+        k = (j + 1) % n
+        keys[k], dst_off[k] = keys[j], dst_off[j] + sizes[j] // 2
+        dst_cap[k] = max(dst_cap[k], dst_off[k] + sizes[k])
+    want = _plan_by_entry(sizes, src_cap, dst_cap, src_off, dst_off, host_off, pin, keys)
+    args = dict(direction="h2d", sizes=sizes, source_capacities=src_cap, destination_capacities=dst_cap,
+                source_offsets=src_off, destination_offsets=dst_off, host_registration_offsets=host_off,
+                pin_chunk_size=pin, destination_keys=keys)
+    if isinstance(want, str):
+        with pytest.raises(ValueError) as err:
+            batch._build_batch_copy_plan(**args)
+        assert str(err.value) == want
+        return
+    plan = batch._build_batch_copy_plan(**args)
+    got = [(e.input_index, e.source_offset, e.destination_offset, e.size, e.host_registration_offset)
+           for e in plan.entries]
+    assert got == want
+    assert plan.total_bytes == sum(sizes) and plan.input_entry_count == n
+    assert all(type(v) is int for e in plan.entries for v in (e.source_offset, e.size))
+
+
 @pytest.mark.parametrize("seed", range(30))
 def test_plan_split_matches_byte_level_rule(seed):
     rng = np.random.default_rng(seed)
@@ -264,5 +340,96 @@ def test_extension_argument_checks(monkeypatch):
     with pytest.raises(RuntimeError, match="overlapping destination"):
         e._prepare([dev, dev], [host, host], [0, 4], [0, 8], [6, 4])
     dsts, srcs, lens, to_gpu, _, _, _ = e._prepare([dev, dev2], [host, host], [0, 0], [3, 5], [4, 4])
-    assert to_gpu and lens == [4, 4] and dsts == [dev.data_ptr(), dev2.data_ptr()]
-    assert srcs == [host.data_ptr() + 3, host.data_ptr() + 5]
+    assert to_gpu and lens.tolist() == [4, 4] and dsts.tolist() == [dev.data_ptr(), dev2.data_ptr()]
+    assert srcs.tolist() == [host.data_ptr() + 3, host.data_ptr() + 5]
+
+
+def _prepare_by_entry(dsts, srcs, d_offs, s_offs, sizes, is_gpu):
+    """The extension's checks restated one entry at a time (lmcache_musa_batch_copy_ext.cpp:76-170 order):
+    the first error message, or the (destination address, source address, size) triples."""
+    to_gpu = device = None
+    out = []
+    for i, (dst, src) in enumerate(zip(dsts, srcs)):
+        if not dst.is_contiguous() or not src.is_contiguous():
+            return "batch-copy tensors must be contiguous"
+        if is_gpu(dst) == is_gpu(src):
+            return "each entry must have exactly one GPU endpoint"
+        if to_gpu is None:
+            to_gpu = is_gpu(dst)
+        if is_gpu(dst) != to_gpu:
+            return "one batch cannot mix h2d and d2h copies"
+        gpu_t, host_t = (dst, src) if to_gpu else (src, dst)
+        if host_t.device.type != "cpu":
+            return "the non-GPU endpoint must be a CPU tensor"
+        if device is None:
+            device = gpu_t.device
+        if d_offs[i] < 0:
+            return f"destination_offsets[{i}] must be non-negative"
+        if s_offs[i] < 0:
+            return f"source_offsets[{i}] must be non-negative"
+        if sizes[i] <= 0:
+            return f"copy_sizes[{i}] must be positive"
+        if d_offs[i] + sizes[i] > dst.numel() * dst.element_size():
+            return f"destination range at index {i} exceeds tensor capacity"
+        if s_offs[i] + sizes[i] > src.numel() * src.element_size():
+            return f"source range at index {i} exceeds tensor capacity"
+        out.append((dst.data_ptr() + d_offs[i], src.data_ptr() + s_offs[i], sizes[i]))
+    spans = sorted((d, d + n) for d, _, n in out)
+    if any(b[0] < a[1] for a, b in zip(spans, spans[1:])):
+        return "overlapping destination ranges are invalid in an unordered batch"
+    return out
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_extension_column_checks_match_per_entry_checks(monkeypatch, seed):
+    # Groups of up to 300 entries over a few host and (faked) GPU tensors with one planted fault each;
+    # the column-wise checks must raise the per-entry restatement's first error or return its triples.
+    gpu_ids = set()
+    monkeypatch.setattr(ext, "_gpu", lambda t: id(t) in gpu_ids)
+    rng = np.random.default_rng(2000 + seed)
+    hosts = [torch.zeros(int(rng.integers(1, 64)) * 64, dtype=torch.uint8) for _ in range(3)]
+    gpus = [torch.zeros(int(rng.integers(1, 64)) * 64, dtype=torch.uint8) for _ in range(3)]
+    gpu_ids.update(id(t) for t in gpus)
+    n = int(rng.integers(1, 300))
+    h2d = bool(seed % 2)
+    dsts, srcs, d_offs, s_offs, sizes, cursor = [], [], [], [], [], {}
+    for _ in range(n):
+        g, h = gpus[int(rng.integers(0, 3))], hosts[int(rng.integers(0, 3))]
+        dst, src = (g, h) if h2d else (h, g)
+        size = int(rng.integers(1, 8))
+        d_off = cursor.get(id(dst), 0)
+        cursor[id(dst)] = d_off + size
+        dsts.append(dst)
+        srcs.append(src)
+        d_offs.append(d_off)
+        s_offs.append(int(rng.integers(0, max(1, src.numel() - size))))
+        sizes.append(size)
+    j = int(rng.integers(0, n))
+    fault = seed % 8
+    if fault == 1:
+        dsts[j] = torch.zeros(4, 4, dtype=torch.uint8).t()
+    elif fault == 2:
+        srcs[j] = dsts[j]
+    elif fault == 3:
+        dsts[j], srcs[j] = srcs[j], dsts[j]
+    elif fault == 4:
+        d_offs[j] = -1
+    elif fault == 5:
+        sizes[j] = 0
+    elif fault == 6:
+        s_offs[j] = srcs[j].numel()
+    elif fault == 7 and n > 1:
+        k = (j + 1) % n
+        dsts[k], d_offs[k] = dsts[j], d_offs[j]
+    want = _prepare_by_entry(dsts, srcs, d_offs, s_offs, sizes, ext._gpu)
+    if isinstance(want, str):
+        with pytest.raises(RuntimeError) as err:
+            ext.HipBatchCopyExtension._prepare(dsts, srcs, d_offs, s_offs, sizes)
+        assert str(err.value) == want
+        return
+    got_d, got_s, got_n, to_gpu, _, gpu_t, host_t = ext.HipBatchCopyExtension._prepare(dsts, srcs, d_offs, s_offs,
+                                                                                        sizes)
+    assert list(zip(got_d.tolist(), got_s.tolist(), got_n.tolist())) == want
+    assert to_gpu == h2d
+    assert {id(t) for t in gpu_t} == {id(t) for t in (*dsts, *srcs) if id(t) in gpu_ids}
+    assert {id(t) for t in host_t} == {id(t) for t in (*dsts, *srcs) if id(t) not in gpu_ids}
