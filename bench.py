@@ -941,10 +941,14 @@ def bench_batch_copy() -> dict:
     memory read or written by the GPU over the host link) on at most 64 workgroups and on at most 16
     (the prefer_overlap_with_compute form), and through one hipMemcpyAsync per range;
     a single torch copy of one contiguous pinned buffer of the same total size gives the runtime's
-    own rate.  Bytes = bytes moved across the host link (each byte once).
+    own rate, and the public lmcache_musa_memcpy_batch_async call (its host planning included) the
+    rate a caller sees, with its host time per call.  Bytes = bytes moved across the host link
+    (each byte once).
     """
     from musa_aiter.ops import _hip
+    from musa_aiter.ops.lmcache_musa_batch_copy import lmcache_musa_memcpy_batch_async
 
+    os.environ["MUSA_AITER_LMCACHE_BATCH_COPY"] = "1"  # the public API's opt-in gate
     dev = torch.device("cuda", 0)
     out = {}
     fn = _hip.fn("musa_aiter_hip_batch_copy")
@@ -994,6 +998,32 @@ def bench_batch_copy() -> dict:
             dst_t, src_t = (gpu, host) if direction == "h2d" else (host, gpu)
             ms = batched_ms(lambda: dst_t.copy_(src_t, non_blocking=True), launches=3, reps=3)
             res[f"{direction}_torch_contiguous_copy"] = link_rate(total, ms)
+            # The public API end to end (host planning and checks included): the same ranges as offsets
+            # into the two tensors, timed between events like the rest, plus its host time per call.
+            g_off = [int(perm[i]) * size for i in range(ranges)]
+            h_off = [i * size for i in range(ranges)]
+            api_d, api_s = ([gpu] * ranges, [host] * ranges) if direction == "h2d" else ([host] * ranges, [gpu] * ranges)
+            d_off, s_off = (g_off, h_off) if direction == "h2d" else (h_off, g_off)
+
+            def api(api_d=api_d, api_s=api_s, d_off=d_off, s_off=s_off):
+                if not lmcache_musa_memcpy_batch_async(api_d, api_s, [size] * ranges, destination_offsets=d_off,
+                                                       source_offsets=s_off, max_batch_entries=ranges):
+                    raise RuntimeError("batch copy API declined the batch")
+
+            (gpu if direction == "h2d" else host).zero_()
+            torch.cuda.synchronize()
+            api()
+            torch.cuda.synchronize()
+            api_ok = bool(torch.equal(gpu, shuffled)) if direction == "h2d" else bool(torch.equal(host, ref))
+            host_s = []
+            for _ in range(5):
+                t0 = time.perf_counter()
+                api()
+                host_s.append(time.perf_counter() - t0)
+                torch.cuda.synchronize()
+            ms = batched_ms(api, launches=3, reps=3)
+            res[f"{direction}_public_api"] = {**link_rate(total, ms), "parity": api_ok,
+                                             "host_ms_per_call": round(1e3 * float(np.median(host_s)), 3)}
         out[label] = res
         del host, gpu, shuffled
 
