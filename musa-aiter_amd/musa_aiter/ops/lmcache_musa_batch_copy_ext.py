@@ -140,18 +140,12 @@ class HipBatchCopyExtension:
             raise RuntimeError("offset vectors must have the same length as sizes")
         if count == 0:
             return np.zeros(0, np.uint64), np.zeros(0, np.uint64), np.zeros(0, np.uint64), True, None, [], []
-        slot: dict[int, int] = {}
-        tensors: list[torch.Tensor] = []
-
-        def index_of(t: torch.Tensor) -> int:
-            k = slot.get(id(t))
-            if k is None:
-                k = slot[id(t)] = len(tensors)
-                tensors.append(t)
-            return k
-
-        di = np.fromiter(map(index_of, destinations), dtype=np.int64, count=count)
-        si = np.fromiter(map(index_of, sources), dtype=np.int64, count=count)
+        # Distinct objects by identity: one sort of the entries' object ids, both sides together.
+        ids = np.fromiter(map(id, (*destinations, *sources)), dtype=np.uint64, count=2 * count)
+        _, first, which = np.unique(ids, return_index=True, return_inverse=True)
+        both = (*destinations, *sources)
+        tensors = [both[i] for i in first.tolist()]
+        di, si = which[:count], which[count:]
         contig = np.array([t.is_contiguous() for t in tensors])
         gpu = np.array([_gpu(t) for t in tensors])
         cpu = np.array([t.device.type == "cpu" for t in tensors])

@@ -134,8 +134,11 @@ def _check_rules(columns: Sequence[tuple[int, ...]], arrays: list[np.ndarray] | 
 def _reject_overlaps(destination_offsets: np.ndarray, sizes: np.ndarray, keys: Sequence[Hashable]) -> None:
     """Sorted by (destination, start), any two overlapping ranges of one destination include an
     adjacent overlapping pair, so one comparison of neighbours finds them."""
-    group: dict[Hashable, int] = {}
-    groups = np.fromiter((group.setdefault(k, len(group)) for k in keys), dtype=np.int64, count=len(keys))
+    if set(map(type, keys)) <= {int} and (not keys or (max(keys) < 1 << 63 and min(keys) >= -(1 << 63))):
+        groups = np.fromiter(keys, dtype=np.int64, count=len(keys))  # integer keys (object ids) group as they are
+    else:
+        group: dict[Hashable, int] = {}
+        groups = np.fromiter((group.setdefault(k, len(group)) for k in keys), dtype=np.int64, count=len(keys))
     order = np.lexsort((destination_offsets, groups))
     g, start, end = groups[order], destination_offsets[order], (destination_offsets + sizes)[order]
     if np.any((g[1:] == g[:-1]) & (start[1:] < end[:-1])):
