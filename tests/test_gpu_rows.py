@@ -25,7 +25,7 @@ def _caches_2xnl(nl, nb, bs, nh, hs, dtype, gen):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("kind", ["sequences", "skips", "random"])
-@pytest.mark.parametrize("nh,hs", [(8, 128), (2, 3), (4, 6)])
+@pytest.mark.parametrize("nh,hs", [(8, 128), (2, 3), (4, 6), (8, 96)])
 def test_two_x_nl_gather_matches_oracle(dtype, kind, nh, hs):
     nl, bs, tokens, mem_tokens = 3, 16, 200, 230
     rng = np.random.default_rng(41)
@@ -43,8 +43,9 @@ def test_two_x_nl_gather_matches_oracle(dtype, kind, nh, hs):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("kind", ["sequences", "skips", "duplicates"])
 @pytest.mark.parametrize("skip", [0, 5])
-def test_two_x_nl_scatter_matches_oracle(dtype, kind, skip):
-    nl, bs, nh, hs, tokens = 4, 16, 8, 128, 150
+@pytest.mark.parametrize("hs", [128, 96])
+def test_two_x_nl_scatter_matches_oracle(dtype, kind, skip, hs):
+    nl, bs, nh, tokens = 4, 16, 8, 150
     rng = np.random.default_rng(42)
     gen = torch.Generator().manual_seed(42)
     slots, nb = make_slots(kind, rng, block_size=bs, tokens=tokens)
@@ -127,12 +128,15 @@ def test_list_and_six_d_layouts_match_oracle(dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("hidden", [576, 5, 64])
-def test_lmcache_mla_layouts_match_oracle(dtype, hidden):
+@pytest.mark.parametrize("hidden", [576, 5, 64, 520, 1000])
+@pytest.mark.parametrize("kind", ["skips", "duplicates"])
+def test_lmcache_mla_layouts_match_oracle(dtype, hidden, kind):
+    # bf16 rows of 1,152 and 2,000 bytes (whole 128-byte lines and not) and 1,040 bytes (not a
+    # multiple of 32) next to tiny rows and fp32 rows above 2 KiB.
     nl, bs, tokens = 3, 64, 300
     rng = np.random.default_rng(44)
     gen = torch.Generator().manual_seed(44)
-    slots, nb = make_slots("skips", rng, block_size=bs, tokens=tokens)
+    slots, nb = make_slots(kind, rng, block_size=bs, tokens=tokens)
     s_d = torch.from_numpy(slots).to(DEV)
     paged = random_payload((nl, nb, bs, hidden), dtype, gen)
     paged_d = paged.to(DEV)
