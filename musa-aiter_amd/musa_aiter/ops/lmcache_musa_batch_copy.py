@@ -30,11 +30,13 @@ import os
 from dataclasses import dataclass
 from typing import Protocol, Sequence
 
+import numpy as np
 import torch
 
 from .kv_backend import KVBackendCapabilities, KVBackendDecision, select_kv_backend
 from .kv_transfer_plan import KVTransferPlan
-from .lmcache_musa_batch_copy_ext import lmcache_musa_batch_copy_requested, load_lmcache_musa_batch_copy_ext
+from .lmcache_musa_batch_copy_ext import HipBatchCopyExtension, lmcache_musa_batch_copy_requested
+from .lmcache_musa_batch_copy_ext import load_lmcache_musa_batch_copy_ext
 from .lmcache_musa_batch_copy_plan import build_batch_copy_plan as _build_batch_copy_plan
 from .lmcache_musa_batch_copy_plan import chunk_batch_copy_plan as _chunk_batch_copy_plan
 from .lmcache_musa_batch_copy_plan import plan_columns as _plan_columns
@@ -118,19 +120,18 @@ class _Endpoints:
     device: tuple[str, int | None]
 
 
-def _classify(destinations: tuple, sources: tuple, require_pinned_host: bool) -> _Endpoints | None:
+def _classify(destinations: tuple, sources: tuple, pair_keys: np.ndarray,
+              require_pinned_host: bool) -> _Endpoints | None:
     """Check every pair in order; ``None`` as soon as a pair is not host <-> GPU (not this backend's).
 
     A batch names the same few tensors many times (one staging buffer, one cache).  An entry whose
     (destination, source) pair of objects already appeared passes or fails exactly as its first
     appearance did, and the first failing entry is always a first appearance, so only the first
-    appearance of each pair is checked, in entry order."""
-    firsts: dict[tuple[int, int], int] = {}
-    for index, key in enumerate(zip(map(id, destinations), map(id, sources))):
-        if key not in firsts:
-            firsts[key] = index
+    appearance of each pair is checked, in entry order.  ``pair_keys[i]`` identifies entry i's pair
+    of objects."""
+    firsts = np.sort(np.unique(pair_keys, return_index=True)[1]).tolist()
     directions, devices = set(), set()
-    for index in firsts.values():
+    for index in firsts:
         destination, source = destinations[index], sources[index]
         if not isinstance(destination, torch.Tensor) or not isinstance(source, torch.Tensor):
             raise TypeError("destinations and sources must contain torch.Tensor values")
@@ -177,30 +178,43 @@ def lmcache_musa_memcpy_batch_async(
         return True
     if not len(destinations) == len(sources) == len(sizes):
         raise ValueError("destinations, sources, and sizes must have the same length")
-    endpoints = _classify(destinations, sources, require_pinned_host)
+    # The batch's distinct objects (by identity) and each entry's index among them: one sort of object ids.
+    count = len(sizes)
+    both = (*destinations, *sources)
+    _, first, which = np.unique(np.fromiter(map(id, both), dtype=np.uint64, count=2 * count),
+                                return_index=True, return_inverse=True)
+    tensors = [both[i] for i in first.tolist()]
+    dst_index, src_index = which[:count], which[count:]
+    endpoints = _classify(destinations, sources, dst_index * len(tensors) + src_index, require_pinned_host)
     if endpoints is None:
         return False
-    capacity: dict[int, int] = {}
-    for t in (*sources, *destinations):
-        if id(t) not in capacity:
-            capacity[id(t)] = t.numel() * t.element_size()
+    capacity = np.array([t.numel() * t.element_size() for t in tensors], dtype=np.int64)
     plan = _plan_columns(
-        direction=endpoints.direction, sizes=sizes, source_capacities=[capacity[id(t)] for t in sources],
-        destination_capacities=[capacity[id(t)] for t in destinations], source_offsets=source_offsets,
+        direction=endpoints.direction, sizes=sizes, source_capacities=capacity[src_index],
+        destination_capacities=capacity[dst_index], source_offsets=source_offsets,
         destination_offsets=destination_offsets, host_registration_offsets=host_registration_offsets,
-        pin_chunk_size=pin_chunk_size, destination_keys=[id(t) for t in destinations])
+        pin_chunk_size=pin_chunk_size, destination_keys=dst_index.tolist())
     extension = _extension_if_requested(need_batch=True)
     if extension is None:
         return False
-    # Groups of max_batch_entries pieces in plan order, each one extension call.
+    # Groups of max_batch_entries pieces in plan order, each one extension call.  This package's own
+    # extension takes a group as columns; any other extension object gets the reference's lists.
     limit = _resolve_max_batch_entries(max_batch_entries)
     total = plan.input_index.shape[0]
+    columns = isinstance(extension, HipBatchCopyExtension) and plan.size.dtype == np.int64
     for number, lo in enumerate(range(0, total, limit)):
-        index = plan.input_index[lo:lo + limit].tolist()
-        ok = extension.execute_batch_copy([destinations[i] for i in index], [sources[i] for i in index],
-                                          plan.destination_offset[lo:lo + limit].tolist(),
-                                          plan.source_offset[lo:lo + limit].tolist(),
-                                          plan.size[lo:lo + limit].tolist(), prefer_overlap_with_compute)
+        piece = slice(lo, lo + limit)
+        if columns:
+            index = plan.input_index[piece]
+            ok = extension.execute_batch_copy_columns(tensors, dst_index[index], src_index[index],
+                                                      plan.destination_offset[piece], plan.source_offset[piece],
+                                                      plan.size[piece], prefer_overlap_with_compute)
+        else:
+            index = plan.input_index[piece].tolist()
+            ok = extension.execute_batch_copy([destinations[i] for i in index], [sources[i] for i in index],
+                                              plan.destination_offset[piece].tolist(),
+                                              plan.source_offset[piece].tolist(), plan.size[piece].tolist(),
+                                              prefer_overlap_with_compute)
         if ok:
             continue
         if number == 0:

@@ -141,23 +141,36 @@ class HipBatchCopyExtension:
         if count == 0:
             return np.zeros(0, np.uint64), np.zeros(0, np.uint64), np.zeros(0, np.uint64), True, None, [], []
         # Distinct objects by identity: one sort of the entries' object ids, both sides together.
-        ids = np.fromiter(map(id, (*destinations, *sources)), dtype=np.uint64, count=2 * count)
-        _, first, which = np.unique(ids, return_index=True, return_inverse=True)
         both = (*destinations, *sources)
+        ids = np.fromiter(map(id, both), dtype=np.uint64, count=2 * count)
+        _, first, which = np.unique(ids, return_index=True, return_inverse=True)
         tensors = [both[i] for i in first.tolist()]
-        di, si = which[:count], which[count:]
+        try:
+            d_off = np.fromiter(map(int, destination_offsets), dtype=np.int64, count=count)
+            s_off = np.fromiter(map(int, source_offsets), dtype=np.int64, count=count)
+            size = np.fromiter(map(int, sizes), dtype=np.int64, count=count)
+        except OverflowError:
+            d_off = s_off = size = None
+        return cls._prepare_columns(
+            tensors, which[:count], which[count:], d_off, s_off, size,
+            lambda i: (destinations[i], sources[i], int(destination_offsets[i]), int(source_offsets[i]), int(sizes[i])))
+
+    @classmethod
+    def _prepare_columns(cls, tensors: Sequence[torch.Tensor], di: np.ndarray, si: np.ndarray,
+                         d_off: np.ndarray | None, s_off: np.ndarray | None, size: np.ndarray | None, entry=None):
+        """``_prepare`` for entries given as indices into distinct ``tensors`` and int64 columns (``None``
+        columns: values beyond int64, checked entry by entry).  ``entry(i)`` gives entry i's
+        (destination, source, destination offset, source offset, size) for the per-entry re-check."""
+        count = int(di.shape[0])
+        if entry is None:
+            def entry(i: int):
+                return tensors[di[i]], tensors[si[i]], int(d_off[i]), int(s_off[i]), int(size[i])
         contig = np.array([t.is_contiguous() for t in tensors])
         gpu = np.array([_gpu(t) for t in tensors])
         cpu = np.array([t.device.type == "cpu" for t in tensors])
         devices = [t.device for t in tensors]
         nbytes = np.array([t.numel() * t.element_size() for t in tensors], dtype=np.int64)
-        try:
-            d_off = np.fromiter(map(int, destination_offsets), dtype=np.int64, count=count)
-            s_off = np.fromiter(map(int, source_offsets), dtype=np.int64, count=count)
-            size = np.fromiter(map(int, sizes), dtype=np.int64, count=count)
-            big = any(int(a.max()) >= 1 << 61 for a in (d_off, s_off, size))
-        except OverflowError:
-            big = True
+        big = d_off is None or any(int(a.max()) >= 1 << 61 for a in (d_off, s_off, size))
         first_gpu = bool(gpu[di[0]]) if gpu[di[0]] != gpu[si[0]] else None
         if big or first_gpu is None:
             bad_index = 0 if first_gpu is None else None
@@ -173,9 +186,8 @@ class HipBatchCopyExtension:
         if big or bad_index is not None:
             to_gpu = device = None
             for i in range(count if big else bad_index + 1):
-                dst, src = destinations[i], sources[i]
-                cls._prepare_entry(i, dst, src, int(destination_offsets[i]), int(source_offsets[i]), int(sizes[i]),
-                                   to_gpu, device)
+                dst, src, d, s, n = entry(i)
+                cls._prepare_entry(i, dst, src, d, s, n, to_gpu, device)
                 if to_gpu is None:
                     to_gpu, device = _gpu(dst), (dst if _gpu(dst) else src).device
             if not big:
@@ -189,13 +201,17 @@ class HipBatchCopyExtension:
         start, stop = dsts[order], (dsts + lens)[order]
         if np.any(start[1:] < stop[:-1]):
             raise RuntimeError("overlapping destination ranges are invalid in an unordered batch")
-        gpu_tensors = [t for t, g in zip(tensors, gpu) if g]
-        host_tensors = [t for t, g in zip(tensors, gpu) if not g]
+        used = np.zeros(len(tensors), dtype=bool)
+        used[di] = used[si] = True
+        gpu_tensors = [t for t, g, u in zip(tensors, gpu, used) if g and u]
+        host_tensors = [t for t, g, u in zip(tensors, gpu, used) if u and not g]
         return dsts, srcs, lens, bool(first_gpu), device, gpu_tensors, host_tensors
 
     def _submit(self, destinations, sources, destination_offsets, source_offsets, sizes, mode: int) -> bool:
-        dsts, srcs, lens, to_gpu, device, gpu_tensors, host_tensors = self._prepare(
-            destinations, sources, destination_offsets, source_offsets, sizes)
+        return self._launch(self._prepare(destinations, sources, destination_offsets, source_offsets, sizes), mode)
+
+    def _launch(self, prepared, mode: int) -> bool:
+        dsts, srcs, lens, to_gpu, device, gpu_tensors, host_tensors = prepared
         n = int(lens.shape[0])
         if n == 0:
             return True
@@ -218,6 +234,19 @@ class HipBatchCopyExtension:
 
     def execute_copy_loop(self, destinations, sources, destination_offsets, source_offsets, sizes) -> bool:
         return self._submit(destinations, sources, destination_offsets, source_offsets, sizes, mode=2)
+
+    def execute_batch_copy_columns(self, tensors: Sequence[torch.Tensor], destination_index: np.ndarray,
+                                   source_index: np.ndarray, destination_offsets: np.ndarray,
+                                   source_offsets: np.ndarray, sizes: np.ndarray,
+                                   prefer_overlap_with_compute: bool) -> bool:
+        """``execute_batch_copy`` for a group given as int64 columns: entry i copies ``sizes[i]`` bytes from
+        ``tensors[source_index[i]]`` to ``tensors[destination_index[i]]``.  Same checks, errors and
+        submission; ``lmcache_musa_memcpy_batch_async`` uses it to hand its plan over without building
+        per-entry lists (this build's addition: the reference extension takes lists only)."""
+        if len(sizes) == 0:
+            return True
+        return self._launch(self._prepare_columns(tensors, destination_index, source_index, destination_offsets,
+                                                  source_offsets, sizes), mode=1 if prefer_overlap_with_compute else 0)
 
 
 def load_lmcache_musa_batch_copy_ext() -> Any | None:

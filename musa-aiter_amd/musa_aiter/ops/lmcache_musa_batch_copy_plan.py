@@ -61,7 +61,14 @@ def _is_int(value: object) -> bool:
     return isinstance(value, int) and not isinstance(value, bool)
 
 
-def _column(name: str, values: Sequence[int], count: int) -> tuple[int, ...]:
+def _column(name: str, values: Sequence[int] | np.ndarray, count: int,
+            arrays: bool = False) -> tuple[int, ...] | np.ndarray:
+    # Capacities may also come as a 1-D int64 array (the submission path computes them that way); the
+    # reference's inputs are sequences of ints, and other arrays fail its integer check as there.
+    if arrays and isinstance(values, np.ndarray) and values.dtype == np.int64 and values.ndim == 1:
+        if values.shape[0] != count:
+            raise ValueError(f"{name} must have the same length as sizes")
+        return values
     column = tuple(values)
     if len(column) != count:
         raise ValueError(f"{name} must have the same length as sizes")
@@ -75,6 +82,8 @@ def _key_column(values: Sequence[Hashable] | None, count: int) -> tuple[Hashable
     keys = tuple(range(count)) if values is None else tuple(values)
     if len(keys) != count:
         raise ValueError("destination_keys must have the same length as sizes")
+    if set(map(type, keys)) <= {int}:
+        return keys
     try:
         for key in keys:
             hash(key)
@@ -103,12 +112,23 @@ _ENTRY_RULES: tuple[tuple[_Rule, Callable[[int], str]], ...] = (
 _LIMIT = 1 << 61
 
 
-def _as_int64(columns: Sequence[tuple[int, ...]]) -> list[np.ndarray] | None:
-    arrays = []
+def _as_int64(columns: Sequence[tuple[int, ...] | np.ndarray]) -> list[np.ndarray] | None:
+    arrays: list[np.ndarray] = []
     for column in columns:
-        if column and (max(column) >= _LIMIT or min(column) <= -_LIMIT):
+        done = [a for c, a in zip(columns, arrays) if c is column]
+        if done:  # the same column twice (host offsets defaulting to copy offsets)
+            arrays.append(done[0])
+            continue
+        if isinstance(column, np.ndarray):
+            array = column
+        else:
+            try:
+                array = np.fromiter(column, dtype=np.int64, count=len(column))
+            except OverflowError:
+                return None
+        if len(column) and (int(array.max()) >= _LIMIT or int(array.min()) <= -_LIMIT):
             return None
-        arrays.append(np.fromiter(column, dtype=np.int64, count=len(column)))
+        arrays.append(array)
     return arrays
 
 
@@ -204,8 +224,8 @@ def plan_columns(
     count = len(sizes)
     zeros = (0,) * count
     n = _column("sizes", sizes, count)
-    src_cap = _column("source_capacities", source_capacities, count)
-    dst_cap = _column("destination_capacities", destination_capacities, count)
+    src_cap = _column("source_capacities", source_capacities, count, arrays=True)
+    dst_cap = _column("destination_capacities", destination_capacities, count, arrays=True)
     src_off = _column("source_offsets", zeros if source_offsets is None else source_offsets, count)
     dst_off = _column("destination_offsets", zeros if destination_offsets is None else destination_offsets, count)
     # The host side of the copy registers its memory: by default its registration offsets are its
@@ -217,6 +237,9 @@ def plan_columns(
 
     columns = (n, src_off, dst_off, host_off, src_cap, dst_cap)
     arrays = None if pin_chunk_size is not None and pin_chunk_size >= _LIMIT else _as_int64(columns)
+    if arrays is None:
+        n, src_off, dst_off, host_off, src_cap, dst_cap = columns = tuple(
+            tuple(c.tolist()) if isinstance(c, np.ndarray) else c for c in columns)
     _check_rules(columns, arrays)
     if arrays is None:
         _reject_overlaps_scalar(dst_off, n, keys)

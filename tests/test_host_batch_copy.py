@@ -200,21 +200,30 @@ def test_column_plan_matches_per_entry_rules(seed):
         k = (j + 1) % n
         keys[k], dst_off[k] = keys[j], dst_off[j] + sizes[j] // 2
         dst_cap[k] = max(dst_cap[k], dst_off[k] + sizes[k])
-    want = _plan_by_entry(sizes, src_cap, dst_cap, src_off, dst_off, host_off, pin, keys)
-    args = dict(direction="h2d", sizes=sizes, source_capacities=src_cap, destination_capacities=dst_cap,
-                source_offsets=src_off, destination_offsets=dst_off, host_registration_offsets=host_off,
-                pin_chunk_size=pin, destination_keys=keys)
-    if isinstance(want, str):
-        with pytest.raises(ValueError) as err:
-            batch._build_batch_copy_plan(**args)
-        assert str(err.value) == want
-        return
-    plan = batch._build_batch_copy_plan(**args)
-    got = [(e.input_index, e.source_offset, e.destination_offset, e.size, e.host_registration_offset)
-           for e in plan.entries]
-    assert got == want
-    assert plan.total_bytes == sum(sizes) and plan.input_entry_count == n
-    assert all(type(v) is int for e in plan.entries for v in (e.source_offset, e.size))
+    if seed % 4 == 1:  # host offsets left to default to the source offsets (one column used twice)
+        host_off = None
+    want = _plan_by_entry(sizes, src_cap, dst_cap, src_off, dst_off, src_off if host_off is None else host_off, pin,
+                          keys)
+    # Capacities as lists of ints and as int64 arrays (the submission path's form).
+    for caps in ((src_cap, dst_cap), (np.array(src_cap, dtype=np.int64), np.array(dst_cap, dtype=np.int64))):
+        args = dict(direction="h2d", sizes=sizes, source_capacities=caps[0], destination_capacities=caps[1],
+                    source_offsets=src_off, destination_offsets=dst_off, host_registration_offsets=host_off,
+                    pin_chunk_size=pin, destination_keys=keys)
+        if isinstance(want, str):
+            with pytest.raises(ValueError) as err:
+                batch._build_batch_copy_plan(**args)
+            assert str(err.value) == want
+            continue
+        plan = batch._build_batch_copy_plan(**args)
+        got = [(e.input_index, e.source_offset, e.destination_offset, e.size, e.host_registration_offset)
+               for e in plan.entries]
+        assert got == want
+        assert plan.total_bytes == sum(sizes) and plan.input_entry_count == n
+        assert all(type(v) is int for e in plan.entries for v in (e.source_offset, e.size))
+    with pytest.raises(ValueError, match="source_capacities must have the same length"):
+        batch._build_batch_copy_plan(**{**args, "source_capacities": np.zeros(n + 1, dtype=np.int64)})
+    with pytest.raises(ValueError, match="sizes must contain integers"):  # arrays: capacities only
+        batch._build_batch_copy_plan(**{**args, "sizes": np.array(sizes, dtype=np.int64)})
 
 
 @pytest.mark.parametrize("seed", range(30))
@@ -433,3 +442,79 @@ def test_extension_column_checks_match_per_entry_checks(monkeypatch, seed):
     assert to_gpu == h2d
     assert {id(t) for t in gpu_t} == {id(t) for t in (*dsts, *srcs) if id(t) in gpu_ids}
     assert {id(t) for t in host_t} == {id(t) for t in (*dsts, *srcs) if id(t) not in gpu_ids}
+
+
+def _distinct(dsts, srcs):
+    both = (*dsts, *srcs)
+    _, first, which = np.unique(np.array([id(t) for t in both], dtype=np.uint64), return_index=True,
+                                return_inverse=True)
+    return [both[i] for i in first], which[:len(dsts)], which[len(dsts):]
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_column_submission_matches_list_submission(monkeypatch, seed):
+    # The public call hands this package's extension its plan as columns (execute_batch_copy_columns);
+    # any other extension object gets the reference's lists.  Both must submit the same
+    # (destination address, source address, size) groups, or raise the same first error.
+    monkeypatch.setenv("MUSA_AITER_LMCACHE_BATCH_COPY", "1")
+    rng = np.random.default_rng(3000 + seed)
+    h2d = bool(seed % 2)
+    hosts = [torch.zeros(int(rng.integers(8, 64)) * 64, dtype=torch.uint8) for _ in range(3)]
+    gpus = [torch.zeros(int(rng.integers(8, 64)) * 64, dtype=torch.uint8) for _ in range(3)]
+    gpu_ids = {id(t) for t in gpus}
+    monkeypatch.setattr(ext, "_gpu", lambda t: id(t) in gpu_ids)
+    monkeypatch.setattr(batch, "_tensor_device_kind", lambda t: "gpu" if id(t) in gpu_ids else "cpu")
+    n = int(rng.integers(1, 200))
+    dsts, srcs, d_offs, s_offs, sizes, cursor = [], [], [], [], [], {}
+    for _ in range(n):
+        g, h = gpus[int(rng.integers(0, 3))], hosts[int(rng.integers(0, 3))]
+        dst, src = (g, h) if h2d else (h, g)
+        size = int(rng.integers(1, 40))
+        d_off = cursor.get(id(dst), 0)
+        if d_off + size > dst.numel():
+            continue
+        cursor[id(dst)] = d_off + size
+        dsts.append(dst)
+        srcs.append(src)
+        d_offs.append(d_off)
+        s_offs.append(int(rng.integers(0, src.numel() - size + 1)))
+        sizes.append(size)
+    pin = [None, 16, 24][seed % 3]
+    limit = int(rng.integers(1, 64))
+    if seed % 4 == 3 and len(dsts) > 1:  # the GPU side of one entry on a second (fake) device
+        other = torch.zeros(64, dtype=torch.uint8, device="meta")
+        monkeypatch.setattr(batch, "_tensor_device_kind", lambda t: "gpu" if id(t) in gpu_ids else "cpu")
+        gpu_ids.add(id(other))
+        j = int(rng.integers(0, len(dsts)))
+        if h2d:
+            dsts[j], d_offs[j] = other, 0
+        else:
+            srcs[j], s_offs[j] = other, 0
+        sizes[j] = min(sizes[j], 64)
+
+    class Lists(_Recorder):
+        def execute_batch_copy(self, d, s, do, so, sz, overlap):
+            dd, ss, nn, to_gpu, _, _, _ = ext.HipBatchCopyExtension._prepare(d, s, do, so, sz)
+            self.calls.append((dd.tolist(), ss.tolist(), nn.tolist(), to_gpu))
+            return True
+
+    launched = []
+    monkeypatch.setattr(ext.HipBatchCopyExtension, "_launch",
+                        lambda self, p, mode: launched.append((p[0].tolist(), p[1].tolist(), p[2].tolist(), p[3]))
+                        or True)
+
+    def run(extension):
+        monkeypatch.setattr(batch, "load_lmcache_musa_batch_copy_ext", lambda: extension)
+        try:
+            return batch.lmcache_musa_memcpy_batch_async(
+                dsts, srcs, sizes, destination_offsets=d_offs, source_offsets=s_offs, require_pinned_host=False,
+                host_registration_offsets=None, pin_chunk_size=pin, max_batch_entries=limit)
+        except (RuntimeError, ValueError) as exc:
+            return type(exc), str(exc)
+
+    lists = Lists()
+    want = run(lists)
+    got = run(ext.HipBatchCopyExtension())
+    assert got == want
+    assert launched == lists.calls
+    assert want is not True or sum(len(c[2]) for c in launched) >= len(sizes)
