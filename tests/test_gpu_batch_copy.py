@@ -284,3 +284,44 @@ def test_batch_alternating_between_host_allocations(direction):
     assert np.array_equal(dev.cpu().numpy(), want_dev)
     for h, w in zip(hosts, want_hosts):
         assert np.array_equal(h.numpy(), w)
+
+
+@pytest.mark.parametrize("direction", ["h2d", "d2h"])
+@pytest.mark.parametrize("pin,limit", [(None, 37), (4096, 64), (1000, 1 << 20)])
+def test_many_tensors_in_groups_match_oracle(direction, pin, limit):
+    # Entries spread over three device and three pinned host tensors, cut at registration boundaries
+    # and sent in groups of `limit` pieces: the public call hands each group to the extension as
+    # columns over the batch's distinct tensors.
+    rng = np.random.default_rng(500 + (pin or 0) + limit + (1 if direction == "d2h" else 0))
+    devs = [torch.randint(0, 256, (int(n),), dtype=torch.uint8, device=DEV) for n in rng.integers(40_000, 90_000, 3)]
+    hosts = [_host(int(n), seed=int(k)) for k, n in enumerate(rng.integers(40_000, 90_000, 3))]
+    dst_side, src_side = (devs, hosts) if direction == "h2d" else (hosts, devs)
+    before = [t.cpu().numpy().copy() for t in dst_side]
+    srcs_np = [t.cpu().numpy() for t in src_side]
+    dsts, srcs, sizes, d_off, s_off = [], [], [], [], []
+    cursor = [0] * 3
+    while len(sizes) < 300:
+        i, j = int(rng.integers(0, 3)), int(rng.integers(0, 3))
+        size = int(rng.integers(1, 3000))
+        if cursor[i] + size > dst_side[i].numel():
+            break
+        dsts.append(dst_side[i])
+        srcs.append(src_side[j])
+        d_off.append(cursor[i])
+        s_off.append(int(rng.integers(0, src_side[j].numel() - size + 1)))
+        sizes.append(size)
+        cursor[i] += size + int(rng.integers(0, 64))
+    order = rng.permutation(len(sizes))  # the batch is unordered
+    pick = lambda xs: [xs[k] for k in order]
+    dsts, srcs, sizes, d_off, s_off = pick(dsts), pick(srcs), pick(sizes), pick(d_off), pick(s_off)
+    host_off = s_off if direction == "h2d" else d_off
+    torch.cuda.synchronize()
+    assert musa_aiter.lmcache_musa_memcpy_batch_async(dsts, srcs, sizes, destination_offsets=d_off,
+                                                      source_offsets=s_off, host_registration_offsets=host_off,
+                                                      pin_chunk_size=pin, max_batch_entries=limit)
+    torch.cuda.synchronize()
+    index = {id(t): k for k, t in enumerate(dst_side)}
+    sindex = {id(t): k for k, t in enumerate(src_side)}
+    bo.apply_batch([before[index[id(t)]] for t in dsts], [srcs_np[sindex[id(t)]] for t in srcs], sizes, d_off, s_off)
+    for got, want in zip(dst_side, before):
+        assert np.array_equal(got.cpu().numpy(), want)
