@@ -33,6 +33,7 @@ from typing import Protocol, Sequence
 import numpy as np
 import torch
 
+from . import _hip
 from .kv_backend import KVBackendCapabilities, KVBackendDecision, select_kv_backend
 from .kv_transfer_plan import KVTransferPlan
 from .lmcache_musa_batch_copy_ext import HipBatchCopyExtension, lmcache_musa_batch_copy_requested
@@ -189,11 +190,25 @@ def lmcache_musa_memcpy_batch_async(
     if endpoints is None:
         return False
     capacity = np.array([t.numel() * t.element_size() for t in tensors], dtype=np.int64)
+    # The columns go to the plan as int64 arrays made here or as tuples that it checks item by item (so
+    # a caller's own array is rejected as the reference rejects it).  When the backend is asked for,
+    # its host helper must load and reads the caller's lists of ints; a list it declines (an item
+    # that is not a plain int, or a large one) stays a tuple.
+    column = _hip.host().int64_column if lmcache_musa_batch_copy_requested() else None
+
+    def own(values):
+        packed = None if values is None or column is None else column(values)
+        if packed is not None:
+            return np.frombuffer(packed, dtype=np.int64)
+        return None if values is None else tuple(values)
+
+    sizes_in, offsets_in = own(sizes), [own(v) for v in (source_offsets, destination_offsets,
+                                                         host_registration_offsets)]
     plan = _plan_columns(
-        direction=endpoints.direction, sizes=sizes, source_capacities=capacity[src_index],
-        destination_capacities=capacity[dst_index], source_offsets=source_offsets,
-        destination_offsets=destination_offsets, host_registration_offsets=host_registration_offsets,
-        pin_chunk_size=pin_chunk_size, destination_keys=dst_index.tolist())
+        direction=endpoints.direction, sizes=sizes_in, source_capacities=capacity[src_index],
+        destination_capacities=capacity[dst_index], source_offsets=offsets_in[0], destination_offsets=offsets_in[1],
+        host_registration_offsets=offsets_in[2], pin_chunk_size=pin_chunk_size,
+        destination_keys=dst_index.astype(np.int64), int64_arrays=True)
     extension = _extension_if_requested(need_batch=True)
     if extension is None:
         return False

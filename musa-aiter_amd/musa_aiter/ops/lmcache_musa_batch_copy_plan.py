@@ -63,8 +63,8 @@ def _is_int(value: object) -> bool:
 
 def _column(name: str, values: Sequence[int] | np.ndarray, count: int,
             arrays: bool = False) -> tuple[int, ...] | np.ndarray:
-    # Capacities may also come as a 1-D int64 array (the submission path computes them that way); the
-    # reference's inputs are sequences of ints, and other arrays fail its integer check as there.
+    # With ``arrays`` (the submission path) a column may come as a 1-D int64 array, taken as it is; the
+    # reference's inputs are sequences of ints, and arrays elsewhere fail its integer check as there.
     if arrays and isinstance(values, np.ndarray) and values.dtype == np.int64 and values.ndim == 1:
         if values.shape[0] != count:
             raise ValueError(f"{name} must have the same length as sizes")
@@ -78,7 +78,12 @@ def _column(name: str, values: Sequence[int] | np.ndarray, count: int,
     return column
 
 
-def _key_column(values: Sequence[Hashable] | None, count: int) -> tuple[Hashable, ...]:
+def _key_column(values: Sequence[Hashable] | np.ndarray | None, count: int,
+                arrays: bool = False) -> tuple[Hashable, ...] | np.ndarray:
+    if arrays and isinstance(values, np.ndarray) and values.dtype == np.int64 and values.ndim == 1:
+        if values.shape[0] != count:
+            raise ValueError("destination_keys must have the same length as sizes")
+        return values
     keys = tuple(range(count)) if values is None else tuple(values)
     if len(keys) != count:
         raise ValueError("destination_keys must have the same length as sizes")
@@ -154,8 +159,10 @@ def _check_rules(columns: Sequence[tuple[int, ...]], arrays: list[np.ndarray] | 
 def _reject_overlaps(destination_offsets: np.ndarray, sizes: np.ndarray, keys: Sequence[Hashable]) -> None:
     """Sorted by (destination, start), any two overlapping ranges of one destination include an
     adjacent overlapping pair, so one comparison of neighbours finds them."""
-    if set(map(type, keys)) <= {int} and (not keys or (max(keys) < 1 << 63 and min(keys) >= -(1 << 63))):
-        groups = np.fromiter(keys, dtype=np.int64, count=len(keys))  # integer keys (object ids) group as they are
+    if isinstance(keys, np.ndarray):
+        groups = keys  # int64 keys (tensor indices) group as they are
+    elif set(map(type, keys)) <= {int} and (not keys or (max(keys) < 1 << 63 and min(keys) >= -(1 << 63))):
+        groups = np.fromiter(keys, dtype=np.int64, count=len(keys))  # so do integer keys
     else:
         group: dict[Hashable, int] = {}
         groups = np.fromiter((group.setdefault(k, len(group)) for k in keys), dtype=np.int64, count=len(keys))
@@ -215,25 +222,29 @@ def plan_columns(
     host_registration_offsets: Sequence[int] | None = None,
     pin_chunk_size: int | None = None,
     destination_keys: Sequence[Hashable] | None = None,
+    int64_arrays: bool = False,
 ) -> PlanColumns:
-    """``build_batch_copy_plan``'s checks and split, returned as int64 columns."""
+    """``build_batch_copy_plan``'s checks and split, returned as int64 columns.  With ``int64_arrays``
+    any column (and the keys) may also be a 1-D int64 array."""
     if direction not in ("h2d", "d2h"):
         raise ValueError("direction must be 'h2d' or 'd2h'")
     if pin_chunk_size is not None and not (_is_int(pin_chunk_size) and pin_chunk_size > 0):
         raise ValueError("pin_chunk_size must be a positive integer")
     count = len(sizes)
-    zeros = (0,) * count
-    n = _column("sizes", sizes, count)
-    src_cap = _column("source_capacities", source_capacities, count, arrays=True)
-    dst_cap = _column("destination_capacities", destination_capacities, count, arrays=True)
-    src_off = _column("source_offsets", zeros if source_offsets is None else source_offsets, count)
-    dst_off = _column("destination_offsets", zeros if destination_offsets is None else destination_offsets, count)
+    zeros = np.zeros(count, dtype=np.int64) if int64_arrays else (0,) * count
+    n = _column("sizes", sizes, count, int64_arrays)
+    src_cap = _column("source_capacities", source_capacities, count, int64_arrays)
+    dst_cap = _column("destination_capacities", destination_capacities, count, int64_arrays)
+    src_off = _column("source_offsets", zeros if source_offsets is None else source_offsets, count, int64_arrays)
+    dst_off = _column("destination_offsets", zeros if destination_offsets is None else destination_offsets, count,
+                      int64_arrays)
     # The host side of the copy registers its memory: by default its registration offsets are its
     # copy offsets (the source of an h2d batch, the destination of a d2h one).
     host_off = _column("host_registration_offsets",
                        (src_off if direction == "h2d" else dst_off) if host_registration_offsets is None
-                       else host_registration_offsets, count)
-    keys = _key_column(destination_keys, count)
+                       else host_registration_offsets, count, int64_arrays)
+    keys = _key_column(destination_keys, count, int64_arrays)
+    total = sum(n.tolist() if isinstance(n, np.ndarray) else n)
 
     columns = (n, src_off, dst_off, host_off, src_cap, dst_cap)
     arrays = None if pin_chunk_size is not None and pin_chunk_size >= _LIMIT else _as_int64(columns)
@@ -250,12 +261,12 @@ def plan_columns(
         so_, do_, ho_ = ([c[i] + s for i, s in zip(index.tolist(), start)] for c in (src_off, dst_off, host_off))
         length = [p[2] for p in pieces]
         as_obj = (lambda v: np.array(v, dtype=object))
-        return PlanColumns(direction, index, as_obj(so_), as_obj(do_), as_obj(length), as_obj(ho_), sum(n), count)
+        return PlanColumns(direction, index, as_obj(so_), as_obj(do_), as_obj(length), as_obj(ho_), total, count)
     n_a, so_a, do_a, ho_a = arrays[:4]
     _reject_overlaps(do_a, n_a, keys)
     index, start, length = _split(n_a, ho_a, pin_chunk_size)
     return PlanColumns(direction, index, so_a[index] + start, do_a[index] + start, length, ho_a[index] + start,
-                       sum(n), count)
+                       total, count)
 
 
 def build_batch_copy_plan(

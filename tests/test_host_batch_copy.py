@@ -16,6 +16,7 @@ import torch
 import musa_aiter
 from musa_aiter.ops import lmcache_musa_batch_copy as batch
 from musa_aiter.ops import lmcache_musa_batch_copy_ext as ext
+from musa_aiter.ops.lmcache_musa_batch_copy_plan import plan_columns
 from oracle import batch_copy_oracle as bo
 
 
@@ -204,26 +205,37 @@ def test_column_plan_matches_per_entry_rules(seed):
         host_off = None
     want = _plan_by_entry(sizes, src_cap, dst_cap, src_off, dst_off, src_off if host_off is None else host_off, pin,
                           keys)
-    # Capacities as lists of ints and as int64 arrays (the submission path's form).
-    for caps in ((src_cap, dst_cap), (np.array(src_cap, dtype=np.int64), np.array(dst_cap, dtype=np.int64))):
-        args = dict(direction="h2d", sizes=sizes, source_capacities=caps[0], destination_capacities=caps[1],
-                    source_offsets=src_off, destination_offsets=dst_off, host_registration_offsets=host_off,
-                    pin_chunk_size=pin, destination_keys=keys)
-        if isinstance(want, str):
-            with pytest.raises(ValueError) as err:
-                batch._build_batch_copy_plan(**args)
-            assert str(err.value) == want
-            continue
+    args = dict(direction="h2d", sizes=sizes, source_capacities=src_cap, destination_capacities=dst_cap,
+                source_offsets=src_off, destination_offsets=dst_off, host_registration_offsets=host_off,
+                pin_chunk_size=pin, destination_keys=keys)
+    if isinstance(want, str):
+        with pytest.raises(ValueError) as err:
+            batch._build_batch_copy_plan(**args)
+        assert str(err.value) == want
+    else:
         plan = batch._build_batch_copy_plan(**args)
         got = [(e.input_index, e.source_offset, e.destination_offset, e.size, e.host_registration_offset)
                for e in plan.entries]
         assert got == want
         assert plan.total_bytes == sum(sizes) and plan.input_entry_count == n
         assert all(type(v) is int for e in plan.entries for v in (e.source_offset, e.size))
+    # The submission path's form: every column that fits int64 as an int64 array, the keys too.
+    as_arrays = {k: (np.array(v, dtype=np.int64) if isinstance(v, list) and all(abs(x) < 1 << 62 for x in v) else v)
+                 for k, v in args.items()}
+    if isinstance(want, str):
+        with pytest.raises(ValueError) as err:
+            plan_columns(**as_arrays, int64_arrays=True)
+        assert str(err.value) == want
+    else:
+        c = plan_columns(**as_arrays, int64_arrays=True)
+        got = list(zip(c.input_index.tolist(), c.source_offset.tolist(), c.destination_offset.tolist(),
+                       c.size.tolist(), c.host_registration_offset.tolist()))
+        assert got == want and c.total_bytes == sum(sizes) and type(c.total_bytes) is int
     with pytest.raises(ValueError, match="source_capacities must have the same length"):
-        batch._build_batch_copy_plan(**{**args, "source_capacities": np.zeros(n + 1, dtype=np.int64)})
-    with pytest.raises(ValueError, match="sizes must contain integers"):  # arrays: capacities only
-        batch._build_batch_copy_plan(**{**args, "sizes": np.array(sizes, dtype=np.int64)})
+        plan_columns(**{**as_arrays, "source_capacities": np.zeros(n + 1, dtype=np.int64)}, int64_arrays=True)
+    for name in ("sizes", "source_capacities"):  # arrays only where the submission path asks for them
+        with pytest.raises(ValueError, match=f"{name} must contain integers"):
+            batch._build_batch_copy_plan(**{**args, name: np.array(args[name], dtype=np.int64)})
 
 
 @pytest.mark.parametrize("seed", range(30))
@@ -306,6 +318,18 @@ def test_submission_validation(monkeypatch):
         batch.lmcache_musa_memcpy_batch_async([destination], [source, source], [8], require_pinned_host=False)
     with pytest.raises(TypeError, match="torch.Tensor"):
         batch.lmcache_musa_memcpy_batch_async([destination], [b"x"], [8], require_pinned_host=False)
+    # Offsets must be Python ints, as in the reference: not a numpy array, not bools (gate on and off).
+    for gate in ("1", "0"):
+        monkeypatch.setenv("MUSA_AITER_LMCACHE_BATCH_COPY", gate)
+        with pytest.raises(ValueError, match="destination_offsets must contain integers"):
+            batch.lmcache_musa_memcpy_batch_async([destination], [source], [8], require_pinned_host=False,
+                                                  destination_offsets=np.zeros(1, dtype=np.int64))
+        with pytest.raises(ValueError, match="source_offsets must contain integers"):
+            batch.lmcache_musa_memcpy_batch_async([destination], [source], [8], require_pinned_host=False,
+                                                  source_offsets=[False])
+        with pytest.raises(ValueError, match="sizes must contain integers"):
+            batch.lmcache_musa_memcpy_batch_async([destination], [source], np.array([8]), require_pinned_host=False)
+    monkeypatch.setenv("MUSA_AITER_LMCACHE_BATCH_COPY", "1")
     with pytest.raises(ValueError, match="contiguous"):
         batch.lmcache_musa_memcpy_batch_async([torch.zeros(4, 4).t()], [source], [8], require_pinned_host=False)
     with pytest.raises(ValueError, match="host registration boundary"):
@@ -518,3 +542,21 @@ def test_column_submission_matches_list_submission(monkeypatch, seed):
     assert got == want
     assert launched == lists.calls
     assert want is not True or sum(len(c[2]) for c in launched) >= len(sizes)
+
+
+def test_host_helper_reads_plain_int_lists_only():
+    # The helper that reads the caller's lists into int64 columns takes lists and tuples of plain ints
+    # within (-2^61, 2^61) and declines everything else, which the plan then checks item by item.
+    from musa_aiter.ops import _hip
+    column = _hip.host().int64_column
+    values = [0, -5, 7, (1 << 61) - 1, -(1 << 61) + 1]
+    assert np.frombuffer(column(values), dtype=np.int64).tolist() == values
+    assert np.frombuffer(column(tuple(values)), dtype=np.int64).tolist() == values
+    assert column([]) == b""
+
+    class Sub(int):
+        pass
+
+    for declined in ([1 << 61], [-(1 << 61)], [1 << 70], [True], [np.int64(1)], [Sub(3)], [1, 2.0], range(3),
+                     np.arange(3)):
+        assert column(declined) is None, declined
