@@ -8,6 +8,8 @@
 // MI355X).  These helpers do the same checks in one C++ pass and return the
 // addresses packed as uint64 values for the C ABI of libmusa_aiter_kv_hip.so.
 // The Python layer keeps every message and the order in which the checks fail.
+// For host <-> device copy batches, int64_column reads the caller's lists of
+// offsets and sizes (thousands of ints) into int64 columns.
 #include <torch/extension.h>
 
 #include <cstdint>
