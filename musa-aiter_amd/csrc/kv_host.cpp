@@ -9,10 +9,12 @@
 // addresses packed as uint64 values for the C ABI of libmusa_aiter_kv_hip.so.
 // The Python layer keeps every message and the order in which the checks fail.
 // For host <-> device copy batches, int64_column reads the caller's lists of
-// offsets and sizes (thousands of ints) into int64 columns.
+// offsets and sizes (thousands of ints) into int64 columns and object_index
+// numbers the few distinct tensors its entries name.
 #include <torch/extension.h>
 
 #include <cstdint>
+#include <unordered_map>
 #include <vector>
 
 namespace py = pybind11;
@@ -91,6 +93,38 @@ py::object int64_column(const py::handle& items) {
   return py::bytes(reinterpret_cast<const char*>(v.data()), v.size() * sizeof(int64_t));
 }
 
+// For the items of `first` and then `second` (lists or tuples), the index of each among their distinct
+// objects by identity, numbered in order of first appearance, packed as int64, and the list of those
+// objects.  A copy batch names a few tensors thousands of times; this replaces reading every id()
+// into numpy and sorting them.
+py::tuple object_index(const py::handle& first, const py::handle& second) {
+  for (const py::handle& seq : {first, second})
+    if (!PyList_Check(seq.ptr()) && !PyTuple_Check(seq.ptr())) throw py::type_error("expected a list or tuple");
+  const Py_ssize_t n1 = PySequence_Fast_GET_SIZE(first.ptr()), n2 = PySequence_Fast_GET_SIZE(second.ptr());
+  std::vector<int64_t> index;
+  index.reserve(static_cast<size_t>(n1 + n2));
+  std::unordered_map<PyObject*, int64_t> seen;
+  py::list distinct;
+  PyObject* last = nullptr;
+  int64_t last_index = -1;
+  for (const py::handle& seq : {first, second}) {
+    const Py_ssize_t n = PySequence_Fast_GET_SIZE(seq.ptr());
+    PyObject** const item = PySequence_Fast_ITEMS(seq.ptr());
+    for (Py_ssize_t i = 0; i < n; ++i) {
+      PyObject* const o = item[i];
+      if (o != last) {
+        const auto found = seen.emplace(o, static_cast<int64_t>(seen.size()));
+        if (found.second) distinct.append(py::reinterpret_borrow<py::object>(o));
+        last = o;
+        last_index = found.first->second;
+      }
+      index.push_back(last_index);
+    }
+  }
+  return py::make_tuple(py::bytes(reinterpret_cast<const char*>(index.data()), index.size() * sizeof(int64_t)),
+                        distinct);
+}
+
 }  // namespace
 
 PYBIND11_MODULE(_kv_host, m) {
@@ -98,6 +132,7 @@ PYBIND11_MODULE(_kv_host, m) {
   m.def("check_tensors", &check_tensors, py::arg("items"), py::arg("shape"), py::arg("like"));
   m.def("strided_table", &strided_table);
   m.def("int64_column", &int64_column, py::arg("items"));
+  m.def("object_index", &object_index, py::arg("first"), py::arg("second"));
   m.attr("OK") = static_cast<int>(kOk);
   m.attr("SHAPE") = static_cast<int>(kShape);
   m.attr("DTYPE") = static_cast<int>(kDtype);

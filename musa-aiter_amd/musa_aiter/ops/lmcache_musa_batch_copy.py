@@ -179,22 +179,28 @@ def lmcache_musa_memcpy_batch_async(
         return True
     if not len(destinations) == len(sources) == len(sizes):
         raise ValueError("destinations, sources, and sizes must have the same length")
-    # The batch's distinct objects (by identity) and each entry's index among them: one sort of object ids.
+    # The batch's distinct objects (by identity) and each entry's index among them.  When the backend is
+    # asked for, its host helper must load and numbers them; otherwise one sort of the object ids does.
     count = len(sizes)
-    both = (*destinations, *sources)
-    _, first, which = np.unique(np.fromiter(map(id, both), dtype=np.uint64, count=2 * count),
-                                return_index=True, return_inverse=True)
-    tensors = [both[i] for i in first.tolist()]
+    host = _hip.host() if lmcache_musa_batch_copy_requested() else None
+    if host is not None:
+        packed, tensors = host.object_index(destinations, sources)
+        which = np.frombuffer(packed, dtype=np.int64)
+    else:
+        both = (*destinations, *sources)
+        _, first, which = np.unique(np.fromiter(map(id, both), dtype=np.uint64, count=2 * count),
+                                    return_index=True, return_inverse=True)
+        tensors = [both[i] for i in first.tolist()]
     dst_index, src_index = which[:count], which[count:]
     endpoints = _classify(destinations, sources, dst_index * len(tensors) + src_index, require_pinned_host)
     if endpoints is None:
         return False
     capacity = np.array([t.numel() * t.element_size() for t in tensors], dtype=np.int64)
     # The columns go to the plan as int64 arrays made here or as tuples that it checks item by item (so
-    # a caller's own array is rejected as the reference rejects it).  When the backend is asked for,
-    # its host helper must load and reads the caller's lists of ints; a list it declines (an item
-    # that is not a plain int, or a large one) stays a tuple.
-    column = _hip.host().int64_column if lmcache_musa_batch_copy_requested() else None
+    # a caller's own array is rejected as the reference rejects it).  The host helper reads the
+    # caller's lists of ints; a list it declines (an item that is not a plain int, or a large one)
+    # stays a tuple.
+    column = None if host is None else host.int64_column
 
     def own(values):
         packed = None if values is None or column is None else column(values)

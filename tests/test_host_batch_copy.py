@@ -560,3 +560,18 @@ def test_host_helper_reads_plain_int_lists_only():
     for declined in ([1 << 61], [-(1 << 61)], [1 << 70], [True], [np.int64(1)], [Sub(3)], [1, 2.0], range(3),
                      np.arange(3)):
         assert column(declined) is None, declined
+
+
+def test_host_helper_numbers_distinct_objects_by_identity():
+    # Entries' objects numbered by identity in order of first appearance, destinations then sources;
+    # equal but distinct objects get their own numbers.
+    from musa_aiter.ops import _hip
+    index = _hip.host().object_index
+    a, b, c = torch.zeros(4), torch.zeros(4), torch.ones(2)
+    packed, distinct = index([b, a, b, b], (c, a, c, b))
+    assert np.frombuffer(packed, dtype=np.int64).tolist() == [0, 1, 0, 0, 2, 1, 2, 0]
+    assert [id(t) for t in distinct] == [id(b), id(a), id(c)]
+    packed, distinct = index([], [])
+    assert packed == b"" and distinct == []
+    with pytest.raises(TypeError):
+        index(iter([a]), [a])
