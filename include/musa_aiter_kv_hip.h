@@ -111,6 +111,30 @@ int musa_aiter_hip_copy_rows(const uint64_t* src_planes, const uint64_t* dst_pla
                              const int64_t* dst_idx, int64_t num_tokens, int64_t num_rows_out, int64_t src_offset,
                              int64_t dst_offset, int64_t src_rows, int64_t dst_rows, int64_t row_bytes,
                              int64_t src_stride, int64_t dst_stride, int zero_invalid, int dedupe, void* stream);
+/* musa_aiter_hip_copy_rows with its arguments in one struct (no reference counterpart; for the
+ * Python host layer, which fills the struct with one struct.pack instead of converting 18
+ * ctypes arguments, about 1.5 us less host time per call).  Fields as in musa_aiter_hip_copy_rows. */
+typedef struct musa_aiter_hip_copy_rows_call {
+  const uint64_t* src_planes;
+  const uint64_t* dst_planes;
+  const uint64_t* src_table;
+  const uint64_t* dst_table;
+  int64_t num_planes;
+  const int64_t* src_idx;
+  const int64_t* dst_idx;
+  int64_t num_tokens;
+  int64_t num_rows_out;
+  int64_t src_offset;
+  int64_t dst_offset;
+  int64_t src_rows;
+  int64_t dst_rows;
+  int64_t row_bytes;
+  int64_t src_stride;
+  int64_t dst_stride;
+  int32_t zero_invalid;
+  int32_t dedupe;
+} musa_aiter_hip_copy_rows_call;
+int musa_aiter_hip_copy_rows_packed(const musa_aiter_hip_copy_rows_call* call, void* stream);
 /* Row copies between two index-addressed plane sets (host arrays of plane bases).  A side
  * with page_rows > 0 is paged: row r sits at (r / page_rows) * page_stride + (r % page_rows) *
  * stride of its plane (the page-first [pages, layers, page, item] tensors of SGLang's direct

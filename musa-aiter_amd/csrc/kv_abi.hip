@@ -12,6 +12,7 @@
 // host layer needs (fill_skipped="preserve", merged layouts, non-contiguous
 // LMCache buffers, skip prefixes); the reference-named symbols are thin
 // wrappers over the same launchers.
+#include <cstring>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -612,6 +613,18 @@ int musa_aiter_hip_copy_rows(const uint64_t* src_planes, const uint64_t* dst_pla
     if (err != hipSuccess) return err;
   }
   return kvhip::launch_row_copy(p, as_stream(stream));
+}
+
+static_assert(sizeof(musa_aiter_hip_copy_rows_call) == 136, "the Python host layer packs 136 bytes");
+
+int musa_aiter_hip_copy_rows_packed(const musa_aiter_hip_copy_rows_call* call, void* stream) {
+  if (call == nullptr) return hipErrorInvalidValue;
+  musa_aiter_hip_copy_rows_call c;
+  std::memcpy(&c, call, sizeof c);  // the caller's buffer need not be aligned
+  return musa_aiter_hip_copy_rows(c.src_planes, c.dst_planes, c.src_table, c.dst_table, c.num_planes, c.src_idx,
+                                  c.dst_idx, c.num_tokens, c.num_rows_out, c.src_offset, c.dst_offset, c.src_rows,
+                                  c.dst_rows, c.row_bytes, c.src_stride, c.dst_stride, c.zero_invalid, c.dedupe,
+                                  stream);
 }
 
 // ----- paged-A copies (kv_transfer.py:350-376, :410-436, :480-508, :542-570) ----------------

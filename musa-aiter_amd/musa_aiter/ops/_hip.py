@@ -12,6 +12,7 @@ from __future__ import annotations
 import contextlib
 import ctypes
 import importlib.util
+import struct
 import sysconfig
 import threading
 from pathlib import Path
@@ -55,6 +56,7 @@ _SIGNATURES: dict[str, list] = {
         _i64, _i64, _i64,                        # row_bytes, src_stride, dst_stride
         _i32, _i32, _c_void_p,                   # zero_invalid, dedupe, stream
     ],
+    "musa_aiter_hip_copy_rows_packed": [ctypes.c_char_p, _c_void_p],  # musa_aiter_hip_copy_rows_call, stream
     "musa_aiter_hip_copy_rows_paged": [
         _u64p, _u64p, _i64,                      # host planes, planes
         _c_void_p, _c_void_p, _i64,              # src_idx, dst_idx, tokens
@@ -215,6 +217,19 @@ def ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
     return ctypes.c_void_p(0 if t is None else t.data_ptr())
 
 
+# musa_aiter_hip_copy_rows_call: four plane pointers, num_planes, two index pointers, nine int64
+# sizes and strides, two int32 flags (136 bytes, no padding).
+_COPY_ROWS_CALL = struct.Struct("<4Qq2Q9q2i")
+
+
+def _address(arr: ctypes.Array | None) -> int:
+    return 0 if arr is None else ctypes.addressof(arr)
+
+
+def _data(t: torch.Tensor | None) -> int:
+    return 0 if t is None else t.data_ptr()
+
+
 def u64_array(values) -> ctypes.Array:
     vals = [int(v) for v in values]
     return (ctypes.c_uint64 * max(1, len(vals)))(*vals)
@@ -296,14 +311,14 @@ def copy_rows(
         return
     src_arr = _as_u64(src_planes)
     dst_arr = _as_u64(dst_planes)
+    # One struct (musa_aiter_hip_copy_rows_call) instead of 18 converted ctypes arguments; the plane
+    # arrays stay referenced by src_arr / dst_arr until the call returns.
+    call = _COPY_ROWS_CALL.pack(
+        _address(src_arr), _address(dst_arr), _data(src_table), _data(dst_table), num_planes,
+        _data(src_idx), _data(dst_idx), num_tokens, num_rows_out, src_offset, dst_offset, src_rows, dst_rows,
+        row_bytes, src_stride, dst_stride, bool(zero_invalid), bool(dedupe))
     with on_device(device):
-        rc = fn("musa_aiter_hip_copy_rows")(
-            src_arr, dst_arr, ptr(src_table), ptr(dst_table), int(num_planes),
-            ptr(src_idx), ptr(dst_idx),
-            int(num_tokens), int(num_rows_out), int(src_offset), int(dst_offset), int(src_rows), int(dst_rows),
-            int(row_bytes), int(src_stride), int(dst_stride),
-            int(bool(zero_invalid)), int(bool(dedupe)), stream_ptr(device),
-        )
+        rc = fn("musa_aiter_hip_copy_rows_packed")(call, stream_ptr(device))
     check(rc, op)
 
 
