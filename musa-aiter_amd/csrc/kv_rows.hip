@@ -238,7 +238,13 @@ __global__ __launch_bounds__(kBlockThreads) void slot_row_kernel(const SlotRowAr
   const int lane = lane_id();
   const int plane = static_cast<int>(blockIdx.y);
   const int shift = a.units_shift;
-  const int64_t w = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave;
+  // A gather starts each plane one workgroup (4 KiB) further on.  Destination planes a power of two
+  // apart (256-token chunk views of a [2, NL, 4096, 1024] buffer: 8 MiB) otherwise have their
+  // resident workgroups write the same offsets of up to 16 planes at once, which made such a chunk
+  // 14 % slower (16.3 against 14.3 us); contiguous and other strides are unchanged, the batched
+  // gather 1.6 % faster.  Scatters keep the natural order (0.7 % slower rotated).
+  const uint32_t bx = SCATTER ? blockIdx.x : (blockIdx.x + blockIdx.y) % gridDim.x;
+  const int64_t w = static_cast<int64_t>(bx) * kWavesPerBlock + wave;
   const int64_t u = w >> shift;
   const int64_t part = (w - (u << shift)) << 10;
   const int64_t slot = a.idx[u < a.num_tokens ? u : a.num_tokens - 1];
