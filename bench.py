@@ -1213,6 +1213,84 @@ def cpu_baseline(slots_np: np.ndarray, kc: torch.Tensor, vc: torch.Tensor, sampl
     }
 
 
+def _pct(gbs: float) -> str:
+    return f"{gbs:.0f} GB/s {100.0 * gbs / HBM_PEAK_GBS:.1f}%"
+
+
+def _of(gbs: float, ceiling: float) -> str:
+    return f"{100.0 * gbs / ceiling:.0f}% of pattern {ceiling:.0f}"
+
+
+def summary_lines(line: dict) -> list[str]:
+    """The run's figures for every BASELINE config in a few short lines (under 1.5 KB in all): the end of
+    the output, where a log tail keeps them.  GB/s are algorithmic read+write bytes; % is of 8 TB/s;
+    'of pattern' is the kernel's fraction of the same-pattern block copy timed in this process."""
+    out = []
+    d, c, p = line["directions"], line["ceilings"], line.get("placements")
+    s2 = (f"cfg2 bf16 32L step {_pct(line['value'])} ({100.0 * line['value'] / c['step_ceiling_gbs']:.0f}% of "
+          f"{c['step_ceiling_gbs']:.0f}) | scatter {_pct(d['scatter']['gbs'])} "
+          f"{_of(d['scatter']['gbs'], c['scatter_pattern']['gbs'])} | gather {_pct(d['gather']['gbs'])} "
+          f"{_of(d['gather']['gbs'], c['gather_pattern']['gbs'])} | seq copy {c['sequential']['gbs']:.0f}")
+    if p:
+        s2 += f" | placements {p['step_gbs_min']:.0f}/{p['step_gbs_median']:.0f}/{p['step_gbs_max']:.0f}"
+    out.append(s2)
+    x = line.get("extra", {})
+    c1 = x.get("config1_fp16_single_layer_gather")
+    if c1:
+        us, fl = c1["gather"]["p50_ms"] * 1e3, c1["floor"]["gather_pattern"]["p50_ms"] * 1e3
+        out.append(f"cfg1 fp16 gather {us:.1f} us {_pct(c1['gather']['gbs'])} (floor {fl:.1f} us, "
+                   f"{100.0 * fl / us:.0f}%)")
+    c3 = x.get("config3_fp8")
+    if c3:
+        qp, dp = c3["ceilings"]["quant_store_pattern"]["gbs"], c3["ceilings"]["dequant_gather_pattern"]["gbs"]
+        parts = []
+        for name in ("e4m3_per_head", "e4m3_scalar", "e5m2_per_head"):
+            v = c3.get(name)
+            if v:
+                q, g = v["quant_store"]["gbs"], v["dequant_gather"]["gbs"]
+                parts.append(f"{name} quant {_pct(q)} ({100.0 * q / qp:.0f}%) dequant {_pct(g)} "
+                             f"({100.0 * g / dp:.0f}%)")
+        out.append(f"cfg3 fp8 [patterns quant {qp:.0f} dequant {dp:.0f}] " + " | ".join(parts))
+    c4 = x.get("config4_lmcache_two_x_nl")
+    if c4:
+        api, ce = c4["gather_per_chunk_call"], c4["gather_per_chunk_c_abi"]
+        fl = c4["per_chunk_floor_pattern_copy"]["p50_ms"] * 1e3
+        out.append(f"cfg4 2xNL chunk api {api['p50_ms'] * 1e3:.1f} us {_pct(api['gbs'])} | C entry "
+                   f"{ce['p50_ms'] * 1e3:.1f} us {_pct(ce['gbs'])} (floor {fl:.1f} us) | batched gather "
+                   f"{_pct(c4['gather_batched_16']['gbs'])} scatter {_pct(c4['scatter_batched_16']['gbs'])}")
+    c5 = x.get("config5_mla_rows")
+    if c5:
+        b = c5["bf16_576"]
+        out.append(f"cfg5 mla bf16 gather {_pct(b['gather']['gbs'])} "
+                   f"{_of(b['gather']['gbs'], b['ceilings']['gather_pattern']['gbs'])} | scatter "
+                   f"{_pct(b['scatter']['gbs'])} {_of(b['scatter']['gbs'], b['ceilings']['scatter_pattern']['gbs'])}"
+                   f" | fp8 656B rows {_pct(c5['fp8_656_rows']['gather']['gbs'])}")
+    nxt = []
+    for key, names in (("dense_preload_and_block_copies",
+                        (("load_and_reshape_flash", "dense load"), ("reshape_and_cache_back_flash", "write-back"),
+                         ("load_and_dequantize_fp8_flash_e4m3", "fp8 dense load"), ("triton_indexed_to_dense", "csr"),
+                         ("copy_paged_blocks_32_layers", "block copy"))),
+                       ("sglang_hicache_transfers", (("all_layer_lf_pf_backup", "hicache backup"),
+                                                     ("per_layer_pf_lf_load_x32", "hicache load")))):
+        v = x.get(key) or {}
+        nxt += [f"{label} {v[k]['gbs']:.0f}" for k, label in names if isinstance(v.get(k), dict)]
+    if nxt:
+        out.append("next rows GB/s: " + ", ".join(nxt))
+    parity = [bool(line.get("parity_roundtrip"))]
+    for v in x.values():
+        if isinstance(v, dict):
+            parity += [bool(w) for k, w in v.items() if k == "parity" and isinstance(w, bool)]
+            parity += [bool(w.get("parity")) for w in v.values() if isinstance(w, dict) and
+                       isinstance(w.get("parity"), bool)]
+    cpu = line.get("cpu_baseline")
+    tail = f"parity {'all ok' if all(parity) else 'FAILED'} ({len(parity)} checks)"
+    if cpu:
+        tail += f" | cpu baseline {cpu['value']:.2f} GB/s on {cpu['cores']} threads ({cpu['kind']})"
+    tail += f" | roofline frac {line['roofline']['frac']:.3f} ({line['roofline']['kernel']})"
+    out.append(tail)
+    return [f"[summary] {s}" for s in out]
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
@@ -1266,7 +1344,7 @@ def main() -> int:
             continue
         key, fn = runners[cfg]
         extra[key] = fn()
-        log(f"config {cfg}: {json.dumps(extra[key])}")
+        log(f"config {cfg} done")
         torch.cuda.empty_cache()
     achieved = c2["bytes_per_direction"] / (c2["dominant_avg_ms"] * 1e-3) / 1e9
     line = {
@@ -1305,6 +1383,8 @@ def main() -> int:
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
+    sys.stderr.write("\n".join(summary_lines(line)) + "\n")
+    sys.stderr.flush()
     return 0
 
 
