@@ -194,6 +194,19 @@ def pattern_copy_fn(src: torch.Tensor, dst: torch.Tensor, *, src_blocks, dst_blo
     return lambda: _check(fn(*args, _stream()), "block pattern copy")
 
 
+ROTATE = 6  # FP8 cache sets rotated through by the configs[2] timings (see bench_config3)
+
+
+def rotating(call, n: int):
+    """A callable that runs ``call(i)`` with i = 0, 1, .., n - 1, 0, .. on successive calls."""
+    state = [0]
+
+    def run():
+        call(state[0] % n)
+        state[0] += 1
+    return run
+
+
 def _run_all(fns):
     """One callable that launches ``fns`` in order."""
     def run():
@@ -453,14 +466,17 @@ def bench_config3() -> dict:
     kl, vl = kl.to(torch.bfloat16), vl.to(torch.bfloat16)
     amax_k = kl.float().abs().amax(dim=(0, 2))
     amax_v = vl.float().abs().amax(dim=(0, 2))
-    kc = torch.zeros((NB, NH, HD, BS), dtype=torch.uint8, device=dev)
-    vc = torch.zeros_like(kc)
+    # ROTATE cache sets (2 x 128 MiB each, 1.5 GiB in all) are written and read in turn, so that a timed call
+    # finds its cache in HBM and not in the 256 MB last-level cache left by the call before.
+    sets = [(torch.zeros((NB, NH, HD, BS), dtype=torch.uint8, device=dev),
+             torch.zeros((NB, NH, HD, BS), dtype=torch.uint8, device=dev)) for _ in range(ROTATE)]
+    kc, vc = sets[0]
     ok = torch.empty_like(kl)
     ov = torch.empty_like(vl)
     lib = _hip.library()
     nbytes = 2 * t * ROW * (2 + 1) + 8 * t
     sample = min(t, 2048)
-    out = {"tokens": t, "bytes_per_call": nbytes}
+    out = {"tokens": t, "bytes_per_call": nbytes, "cache_sets_rotated": ROTATE}
     variants = (("e4m3_per_head", "e4m3", 1, 448.0), ("e4m3_scalar", "e4m3", 0, 448.0),
                 ("e5m2_per_head", "e5m2", 1, 57344.0))
     for name, fmt, mode, fmax in variants:
@@ -472,12 +488,13 @@ def bench_config3() -> dict:
         d = _bind(lib, f"musa_aiter_kv_paged_fp8_to_linear_vec4_{fmt}", 7, 5)
         q.argtypes = q.argtypes[:-1] + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int]
         d.argtypes = d.argtypes[:-1] + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int]
-        qa = (kl.data_ptr(), vl.data_ptr(), slots.data_ptr(), kc.data_ptr(), vc.data_ptr(), ks.data_ptr(),
-              vs.data_ptr(), t, NB, NH, HD, BS, 2)
-        da = (kc.data_ptr(), vc.data_ptr(), slots.data_ptr(), ks.data_ptr(), vs.data_ptr(), ok.data_ptr(),
-              ov.data_ptr(), t, NB, NH, HD, BS, 2)
-        _check(q(*qa, _stream(), mode), name)
-        _check(d(*da, _stream(), mode), name)
+        qas = [(kl.data_ptr(), vl.data_ptr(), slots.data_ptr(), a.data_ptr(), b.data_ptr(), ks.data_ptr(),
+                vs.data_ptr(), t, NB, NH, HD, BS, 2) for a, b in sets]
+        das = [(a.data_ptr(), b.data_ptr(), slots.data_ptr(), ks.data_ptr(), vs.data_ptr(), ok.data_ptr(),
+                ov.data_ptr(), t, NB, NH, HD, BS, 2) for a, b in sets]
+        for qa in qas:
+            _check(q(*qa, _stream(), mode), name)
+        _check(d(*das[0], _stream(), mode), name)
         torch.cuda.synchronize()
         # Parity on a sample of tokens, outside the timed region (on the CPU): cache bytes vs the
         # reference encoder's steps in torch, dequantised rows vs its decoder (tests/torch_ref.py).
@@ -486,12 +503,16 @@ def bench_config3() -> dict:
         want = torch_ref.fp8_quantize(kl[:sample].cpu(), scale, fmt)
         want_deq = torch_ref.fp8_dequantize(want, scale, fmt, torch.bfloat16)
         parity = bool(torch.equal(got, want) and torch.equal(ok[:sample].cpu(), want_deq))
-        mq = batched_ms(lambda: _check(q(*qa, _stream(), mode), name))
-        md = batched_ms(lambda: _check(d(*da, _stream(), mode), name))
+        mq = batched_ms(rotating(lambda i: _check(q(*qas[i], _stream(), mode), name), ROTATE), launches=2 * ROTATE)
+        md = batched_ms(rotating(lambda i: _check(d(*das[i], _stream(), mode), name), ROTATE), launches=2 * ROTATE)
         qr, dr = rate(nbytes, mq, t), rate(nbytes, md, t)
         if name == "e4m3_per_head":
             qr["traffic"] = profiled_traffic("fp8_quant")
             dr["traffic"] = profiled_traffic("fp8_dequant")
+            # The same dequant-gather on one cache set, called back to back: its 256 MiB of codes stay in the
+            # last-level cache between calls (a cache re-read while resident), so this is not an HBM rate.
+            dr["one_cache_set_repeated"] = rate(nbytes, batched_ms(lambda: _check(d(*das[0], _stream(), mode),
+                                                                                  name)), t)
         out[name] = {"quant_store": qr, "dequant_gather": dr,
                      "scale_rule": f"amax/{fmax:g}" + (" per kv-head" if mode == 1 else " over all heads"),
                      "parity_sample_tokens": sample, "parity": parity,
@@ -507,18 +528,23 @@ def bench_config3() -> dict:
     lin_blk, cache_blk = ROW * BS * 2, ROW * BS
     ceil_bytes = 2 * nblk * (lin_blk + cache_blk)
     out["ceilings"] = {"blocks": nblk, "bytes_per_launch_pair": ceil_bytes}
-    for name, src_pair, dst_pair, sbytes, dbytes, sblocks, dblocks, sreg, dreg in (
-            ("quant_store_pattern", (kl, vl), (kc, vc), lin_blk, cache_blk, None, order, t // BS, NB),
-            ("dequant_gather_pattern", (kc, vc), (ok, ov), cache_blk, lin_blk, order, None, NB, t // BS)):
-        def make(wt, src_pair=src_pair, dst_pair=dst_pair, sbytes=sbytes, dbytes=dbytes, sblocks=sblocks,
-                 dblocks=dblocks, sreg=sreg, dreg=dreg):
-            return _run_all([pattern_copy_fn(a, b, src_blocks=sblocks, dst_blocks=dblocks, num_blocks=nblk,
-                                             src_region_blocks=sreg, dst_region_blocks=dreg, src_block_bytes=sbytes,
-                                             dst_block_bytes=dbytes, planes=1, src_plane_stride=0,
-                                             dst_plane_stride=0, write_through=wt)
-                             for a, b in zip(src_pair, dst_pair)])
+    for name, quant, sbytes, dbytes, sblocks, dblocks, sreg, dreg in (
+            ("quant_store_pattern", True, lin_blk, cache_blk, None, order, t // BS, NB),
+            ("dequant_gather_pattern", False, cache_blk, lin_blk, order, None, NB, t // BS)):
+        def make(wt, quant=quant, sbytes=sbytes, dbytes=dbytes, sblocks=sblocks, dblocks=dblocks, sreg=sreg,
+                 dreg=dreg):
+            per_set = []
+            for cache_pair in sets:
+                src_pair, dst_pair = ((kl, vl), cache_pair) if quant else (cache_pair, (ok, ov))
+                per_set.append(_run_all([pattern_copy_fn(a, b, src_blocks=sblocks, dst_blocks=dblocks,
+                                                         num_blocks=nblk, src_region_blocks=sreg,
+                                                         dst_region_blocks=dreg, src_block_bytes=sbytes,
+                                                         dst_block_bytes=dbytes, planes=1, src_plane_stride=0,
+                                                         dst_plane_stride=0, write_through=wt)
+                                         for a, b in zip(src_pair, dst_pair)]))
+            return rotating(lambda i: per_set[i](), ROTATE)
 
-        out["ceilings"][name] = pattern_rate(make, ceil_bytes)
+        out["ceilings"][name] = pattern_rate(make, ceil_bytes, launches=2 * ROTATE)
     log(f"config 3 ceilings: quant pattern {out['ceilings']['quant_store_pattern']['gbs']:.0f}, dequant pattern "
         f"{out['ceilings']['dequant_gather_pattern']['gbs']:.0f} GB/s")
     return out
@@ -764,26 +790,31 @@ def bench_dense() -> dict:
                                                            "unchanged"}
 
     # FP8 E4M3 per-head dequant-load into bf16, through the generic entry.
-    k8 = torch.randint(0, 256, (NB, NH, HD, BS), generator=gen, device=dev, dtype=torch.uint8)
-    v8 = k8.flip(0)
+    # ROTATE code sets, read in turn (as for configs[2]), so that each timed call reads its codes from HBM.
+    sets8 = [torch.randint(0, 256, (NB, NH, HD, BS), generator=gen, device=dev, dtype=torch.uint8)
+             for _ in range(ROTATE)]
+    sets8 = [(k8, k8.flip(0)) for k8 in sets8]
+    k8 = sets8[0][0]
     ks = torch.rand(NH, generator=gen, device=dev) + 0.01
     vs = torch.rand(NH, generator=gen, device=dev) + 0.01
     dq = _hip.fn("musa_aiter_hip_paged_dense_tiles")
-    qa = (0, 1, 1, 2, 2, k8.data_ptr(), v8.data_ptr(), dk.data_ptr(), dv.data_ptr(), tables.data_ptr(),
-          seq_lens.data_ptr(), batch, dense_len, max_blocks, NB, NH, HD, BS, ROW, ks.data_ptr(), vs.data_ptr(), 1,
-          1, 0)
-    _check(dq(*qa, _stream()), "fp8 dense load")
+    qas = [(0, 1, 1, 2, 2, a.data_ptr(), b.data_ptr(), dk.data_ptr(), dv.data_ptr(), tables.data_ptr(),
+            seq_lens.data_ptr(), batch, dense_len, max_blocks, NB, NH, HD, BS, ROW, ks.data_ptr(), vs.data_ptr(), 1,
+            1, 0) for a, b in sets8]
+    _check(dq(*qas[0], _stream()), "fp8 dense load")
     torch.cuda.synchronize()
     want = torch_ref.fp8_dequantize(rows_of(k8)[flat_slots], ks[None, :, None], "e4m3", torch.bfloat16)
     ok8 = bool(torch.equal(dk[mask], want) and not bool(dk[~mask].any()))
     del want
-    mq = batched_ms(lambda: _check(dq(*qa, _stream()), "fp8 dense load"), launches=5, reps=5)
+    mq = batched_ms(rotating(lambda i: _check(dq(*qas[i], _stream()), "fp8 dense load"), ROTATE),
+                    launches=2 * ROTATE, reps=5)
     nbytes = 2 * valid * ROW + 2 * batch * dense_len * row_b + idx_bytes + 2 * NH * 4
     out["load_and_dequantize_fp8_flash_e4m3"] = {**rate(nbytes, mq, valid), "bytes_per_call": nbytes, "parity": ok8,
                                                  "parity_check": "valid rows equal the reference decoder's value "
                                                                  "x per-head scale rounded to bf16 "
-                                                                 "(tests/torch_ref.py)"}
-    del k8, v8
+                                                                 "(tests/torch_ref.py)",
+                                                 "code_sets_rotated": ROTATE}
+    del k8, sets8
 
     # SGLang Triton-decode CSR indices over token-major caches [NB*BS, NH, HD].
     key_tok, val_tok = rows_of(kc).contiguous(), rows_of(vc).contiguous()
@@ -1250,7 +1281,8 @@ def summary_lines(line: dict) -> list[str]:
                 q, g = v["quant_store"]["gbs"], v["dequant_gather"]["gbs"]
                 parts.append(f"{name} quant {_pct(q)} ({100.0 * q / qp:.0f}%) dequant {_pct(g)} "
                              f"({100.0 * g / dp:.0f}%)")
-        out.append(f"cfg3 fp8 [patterns quant {qp:.0f} dequant {dp:.0f}] " + " | ".join(parts))
+        out.append(f"cfg3 fp8 ({c3.get('cache_sets_rotated', 1)} cache sets rotated) [patterns quant {qp:.0f} "
+                   f"dequant {dp:.0f}] " + " | ".join(parts))
     c4 = x.get("config4_lmcache_two_x_nl")
     if c4:
         api, ce = c4["gather_per_chunk_call"], c4["gather_per_chunk_c_abi"]

@@ -94,6 +94,11 @@ __device__ __forceinline__ u32x4 buf_ld16(buf_t r, uint32_t off) {
 __device__ __forceinline__ u32x4 buf_ld16(buf_t r, uint32_t off, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, kBufNT);
 }
+// Cached (default policy) load, for wave instructions that touch lines
+// partially and leave the rest of each line to later instructions.
+__device__ __forceinline__ u32x4 buf_ld16_cached(buf_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
 __device__ __forceinline__ void buf_st16(buf_t r, uint32_t off, u32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kBufNT);
 }

@@ -456,9 +456,12 @@ hipError_t dispatch_bs(const TileArgs& a, int64_t bs, bool fast, int64_t planes,
       if (bs == 16) return launch_tile<ELT_C, 16, SCATTER>(a, planes, stream);
       if (bs == 32) return launch_tile<ELT_C, 32, SCATTER>(a, planes, stream);
     } else if constexpr (!SCATTER) {
-      // FP8 dequant-gather: per-wave kernel (kv_paged_waves.hip).
-      if (bs == 16) return launch_wave_gather<ELT_C, ELT_L, CODEC, LDT, 16>(a, planes, stream);
-      if (bs == 32) return launch_wave_gather<ELT_C, ELT_L, CODEC, LDT, 32>(a, planes, stream);
+      // FP8 dequant-gather: per-wave kernel (kv_paged_waves.hip), unless a chunk
+      // of its rows spans more heads than its decode tables hold.
+      hipError_t err = hipErrorNotSupported;
+      if (bs == 16) err = launch_wave_gather<ELT_C, ELT_L, CODEC, LDT, 16>(a, planes, stream);
+      if (bs == 32) err = launch_wave_gather<ELT_C, ELT_L, CODEC, LDT, 32>(a, planes, stream);
+      if (err != hipErrorNotSupported) return err;
     } else {
       // FP8 quant-store: per-wave kernel (kv_paged_waves.hip).
       if (bs == 16) return launch_wave_scatter<ELT_C, ELT_L, CODEC, LDT, 16>(a, planes, stream);

@@ -1,18 +1,20 @@
-// Per-wave paged-A -> linear gather for MI355X (gfx950), used for the FP8
-// dequant-gather.
+// Per-wave paged-A <-> linear FP8 kernels for MI355X (gfx950): the
+// dequant-gather and the quant-store.
 //
-// One wave owns the runs (consecutive tokens in consecutive slots of one
-// block) that start in its 16-token tile, for one chunk of cache rows (grid z).
-// A chunk is 64 lane tiles of RPL rows x CG block columns, i.e. RPL KiB of
-// contiguous cache bytes: the cache side moves as RPL coalesced wave loads
-// (lane l takes piece k*64 + l), the pieces are exchanged through the wave's
-// private LDS region so that each lane holds an RPL x CG tile, and the lane
-// transposes its tile in registers while decoding (byte selects, decode,
-// scale, round), writing 16-byte pieces of token rows.  For one-byte cache
-// elements this needs RPL / (RPL * CG) = 1/16 LDS instruction per element,
-// against the 1 to 1.25 of the workgroup-cooperative kernel's column reads,
-// which makes it the faster dequant-gather.  Runs that do not cover every
-// column group of the block row use lane tiles directly and load only the
+// Dequant-gather.  One wave owns the runs (consecutive tokens in consecutive
+// slots of one block) that start in its 16-token tile, for one chunk of cache
+// rows (grid z).  A chunk is 64 lane tiles of RPL rows x CG block columns:
+// each lane loads its own tile, RPL 16-byte pieces of consecutive cache rows
+// (cached loads: a wave instruction touches 64 lines partially and the L2
+// serves the rest of each line to the next instructions), so the lane holds
+// RPL rows x CG tokens and writes 16-byte pieces of token rows.  Each code is
+// decoded by one LDS read from the workgroup's decode tables (value x scale
+// already rounded to the linear type), about 2.5 VALU instructions per
+// element against 16.8 for decoding, scaling and rounding in registers.  The
+// LDS holds only those tables (4 KiB), so the kernel's 66 VGPRs set its
+// occupancy.  Copies (no decode) stage the chunk through the wave's LDS
+// region instead: coalesced loads, exchanged so that each lane holds its tile.
+// Runs that do not cover every column group of the block row load only the
 // column groups they cover.
 #include "kv_hip_common.h"
 #include "kv_launch.h"
@@ -23,9 +25,11 @@ namespace kvhip {
 namespace {
 
 // d[q] holds 16 bytes of cache row (r0+q) for one column group; returns the
-// 16-byte linear piece (rows r0..r0+RPL-1) of block column `cc`.
-template <int ELT_C, int ELT_L, int CODEC, int LDT, int RPL>
-__device__ __forceinline__ u32x4 gather_column(const u32x4 (&d)[RPL], int cc, float sc) {
+// 16-byte linear piece (rows r0..r0+RPL-1) of block column `cc`.  FP8 codes
+// are decoded through `lut`, the lane's head's table of 256 linear-side
+// values (decode(code) * scale, rounded to the linear type).
+template <int ELT_C, int ELT_L, int CODEC, int RPL, typename LutT>
+__device__ __forceinline__ u32x4 gather_column(const u32x4 (&d)[RPL], int cc, const LutT* lut) {
   u32x4 o;
   if constexpr (CODEC == kCopy && ELT_C == 2) {
     static_assert(RPL == 8, "16-bit tiles are 8x8");
@@ -39,17 +43,36 @@ __device__ __forceinline__ u32x4 gather_column(const u32x4 (&d)[RPL], int cc, fl
     static_assert(ELT_C == 1, "fp8 caches hold one byte per element");
     if constexpr (ELT_L == 2) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t lo = f32_to_lin<LDT>(fp8_decode<CODEC>(elem8(d[2 * k], cc)) * sc);
-        const uint32_t hi = f32_to_lin<LDT>(fp8_decode<CODEC>(elem8(d[2 * k + 1], cc)) * sc);
-        o[k] = pack16(lo, hi);
-      }
+      for (int k = 0; k < 4; ++k) o[k] = pack16(lut[elem8(d[2 * k], cc)], lut[elem8(d[2 * k + 1], cc)]);
     } else {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) o[k] = __float_as_uint(fp8_decode<CODEC>(elem8(d[k], cc)) * sc);
+      for (int k = 0; k < 4; ++k) o[k] = lut[elem8(d[k], cc)];
     }
   }
   return o;
+}
+
+// Decoded-value tables of the FP8 dequant-gather, built once per workgroup in
+// LDS: entry (j, code) holds the linear-side bits of decode(code) * scale of
+// head h_lo + j (for a scalar scale, one table), computed by the same scalar
+// steps as the per-element decode (fp8_decode, fp32 multiply, f32_to_lin), so
+// a lookup returns exactly what decoding the element would.  A chunk spans at
+// most kLutHeads heads at the shapes this kernel serves (head_dim >= 64);
+// chunks spanning more decode per element.
+constexpr int kLutHeads = 8;
+
+template <int ELT_L>
+struct LutEntry {
+  using T = uint32_t;
+};
+template <>
+struct LutEntry<2> {
+  using T = uint16_t;
+};
+
+template <int CODEC, int LDT, typename T>
+__device__ __forceinline__ T lut_value(uint32_t code, float sc) {
+  return static_cast<T>(f32_to_lin<LDT>(fp8_decode<CODEC>(code) * sc));
 }
 
 // Piece s of a chunk lives at LDS slot lds_slot(s): the low four bits are
@@ -81,30 +104,51 @@ struct WaveShape {
   static_assert(BS % CG == 0, "block row must be a whole number of 16-byte groups");
 };
 
-template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS>
+// STP: cache-policy bits of the full runs' linear stores (kBufWT when every
+// linear row is whole 128-byte lines).
+template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS, int STP>
 __global__ __launch_bounds__(kBlockThreads) void paged_wave_gather_kernel(const TileArgs a) {
   using W = WaveShape<ELT_C, ELT_L, BS>;
   constexpr int RPL = W::RPL, CG = W::CG, NCG = W::NCG, kChunkRows = W::kChunkRows;
   static_assert(kTileTokens + BS + 1 <= kWave, "run window must fit one wave");
-  __shared__ u32x4 lds_all[kWavesPerBlock * kWave * RPL];
+  using LutT = typename LutEntry<ELT_L>::T;
+  constexpr bool kLut = CODEC != kCopy;
+  // Full runs stage the chunk through LDS (copies) or load lane tiles
+  // directly (FP8, whose LDS holds the decode tables).
+  constexpr bool kStage = !kLut;
+  __shared__ u32x4 lds_all[kStage ? kWavesPerBlock * kWave * RPL : 1];
+  __shared__ LutT lut_all[kLut ? kLutHeads * 256 : 1];
   u32x4* const lds = lds_all + wave_in_block() * (kWave * RPL);
 
   const int lane = lane_id();
   const int64_t tile = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();
   const int64_t t0 = tile * kTileTokens;
-  if (t0 >= a.num_tokens) return;
   const int plane = static_cast<int>(blockIdx.y);
   const int layer = plane >> 1;
   const int kv = plane & 1;
-  uint8_t* const cache = a.cache[kv] + static_cast<int64_t>(layer) * a.cache_layer_stride;
-  uint8_t* const lin = a.lin[kv] + static_cast<int64_t>(layer) * a.lin_layer_stride;
   const int64_t r0 = static_cast<int64_t>(blockIdx.z) * kChunkRows;  // this wave's cache rows
   const int64_t r_end = (r0 + kChunkRows < a.nrows) ? r0 + kChunkRows : a.nrows;
 
-  // Slot window: lane i holds token t0 - 1 + i.
+  // Slot window: lane i holds token t0 - 1 + i (loaded before the table is
+  // built, so that the two loads overlap).
   const int64_t t = t0 - 1 + lane;
   int64_t s = -1;
   if (t >= 0 && t < a.num_tokens) s = slot_at(a, t);
+
+  // The workgroup's decode tables: its waves share the chunk (grid z), so the
+  // heads h_lo .. of rows [r0, r_end) (one table for a scalar scale).  The
+  // launcher routes chunks spanning more than kLutHeads heads elsewhere.
+  const int h_lo = (kLut && a.scale_mode != 0) ? head_of_row(a, static_cast<int>(r0)) : 0;
+  if constexpr (kLut) {
+    const int nh = a.scale_mode != 0 ? head_of_row(a, static_cast<int>(r_end - 1)) - h_lo + 1 : 1;
+    for (int e = static_cast<int>(threadIdx.x); e < nh * 256; e += kBlockThreads)
+      lut_all[e] = lut_value<CODEC, LDT, LutT>(static_cast<uint32_t>(e & 255), load_scale(a, kv, layer, h_lo + (e >> 8)));
+    __syncthreads();
+  }
+  if (t0 >= a.num_tokens) return;
+  uint8_t* const cache = a.cache[kv] + static_cast<int64_t>(layer) * a.cache_layer_stride;
+  uint8_t* const lin = a.lin[kv] + static_cast<int64_t>(layer) * a.lin_layer_stride;
+
   const bool valid = (s >= 0) && (s < a.num_slots);
   const uint64_t vmask = ballot(valid);
   const int64_t s_prev = from_prev_lane(s);
@@ -120,10 +164,10 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_gather_kernel(const 
   const int ct = lane % NCG;
   const int64_t trow = r0 + rg * RPL;
   const bool tile_in = trow < r_end;
-  float sc = 1.0f;
-  if constexpr (CODEC != kCopy) {
-    if (tile_in) sc = load_scale(a, kv, layer, trow / a.head_dim);
-  }
+  // The lane's table: all RPL rows of its tile lie in one head (head_dim is a
+  // multiple of RPL on this path).
+  const LutT* lut = lut_all;
+  if (kLut && a.scale_mode != 0 && tile_in) lut += (head_of_row(a, static_cast<int>(trow)) - h_lo) * 256;
 
   while (heads) {
     const int i = __builtin_ctzll(heads);
@@ -143,19 +187,29 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_gather_kernel(const 
       // 64-bit address registers, so the compiler issues all RPL loads back to
       // back and never waits on one access before the next address.
       const buf_t cb = make_buf(chunk);
-      u32x4 v[RPL];
-#pragma unroll
-      for (int k = 0; k < RPL; ++k) {
-        const int pc = k * kWave + lane;
-        v[k] = buf_ld16(cb, r0 + pc / NCG < r_end ? static_cast<uint32_t>(pc) * 16u : kOffOob);
-      }
-#pragma unroll
-      for (int k = 0; k < RPL; ++k) lds[lds_slot<RPL, NCG>(k * kWave + lane)] = v[k];
-      wave_lds_sync();
       u32x4 d[RPL];
+      if constexpr (kStage) {
+        u32x4 v[RPL];
 #pragma unroll
-      for (int q = 0; q < RPL; ++q) d[q] = lds[lds_slot<RPL, NCG>((rg * RPL + q) * NCG + ct)];
-      wave_lds_sync();
+        for (int k = 0; k < RPL; ++k) {
+          const int pc = k * kWave + lane;
+          v[k] = buf_ld16(cb, r0 + pc / NCG < r_end ? static_cast<uint32_t>(pc) * 16u : kOffOob);
+        }
+#pragma unroll
+        for (int k = 0; k < RPL; ++k) lds[lds_slot<RPL, NCG>(k * kWave + lane)] = v[k];
+        wave_lds_sync();
+#pragma unroll
+        for (int q = 0; q < RPL; ++q) d[q] = lds[lds_slot<RPL, NCG>((rg * RPL + q) * NCG + ct)];
+        wave_lds_sync();
+      } else {
+        // Each lane loads its own tile: RPL pieces 16 * NCG bytes apart.  A wave
+        // instruction touches 64 lines partially; the loads are cached so that
+        // the L2 serves the rest of each line to the wave's next instructions.
+        const uint32_t toff = static_cast<uint32_t>((rg * RPL * NCG + ct) * 16);
+#pragma unroll
+        for (int q = 0; q < RPL; ++q)
+          d[q] = buf_ld16_cached(cb, tile_in ? toff + static_cast<uint32_t>(q * NCG * 16) : kOffOob);
+      }
       // The run's first token row at row r0; the lane's rows start rg * RPL
       // further.  Token offsets stay below 2 GiB (token stride <= 32 MiB).
       const buf_t lb = make_buf(lin + tf * a.lin_token_stride + r0 * ELT_L);
@@ -165,8 +219,8 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_gather_kernel(const 
       for (int cc = 0; cc < CG; ++cc) {
         const int c = ct * CG + cc;
         const bool mine = tile_in && c >= c0 && c < c1;
-        buf_st16(lb, mine ? lane_off + static_cast<uint32_t>(c - c0) * stride32 : kOffOob,
-                 gather_column<ELT_C, ELT_L, CODEC, LDT, RPL>(d, cc, sc));
+        buf_st16_p<STP>(lb, mine ? lane_off + static_cast<uint32_t>(c - c0) * stride32 : kOffOob,
+                 gather_column<ELT_C, ELT_L, CODEC, RPL>(d, cc, lut));
       }
       continue;
     }
@@ -176,8 +230,8 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_gather_kernel(const 
     const int j1 = (c1 - 1) / CG;
     for (int g = static_cast<int>(r0 / RPL) + lane; g < static_cast<int>(r_end / RPL); g += kWave) {
       const int64_t gr = static_cast<int64_t>(g) * RPL;
-      float gsc = 1.0f;
-      if constexpr (CODEC != kCopy) gsc = load_scale(a, kv, layer, gr / a.head_dim);
+      const LutT* glut = lut_all;
+      if (kLut && a.scale_mode != 0) glut += (head_of_row(a, static_cast<int>(gr)) - h_lo) * 256;
       uint8_t* const crow = cache + (blk * a.nrows + gr) * BS * ELT_C;
       uint8_t* const grow = lin + tf * a.lin_token_stride + gr * ELT_L;
 #pragma unroll 1
@@ -191,7 +245,7 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_gather_kernel(const 
           const int c = lo + cc;
           if (c >= c0 && c < c1)
             st16(grow + static_cast<int64_t>(c - c0) * a.lin_token_stride,
-                 gather_column<ELT_C, ELT_L, CODEC, LDT, RPL>(d, cc, gsc));
+                 gather_column<ELT_C, ELT_L, CODEC, RPL>(d, cc, glut));
         }
       }
     }
@@ -442,17 +496,39 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const
 
 }  // namespace
 
+// True when every linear token row covers whole 128-byte lines (row size,
+// token and layer strides, both bases).
+bool whole_line_rows(const TileArgs& a, int elt) {
+  constexpr int64_t kLine = 128;
+  return (a.nrows * elt) % kLine == 0 && a.lin_token_stride % kLine == 0 && a.lin_layer_stride % kLine == 0 &&
+         reinterpret_cast<uintptr_t>(a.lin[0]) % kLine == 0 && reinterpret_cast<uintptr_t>(a.lin[1]) % kLine == 0;
+}
+
 template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS>
 hipError_t launch_wave_gather(const TileArgs& a, int64_t planes, hipStream_t stream) {
   using W = WaveShape<ELT_C, ELT_L, BS>;
   const int64_t chunks = (a.nrows + W::kChunkRows - 1) / W::kChunkRows;
   if (chunks > 65535) return hipErrorInvalidValue;
+  if (CODEC != kCopy && a.scale_mode != 0) {
+    // Every chunk's heads must fit the workgroup's decode tables.
+    for (int64_t z = 0; z < chunks; ++z) {
+      const int64_t r0 = z * W::kChunkRows;
+      const int64_t r1 = (r0 + W::kChunkRows < a.nrows ? r0 + W::kChunkRows : a.nrows) - 1;
+      if (r1 / a.head_dim - r0 / a.head_dim + 1 > kLutHeads) return hipErrorNotSupported;
+    }
+  }
   const int64_t tiles = (a.num_tokens + kTileTokens - 1) / kTileTokens;
   const int64_t blocks = (tiles + kWavesPerBlock - 1) / kWavesPerBlock;
   if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((paged_wave_gather_kernel<ELT_C, ELT_L, CODEC, LDT, BS>),
-                     dim3(static_cast<uint32_t>(blocks), static_cast<uint32_t>(planes), static_cast<uint32_t>(chunks)),
-                     dim3(kBlockThreads), 0, stream, a);
+  const dim3 grid(static_cast<uint32_t>(blocks), static_cast<uint32_t>(planes), static_cast<uint32_t>(chunks));
+  // Linear rows of whole lines are written through the L2 (cfg 3
+  // dequant-gather 5.39 -> 5.48 TB/s, caches read from HBM).
+  if (whole_line_rows(a, ELT_L))
+    hipLaunchKernelGGL((paged_wave_gather_kernel<ELT_C, ELT_L, CODEC, LDT, BS, kBufWT>), grid, dim3(kBlockThreads), 0,
+                       stream, a);
+  else
+    hipLaunchKernelGGL((paged_wave_gather_kernel<ELT_C, ELT_L, CODEC, LDT, BS, kBufNT>), grid, dim3(kBlockThreads), 0,
+                       stream, a);
   return hipGetLastError();
 }
 
