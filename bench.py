@@ -800,7 +800,7 @@ def bench_dense() -> dict:
     dq = _hip.fn("musa_aiter_hip_paged_dense_tiles")
     qas = [(0, 1, 1, 2, 2, a.data_ptr(), b.data_ptr(), dk.data_ptr(), dv.data_ptr(), tables.data_ptr(),
             seq_lens.data_ptr(), batch, dense_len, max_blocks, NB, NH, HD, BS, ROW, ks.data_ptr(), vs.data_ptr(), 1,
-            1, 0) for a, b in sets8]
+            1, 0, None) for a, b in sets8]
     _check(dq(*qas[0], _stream()), "fp8 dense load")
     torch.cuda.synchronize()
     want = torch_ref.fp8_dequantize(rows_of(k8)[flat_slots], ks[None, :, None], "e4m3", torch.bfloat16)

@@ -16,9 +16,11 @@
  *   write zeros, scatters leave the destination untouched); slots outside
  *   the cache are treated as skipped.  Scatters keep last-writer-wins for
  *   duplicate destinations, like the reference's token loop: a claim pass
- *   records the last token per destination in a per-(device, stream) scratch
- *   array owned by the library (allocated on first use, grown on demand;
- *   calls captured into a HIP graph get an array per capture and stream).
+ *   records the last token per destination in a tag array: the caller's
+ *   (generic entries given musa_aiter_hip_claims), or one the library owns
+ *   per (device, stream) (allocated on first use, grown on demand; calls
+ *   captured into a HIP graph get an array per capture and stream, reused
+ *   once that graph is destroyed).
  *   Element types: "_float" = fp32, "_half" = fp16, "_bfloat16" / "_u16" =
  *   16-bit payloads (bf16 or fp16, copied bit-exactly).
  */
@@ -39,9 +41,16 @@ int musa_aiter_dsv4_kv_copy_abi_version(void);
 /* No reference counterpart: backend label and HIP error text for diagnostics. */
 const char* musa_aiter_hip_backend_name(void);
 const char* musa_aiter_hip_error_string(int code);
-/* No reference counterpart: number of duplicate-slot claim arrays held for scatters captured into
- * HIP graphs (one per capture and capturing stream; never freed, as graphs keep their addresses). */
+/* No reference counterpart: number of duplicate-slot claim arrays the library has allocated for
+ * scatters captured into HIP graphs.  Each capture (and capturing stream) takes one; an array
+ * returns to a free list when the graph that holds it is destroyed, and later captures reuse it,
+ * so the count follows the number of graphs alive at once, not the number ever captured. */
 int64_t musa_aiter_hip_graph_claim_arrays(void);
+/* No reference counterpart: bytes of device and pinned host memory the library has allocated
+ * itself since it was loaded (duplicate-slot claim arrays of the reference-named scatter entries,
+ * descriptor rings of large host batches; the static array of musa_aiter_hip_paged_tiles_noalloc
+ * is not counted).  The generic entries below allocate nothing when given caller-owned claims. */
+int64_t musa_aiter_hip_allocated_bytes(void);
 /* No reference counterpart: the access-pattern ceiling of a paged copy, timed by bench.py.  Copies
  * num_blocks whole blocks of every plane: block i reads block src_blocks[i] (NULL: i) of the source
  * region and writes block dst_blocks[i] (NULL: i) of the destination; block sizes are multiples of
@@ -55,22 +64,39 @@ int musa_aiter_hip_block_pattern_copy(const void* src, void* dst, const int32_t*
                                       int write_through, void* stream);
 
 /* ---- Generic entries used by this package's Python host layer (no reference counterpart) ----
- * Paged-A caches [NL, NB, NH, HD, BS] <-> linear rows with explicit strides.
+ * Caller-owned duplicate-slot claim tags for the generic scatter entries.  With `claims` NULL a
+ * scatter uses an array the library allocates per (device, stream); the Python host layer passes
+ * a tensor from torch's caching allocator instead, so the library allocates nothing on that path.
+ *   tags:     `capacity` uint64 on the call's device; capacity >= the destination rows of the call
+ *             (otherwise the call returns hipErrorInvalidValue and launches nothing).
+ *   epoch 0:  the call first clears the tags its tokens compete for, then claims; nothing is assumed
+ *             of the array's contents (for calls captured into graphs, whose replays repeat it).
+ *   epoch k:  every tag in the array was written with an epoch below k (a zeroed array, then
+ *             epochs 1, 2, .. one per call); no clearing pass.
+ * Calls that share an array must be ordered (one stream). */
+typedef struct musa_aiter_hip_claims {
+  uint64_t* tags;
+  int64_t capacity;
+  uint32_t epoch;
+  uint32_t reserved;
+} musa_aiter_hip_claims;
+
+/* Paged-A caches [NL, NB, NH, HD, BS] <-> linear rows with explicit strides.
  * scatter: 0 gather, 1 scatter; codec: 0 copy, 1 FP8 E4M3, 2 FP8 E5M2;
  * cache_elt / lin_elt: element bytes; lin_dtype (FP8 only): 0 f32, 1 f16, 2 bf16;
  * lin_token_stride / lin_layer_stride in linear elements; scale_mode: 0 scalar,
  * 1 [NH], 2 [NL, NH]; fill_zeros: gather writes zeros for skipped tokens;
- * dedupe: scatter runs the last-writer claim pass. */
+ * dedupe: scatter runs the last-writer claim pass; claims: caller-owned tags or NULL. */
 int musa_aiter_hip_paged_tiles(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtype, void* key_cache,
                                void* value_cache, void* key_linear, void* value_linear, const int64_t* slot_mapping,
                                int64_t num_layers, int64_t num_tokens, int64_t num_blocks, int64_t num_heads,
                                int64_t head_dim, int64_t block_size, int64_t lin_token_stride,
                                int64_t lin_layer_stride, const float* k_scale, const float* v_scale, int scale_mode,
-                               int fill_zeros, int dedupe, void* stream);
+                               int fill_zeros, int dedupe, const musa_aiter_hip_claims* claims, void* stream);
 /* No reference counterpart.  For callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc): musa_aiter_hip_paged_tiles with the
- * same arguments and results, allocating nothing.  A scatter with dedupe keeps its last-writer claim
- * tags in a static device array of MUSA_AITER_HIP_NOALLOC_MAX_SLOTS uint64 entries (16 MiB per
+ * same arguments (but no `claims`) and results, allocating nothing.  A scatter with dedupe keeps
+ * its last-writer claim tags in a static device array of MUSA_AITER_HIP_NOALLOC_MAX_SLOTS uint64 entries (16 MiB per
  * device, held until the process ends), cleared and claimed by every call; a scatter with dedupe
  * whose num_blocks * block_size exceeds that maximum returns hipErrorInvalidValue (1) and launches
  * nothing.  All calls on one device share the array: calls that overlap in time on one device
@@ -94,7 +120,7 @@ int musa_aiter_hip_paged_dense_tiles(int scatter, int codec, int cache_elt, int 
                                      int64_t dense_len, int64_t max_blocks, int64_t num_blocks, int64_t num_heads,
                                      int64_t head_dim, int64_t block_size, int64_t dense_token_stride,
                                      const float* k_scale, const float* v_scale, int scale_mode, int fill_zeros,
-                                     int dedupe, void* stream);
+                                     int dedupe, const musa_aiter_hip_claims* claims, void* stream);
 /* Dense [batch, dense_len, row_bytes] rows gathered from token-major caches [num_tokens, row_bytes]
  * through CSR indices (kv_indptr [batch + 1], kv_indices [index_count]); the byte-row form of
  * musa_aiter_kv_triton_indexed_to_dense_* for any element type. */
@@ -110,9 +136,10 @@ int musa_aiter_hip_copy_rows(const uint64_t* src_planes, const uint64_t* dst_pla
                              const uint64_t* dst_table, int64_t num_planes, const int64_t* src_idx,
                              const int64_t* dst_idx, int64_t num_tokens, int64_t num_rows_out, int64_t src_offset,
                              int64_t dst_offset, int64_t src_rows, int64_t dst_rows, int64_t row_bytes,
-                             int64_t src_stride, int64_t dst_stride, int zero_invalid, int dedupe, void* stream);
+                             int64_t src_stride, int64_t dst_stride, int zero_invalid, int dedupe,
+                             const musa_aiter_hip_claims* claims, void* stream);
 /* musa_aiter_hip_copy_rows with its arguments in one struct (no reference counterpart; for the
- * Python host layer, which fills the struct with one struct.pack instead of converting 18
+ * Python host layer, which fills the struct with one struct.pack instead of converting 19
  * ctypes arguments, about 1.5 us less host time per call).  Fields as in musa_aiter_hip_copy_rows. */
 typedef struct musa_aiter_hip_copy_rows_call {
   const uint64_t* src_planes;
@@ -133,6 +160,7 @@ typedef struct musa_aiter_hip_copy_rows_call {
   int64_t dst_stride;
   int32_t zero_invalid;
   int32_t dedupe;
+  const musa_aiter_hip_claims* claims;
 } musa_aiter_hip_copy_rows_call;
 int musa_aiter_hip_copy_rows_packed(const musa_aiter_hip_copy_rows_call* call, void* stream);
 /* Row copies between two index-addressed plane sets (host arrays of plane bases).  A side
@@ -144,7 +172,17 @@ int musa_aiter_hip_copy_rows_paged(const uint64_t* src_planes, const uint64_t* d
                                    const int64_t* src_idx, const int64_t* dst_idx, int64_t num_tokens,
                                    int64_t src_rows, int64_t dst_rows, int64_t row_bytes, int64_t src_stride,
                                    int64_t dst_stride, int64_t src_page_rows, int64_t src_page_stride,
-                                   int64_t dst_page_rows, int64_t dst_page_stride, int dedupe, void* stream);
+                                   int64_t dst_page_rows, int64_t dst_page_stride, int dedupe,
+                                   const musa_aiter_hip_claims* claims, void* stream);
+/* Whole blocks copied between same-layout caches of num_layers layers (block_bytes per block and
+ * layer, blocks contiguous per layer; K and V): block_mapping holds [num_pairs, 2] int64 (source,
+ * destination) block ids; a pair with an id outside its cache is skipped, and a destination named
+ * by several pairs keeps the last one.  The byte form of musa_aiter_kv_copy_paged_blocks_* with
+ * caller-owned claims. */
+int musa_aiter_hip_copy_blocks(const void* src_k, const void* src_v, void* dst_k, void* dst_v,
+                               const int64_t* block_mapping, int64_t num_pairs, int64_t num_layers,
+                               int64_t src_blocks, int64_t dst_blocks, int64_t block_bytes,
+                               const musa_aiter_hip_claims* claims, void* stream);
 
 /* ---- Paged-A [NB,NH,HD,BS] <-> linear [T,NH,HD] -------------------------------------------------
  * binding kv_transfer.py:350-376 (gather), :410-436 (scatter), :480-508 / :542-570 (multi-layer),

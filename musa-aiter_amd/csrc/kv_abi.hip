@@ -12,6 +12,7 @@
 // host layer needs (fill_skipped="preserve", merged layouts, non-contiguous
 // LMCache buffers, skip prefixes); the reference-named symbols are thin
 // wrappers over the same launchers.
+#include <atomic>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -61,11 +62,46 @@ struct GraphKey {
 
 std::mutex g_claim_mu;
 std::map<EagerKey, ClaimScratch>* g_claims = nullptr;
-std::map<GraphKey, ClaimScratch>* g_graph_claims = nullptr;
 // Outgrown eager arrays.  Kernels queued before the growth may still read
 // them, and freeing would synchronise the device, so they stay allocated;
 // capacities double, so they add at most the size of the live arrays.
 std::vector<uint64_t*>* g_retired_claims = nullptr;
+
+// Arrays of captured calls.  Each is tied to the graph it was captured into
+// by a HIP user object: when the graph (and every executable graph made from
+// it) is destroyed, the object's destructor moves the array to a free list
+// that later captures on the same device reuse.  g_graph_mu guards only these
+// structures and is never held across a HIP call, since the runtime may run
+// the destructor from any thread.
+struct GraphArray {
+  int dev = 0;
+  uint64_t* owner = nullptr;
+  int64_t capacity = 0;
+};
+std::mutex g_graph_mu;
+std::map<GraphKey, GraphArray>* g_graph_claims = nullptr;  // the live capture's current array, by capture
+std::vector<GraphArray>* g_graph_free = nullptr;          // arrays whose graphs were destroyed
+int64_t g_graph_arrays = 0;                               // arrays ever allocated for captures
+
+struct GraphRelease {
+  GraphKey key;
+  GraphArray arr;
+};
+
+// User-object destructor (no HIP calls): the graph holding `arr` is gone.
+void release_graph_array(void* p) {
+  auto* r = static_cast<GraphRelease*>(p);
+  {
+    std::lock_guard<std::mutex> lock(g_graph_mu);
+    auto it = g_graph_claims->find(r->key);
+    if (it != g_graph_claims->end() && it->second.owner == r->arr.owner) g_graph_claims->erase(it);
+    g_graph_free->push_back(r->arr);
+  }
+  delete r;
+}
+
+// Bytes of device and pinned host memory allocated by the library.
+std::atomic<int64_t> g_allocated_bytes{0};
 
 // hipMalloc in relaxed capture mode: another thread's global-mode capture is
 // not invalidated, and nothing is recorded into a graph being captured.
@@ -73,12 +109,14 @@ hipError_t malloc_relaxed(uint64_t** p, int64_t count) {
   hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
   hipError_t err = hipThreadExchangeStreamCaptureMode(&mode);
   if (err != hipSuccess) return err;
-  const hipError_t merr = hipMalloc(reinterpret_cast<void**>(p), static_cast<size_t>(count) * sizeof(uint64_t));
+  const size_t bytes = static_cast<size_t>(count) * sizeof(uint64_t);
+  const hipError_t merr = hipMalloc(reinterpret_cast<void**>(p), bytes);
   err = hipThreadExchangeStreamCaptureMode(&mode);
   if (merr != hipSuccess) {
     *p = nullptr;
     return merr;
   }
+  g_allocated_bytes.fetch_add(static_cast<int64_t>(bytes));
   return err;
 }
 
@@ -105,44 +143,94 @@ hipError_t reset_and_claim(const kvhip::ClaimSource& src, int64_t n, int64_t row
   return hipSuccess;
 }
 
-// Claim pass of a call being captured into a graph.  A graph keeps the array
-// address it was captured with, so arrays of captures are never freed.
+// Claim pass of a call being captured into `graph`: the capture's array (one
+// of at least `rows` entries, from the free list or newly allocated and then
+// tied to the graph), cleared and claimed by the call itself.
 hipError_t prepare_graph_claims(const kvhip::ClaimSource& src, int64_t n, int64_t rows, hipStream_t stream, int dev,
-                                unsigned long long capture_id, const uint64_t** owner, uint32_t* epoch) {
-  if (g_graph_claims == nullptr) g_graph_claims = new std::map<GraphKey, ClaimScratch>();
-  ClaimScratch& cs = (*g_graph_claims)[GraphKey{dev, capture_id, reinterpret_cast<uintptr_t>(stream)}];
-  if (cs.capacity < rows) {
-    const int64_t cap = grown_capacity(cs.capacity, rows);
-    uint64_t* p = nullptr;
-    const hipError_t err = malloc_relaxed(&p, cap);
-    if (err != hipSuccess) return err;
-    cs.owner = p;
-    cs.capacity = cap;
+                                unsigned long long capture_id, hipGraph_t graph, const uint64_t** owner,
+                                uint32_t* epoch) {
+  const GraphKey key{dev, capture_id, reinterpret_cast<uintptr_t>(stream)};
+  GraphArray arr;
+  bool fresh = false;
+  {
+    std::lock_guard<std::mutex> lock(g_graph_mu);
+    if (g_graph_claims == nullptr) {
+      g_graph_claims = new std::map<GraphKey, GraphArray>();
+      g_graph_free = new std::vector<GraphArray>();
+    }
+    auto it = g_graph_claims->find(key);
+    if (it != g_graph_claims->end() && it->second.capacity >= rows) {
+      arr = it->second;
+    } else {
+      for (size_t i = 0; i < g_graph_free->size(); ++i) {
+        const GraphArray& f = (*g_graph_free)[i];
+        if (f.dev == dev && f.capacity >= rows) {
+          arr = f;
+          (*g_graph_free)[i] = g_graph_free->back();
+          g_graph_free->pop_back();
+          break;
+        }
+      }
+      fresh = true;
+    }
   }
-  return reset_and_claim(src, n, rows, cs.owner, stream, owner, epoch);
+  if (fresh) {
+    if (arr.owner == nullptr) {
+      arr.dev = dev;
+      arr.capacity = grown_capacity(0, rows);
+      const hipError_t err = malloc_relaxed(&arr.owner, arr.capacity);
+      if (err != hipSuccess) return err;
+      std::lock_guard<std::mutex> lock(g_graph_mu);
+      ++g_graph_arrays;
+    }
+    // Tie the array to the graph.  If that fails the array stays with this
+    // capture for the life of the process.
+    auto* rel = new GraphRelease{key, arr};
+    hipUserObject_t obj = nullptr;
+    if (hipUserObjectCreate(&obj, rel, release_graph_array, 1, hipUserObjectNoDestructorSync) != hipSuccess) {
+      (void)hipGetLastError();
+      delete rel;
+    } else if (hipGraphRetainUserObject(graph, obj, 1, hipGraphUserObjectMove) != hipSuccess) {
+      (void)hipGetLastError();  // the object keeps its reference: the array is never released
+    }
+    std::lock_guard<std::mutex> lock(g_graph_mu);
+    (*g_graph_claims)[key] = arr;
+  }
+  return reset_and_claim(src, n, rows, arr.owner, stream, owner, epoch);
 }
 
 // Runs the claim pass for the `n` destinations of `src` into a destination
 // of `rows` rows and returns the tag array and epoch the copy kernel must
-// check.  A call that cannot collide (n <= 1) skips the pass.  Eager calls on
-// one stream share that stream's array (stream order keeps them apart); a
-// captured graph has arrays of its own, so one graph must not replay on two
-// streams at once.
+// check.  A call that cannot collide (n <= 1) skips the pass.  With caller
+// claims (`ws`) the caller's array is used as musa_aiter_hip_claims
+// describes.  Otherwise eager calls on one stream share that stream's array
+// (stream order keeps them apart), and a captured graph has arrays of its
+// own, so one graph must not replay on two streams at once.
 hipError_t prepare_claims(const kvhip::ClaimSource& src, int64_t n, int64_t rows, hipStream_t stream,
-                          const uint64_t** owner, uint32_t* epoch) {
+                          const musa_aiter_hip_claims* ws, const uint64_t** owner, uint32_t* epoch) {
   *owner = nullptr;
   *epoch = 0;
   if (n <= 1 || rows <= 0 || (src.idx == nullptr && src.bt.block_tables == nullptr)) return hipSuccess;
+  if (ws != nullptr) {
+    if (ws->tags == nullptr || ws->capacity < rows) return hipErrorInvalidValue;
+    if (ws->epoch == 0) return reset_and_claim(src, n, rows, ws->tags, stream, owner, epoch);
+    const hipError_t err = kvhip::launch_claim(src, n, rows, ws->tags, ws->epoch, stream);
+    if (err != hipSuccess) return err;
+    *owner = ws->tags;
+    *epoch = ws->epoch;
+    return hipSuccess;
+  }
   int dev = 0;
   hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess) return err;
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
   unsigned long long capture_id = 0;
-  err = hipStreamGetCaptureInfo(stream, &capture, &capture_id);
+  hipGraph_t graph = nullptr;
+  err = hipStreamGetCaptureInfo_v2(stream, &capture, &capture_id, &graph, nullptr, nullptr);
   if (err != hipSuccess) return err;
-  std::lock_guard<std::mutex> lock(g_claim_mu);
   if (capture != hipStreamCaptureStatusNone)
-    return prepare_graph_claims(src, n, rows, stream, dev, capture_id, owner, epoch);
+    return prepare_graph_claims(src, n, rows, stream, dev, capture_id, graph, owner, epoch);
+  std::lock_guard<std::mutex> lock(g_claim_mu);
   if (g_claims == nullptr) g_claims = new std::map<EagerKey, ClaimScratch>();
   ClaimScratch& cs = (*g_claims)[{dev, reinterpret_cast<uintptr_t>(stream)}];
   if (cs.capacity < rows) {
@@ -178,7 +266,7 @@ hipError_t prepare_claims(const int64_t* idx, int64_t n, int64_t rows, hipStream
                           uint32_t* epoch) {
   kvhip::ClaimSource src;
   src.idx = idx;
-  return prepare_claims(src, n, rows, stream, owner, epoch);
+  return prepare_claims(src, n, rows, stream, nullptr, owner, epoch);
 }
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
@@ -196,8 +284,15 @@ hipError_t noalloc_scratch(uint64_t** out) {
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
+    // Relaxed capture mode, as for malloc_relaxed: a first call made inside a
+    // global-mode capture must not invalidate it.
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    err = hipThreadExchangeStreamCaptureMode(&mode);
+    if (err != hipSuccess) return err;
     void* ptr = nullptr;
     err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    const hipError_t merr = hipThreadExchangeStreamCaptureMode(&mode);
+    if (err == hipSuccess) err = merr;
     if (err != hipSuccess) return err;
     if (ptr == nullptr) return hipErrorInvalidSymbol;
     g_scratch_ptr[dev] = static_cast<uint64_t*>(ptr);
@@ -212,7 +307,8 @@ int paged_tiles(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtyp
                 void* vl, const int64_t* slots, int64_t nl, int64_t t, int64_t nb, int64_t nh, int64_t hd, int64_t bs,
                 int64_t tok_stride_elems, int64_t layer_stride_elems, const float* ks, const float* vs,
                 int scale_mode, int fill_zeros, int dedupe, hipStream_t stream,
-                const kvhip::BlockTableSlots* bt = nullptr, uint64_t* fixed_owner = nullptr) {
+                const kvhip::BlockTableSlots* bt = nullptr, uint64_t* fixed_owner = nullptr,
+                const musa_aiter_hip_claims* ws = nullptr) {
   if (t <= 0 || nl <= 0) return hipSuccess;
   PagedTileParams p{};
   p.scatter = scatter;
@@ -242,10 +338,10 @@ int paged_tiles(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtyp
     kvhip::ClaimSource src;
     src.idx = slots;
     if (bt != nullptr) src.bt = *bt;
-    // A caller-provided tag array (the allocation-free entry) is cleared and
-    // claimed per call; otherwise the library's per-stream array is used.
+    // The allocation-free entry's static array is cleared and claimed per
+    // call; otherwise the caller's claims or the library's arrays are used.
     hipError_t err = hipSuccess;
-    if (fixed_owner == nullptr) err = prepare_claims(src, t, nb * bs, stream, &p.owner, &p.epoch);
+    if (fixed_owner == nullptr) err = prepare_claims(src, t, nb * bs, stream, ws, &p.owner, &p.epoch);
     else if (t > 1) err = reset_and_claim(src, t, nb * bs, fixed_owner, stream, &p.owner, &p.epoch);
     if (err != hipSuccess) return err;
   }
@@ -258,7 +354,8 @@ int paged_tiles(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtyp
 int dense_tiles(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtype, void* kc, void* vc, void* dk,
                 void* dv, const int64_t* block_tables, const int64_t* seq_lens, int64_t batch, int64_t dense_len,
                 int64_t max_blocks, int64_t nb, int64_t nh, int64_t hd, int64_t bs, int64_t tok_stride_elems,
-                const float* ks, const float* vs, int scale_mode, int fill_zeros, int dedupe, hipStream_t stream) {
+                const float* ks, const float* vs, int scale_mode, int fill_zeros, int dedupe,
+                const musa_aiter_hip_claims* ws, hipStream_t stream) {
   if (batch <= 0 || dense_len <= 0) return hipSuccess;
   if (block_tables == nullptr || seq_lens == nullptr || max_blocks < 0 || max_blocks >= (int64_t{1} << 31) ||
       dense_len >= (int64_t{1} << 31) || batch >= ((int64_t{1} << 31) - 1) / dense_len + 1)
@@ -271,7 +368,8 @@ int dense_tiles(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtyp
   bt.max_blocks = static_cast<int32_t>(max_blocks);
   bt.block_size = static_cast<int32_t>(bs);
   return paged_tiles(scatter, codec, cache_elt, lin_elt, lin_dtype, kc, vc, dk, dv, nullptr, 1, batch * dense_len,
-                     nb, nh, hd, bs, tok_stride_elems, 0, ks, vs, scale_mode, fill_zeros, dedupe, stream, &bt);
+                     nb, nh, hd, bs, tok_stride_elems, 0, ks, vs, scale_mode, fill_zeros, dedupe, stream, &bt,
+                     nullptr, ws);
 }
 
 // Dense [batch, dense_len, NH, HD] rows gathered from a token-major cache
@@ -405,7 +503,7 @@ uint64_t addr(const void* base, int64_t byte_offset) {
 // block of one plane is one row of nh * hd * bs * elt bytes.
 int copy_blocks(int64_t elt, const void* sk, const void* sv, void* dk, void* dv, const int64_t* mapping,
                 int64_t num_pairs, int64_t nl, int64_t src_blocks, int64_t dst_blocks, int64_t nh, int64_t hd,
-                int64_t bs, hipStream_t stream) {
+                int64_t bs, hipStream_t stream, const musa_aiter_hip_claims* ws = nullptr) {
   if (num_pairs <= 0 || nl <= 0) return hipSuccess;
   if (mapping == nullptr || nh <= 0 || hd <= 0 || bs <= 0 || src_blocks < 0 || dst_blocks < 0)
     return hipErrorInvalidValue;
@@ -435,7 +533,7 @@ int copy_blocks(int64_t elt, const void* sk, const void* sv, void* dk, void* dv,
   claims.idx_stride = 2;
   claims.src_idx = mapping;
   claims.src_rows = src_blocks;
-  hipError_t err = prepare_claims(claims, num_pairs, dst_blocks, stream, &p.owner, &p.epoch);
+  hipError_t err = prepare_claims(claims, num_pairs, dst_blocks, stream, ws, &p.owner, &p.epoch);
   if (err != hipSuccess) return err;
   return kvhip::launch_row_copy(p, stream);
 }
@@ -523,9 +621,11 @@ int musa_aiter_hip_block_pattern_copy(const void* src, void* dst, const int32_t*
 }
 
 int64_t musa_aiter_hip_graph_claim_arrays() {
-  std::lock_guard<std::mutex> lock(g_claim_mu);
-  return g_graph_claims == nullptr ? 0 : static_cast<int64_t>(g_graph_claims->size());
+  std::lock_guard<std::mutex> lock(g_graph_mu);
+  return g_graph_arrays;
 }
+
+int64_t musa_aiter_hip_allocated_bytes() { return g_allocated_bytes.load(); }
 
 // ----- generic entries used by the Python host layer ----------------------------------------
 
@@ -534,11 +634,11 @@ int musa_aiter_hip_paged_tiles(int scatter, int codec, int cache_elt, int lin_el
                                int64_t num_layers, int64_t num_tokens, int64_t num_blocks, int64_t num_heads,
                                int64_t head_dim, int64_t block_size, int64_t lin_token_stride,
                                int64_t lin_layer_stride, const float* k_scale, const float* v_scale, int scale_mode,
-                               int fill_zeros, int dedupe, void* stream) {
+                               int fill_zeros, int dedupe, const musa_aiter_hip_claims* claims, void* stream) {
   return paged_tiles(scatter, codec, cache_elt, lin_elt, lin_dtype, key_cache, value_cache, key_linear, value_linear,
                      slot_mapping, num_layers, num_tokens, num_blocks, num_heads, head_dim, block_size,
                      lin_token_stride, lin_layer_stride, k_scale, v_scale, scale_mode, fill_zeros, dedupe,
-                     as_stream(stream));
+                     as_stream(stream), nullptr, nullptr, claims);
 }
 
 int musa_aiter_hip_paged_tiles_noalloc(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtype,
@@ -566,10 +666,10 @@ int musa_aiter_hip_paged_dense_tiles(int scatter, int codec, int cache_elt, int 
                                      int64_t dense_len, int64_t max_blocks, int64_t num_blocks, int64_t num_heads,
                                      int64_t head_dim, int64_t block_size, int64_t dense_token_stride,
                                      const float* k_scale, const float* v_scale, int scale_mode, int fill_zeros,
-                                     int dedupe, void* stream) {
+                                     int dedupe, const musa_aiter_hip_claims* claims, void* stream) {
   return dense_tiles(scatter, codec, cache_elt, lin_elt, lin_dtype, key_cache, value_cache, dense_k, dense_v,
                      block_tables, seq_lens, batch, dense_len, max_blocks, num_blocks, num_heads, head_dim,
-                     block_size, dense_token_stride, k_scale, v_scale, scale_mode, fill_zeros, dedupe,
+                     block_size, dense_token_stride, k_scale, v_scale, scale_mode, fill_zeros, dedupe, claims,
                      as_stream(stream));
 }
 
@@ -585,7 +685,8 @@ int musa_aiter_hip_copy_rows(const uint64_t* src_planes, const uint64_t* dst_pla
                              const uint64_t* dst_table, int64_t num_planes, const int64_t* src_idx,
                              const int64_t* dst_idx, int64_t num_tokens, int64_t num_rows_out, int64_t src_offset,
                              int64_t dst_offset, int64_t src_rows, int64_t dst_rows, int64_t row_bytes,
-                             int64_t src_stride, int64_t dst_stride, int zero_invalid, int dedupe, void* stream) {
+                             int64_t src_stride, int64_t dst_stride, int zero_invalid, int dedupe,
+                             const musa_aiter_hip_claims* claims, void* stream) {
   RowCopyParams p{};
   p.src_planes = src_planes;
   p.dst_planes = dst_planes;
@@ -605,17 +706,17 @@ int musa_aiter_hip_copy_rows(const uint64_t* src_planes, const uint64_t* dst_pla
   p.dst_stride = dst_stride;
   p.zero_invalid = zero_invalid;
   if (dedupe && dst_idx != nullptr) {
-    kvhip::ClaimSource claims;
-    claims.idx = dst_idx;
-    claims.src_idx = src_idx;
-    claims.src_rows = src_rows;
-    hipError_t err = prepare_claims(claims, num_tokens, dst_rows, as_stream(stream), &p.owner, &p.epoch);
+    kvhip::ClaimSource src;
+    src.idx = dst_idx;
+    src.src_idx = src_idx;
+    src.src_rows = src_rows;
+    hipError_t err = prepare_claims(src, num_tokens, dst_rows, as_stream(stream), claims, &p.owner, &p.epoch);
     if (err != hipSuccess) return err;
   }
   return kvhip::launch_row_copy(p, as_stream(stream));
 }
 
-static_assert(sizeof(musa_aiter_hip_copy_rows_call) == 136, "the Python host layer packs 136 bytes");
+static_assert(sizeof(musa_aiter_hip_copy_rows_call) == 144, "the Python host layer packs 144 bytes");
 
 int musa_aiter_hip_copy_rows_packed(const musa_aiter_hip_copy_rows_call* call, void* stream) {
   if (call == nullptr) return hipErrorInvalidValue;
@@ -624,7 +725,7 @@ int musa_aiter_hip_copy_rows_packed(const musa_aiter_hip_copy_rows_call* call, v
   return musa_aiter_hip_copy_rows(c.src_planes, c.dst_planes, c.src_table, c.dst_table, c.num_planes, c.src_idx,
                                   c.dst_idx, c.num_tokens, c.num_rows_out, c.src_offset, c.dst_offset, c.src_rows,
                                   c.dst_rows, c.row_bytes, c.src_stride, c.dst_stride, c.zero_invalid, c.dedupe,
-                                  stream);
+                                  c.claims, stream);
 }
 
 // ----- paged-A copies (kv_transfer.py:350-376, :410-436, :480-508, :542-570) ----------------
@@ -753,7 +854,7 @@ KVHIP_PAGED_COPY(bfloat16, 2)
     return dense_tiles(0, kvhip::kCopy, ELT, ELT, kvhip::kLinBF16, const_cast<void*>(key_cache),                  \
                        const_cast<void*>(value_cache), out_k, out_v, block_tables, seq_lens, batch, dense_len,    \
                        max_blocks, num_blocks, num_heads, head_dim, block_size, num_heads * head_dim, nullptr,    \
-                       nullptr, 0, 1, 0, as_stream(stream));                                                     \
+                       nullptr, 0, 1, 0, nullptr, as_stream(stream));                                            \
   }                                                                                                               \
   int musa_aiter_kv_reshape_and_cache_back_flash_##SUFFIX(                                                        \
       const void* dense_k, const void* dense_v, const int64_t* block_tables, const int64_t* seq_lens,             \
@@ -762,7 +863,7 @@ KVHIP_PAGED_COPY(bfloat16, 2)
     return dense_tiles(1, kvhip::kCopy, ELT, ELT, kvhip::kLinBF16, key_cache, value_cache,                        \
                        const_cast<void*>(dense_k), const_cast<void*>(dense_v), block_tables, seq_lens, batch,     \
                        dense_len, max_blocks, num_blocks, num_heads, head_dim, block_size, num_heads * head_dim,  \
-                       nullptr, nullptr, 0, 0, 1, as_stream(stream));                                            \
+                       nullptr, nullptr, 0, 0, 1, nullptr, as_stream(stream));                                   \
   }                                                                                                               \
   int musa_aiter_kv_triton_indexed_to_dense_##SUFFIX(                                                             \
       const void* key_cache, const void* value_cache, const int64_t* kv_indptr, const int64_t* kv_indices,        \
@@ -794,6 +895,14 @@ KVHIP_BLOCKS(musa_aiter_kv_copy_paged_blocks_half, 2)
 KVHIP_BLOCKS(musa_aiter_kv_copy_paged_blocks_bfloat16, 2)
 KVHIP_BLOCKS(musa_aiter_kv_copy_paged_blocks_fp8_vec8, 1)
 #undef KVHIP_BLOCKS
+
+int musa_aiter_hip_copy_blocks(const void* src_k, const void* src_v, void* dst_k, void* dst_v,
+                               const int64_t* block_mapping, int64_t num_pairs, int64_t num_layers,
+                               int64_t src_blocks, int64_t dst_blocks, int64_t block_bytes,
+                               const musa_aiter_hip_claims* claims, void* stream) {
+  return copy_blocks(1, src_k, src_v, dst_k, dst_v, block_mapping, num_pairs, num_layers, src_blocks, dst_blocks, 1,
+                     block_bytes, 1, as_stream(stream), claims);
+}
 
 // ----- FP8 quant-store / dequant-gather (kv_transfer.py:2446-2480 and the other FP8 shims) -----
 
@@ -1060,7 +1169,8 @@ int musa_aiter_kv_copy_paged_rows_u8(const void* src, void* dst, const int64_t* 
                                      int64_t src_num_rows, int64_t dst_num_rows, void* stream) {
   const uint64_t s = addr(src, 0), d = addr(dst, 0);
   return musa_aiter_hip_copy_rows(&s, &d, nullptr, nullptr, 1, src_indices, dst_indices, num_rows, num_rows, 0, 0,
-                                  src_num_rows, dst_num_rows, item_bytes, item_bytes, item_bytes, 0, 1, stream);
+                                  src_num_rows, dst_num_rows, item_bytes, item_bytes, item_bytes, 0, 1, nullptr,
+                                  stream);
 }
 
 int musa_aiter_kv_copy_paged_rows_layer_table_u8(const uint64_t* src_ptr_table, const uint64_t* dst_ptr_table,
@@ -1069,7 +1179,7 @@ int musa_aiter_kv_copy_paged_rows_layer_table_u8(const uint64_t* src_ptr_table, 
                                                  int64_t src_num_rows, int64_t dst_num_rows, void* stream) {
   return musa_aiter_hip_copy_rows(nullptr, nullptr, src_ptr_table, dst_ptr_table, num_layers, src_indices,
                                   dst_indices, num_rows, num_rows, 0, 0, src_num_rows, dst_num_rows, item_bytes,
-                                  item_bytes, item_bytes, 0, 1, stream);
+                                  item_bytes, item_bytes, 0, 1, nullptr, stream);
 }
 
 int musa_aiter_kv_copy_paged_rows_contig_layers_u8(const void* src_base, void* dst_base, const int64_t* src_indices,
@@ -1084,7 +1194,7 @@ int musa_aiter_kv_copy_paged_rows_contig_layers_u8(const void* src_base, void* d
   }
   return musa_aiter_hip_copy_rows(s.data(), d.data(), nullptr, nullptr, num_layers, src_indices, dst_indices,
                                   num_rows, num_rows, 0, 0, src_num_rows, dst_num_rows, item_bytes, item_bytes,
-                                  item_bytes, 0, 1, stream);
+                                  item_bytes, 0, 1, nullptr, stream);
 }
 
 // ----- LMCache DSV4 strided block transfer (lmcache_kv_transfer.py:1355-1400) ----------------------
@@ -1125,7 +1235,8 @@ int musa_aiter_hip_copy_rows_paged(const uint64_t* src_planes, const uint64_t* d
                                    const int64_t* src_idx, const int64_t* dst_idx, int64_t num_tokens,
                                    int64_t src_rows, int64_t dst_rows, int64_t row_bytes, int64_t src_stride,
                                    int64_t dst_stride, int64_t src_page_rows, int64_t src_page_stride,
-                                   int64_t dst_page_rows, int64_t dst_page_stride, int dedupe, void* stream) {
+                                   int64_t dst_page_rows, int64_t dst_page_stride, int dedupe,
+                                   const musa_aiter_hip_claims* claims, void* stream) {
   if (num_tokens <= 0 || num_planes <= 0 || row_bytes <= 0) return hipSuccess;
   if (src_idx == nullptr || dst_idx == nullptr) return hipErrorInvalidValue;
   RowCopyParams p{};
@@ -1146,11 +1257,11 @@ int musa_aiter_hip_copy_rows_paged(const uint64_t* src_planes, const uint64_t* d
   p.dst_page_rows = dst_page_rows;
   p.dst_page_stride = dst_page_stride;
   if (dedupe) {
-    kvhip::ClaimSource claims;
-    claims.idx = dst_idx;
-    claims.src_idx = src_idx;
-    claims.src_rows = src_rows;
-    hipError_t err = prepare_claims(claims, num_tokens, dst_rows, as_stream(stream), &p.owner, &p.epoch);
+    kvhip::ClaimSource src;
+    src.idx = dst_idx;
+    src.src_idx = src_idx;
+    src.src_rows = src_rows;
+    hipError_t err = prepare_claims(src, num_tokens, dst_rows, as_stream(stream), claims, &p.owner, &p.epoch);
     if (err != hipSuccess) return err;
   }
   return kvhip::launch_row_copy(p, as_stream(stream));
@@ -1182,7 +1293,7 @@ int musa_aiter_hicache_transfer_bytes(const void* src_k, void* dst_k, const void
   const int64_t unbounded = INT64_MAX;
   return musa_aiter_hip_copy_rows_paged(s.data(), d.data(), static_cast<int64_t>(s.size()), src_indices,
                                         dst_indices, num_items, unbounded, unbounded, row, src_page_stride_bytes,
-                                        dst_page_stride_bytes, 0, 0, 0, 0, 0, stream);
+                                        dst_page_stride_bytes, 0, 0, 0, 0, 0, nullptr, stream);
 }
 
 // ----- LMCache host <-> device batch copies (lmcache_musa_batch_copy_ext.cpp:41-277) -------------
@@ -1277,6 +1388,7 @@ hipError_t batch_copy_by_descriptors(const std::vector<uint64_t>& src, const std
     err = hipHostMalloc(reinterpret_cast<void**>(&host), cap * sizeof(uint64_t),
                         hipHostMallocMapped | hipHostMallocCoherent);
     if (err != hipSuccess) return err;
+    g_allocated_bytes.fetch_add(static_cast<int64_t>(cap * sizeof(uint64_t)));
     if (slot.host != nullptr) {
       std::lock_guard<std::mutex> lock(g_desc_mu);
       if (g_retired_desc == nullptr) g_retired_desc = new std::vector<uint64_t*>();

@@ -38,7 +38,17 @@ _SIGNATURES: dict[str, list] = {
         _i64, _i64, _i64, _i64, _i64, _i64,      # layers, tokens, blocks, heads, head_dim, block_size
         _i64, _i64,                              # linear token / layer stride (elements)
         _c_void_p, _c_void_p, _i32,              # k_scale, v_scale, scale_mode
-        _i32, _i32, _c_void_p,                   # fill_zeros, dedupe, stream
+        _i32, _i32, _c_void_p, _c_void_p,        # fill_zeros, dedupe, claims, stream
+    ],
+    # musa_aiter_hip_paged_tiles without the claims argument (allocation-free entry; tests only).
+    "musa_aiter_hip_paged_tiles_noalloc": [
+        _i32, _i32, _i32, _i32, _i32,
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+        _c_void_p,
+        _i64, _i64, _i64, _i64, _i64, _i64,
+        _i64, _i64,
+        _c_void_p, _c_void_p, _i32,
+        _i32, _i32, _c_void_p,
     ],
     "musa_aiter_hip_paged_dense_tiles": [
         _i32, _i32, _i32, _i32, _i32,            # scatter, codec, cache_elt, lin_elt, lin_dtype
@@ -47,14 +57,14 @@ _SIGNATURES: dict[str, list] = {
         _i64, _i64, _i64, _i64,                  # batch, dense_len, max_blocks, blocks
         _i64, _i64, _i64, _i64,                  # heads, head_dim, block_size, dense token stride (elements)
         _c_void_p, _c_void_p, _i32,              # k_scale, v_scale, scale_mode
-        _i32, _i32, _c_void_p,                   # fill_zeros, dedupe, stream
+        _i32, _i32, _c_void_p, _c_void_p,        # fill_zeros, dedupe, claims, stream
     ],
     "musa_aiter_hip_copy_rows": [
         _u64p, _u64p, _c_void_p, _c_void_p, _i64,  # host planes, device tables, planes
         _c_void_p, _c_void_p,                    # src_idx, dst_idx
         _i64, _i64, _i64, _i64, _i64, _i64,      # tokens, rows_out, src_off, dst_off, src_rows, dst_rows
         _i64, _i64, _i64,                        # row_bytes, src_stride, dst_stride
-        _i32, _i32, _c_void_p,                   # zero_invalid, dedupe, stream
+        _i32, _i32, _c_void_p, _c_void_p,        # zero_invalid, dedupe, claims, stream
     ],
     "musa_aiter_hip_copy_rows_packed": [ctypes.c_char_p, _c_void_p],  # musa_aiter_hip_copy_rows_call, stream
     "musa_aiter_hip_copy_rows_paged": [
@@ -62,8 +72,10 @@ _SIGNATURES: dict[str, list] = {
         _c_void_p, _c_void_p, _i64,              # src_idx, dst_idx, tokens
         _i64, _i64, _i64, _i64, _i64,            # src_rows, dst_rows, row_bytes, src_stride, dst_stride
         _i64, _i64, _i64, _i64,                  # src page rows / stride, dst page rows / stride
-        _i32, _c_void_p,                         # dedupe, stream
+        _i32, _c_void_p, _c_void_p,              # dedupe, claims, stream
     ],
+    # (src_k, src_v, dst_k, dst_v, block_mapping, pairs, layers, src_blocks, dst_blocks, block_bytes, claims, stream)
+    "musa_aiter_hip_copy_blocks": [_c_void_p] * 5 + [_i64] * 5 + [_c_void_p, _c_void_p],
     # (src_k, dst_k, src_v, dst_v, src_indices, dst_indices, items, start_layer, layers, item_bytes,
     #  src_page_stride, src_layer_stride, dst_page_stride, dst_layer_stride, stream)
     "musa_aiter_hicache_transfer_bytes": [_c_void_p] * 6 + [_i64] * 8 + [_c_void_p],
@@ -81,6 +93,7 @@ _SIGNATURES: dict[str, list] = {
     "musa_aiter_hip_error_string": [_i32],
     "musa_aiter_hip_backend_name": [],
     "musa_aiter_hip_graph_claim_arrays": [],
+    "musa_aiter_hip_allocated_bytes": [],
     "musa_aiter_kv_transfer_abi_version": [],
     "native_lmcache_kv_transfer_abi_version": [],
     "musa_aiter_fp8_kv_cache_abi_version": [],
@@ -115,6 +128,7 @@ _RESTYPES = {
     "musa_aiter_hip_backend_name": ctypes.c_char_p,
     "musa_aiter_hip_cachegen_workspace_bytes": ctypes.c_int64,
     "musa_aiter_hip_graph_claim_arrays": ctypes.c_int64,
+    "musa_aiter_hip_allocated_bytes": ctypes.c_int64,
 }
 
 _lock = threading.Lock()
@@ -218,8 +232,55 @@ def ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
 
 
 # musa_aiter_hip_copy_rows_call: four plane pointers, num_planes, two index pointers, nine int64
-# sizes and strides, two int32 flags (136 bytes, no padding).
-_COPY_ROWS_CALL = struct.Struct("<4Qq2Q9q2i")
+# sizes and strides, two int32 flags, the claims pointer (144 bytes, no padding).
+_COPY_ROWS_CALL = struct.Struct("<4Qq2Q9q2iQ")
+
+
+class _Claims(ctypes.Structure):
+    """musa_aiter_hip_claims: caller-owned duplicate-slot claim tags of one scatter call."""
+    _fields_ = [("tags", ctypes.c_void_p), ("capacity", ctypes.c_int64), ("epoch", ctypes.c_uint32),
+                ("reserved", ctypes.c_uint32)]
+
+
+_EPOCH_LAST = 0xFFFFFFFF
+_MIN_CLAIM_TAGS = 1 << 16
+# (device index, stream handle) -> (tag tensor, its _Claims).  The tags come from torch's caching
+# allocator on the stream that uses them, so the library allocates nothing for these scatters.
+_claim_sets: dict[tuple[int, int], tuple[torch.Tensor, _Claims]] = {}
+
+
+def claims_for(device: torch.device, stream: ctypes.c_void_p, rows: int):
+    """The claims of one scatter with ``rows`` destination rows on ``stream``: returns the address of a
+    musa_aiter_hip_claims to pass and the objects to keep alive until the call has returned.
+
+    Eager calls share one tag array per (device, stream), zeroed when allocated, with an epoch that
+    advances per call (no clearing pass; the array is re-zeroed when the 32-bit epoch runs out).
+    A call being captured into a graph gets a fresh array from the graph's memory pool and epoch 0,
+    so that the library clears the tags it claims on every replay."""
+    rows = max(int(rows), 1)
+    if torch.cuda.is_current_stream_capturing():
+        tags = torch.empty(rows, dtype=torch.int64, device=device)
+        c = _Claims(tags.data_ptr(), rows, 0, 0)
+        return ctypes.addressof(c), (tags, c)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream.value or 0)
+    entry = _claim_sets.get(key)
+    if entry is None or entry[1].capacity < rows:
+        have = entry[1].capacity if entry is not None else 0
+        cap = max(rows, 2 * have, _MIN_CLAIM_TAGS)
+        tags = torch.zeros(cap, dtype=torch.int64, device=device)
+        entry = (tags, _Claims(tags.data_ptr(), cap, 0, 0))
+        _claim_sets[key] = entry
+    tags, c = entry
+    if c.epoch == _EPOCH_LAST:
+        tags.zero_()
+        c.epoch = 0
+    c.epoch += 1
+    return ctypes.addressof(c), entry
+
+
+def allocated_bytes() -> int:
+    """Device and pinned host bytes the HIP library has allocated itself (musa_aiter_hip_allocated_bytes)."""
+    return int(fn("musa_aiter_hip_allocated_bytes")())
 
 
 def _address(arr: ctypes.Array | None) -> int:
@@ -273,14 +334,18 @@ def paged_tiles(
         return
     device = key_cache.device
     with on_device(device):
+        stream = stream_ptr(device)
+        claims, keep = (claims_for(device, stream, num_blocks * block_size) if scatter and dedupe
+                        else (None, None))
         rc = fn("musa_aiter_hip_paged_tiles")(
             int(scatter), int(codec), int(cache_elt), int(lin_elt), int(lin_dtype),
             ptr(key_cache), ptr(value_cache), ptr(key_linear), ptr(value_linear), ptr(slots),
             int(num_layers), int(num_tokens), int(num_blocks), int(num_heads), int(head_dim), int(block_size),
             int(lin_token_stride), int(lin_layer_stride),
             ptr(k_scale), ptr(v_scale), int(scale_mode),
-            int(bool(fill_zeros)), int(bool(dedupe)), stream_ptr(device),
+            int(bool(fill_zeros)), int(bool(dedupe)), claims, stream,
         )
+        del keep
     check(rc, op)
 
 
@@ -311,14 +376,18 @@ def copy_rows(
         return
     src_arr = _as_u64(src_planes)
     dst_arr = _as_u64(dst_planes)
-    # One struct (musa_aiter_hip_copy_rows_call) instead of 18 converted ctypes arguments; the plane
-    # arrays stay referenced by src_arr / dst_arr until the call returns.
-    call = _COPY_ROWS_CALL.pack(
-        _address(src_arr), _address(dst_arr), _data(src_table), _data(dst_table), num_planes,
-        _data(src_idx), _data(dst_idx), num_tokens, num_rows_out, src_offset, dst_offset, src_rows, dst_rows,
-        row_bytes, src_stride, dst_stride, bool(zero_invalid), bool(dedupe))
     with on_device(device):
-        rc = fn("musa_aiter_hip_copy_rows_packed")(call, stream_ptr(device))
+        stream = stream_ptr(device)
+        claims, keep = (claims_for(device, stream, dst_rows) if dedupe and dst_idx is not None
+                        else (0, None))
+        # One struct (musa_aiter_hip_copy_rows_call) instead of 19 converted ctypes arguments; the plane
+        # arrays stay referenced by src_arr / dst_arr until the call returns.
+        call = _COPY_ROWS_CALL.pack(
+            _address(src_arr), _address(dst_arr), _data(src_table), _data(dst_table), num_planes,
+            _data(src_idx), _data(dst_idx), num_tokens, num_rows_out, src_offset, dst_offset, src_rows, dst_rows,
+            row_bytes, src_stride, dst_stride, bool(zero_invalid), bool(dedupe), claims)
+        rc = fn("musa_aiter_hip_copy_rows_packed")(call, stream)
+        del keep
     check(rc, op)
 
 
@@ -355,13 +424,17 @@ def paged_dense_tiles(
         return
     device = key_cache.device
     with on_device(device):
+        stream = stream_ptr(device)
+        claims, keep = (claims_for(device, stream, num_blocks * block_size) if scatter and dedupe
+                        else (None, None))
         rc = fn("musa_aiter_hip_paged_dense_tiles")(
             int(scatter), int(codec), int(cache_elt), int(lin_elt), int(lin_dtype),
             ptr(key_cache), ptr(value_cache), ptr(dense_k), ptr(dense_v), ptr(block_tables), ptr(seq_lens),
             int(batch), int(dense_len), int(max_blocks), int(num_blocks), int(num_heads), int(head_dim),
             int(block_size), int(dense_token_stride), ptr(k_scale), ptr(v_scale), int(scale_mode),
-            int(bool(fill_zeros)), int(bool(dedupe)), stream_ptr(device),
+            int(bool(fill_zeros)), int(bool(dedupe)), claims, stream,
         )
+        del keep
     check(rc, op)
 
 
@@ -420,12 +493,15 @@ def copy_rows_paged(
     if len(dst_planes) != planes:
         raise ValueError(f"{op}: source and destination plane lists differ in length")
     with on_device(device):
+        stream = stream_ptr(device)
+        claims, keep = claims_for(device, stream, dst_rows) if dedupe else (None, None)
         rc = fn("musa_aiter_hip_copy_rows_paged")(
             u64_array(src_planes), u64_array(dst_planes), planes, ptr(src_idx), ptr(dst_idx), tokens,
             int(src_rows), int(dst_rows), int(row_bytes), int(src_stride), int(dst_stride),
             int(src_page_rows), int(src_page_stride), int(dst_page_rows), int(dst_page_stride),
-            int(bool(dedupe)), stream_ptr(device),
+            int(bool(dedupe)), claims, stream,
         )
+        del keep
     check(rc, op)
 
 
@@ -444,18 +520,22 @@ def copy_blocks(
 ) -> None:
     """Whole-block byte copies; `block_mapping` is a contiguous int64 [pairs, 2] device tensor.
 
-    Blocks are opaque bytes, so every element type goes through the one-byte
-    entry with the block described as [1 head, block_bytes, 1 position].
+    Blocks are opaque bytes, so every element type goes through the byte entry
+    musa_aiter_hip_copy_blocks (the form of musa_aiter_kv_copy_paged_blocks_*
+    that takes caller-owned claims).
     """
     pairs = int(block_mapping.shape[0])
     if pairs <= 0 or num_layers <= 0:
         return
     device = dst_k.device
     with on_device(device):
-        rc = fn("musa_aiter_kv_copy_paged_blocks_fp8_vec8")(
+        stream = stream_ptr(device)
+        claims, keep = claims_for(device, stream, dst_blocks)
+        rc = fn("musa_aiter_hip_copy_blocks")(
             ptr(src_k), ptr(src_v), ptr(dst_k), ptr(dst_v), ptr(block_mapping), pairs, int(num_layers),
-            int(src_blocks), int(dst_blocks), 1, int(block_bytes), 1, stream_ptr(device),
+            int(src_blocks), int(dst_blocks), int(block_bytes), claims, stream,
         )
+        del keep
     check(rc, op)
 
 

@@ -5,8 +5,9 @@ by ``musa_aiter/ops/lmcache_kv_transfer_ext.py:21-52``) exposing four tensor-lev
 ``kv_buffer_to_paged_list2``, ``paged_to_kv_buffer_list2``, ``kv_buffer_to_paged_two_x_nl`` and
 ``paged_to_kv_buffer_two_x_nl`` (``lmcache_kv_transfer_ext.cpp:587-592``).  Here the loader
 returns an object with the same four methods, the same argument checks and messages (raised as
-``RuntimeError``, as ``TORCH_CHECK`` does) and the same return value, each one launch of the
-library's reference-named C entries on the current stream.  The reference's environment-selected
+``RuntimeError``, as ``TORCH_CHECK`` does) and the same return value, each one launch on the current stream: gathers through the library's
+reference-named C entries, scatters through its generic row copy with claim tags from torch's
+allocator (so that no call makes the library allocate device memory).  The reference's environment-selected
 kernel variants (aten / coalesced / sorted / contiguous / torchmusa-style) all compute the same
 bytes; one kernel serves them all here.  ``MUSA_AITER_LMCACHE_CPP_EXTENSION=0`` disables the
 extension as in the reference; ``MUSA_AITER_LMCACHE_CPP_TIMING=1`` (or
@@ -169,14 +170,10 @@ class HipLMCacheKVTransferExtension:
         _check(skip >= 0, "skip_prefix_n_tokens must be non-negative")
         _check(skip + slot_mapping.numel() <= memory_tensor.size(2),
                "transfer range exceeds memory_tensor token extent")
-        ptrs = self._pointers(kvcaches)
-        device = memory_tensor.device
-        with torch.cuda.device(device):
-            rc = _hip.fn("lmcache_kv_buffer_to_paged_two_x_nl_coalesced_u16")(
-                _hip.ptr(memory_tensor), ptrs, _hip.ptr(slot_mapping), memory_tensor.size(1),
-                memory_tensor.size(2), slot_mapping.numel(), skip, kvcaches[0][0].size(0), block_size, num_heads,
-                head_size, _hip.stream_ptr(device))
-        _hip.check(rc, "kv_buffer_to_paged_two_x_nl")
+        caches = [cache for group in kvcaches for cache in group]
+        nl = memory_tensor.size(1)
+        self._scatter(memory_tensor, [(a, l) for a in range(2) for l in range(nl)], caches, slot_mapping, skip,
+                      kvcaches[0][0].size(0) * block_size, num_heads * head_size, "kv_buffer_to_paged_two_x_nl")
         return True
 
     def paged_to_kv_buffer_two_x_nl(self, kvcaches: list[list[torch.Tensor]], memory_tensor: torch.Tensor,
@@ -199,19 +196,43 @@ class HipLMCacheKVTransferExtension:
         return _hip.u64_array([cache.data_ptr() for group in kvcaches for cache in group])
 
     @staticmethod
+    def _scatter(memory_tensor: torch.Tensor, planes: list[tuple[int, int]], caches: list[int | torch.Tensor],
+                 slot_mapping: torch.Tensor, skip: int, num_slots: int, hidden: int, op: str) -> None:
+        """Rows skip + i of the memory planes (axis, layer) -> slot rows of the matching caches (a
+        cache tensor or a plane address), the last token of a repeated slot winning."""
+        row = hidden * memory_tensor.element_size()
+        nl, m = memory_tensor.size(1), memory_tensor.size(2)
+        base = memory_tensor.data_ptr()
+        _hip.copy_rows(op=op, device=memory_tensor.device,
+                       src_planes=[base + (a * nl + l) * m * row for a, l in planes],
+                       dst_planes=[c.data_ptr() if isinstance(c, torch.Tensor) else int(c) for c in caches],
+                       num_planes=len(planes), src_idx=None, dst_idx=slot_mapping,
+                       num_tokens=slot_mapping.numel(), num_rows_out=slot_mapping.numel(), src_offset=skip,
+                       src_rows=m, dst_rows=num_slots, row_bytes=row, src_stride=row, dst_stride=row,
+                       zero_invalid=False)
+
+    @staticmethod
     def _list2(scatter: int, memory_tensor: torch.Tensor, kvcaches: list[torch.Tensor], slot_mapping: torch.Tensor,
                skip: int, block_size: int, num_heads: int, head_size: int, op: str) -> bool:
         device = memory_tensor.device
         hidden = num_heads * head_size
         nbytes = 2 * len(kvcaches) * slot_mapping.numel() * hidden * memory_tensor.element_size()
-        name = "lmcache_kv_buffer_to_paged_list2_u16" if scatter else "lmcache_paged_to_kv_buffer_list2_u16"
         with torch.cuda.device(device):
             timing = _Timing(op, slot_mapping.numel(), hidden, nbytes, device)
-            rc = _hip.fn(name)(
-                _hip.ptr(memory_tensor), _hip.ptr(kvcaches[0]), _hip.ptr(kvcaches[1]), _hip.ptr(slot_mapping),
-                memory_tensor.size(2), slot_mapping.numel(), skip, kvcaches[0].size(1), block_size, num_heads,
-                head_size, _hip.stream_ptr(device))
-            _hip.check(rc, op)
+            if scatter:
+                # Planes (axis, layer) of the memory, and of the caches: layer l's [2, NB, BS, NH, HS]
+                # tensor holds its K plane, then its V plane.
+                half = kvcaches[0][0].numel() * kvcaches[0].element_size()
+                caches = [kvcaches[l].data_ptr() + a * half for a in range(2) for l in range(2)]
+                HipLMCacheKVTransferExtension._scatter(
+                    memory_tensor, [(a, l) for a in range(2) for l in range(2)], caches, slot_mapping, skip,
+                    kvcaches[0].size(1) * block_size, hidden, op)
+            else:
+                rc = _hip.fn("lmcache_paged_to_kv_buffer_list2_u16")(
+                    _hip.ptr(memory_tensor), _hip.ptr(kvcaches[0]), _hip.ptr(kvcaches[1]), _hip.ptr(slot_mapping),
+                    memory_tensor.size(2), slot_mapping.numel(), skip, kvcaches[0].size(1), block_size, num_heads,
+                    head_size, _hip.stream_ptr(device))
+                _hip.check(rc, op)
             timing.finish_after_launch()
         return True
 

@@ -182,7 +182,12 @@ def lmcache_musa_memcpy_batch_async(
     # The batch's distinct objects (by identity) and each entry's index among them.  When the backend is
     # asked for, its host helper must load and numbers them; otherwise one sort of the object ids does.
     count = len(sizes)
-    host = _hip.host() if lmcache_musa_batch_copy_requested() else None
+    host = None
+    if lmcache_musa_batch_copy_requested():
+        try:
+            host = _hip.host()
+        except (_hip.HipBackendError, OSError, ImportError):
+            host = None  # no helper module: the numpy numbering below serves, and the checks decide
     if host is not None:
         packed, tensors = host.object_index(destinations, sources)
         which = np.frombuffer(packed, dtype=np.int64)

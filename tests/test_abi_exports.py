@@ -37,7 +37,7 @@ def _declared_symbols() -> set[str]:
 
 def test_header_declares_expected_families():
     names = _declared_symbols()
-    assert len(names) == 118
+    assert len(names) == 120
     for required in ("musa_aiter_kv_load_and_reshape_flash_half", "musa_aiter_kv_triton_indexed_to_dense_bfloat16",
                      "musa_aiter_kv_reshape_and_cache_back_flash_float", "musa_aiter_kv_copy_paged_blocks_fp8_vec8",
                      "musa_aiter_hip_paged_dense_tiles","musa_aiter_kv_paged_to_linear_bfloat16", "musa_aiter_kv_linear_to_paged_multi_layer_half",
@@ -45,7 +45,8 @@ def test_header_declares_expected_families():
                      "lmcache_mla_paged_to_buffer_list_bfloat16", "musa_aiter_kv_copy_paged_rows_layer_table_u8",
                      "lmcache_kv_strided_block_transfer", "musa_aiter_hip_paged_tiles",
                      "musa_aiter_hicache_transfer_bytes", "musa_aiter_hicache_transfer_abi_version",
-                     "musa_aiter_hip_copy_rows_paged", "musa_aiter_hip_copy_rows_packed"):
+                     "musa_aiter_hip_copy_rows_paged", "musa_aiter_hip_copy_rows_packed", "musa_aiter_hip_copy_blocks",
+                     "musa_aiter_hip_allocated_bytes"):
         assert required in names
 
 
@@ -73,7 +74,7 @@ def test_noalloc_entry_rejects_caches_beyond_its_scratch_without_a_gpu():
     # scatter into more than MUSA_AITER_HIP_NOALLOC_MAX_SLOTS slots returns hipErrorInvalidValue.
     lib = ctypes.CDLL(str(_hip.LIB_PATH))
     f = lib.musa_aiter_hip_paged_tiles_noalloc
-    f.argtypes = _hip._SIGNATURES["musa_aiter_hip_paged_tiles"]
+    f.argtypes = _hip._SIGNATURES["musa_aiter_hip_paged_tiles_noalloc"]
     f.restype = ctypes.c_int
     text = HEADER.read_text()
     max_slots = int(re.search(r"#define MUSA_AITER_HIP_NOALLOC_MAX_SLOTS (\d+)", text).group(1))
@@ -87,18 +88,19 @@ def test_noalloc_entry_rejects_caches_beyond_its_scratch_without_a_gpu():
 
 def test_packed_row_copy_call_layout_matches_the_header():
     # The host layer packs musa_aiter_hip_copy_rows_call with struct; its fields, in order, must be the
-    # header's (pointers and int64 as 8 bytes, the two flags as int32), 136 bytes in all.
+    # header's (pointers and int64 as 8 bytes, the two flags as int32), 144 bytes in all.
     text = HEADER.read_text()
     body = re.search(r"typedef struct musa_aiter_hip_copy_rows_call \{(.*?)\}", text, re.S).group(1)
-    fields = re.findall(r"(const uint64_t\*|const int64_t\*|int64_t|int32_t)\s+(\w+);", body)
+    fields = re.findall(r"(const uint64_t\*|const int64_t\*|const musa_aiter_hip_claims\*|int64_t|int32_t)\s+(\w+);",
+                        body)
     codes = "".join("i" if kind == "int32_t" else ("q" if kind == "int64_t" else "Q") for kind, _ in fields)
-    assert codes == "QQQQqQQqqqqqqqqqii"
-    assert _hip._COPY_ROWS_CALL.format == "<4Qq2Q9q2i" and _hip._COPY_ROWS_CALL.size == 136
+    assert codes == "QQQQqQQqqqqqqqqqiiQ"
+    assert _hip._COPY_ROWS_CALL.format == "<4Qq2Q9q2iQ" and _hip._COPY_ROWS_CALL.size == 144
     # Nothing to copy returns success before any HIP call, so the entry is callable without a GPU.
     lib = ctypes.CDLL(str(_hip.LIB_PATH))
     f = lib.musa_aiter_hip_copy_rows_packed
     f.argtypes = _hip._SIGNATURES["musa_aiter_hip_copy_rows_packed"]
     f.restype = ctypes.c_int
-    empty = _hip._COPY_ROWS_CALL.pack(0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0, 0, 0, 16, 16, 16, 1, 1)
+    empty = _hip._COPY_ROWS_CALL.pack(0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0, 0, 0, 16, 16, 16, 1, 1, 0)
     assert f(empty, None) == 0
     assert f(None, None) != 0

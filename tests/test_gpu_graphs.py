@@ -118,17 +118,14 @@ def test_triton_indexed_to_dense_replays():
         assert np.array_equal(bits(ok), bits(wk)) and np.array_equal(bits(ov), bits(wv)), rep
 
 
-def test_graphs_on_the_default_capture_stream_get_their_own_claim_arrays():
+def test_graphs_on_the_default_capture_stream_get_their_own_claim_tags():
     # torch captures every graph on one process-wide stream; two graphs captured there must not
-    # share a claim array, or replays of both on different streams would clear each other's tags.
-    from musa_aiter.ops import _hip
-
+    # share claim tags, or replays of both on different streams would clear each other's tags.  A
+    # captured public-API scatter takes its tags from the graph's own memory pool.
     nl, nb, bs, nh, hs, t = 2, 16, 16, 2, 64, 96
     rng = np.random.default_rng(9)
     gen = torch.Generator().manual_seed(9)
-    count = _hip.fn("musa_aiter_hip_graph_claim_arrays")
     graphs, cases = [], []
-    before = int(count())
     for _ in range(2):
         caches = [[random_payload((nb, bs, nh, hs), torch.bfloat16, gen).to(DEV) for _ in range(nl)]
                   for _ in range(2)]
@@ -138,7 +135,6 @@ def test_graphs_on_the_default_capture_stream_get_their_own_claim_arrays():
             m, c, s, 0, bs, nh, hs))
         graphs.append(g)
         cases.append((caches, src, slots))
-    assert int(count()) - before == 2
     # both graphs still replay correctly, on two different streams
     streams = [torch.cuda.Stream(), torch.cuda.Stream()]
     want = []

@@ -575,3 +575,17 @@ def test_host_helper_numbers_distinct_objects_by_identity():
     assert packed == b"" and distinct == []
     with pytest.raises(TypeError):
         index(iter([a]), [a])
+
+
+def test_missing_host_helper_falls_back_to_false(monkeypatch, tmp_path):
+    # With the backend requested but neither the host helper module nor the extension loadable, the
+    # call returns False (the caller keeps its own transfer path) instead of raising.
+    from musa_aiter.ops import _hip
+
+    monkeypatch.setenv("MUSA_AITER_LMCACHE_BATCH_COPY", "1")
+    monkeypatch.setattr(_hip, "HOST_PATH", tmp_path / "missing_kv_host.so")
+    monkeypatch.setattr(_hip, "_host", None)
+    monkeypatch.setattr(batch, "load_lmcache_musa_batch_copy_ext", lambda: None)
+    source, destination = torch.arange(10, dtype=torch.uint8), torch.zeros(10, dtype=torch.uint8)
+    _fake_kinds(monkeypatch, source, destination)
+    assert batch.lmcache_musa_memcpy_batch_async([destination], [source], [8], require_pinned_host=False) is False

@@ -27,7 +27,7 @@ LIN_BF16 = 2
 
 def _entry(name):
     f = getattr(_hip.library(), name)
-    f.argtypes = _hip._SIGNATURES["musa_aiter_hip_paged_tiles"]
+    f.argtypes = _hip._SIGNATURES[name]
     f.restype = ctypes.c_int
     return f
 
@@ -35,8 +35,10 @@ def _entry(name):
 def _call(name, *, scatter, codec, cache_elt, kc, vc, kl, vl, slots, nl, t, nb, nh, hd, bs, scale=None,
           fill_zeros=1, dedupe=1):
     p = lambda x: None if x is None else x.data_ptr()  # noqa: E731
+    # The allocating entry takes a claims argument (NULL: the library's own tags) before the stream.
+    claims = () if name.endswith("_noalloc") else (None,)
     rc = _entry(name)(scatter, codec, cache_elt, 2, LIN_BF16, p(kc), p(vc), p(kl), p(vl), p(slots), nl, t, nb,
-                      nh, hd, bs, nh * hd, t * nh * hd, p(scale), p(scale), 0, fill_zeros, dedupe,
+                      nh, hd, bs, nh * hd, t * nh * hd, p(scale), p(scale), 0, fill_zeros, dedupe, *claims,
                       torch.cuda.current_stream().cuda_stream)
     assert rc == 0, f"{name}: {rc}"
 
@@ -112,3 +114,54 @@ def test_noalloc_after_eager_and_on_a_side_stream():
             _call("musa_aiter_hip_paged_tiles_noalloc", kc=bk, vc=bv, **common)
         torch.cuda.synchronize()
         assert np.array_equal(bits(ak), bits(bk)) and np.array_equal(bits(av), bits(bv)), rep
+
+
+def test_noalloc_scatter_and_gather_replay_from_a_graph():
+    # Captured once, replayed with new inputs (repeated and skipped slots): every replay equals the
+    # allocating entry run eagerly on the same inputs, bit for bit.
+    rng = np.random.default_rng(75)
+    gen = torch.Generator().manual_seed(75)
+    nl, nb, nh, hd, bs, t = 2, 48, 8, 128, 16, 400
+    kl = random_payload((nl, t, nh, hd), torch.bfloat16, gen).to(DEV)
+    vl = random_payload((nl, t, nh, hd), torch.bfloat16, gen).to(DEV)
+    slots = _slots(rng, nb, bs, t)
+    kc = torch.zeros((nl, nb, nh, hd, bs), dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    ok = torch.empty_like(kl)
+    ov = torch.empty_like(vl)
+    scatter = dict(scatter=1, codec=COPY, cache_elt=2, kc=kc, vc=vc, kl=kl, vl=vl, slots=slots, nl=nl, t=t, nb=nb,
+                   nh=nh, hd=hd, bs=bs)
+    gather = dict(scatter, scatter=0, kl=ok, vl=ov, dedupe=0)
+
+    def step():
+        _call("musa_aiter_hip_paged_tiles_noalloc", **scatter)
+        _call("musa_aiter_hip_paged_tiles_noalloc", **gather)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        print(f"noalloc graph replay {rep}", flush=True)
+        kl.copy_(random_payload((nl, t, nh, hd), torch.bfloat16, gen).to(DEV))
+        vl.copy_(random_payload((nl, t, nh, hd), torch.bfloat16, gen).to(DEV))
+        slots.copy_(_slots(rng, nb, bs, t))
+        base = random_payload((nl, nb, nh, hd, bs), torch.bfloat16, gen).to(DEV)
+        kc.copy_(base)
+        vc.copy_(base)
+        wk, wv = base.clone(), base.clone()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        wok, wov = torch.empty_like(kl), torch.empty_like(vl)
+        _call("musa_aiter_hip_paged_tiles", **dict(scatter, kc=wk, vc=wv))
+        _call("musa_aiter_hip_paged_tiles", **dict(gather, kc=wk, vc=wv, kl=wok, vl=wov))
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(kc), bits(wk)) and np.array_equal(bits(vc), bits(wv)), rep
+        assert np.array_equal(bits(ok), bits(wok)) and np.array_equal(bits(ov), bits(wov)), rep
