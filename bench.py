@@ -18,10 +18,12 @@ of K steps / device time of the K steps between HIP events, in GB/s.
 ``roofline`` is reported for the dominant kernel (the direction with the
 larger total time) against the 8 TB/s HBM peak; its ``traffic`` comes from the
 committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes.  ``ceilings`` times, on the
-same caches and linear buffers, a plain whole-block copy in the block order of
-the slot mapping (random cache blocks read with the linear side written in
-order, and the reverse): the rate that access pattern allows a copy with no
-index work, which the two kernels are measured against.  Each ceiling and
+same caches and linear buffers, a plain whole-block copy in each kernel's own
+visiting order (the gather: cache blocks read in the order the slot mapping
+visits them, the linear side written in order; the scatter: cache blocks
+written in block order, each block's linear rows read wherever they are; and,
+for reference, the scatter's token order): the rate that access pattern allows
+a copy with no index work, which the two kernels are measured against.  Each ceiling and
 floor is timed with non-temporal and with write-through stores and keeps the
 faster.  ``placements``
 re-allocates the caches several times in this process and times the step on
@@ -238,15 +240,23 @@ def config2_ceilings(slots_np: np.ndarray, kc: torch.Tensor, vc: torch.Tensor, k
     order_np = run_blocks(slots_np, BS)
     nblk = min(order_np.size, t // BS)
     order = torch.from_numpy(order_np[:nblk].copy()).to(dev)
+    # The scatter writes cache blocks in block order (its block-major kernel), reading each block's
+    # linear rows wherever they are: sorted destinations, linear blocks in the matching order.
+    by_dst = np.argsort(order_np[:nblk], kind="stable")
+    dst_sorted = torch.from_numpy(order_np[:nblk][by_dst].astype(np.int32)).to(dev)
+    src_by_dst = torch.from_numpy(by_dst.astype(np.int32)).to(dev)
     blk_bytes = ROW * BS * 2
     cache_stride, lin_stride = NB * blk_bytes, t * ROW * 2
     legs = {
         "gather_pattern": dict(src=(kc, vc), dst=(kl, vl), src_blocks=order, dst_blocks=None,
                                src_region_blocks=NB, dst_region_blocks=t // BS, src_plane_stride=cache_stride,
                                dst_plane_stride=lin_stride),
-        "scatter_pattern": dict(src=(kl, vl), dst=(kc, vc), src_blocks=None, dst_blocks=order,
+        "scatter_pattern": dict(src=(kl, vl), dst=(kc, vc), src_blocks=src_by_dst, dst_blocks=dst_sorted,
                                 src_region_blocks=t // BS, dst_region_blocks=NB, src_plane_stride=lin_stride,
                                 dst_plane_stride=cache_stride),
+        "scatter_token_order_pattern": dict(src=(kl, vl), dst=(kc, vc), src_blocks=None, dst_blocks=order,
+                                            src_region_blocks=t // BS, dst_region_blocks=NB,
+                                            src_plane_stride=lin_stride, dst_plane_stride=cache_stride),
         "sequential": dict(src=(kc, vc), dst=(kl, vl), src_blocks=None, dst_blocks=None, src_region_blocks=NB,
                            dst_region_blocks=t // BS, src_plane_stride=cache_stride, dst_plane_stride=lin_stride),
     }
@@ -266,8 +276,9 @@ def config2_ceilings(slots_np: np.ndarray, kc: torch.Tensor, vc: torch.Tensor, k
         out[name] = pattern_rate(make, nbytes, launches=5, reps=5)
     g, sc = out["gather_pattern"]["gbs"], out["scatter_pattern"]["gbs"]
     out["step_ceiling_gbs"] = 2.0 / (1.0 / g + 1.0 / sc)
-    log(f"config 2 ceilings: gather pattern {g:.0f}, scatter pattern {sc:.0f}, sequential "
-        f"{out['sequential']['gbs']:.0f}, step {out['step_ceiling_gbs']:.0f} GB/s")
+    log(f"config 2 ceilings: gather pattern {g:.0f}, scatter pattern {sc:.0f} (cache blocks in token order "
+        f"{out['scatter_token_order_pattern']['gbs']:.0f}), sequential {out['sequential']['gbs']:.0f}, step "
+        f"{out['step_ceiling_gbs']:.0f} GB/s")
     return out
 
 
@@ -1401,7 +1412,9 @@ def main() -> int:
                           "gather": round(c2["gather"]["tokens_per_ms"], 1)},
         "directions": {"scatter": c2["scatter"], "gather": c2["gather"]},
         "parity_roundtrip": c2["parity_roundtrip"],
-        "roofline": {"bound": "hbm", "kernel": f"paged_tile_kernel ({c2['dominant']}, 64 planes)",
+        "roofline": {"bound": "hbm", "kernel": ("paged_block_scatter_kernel (scatter, 64 planes)"
+                                                if c2["dominant"] == "scatter"
+                                                else "paged_tile_kernel (gather, 64 planes)"),
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(c2["dominant"]),
                      "traffic_source": "rocprofv3 FETCH_SIZE x2.000 + WRITE_SIZE x1.000 per dispatch "

@@ -206,10 +206,17 @@ hipError_t prepare_graph_claims(const kvhip::ClaimSource& src, int64_t n, int64_
 // describes.  Otherwise eager calls on one stream share that stream's array
 // (stream order keeps them apart), and a captured graph has arrays of its
 // own, so one graph must not replay on two streams at once.
+//
+// *exclusive (optional) tells whether the tags of the returned epoch are
+// exactly this call's claims, i.e. the array is the call's inverse map: true
+// for epochs no earlier call on the array used, false after a
+// reset-and-claim pass.
 hipError_t prepare_claims(const kvhip::ClaimSource& src, int64_t n, int64_t rows, hipStream_t stream,
-                          const musa_aiter_hip_claims* ws, const uint64_t** owner, uint32_t* epoch) {
+                          const musa_aiter_hip_claims* ws, const uint64_t** owner, uint32_t* epoch,
+                          int* exclusive = nullptr) {
   *owner = nullptr;
   *epoch = 0;
+  if (exclusive != nullptr) *exclusive = 0;
   if (n <= 1 || rows <= 0 || (src.idx == nullptr && src.bt.block_tables == nullptr)) return hipSuccess;
   if (ws != nullptr) {
     if (ws->tags == nullptr || ws->capacity < rows) return hipErrorInvalidValue;
@@ -218,6 +225,7 @@ hipError_t prepare_claims(const kvhip::ClaimSource& src, int64_t n, int64_t rows
     if (err != hipSuccess) return err;
     *owner = ws->tags;
     *epoch = ws->epoch;
+    if (exclusive != nullptr) *exclusive = 1;
     return hipSuccess;
   }
   int dev = 0;
@@ -258,6 +266,7 @@ hipError_t prepare_claims(const kvhip::ClaimSource& src, int64_t n, int64_t rows
   if (err != hipSuccess) return err;
   *owner = cs.owner;
   *epoch = cs.epoch;
+  if (exclusive != nullptr) *exclusive = 1;
   return hipSuccess;
 }
 
@@ -341,7 +350,7 @@ int paged_tiles(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtyp
     // The allocation-free entry's static array is cleared and claimed per
     // call; otherwise the caller's claims or the library's arrays are used.
     hipError_t err = hipSuccess;
-    if (fixed_owner == nullptr) err = prepare_claims(src, t, nb * bs, stream, ws, &p.owner, &p.epoch);
+    if (fixed_owner == nullptr) err = prepare_claims(src, t, nb * bs, stream, ws, &p.owner, &p.epoch, &p.owner_exclusive);
     else if (t > 1) err = reset_and_claim(src, t, nb * bs, fixed_owner, stream, &p.owner, &p.epoch);
     if (err != hipSuccess) return err;
   }

@@ -35,6 +35,11 @@ struct PagedTileParams {
   int fill_zeros;            // gather: write zeros for skipped tokens
   const uint64_t* owner;     // scatter claim tags (nullable)
   uint32_t epoch;
+  // The tags of `epoch` in owner are exactly this call's claims (an epoch no
+  // earlier call on the array used), so owner is the call's inverse map; false
+  // after a reset-and-claim pass, which leaves earlier calls' tags of the same
+  // epoch on slots this call does not write.
+  int owner_exclusive;
   BlockTableSlots bt;        // block_tables set: slots derived per dense token, `slots` unused
 };
 

@@ -24,6 +24,7 @@ struct TileArgs {
   int32_t scale_mode;
   int32_t fill_zeros;
   uint32_t epoch;
+  int32_t owner_exclusive;     // every tag of `epoch` in owner was claimed by this call
   int32_t block_size;          // used by the generic kernel only
   float inv_head_dim;          // 1 / head_dim, for small-integer division by head_dim
   BlockTableSlots bt;          // block_tables set: slots derived per dense token
