@@ -531,16 +531,21 @@ def bench_config3() -> dict:
                                      "encode/decode steps in torch (tests/torch_ref.py)"}
         log(f"config 3 {name}: quant {out[name]['quant_store']['gbs']:.0f} GB/s, "
             f"dequant {out[name]['dequant_gather']['gbs']:.0f} GB/s, parity {parity}")
-    # Access-pattern ceilings on the same buffers: 32 KiB of bf16 rows (16 tokens) per 16 KiB FP8 block,
-    # cache blocks in the order the slot mapping visits them.
+    # Access-pattern ceilings on the same buffers: 32 KiB of bf16 rows (16 tokens) per 16 KiB FP8 block; the
+    # quant-store writes cache blocks in block order (its block-major form), the dequant-gather reads them in
+    # the order the slot mapping visits them.
     order_np = run_blocks(slots_np, BS)
     nblk = min(order_np.size, t // BS)
     order = torch.from_numpy(order_np[:nblk].copy()).to(dev)
+    by_dst = np.argsort(order_np[:nblk], kind="stable")
+    dst_sorted = torch.from_numpy(order_np[:nblk][by_dst].astype(np.int32)).to(dev)
+    src_by_dst = torch.from_numpy(by_dst.astype(np.int32)).to(dev)
     lin_blk, cache_blk = ROW * BS * 2, ROW * BS
     ceil_bytes = 2 * nblk * (lin_blk + cache_blk)
     out["ceilings"] = {"blocks": nblk, "bytes_per_launch_pair": ceil_bytes}
     for name, quant, sbytes, dbytes, sblocks, dblocks, sreg, dreg in (
-            ("quant_store_pattern", True, lin_blk, cache_blk, None, order, t // BS, NB),
+            ("quant_store_pattern", True, lin_blk, cache_blk, src_by_dst, dst_sorted, t // BS, NB),
+            ("quant_store_token_order_pattern", True, lin_blk, cache_blk, None, order, t // BS, NB),
             ("dequant_gather_pattern", False, cache_blk, lin_blk, order, None, NB, t // BS)):
         def make(wt, quant=quant, sbytes=sbytes, dbytes=dbytes, sblocks=sblocks, dblocks=dblocks, sreg=sreg,
                  dreg=dreg):

@@ -355,7 +355,11 @@ __device__ __forceinline__ float tile_elem(const u32x4& piece, int q) {
   else return __uint_as_float(piece[q]);
 }
 
-template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS>
+// BM (block-major): the waves visit cache blocks in block order instead of
+// token tiles (wave w of the grid owns block w), reading each block's claim
+// tags as the inverse map of the scatter (see paged_block_scatter_kernel):
+// the cache is then written in address order.
+template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS, bool BM>
 __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const TileArgs a) {
   static_assert(ELT_C == 1 && CODEC != kCopy, "the per-wave scatter quantises into one-byte caches");
   using W = ScatterShape<ELT_L, BS>;
@@ -366,9 +370,7 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const
   u32x4* const lds = lds_all + wave_in_block() * kPieces;
 
   const int lane = lane_id();
-  const int64_t tile = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();
-  const int64_t t0 = tile * kTileTokens;
-  if (t0 >= a.num_tokens) return;
+  const int64_t unit = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();  // tile or block
   const int plane = static_cast<int>(blockIdx.y);
   const int layer = plane >> 1;
   const int kv = plane & 1;
@@ -379,22 +381,40 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const
   const int rw_end = (rw0 + kChunkRows * W::kWaveChunks < a.nrows) ? rw0 + kChunkRows * W::kWaveChunks
                                                                     : static_cast<int>(a.nrows);
 
-  // Slot window: lane i holds token t0 - 1 + i; a token whose claim lost to a
-  // later duplicate writes nothing.
-  const int64_t t = t0 - 1 + lane;
-  int64_t s = -1;
-  if (t >= 0 && t < a.num_tokens) s = slot_at(a, t);
-  bool valid = (s >= 0) && (s < a.num_slots);
-  if (valid && a.owner != nullptr) valid = (a.owner[s] == claim_tag(a.epoch, t));
-  const uint64_t vmask = ballot(valid);
-  const int64_t s_prev = from_prev_lane(s);
-  const bool prev_valid = lane > 0 && ((vmask >> (lane - 1)) & 1ull);
-  const bool cont = valid && prev_valid && (s == s_prev + 1) && ((s % BS) != 0);
-  const uint64_t cmask = ballot(cont);
-  const int64_t remaining = a.num_tokens - t0;
-  const int ntile = remaining < kTileTokens ? static_cast<int>(remaining) : kTileTokens;
-  const uint64_t window = ((1ull << ntile) - 1ull) << 1;
-  const uint64_t heads = vmask & ~cmask & window;
+  // Runs: `heads` marks the first lane of each, `cmask` the lanes continuing
+  // one, `first` gives a run's (block, first column, first token).
+  uint64_t heads, cmask;
+  int64_t s = -1, tok = -1;
+  const int64_t t0 = unit * kTileTokens;
+  if constexpr (!BM) {
+    // Slot window: lane i holds token t0 - 1 + i; a token whose claim lost to a
+    // later duplicate writes nothing.
+    if (t0 >= a.num_tokens) return;
+    const int64_t t = t0 - 1 + lane;
+    if (t >= 0 && t < a.num_tokens) s = slot_at(a, t);
+    bool valid = (s >= 0) && (s < a.num_slots);
+    if (valid && a.owner != nullptr) valid = (a.owner[s] == claim_tag(a.epoch, t));
+    const uint64_t vmask = ballot(valid);
+    const int64_t s_prev = from_prev_lane(s);
+    const bool prev_valid = lane > 0 && ((vmask >> (lane - 1)) & 1ull);
+    cmask = ballot(valid && prev_valid && (s == s_prev + 1) && ((s % BS) != 0));
+    const int64_t remaining = a.num_tokens - t0;
+    const int ntile = remaining < kTileTokens ? static_cast<int>(remaining) : kTileTokens;
+    const uint64_t window = ((1ull << ntile) - 1ull) << 1;
+    heads = vmask & ~cmask & window;
+  } else {
+    // Lane p < BS holds the tag of slot unit * BS + p.
+    if (unit * BS >= a.num_slots) return;
+    uint64_t tag = 0;
+    if (lane < BS) tag = a.owner[unit * BS + lane];
+    const bool valid = lane < BS && static_cast<uint32_t>(tag >> 32) == a.epoch && static_cast<uint32_t>(tag) != 0u;
+    tok = static_cast<int64_t>(static_cast<uint32_t>(tag)) - 1;
+    const uint64_t vmask = ballot(valid);
+    const int64_t tok_prev = from_prev_lane(tok);
+    const bool prev_valid = lane > 0 && ((vmask >> (lane - 1)) & 1ull);
+    cmask = ballot(valid && prev_valid && tok == tok_prev + 1);
+    heads = vmask & ~cmask;
+  }
   if (heads == 0) return;
 
   // Lane tile: rows trow .. trow + RPL - 1 of the chunk, block columns lo .. lo + COLS - 1.
@@ -414,17 +434,8 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const
     const bool scale_ok = fast_scale_ok(sc);
     const float r = scale_ok ? 1.0f / sc : 0.0f;
 
-    uint64_t hs = heads;
-    while (hs) {
-      const int i = __builtin_ctzll(hs);
-      hs &= hs - 1;
-      const uint64_t after = cmask >> (i + 1);  // i <= kTileTokens < 63
-      const int len = 1 + __builtin_ctzll(~after);
-      const int64_t sh = readlane64(s, i);
-      const int64_t blk = sh / BS;
-      const int c0 = static_cast<int>(sh - blk * BS);
-      const int c1 = c0 + len;
-      const int64_t tf = t0 - 1 + i;  // token of column c0
+    // One run: block columns [c0, c1) of block blk from tokens tf, tf + 1, ...
+    auto run = [&](int64_t blk, int c0, int c1, int64_t tf) {
       uint8_t* const chunk = cache + (blk * a.nrows + r0) * BS;
       const uint8_t* const lrow = lin + tf * a.lin_token_stride + static_cast<int64_t>(trow) * ELT_L;
 
@@ -472,7 +483,7 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const
             buf_st16(cbuf, (r0 + pc / NCG < r_end) ? static_cast<uint32_t>(pc) * 16u : kOffOob, v);
           }
           wave_lds_sync();
-          continue;
+          return;
         }
       }
 
@@ -480,7 +491,7 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const
       // lane's columns inside the run, byte by byte.
       const int ca = c0 > lo ? c0 : lo;
       const int cb = c1 < lo + COLS ? c1 : lo + COLS;
-      if (!tile_in) continue;
+      if (!tile_in) return;
       uint8_t* const crow = chunk + static_cast<int64_t>(rg * RPL) * BS;
 #pragma unroll 1
       for (int c = ca; c < cb; ++c) {
@@ -489,6 +500,21 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const
         for (int q = 0; q < RPL; ++q)
           crow[q * BS + c] =
               static_cast<uint8_t>(quant_one<CODEC, LDT>(tile_elem<ELT_L, LDT, RPL>(piece, q), sc, r, scale_ok));
+      }
+    };
+
+    uint64_t hs = heads;
+    while (hs) {
+      const int i = __builtin_ctzll(hs);
+      hs &= hs - 1;
+      const int len = 1 + __builtin_ctzll(~(cmask >> (i + 1)));  // i < 63
+      if constexpr (!BM) {
+        const int64_t sh = readlane64(s, i);
+        const int64_t blk = sh / BS;
+        const int c0 = static_cast<int>(sh - blk * BS);
+        run(blk, c0, c0 + len, t0 - 1 + i);
+      } else {
+        run(unit, i, i + len, readlane64(tok, i));
       }
     }
   }
@@ -537,12 +563,19 @@ hipError_t launch_wave_scatter(const TileArgs& a, int64_t planes, hipStream_t st
   using W = ScatterShape<ELT_L, BS>;
   const int64_t chunks = (a.nrows + W::kChunkRows * W::kWaveChunks - 1) / (W::kChunkRows * W::kWaveChunks);
   if (chunks > 65535) return hipErrorInvalidValue;
-  const int64_t tiles = (a.num_tokens + kTileTokens - 1) / kTileTokens;
-  const int64_t blocks = (tiles + kWavesPerBlock - 1) / kWavesPerBlock;
+  // Block order when the claim tags are this call's inverse map and the tokens
+  // cover a good share of the slots (as for the 16- and 32-bit scatter).
+  const bool bm = a.owner != nullptr && a.owner_exclusive && a.num_tokens * 4 >= a.num_slots;
+  const int64_t units = bm ? a.num_slots / BS : (a.num_tokens + kTileTokens - 1) / kTileTokens;
+  const int64_t blocks = (units + kWavesPerBlock - 1) / kWavesPerBlock;
   if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((paged_wave_scatter_kernel<ELT_C, ELT_L, CODEC, LDT, BS>),
-                     dim3(static_cast<uint32_t>(blocks), static_cast<uint32_t>(planes), static_cast<uint32_t>(chunks)),
-                     dim3(kBlockThreads), 0, stream, a);
+  const dim3 grid(static_cast<uint32_t>(blocks), static_cast<uint32_t>(planes), static_cast<uint32_t>(chunks));
+  if (bm)
+    hipLaunchKernelGGL((paged_wave_scatter_kernel<ELT_C, ELT_L, CODEC, LDT, BS, true>), grid, dim3(kBlockThreads), 0,
+                       stream, a);
+  else
+    hipLaunchKernelGGL((paged_wave_scatter_kernel<ELT_C, ELT_L, CODEC, LDT, BS, false>), grid, dim3(kBlockThreads), 0,
+                       stream, a);
   return hipGetLastError();
 }
 
