@@ -272,10 +272,10 @@ hipError_t prepare_claims(const kvhip::ClaimSource& src, int64_t n, int64_t rows
 
 // Destinations read from one index vector.
 hipError_t prepare_claims(const int64_t* idx, int64_t n, int64_t rows, hipStream_t stream, const uint64_t** owner,
-                          uint32_t* epoch) {
+                          uint32_t* epoch, int* exclusive = nullptr) {
   kvhip::ClaimSource src;
   src.idx = idx;
-  return prepare_claims(src, n, rows, stream, nullptr, owner, epoch);
+  return prepare_claims(src, n, rows, stream, nullptr, owner, epoch, exclusive);
 }
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
@@ -496,7 +496,7 @@ int rows_scatter(const uint64_t* lin_planes, const uint64_t* cache_planes, int64
   p.row_bytes = row_bytes;
   p.src_stride = lin_stride;
   p.dst_stride = cache_stride;
-  hipError_t err = prepare_claims(slots, t, slot_rows, stream, &p.owner, &p.epoch);
+  hipError_t err = prepare_claims(slots, t, slot_rows, stream, &p.owner, &p.epoch, &p.owner_exclusive);
   if (err != hipSuccess) return err;
   return kvhip::launch_row_copy(p, stream);
 }
@@ -542,7 +542,7 @@ int copy_blocks(int64_t elt, const void* sk, const void* sv, void* dk, void* dv,
   claims.idx_stride = 2;
   claims.src_idx = mapping;
   claims.src_rows = src_blocks;
-  hipError_t err = prepare_claims(claims, num_pairs, dst_blocks, stream, ws, &p.owner, &p.epoch);
+  hipError_t err = prepare_claims(claims, num_pairs, dst_blocks, stream, ws, &p.owner, &p.epoch, &p.owner_exclusive);
   if (err != hipSuccess) return err;
   return kvhip::launch_row_copy(p, stream);
 }
@@ -719,7 +719,8 @@ int musa_aiter_hip_copy_rows(const uint64_t* src_planes, const uint64_t* dst_pla
     src.idx = dst_idx;
     src.src_idx = src_idx;
     src.src_rows = src_rows;
-    hipError_t err = prepare_claims(src, num_tokens, dst_rows, as_stream(stream), claims, &p.owner, &p.epoch);
+    hipError_t err =
+        prepare_claims(src, num_tokens, dst_rows, as_stream(stream), claims, &p.owner, &p.epoch, &p.owner_exclusive);
     if (err != hipSuccess) return err;
   }
   return kvhip::launch_row_copy(p, as_stream(stream));
@@ -833,7 +834,8 @@ int musa_aiter_hip_copy_rows_packed(const musa_aiter_hip_copy_rows_call* call, v
     p.num_rows_out = num_tokens;                                                                                  \
     p.src_rows = num_tokens;                                                                                      \
     p.dst_rows = slots;                                                                                           \
-    int err = prepare_claims(slot_mapping, num_tokens, slots, as_stream(stream), &p.owner, &p.epoch);             \
+    int err = prepare_claims(slot_mapping, num_tokens, slots, as_stream(stream), &p.owner, &p.epoch,              \
+                             &p.owner_exclusive);                                                                 \
     if (err != 0) return err;                                                                                     \
     const int64_t dims[2] = {kv_dim, pe_dim};                                                                     \
     for (int i = 0; i < 2; ++i) {                                                                                 \
@@ -1270,7 +1272,8 @@ int musa_aiter_hip_copy_rows_paged(const uint64_t* src_planes, const uint64_t* d
     src.idx = dst_idx;
     src.src_idx = src_idx;
     src.src_rows = src_rows;
-    hipError_t err = prepare_claims(src, num_tokens, dst_rows, as_stream(stream), claims, &p.owner, &p.epoch);
+    hipError_t err =
+        prepare_claims(src, num_tokens, dst_rows, as_stream(stream), claims, &p.owner, &p.epoch, &p.owner_exclusive);
     if (err != hipSuccess) return err;
   }
   return kvhip::launch_row_copy(p, as_stream(stream));

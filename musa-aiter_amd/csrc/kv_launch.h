@@ -68,6 +68,7 @@ struct RowCopyParams {
   int zero_invalid;             // direct destination: zero rows whose source is skipped
   const uint64_t* owner;        // claim tags over destination rows (nullable)
   uint32_t epoch;
+  int owner_exclusive;          // the tags of `epoch` are exactly this call's claims (see PagedTileParams)
   // CSR source addressing (nullable): token u = b * dense_len + pos reads
   // row src_idx[src_indptr[b] + pos]; src_idx holds index_count entries.
   const int64_t* src_indptr;

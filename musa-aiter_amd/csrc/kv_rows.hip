@@ -54,6 +54,7 @@ struct RowArgs {
   int64_t dst_page_rows;
   int64_t dst_page_stride;
   int32_t plane_inner;        // 1: one grid over (row, plane, piece), planes inside rows
+  int32_t dst_major;          // 1: rows are destination rows, their tokens read from the claim tags (plane-major)
 };
 
 // Work of one block: kBlockPieces consecutive VEC-byte pieces of the
@@ -76,10 +77,23 @@ __device__ __forceinline__ int64_t row_offset(int64_t r, int64_t page_rows, int6
 }
 
 // Byte offsets of token u's source and destination rows, with the skip and
-// zero-fill marks above.
+// zero-fill marks above.  With DM (destination-major), u is a destination row
+// instead: the claim tags (this call's inverse map) name the token that
+// writes it, if any.
+template <bool DM>
 __device__ __forceinline__ void resolve_row(const RowArgs& a, int64_t u, int64_t* so, int64_t* dof) {
   *so = kZeroRow;
   *dof = kSkipRow;
+  if constexpr (DM) {
+    const uint64_t tag = a.owner[u];
+    if (static_cast<uint32_t>(tag >> 32) != a.epoch || static_cast<uint32_t>(tag) == 0u) return;
+    const int64_t t = static_cast<int64_t>(static_cast<uint32_t>(tag)) - 1;
+    const int64_t srow = a.src_idx ? a.src_idx[t * a.idx_stride] : t + a.src_offset;
+    if (srow < 0 || srow >= a.src_rows) return;
+    *so = row_offset(srow, a.src_page_rows, a.src_page_stride, a.src_stride);
+    *dof = row_offset(u, a.dst_page_rows, a.dst_page_stride, a.dst_stride);
+    return;
+  }
   int64_t srow = -1;
   int64_t drow = u + a.dst_offset;
   bool valid = false;
@@ -109,7 +123,7 @@ __device__ __forceinline__ void resolve_row(const RowArgs& a, int64_t u, int64_t
 // cfg 5 gather 1.3 % and scatter 0.7 % faster).  Rows that end inside a line
 // keep write-back stores: written through, the 656-byte rows of cfg 5 were
 // 7 % slower, their shared lines leaving the L2 once per row.
-template <int VEC, bool INNER, bool WT = false>
+template <int VEC, bool INNER, bool WT = false, bool DM = false>
 __global__ __launch_bounds__(kBlockThreads) void row_flat_kernel(const RowArgs a, const int32_t pieces,
                                                                  const float inv_pieces) {
   using V = typename VecType<VEC>::T;
@@ -138,12 +152,12 @@ __global__ __launch_bounds__(kBlockThreads) void row_flat_kernel(const RowArgs a
   for (int i = static_cast<int>(threadIdx.x); i < nrows; i += kBlockThreads) {
     int64_t so, dof;
     if constexpr (!inner) {
-      resolve_row(a, u0 + i, &so, &dof);
+      resolve_row<DM>(a, u0 + i, &so, &dof);
     } else {
       const int64_t unit = u0 + i;
       const int64_t row = unit / a.num_planes;
       const int plane = static_cast<int>(unit - row * a.num_planes);
-      resolve_row(a, row, &so, &dof);
+      resolve_row<false>(a, row, &so, &dof);
       if (dof != kSkipRow) dof += static_cast<int64_t>(a.dst_planes[plane]);
       if (so != kZeroRow) so += static_cast<int64_t>(a.src_planes[plane]);
     }
@@ -232,7 +246,10 @@ struct SlotRowArgs {
   uint64_t dst_planes[kMaxPlanes];
 };
 
-template <bool SCATTER, int STP>
+// DM (destination-major scatter): unit u is a destination row, its token read
+// from the claim tags (this call's inverse map), so rows are written in
+// address order.
+template <bool SCATTER, int STP, bool DM = false>
 __global__ __launch_bounds__(kBlockThreads) void slot_row_kernel(const SlotRowArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int lane = lane_id();
@@ -247,7 +264,8 @@ __global__ __launch_bounds__(kBlockThreads) void slot_row_kernel(const SlotRowAr
   const int64_t w = static_cast<int64_t>(bx) * kWavesPerBlock + wave;
   const int64_t u = w >> shift;
   const int64_t part = (w - (u << shift)) << 10;
-  const int64_t slot = a.idx[u < a.num_tokens ? u : a.num_tokens - 1];
+  const int64_t slot = DM ? static_cast<int64_t>(a.owner[u < a.dst_rows ? u : a.dst_rows - 1])
+                          : a.idx[u < a.num_tokens ? u : a.num_tokens - 1];
   const uint64_t sbase = a.src_planes[plane];
   const uint64_t dbase = a.dst_planes[plane];
   // Every argument is read before the first (uniform) branch: one batch of scalar loads.
@@ -260,6 +278,14 @@ __global__ __launch_bounds__(kBlockThreads) void slot_row_kernel(const SlotRowAr
     drow = u + a.dst_offset;
     copy = srow >= 0 && srow < a.src_rows;
     live = u < a.num_rows_out && drow >= 0 && drow < a.dst_rows && (copy || a.zero_invalid);
+  } else if constexpr (DM) {
+    // `slot` holds the tag of destination row u (< dst_rows: the grid covers them).
+    const uint64_t tag = static_cast<uint64_t>(slot);
+    srow = static_cast<int64_t>(static_cast<uint32_t>(tag)) - 1 + a.src_offset;
+    drow = u;
+    copy = u < a.dst_rows && static_cast<uint32_t>(tag >> 32) == a.epoch && static_cast<uint32_t>(tag) != 0u &&
+           srow >= 0 && srow < a.src_rows;
+    live = copy;
   } else {
     srow = u + a.src_offset;
     drow = slot;
@@ -400,21 +426,34 @@ hipError_t launch_rows_vec(const RowArgs& a, int64_t planes, hipStream_t stream)
   const int64_t units = a.plane_inner ? a.num_rows_out * planes : a.num_rows_out;
   const int64_t blocks = (units * pieces + kBlockPieces - 1) / kBlockPieces;
   if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
+  const dim3 grid(static_cast<uint32_t>(blocks), static_cast<uint32_t>(planes));
+  const int32_t np = static_cast<int32_t>(pieces);
+  const float inv = 1.0f / static_cast<float>(pieces);
+  const bool wt = VEC == 16 && write_through_rows(a, planes);
   if (a.plane_inner)
     hipLaunchKernelGGL((row_flat_kernel<VEC, true>), dim3(static_cast<uint32_t>(blocks)), dim3(kBlockThreads), 0,
-                       stream, a, static_cast<int32_t>(pieces), 1.0f / static_cast<float>(pieces));
-  else if (VEC == 16 && write_through_rows(a, planes))
-    hipLaunchKernelGGL((row_flat_kernel<16, false, true>),
-                       dim3(static_cast<uint32_t>(blocks), static_cast<uint32_t>(planes)), dim3(kBlockThreads), 0,
-                       stream, a, static_cast<int32_t>(pieces), 1.0f / static_cast<float>(pieces));
+                       stream, a, np, inv);
+  else if (a.dst_major && wt)
+    hipLaunchKernelGGL((row_flat_kernel<16, false, true, true>), grid, dim3(kBlockThreads), 0, stream, a, np, inv);
+  else if (a.dst_major)
+    hipLaunchKernelGGL((row_flat_kernel<VEC, false, false, true>), grid, dim3(kBlockThreads), 0, stream, a, np, inv);
+  else if (wt)
+    hipLaunchKernelGGL((row_flat_kernel<16, false, true>), grid, dim3(kBlockThreads), 0, stream, a, np, inv);
   else
-    hipLaunchKernelGGL((row_flat_kernel<VEC, false>),
-                       dim3(static_cast<uint32_t>(blocks), static_cast<uint32_t>(planes)), dim3(kBlockThreads), 0,
-                       stream, a, static_cast<int32_t>(pieces), 1.0f / static_cast<float>(pieces));
+    hipLaunchKernelGGL((row_flat_kernel<VEC, false>), grid, dim3(kBlockThreads), 0, stream, a, np, inv);
   return hipGetLastError();
 }
 
 }  // namespace
+
+// Scatters whose claim tags are this call's inverse map, with tokens covering
+// at least half of the destination rows, run destination-major: rows written
+// in address order, sources read wherever they are (random writes cost more
+// than random reads on this GPU; each destination row costs one tag read).
+bool dst_major(const RowCopyParams& p) {
+  return p.owner != nullptr && p.owner_exclusive && p.dst_idx != nullptr && p.idx_stride <= 1 &&
+         p.num_tokens * 2 >= p.dst_rows && p.dst_rows <= (int64_t{1} << 32);
+}
 
 hipError_t launch_row_copy(const RowCopyParams& p, hipStream_t stream) {
   if (p.num_rows_out <= 0 || p.num_planes <= 0 || p.row_bytes <= 0) return hipSuccess;
@@ -466,7 +505,8 @@ hipError_t launch_row_copy(const RowCopyParams& p, hipStream_t stream) {
       p.src_page_rows == 0 && p.dst_page_rows == 0 && p.idx_stride <= 1 && !inner && one_indexed &&
       p.num_tokens >= 1) {
     const bool scatter = p.dst_idx != nullptr;
-    const int64_t rows = scatter ? p.num_tokens : p.num_rows_out;
+    const bool dm = scatter && dst_major(p);
+    const int64_t rows = dm ? p.dst_rows : (scatter ? p.num_tokens : p.num_rows_out);
     const int64_t groups = ((rows << shift) + kWavesPerBlock - 1) / kWavesPerBlock;
     if (rows > (int64_t{1} << 40) || groups > 0x7FFFFFFF) return hipErrorInvalidValue;
     for (int64_t base = 0; base < p.num_planes; base += kMaxPlanes) {
@@ -492,7 +532,9 @@ hipError_t launch_row_copy(const RowCopyParams& p, hipStream_t stream) {
       const dim3 grid(static_cast<uint32_t>(groups), static_cast<uint32_t>(n));
       bool lines = p.dst_stride % 128 == 0;
       for (int64_t i = 0; i < n; ++i) lines = lines && a.dst_planes[i] % 128 == 0;
-      if (scatter && lines) hipLaunchKernelGGL((slot_row_kernel<true, kBufWT>), grid, dim3(kBlockThreads), 0, stream, a);
+      if (dm && lines) hipLaunchKernelGGL((slot_row_kernel<true, kBufWT, true>), grid, dim3(kBlockThreads), 0, stream, a);
+      else if (dm) hipLaunchKernelGGL((slot_row_kernel<true, kBufNT, true>), grid, dim3(kBlockThreads), 0, stream, a);
+      else if (scatter && lines) hipLaunchKernelGGL((slot_row_kernel<true, kBufWT>), grid, dim3(kBlockThreads), 0, stream, a);
       else if (scatter) hipLaunchKernelGGL((slot_row_kernel<true, kBufNT>), grid, dim3(kBlockThreads), 0, stream, a);
       else if (lines) hipLaunchKernelGGL((slot_row_kernel<false, kBufWT>), grid, dim3(kBlockThreads), 0, stream, a);
       else hipLaunchKernelGGL((slot_row_kernel<false, kBufNT>), grid, dim3(kBlockThreads), 0, stream, a);
@@ -536,6 +578,10 @@ hipError_t launch_row_copy(const RowCopyParams& p, hipStream_t stream) {
     a.dst_page_rows = p.dst_page_rows;
     a.dst_page_stride = p.dst_page_stride;
     a.plane_inner = inner ? 1 : 0;
+    if (!inner && p.src_indptr == nullptr && dst_major(p)) {
+      a.dst_major = 1;
+      a.num_rows_out = p.dst_rows;
+    }
     hipError_t err;
     switch (vec) {
       case 16: err = launch_rows_vec<16>(a, n, stream); break;
