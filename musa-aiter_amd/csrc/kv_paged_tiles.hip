@@ -100,8 +100,10 @@ constexpr int kChunksPerGroup = SCATTER ? 4 : 2;
 // linear rows of its first token at `lbuf`, both at the workgroup's first
 // row), chunk by chunk with the next chunk's load in flight (2 % faster than
 // issuing every load first when the grid is many rounds of workgroups,
-// measured; their time is the cache writes).  Ends with the LDS tile free.
-template <int ELT, int BS, int NT>
+// measured; their time is the cache writes).  CSTP: cache policy of the
+// stores of runs that fill the whole block (every line of the chunk written
+// at once); partial runs store non-temporally.  Ends with the LDS tile free.
+template <int ELT, int BS, int NT, int CSTP = kBufNT>
 __device__ __forceinline__ void scatter_run_chunks(uint8_t* tile, buf_t cbuf, buf_t lbuf, int c0, int c1,
                                                    int nchunks, int rows_left, uint32_t stride32) {
   using S = CoopShape<ELT, BS, NT>;
@@ -132,7 +134,7 @@ __device__ __forceinline__ void scatter_run_chunks(uint8_t* tile, buf_t cbuf, bu
     const uint32_t off = coff(k);
     const int lo = pg * CG;
     if (full_run) {
-      buf_st16(cbuf, off, w);
+      buf_st16_p<CSTP>(cbuf, off, w);
     } else {
       const bool whole = lo >= c0 && lo + CG <= c1;
       buf_st16(cbuf, whole ? off : kOffOob, w);
@@ -341,7 +343,7 @@ constexpr int kBlockScatterChunks = 2;  // chunks per workgroup of the block-maj
 
 // Grid: x = block * row_groups + group (the row groups of one block next to
 // each other), y = plane.
-template <int ELT, int BS, int NT = kCoopThreads>
+template <int ELT, int BS, int CSTP = kBufNT, int NT = kCoopThreads>
 __global__ __launch_bounds__(NT) void paged_block_scatter_kernel(const TileArgs a) {
   using S = CoopShape<ELT, BS, NT>;
   constexpr int ROWB = S::ROWB, kRows = S::kRows;
@@ -383,7 +385,8 @@ __global__ __launch_bounds__(NT) void paged_block_scatter_kernel(const TileArgs 
     const int len = 1 + __builtin_ctzll(~(cmask >> (c0 + 1)));  // c0 < BS <= 32
     const int64_t tf = readlane64(tok, c0);
     const buf_t lbuf = make_buf(lin + tf * a.lin_token_stride + rb * ELT);
-    scatter_run_chunks<ELT, BS, NT>(tile, cbuf, lbuf, c0, c0 + len, nchunks, static_cast<int>(re - rb), stride32);
+    scatter_run_chunks<ELT, BS, NT, CSTP>(tile, cbuf, lbuf, c0, c0 + len, nchunks, static_cast<int>(re - rb),
+                                          stride32);
   }
 }
 
@@ -512,7 +515,9 @@ hipError_t launch_tile(const TileArgs& a0, int64_t planes, hipStream_t stream) {
       if (nblk * groups <= 0x7FFFFFFF) {
         TileArgs a = a0;
         a.row_groups = static_cast<int32_t>(groups);
-        hipLaunchKernelGGL((paged_block_scatter_kernel<ELT, BS>),
+        // Whole blocks are written through the L2 (kBufWT): +1.1 % on the
+        // configs[1] scatter.
+        hipLaunchKernelGGL((paged_block_scatter_kernel<ELT, BS, kBufWT>),
                            dim3(static_cast<uint32_t>(nblk * groups), static_cast<uint32_t>(planes), 1),
                            dim3(kCoopThreads), 0, stream, a);
         return hipGetLastError();

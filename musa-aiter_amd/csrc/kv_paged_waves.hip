@@ -570,6 +570,8 @@ hipError_t launch_wave_scatter(const TileArgs& a, int64_t planes, hipStream_t st
   const int64_t blocks = (units + kWavesPerBlock - 1) / kWavesPerBlock;
   if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
   const dim3 grid(static_cast<uint32_t>(blocks), static_cast<uint32_t>(planes), static_cast<uint32_t>(chunks));
+  // (Grid z order: the chunks of a block folded next to each other in x, and
+  // write-through cache stores, measured no faster in block order.)
   if (bm)
     hipLaunchKernelGGL((paged_wave_scatter_kernel<ELT_C, ELT_L, CODEC, LDT, BS, true>), grid, dim3(kBlockThreads), 0,
                        stream, a);
