@@ -86,7 +86,8 @@ def _build_host() -> Path:
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
     cmd = [os.environ.get("CXX", "g++"), "-O2", "-shared", "-fPIC", "-std=c++17", "-Wall",
            f"-D_GLIBCXX_USE_CXX11_ABI={abi}", f"-DTORCH_EXTENSION_NAME={HOST_MODULE}",
-           f"-I{sysconfig.get_paths()['include']}", *[f"-I{p}" for p in cpp_extension.include_paths()],
+           f"-I{sysconfig.get_paths()['include']}", f"-I{ROOT.parent / 'include'}",
+           *[f"-I{p}" for p in cpp_extension.include_paths()],
            str(CSRC / HOST_SOURCE), "-o", str(tmp),
            *[f"-L{p}" for p in cpp_extension.library_paths()], "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python"]
     proc = subprocess.run(cmd, capture_output=True, text=True)

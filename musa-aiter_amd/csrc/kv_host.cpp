@@ -17,6 +17,8 @@
 #include <unordered_map>
 #include <vector>
 
+#include "musa_aiter_kv_hip.h"
+
 namespace py = pybind11;
 
 namespace {
@@ -125,6 +127,97 @@ py::tuple object_index(const py::handle& first, const py::handle& second) {
                         distinct);
 }
 
+// One LMCache 2 x NL row copy (lmcache_kv_paged_to_buffer_two_x_nl / _buffer_to_paged_two_x_nl)
+// checked and launched in one pass: the K/V layer caches [NB, BS, NH, HS] of `kvcaches` (a list of
+// two lists) <-> memory [2, NL, M, NH*HS], through musa_aiter_hip_copy_rows_packed (`entry`, its
+// address) on `stream`.  Returns -1, having launched nothing, unless every argument is one the fast
+// path takes as is: a CUDA memory tensor on the current device (`device`) with contiguous rows and
+// dtype float16 / bfloat16 / float32, the reference's contract shapes, contiguous caches of
+// memory's dtype and device, and a contiguous one-dimensional int64 slot tensor on that device; the
+// Python layer then runs its own checks, which raise the reference's errors.  Otherwise returns the
+// HIP status of the launch.  `claims`: address of the scatter's musa_aiter_hip_claims (0 for a
+// gather).  Device-resident slots are not range-checked, as in the reference (the kernels skip
+// slots outside the caches).
+int64_t two_x_nl_rows(const py::handle& kvcaches, const py::handle& memory_obj, const py::handle& slots_obj,
+                      int64_t skip, int64_t block_size, int64_t num_heads, int64_t head_size, bool scatter,
+                      uint64_t entry, uint64_t claims, uint64_t stream, int64_t device) {
+  constexpr int64_t kNo = -1;
+  if (!THPVariable_Check(memory_obj.ptr()) || !THPVariable_Check(slots_obj.ptr())) return kNo;
+  const at::Tensor& mem = THPVariable_Unpack(memory_obj.ptr());
+  const at::Tensor& slots = THPVariable_Unpack(slots_obj.ptr());
+  if (!mem.is_cuda() || mem.device().index() != device || mem.dim() != 4 || mem.size(0) != 2) return kNo;
+  const at::ScalarType dt = mem.scalar_type();
+  if (dt != at::kHalf && dt != at::kBFloat16 && dt != at::kFloat) return kNo;
+  if (block_size <= 0 || num_heads <= 0 || head_size <= 0 || mem.size(3) != num_heads * head_size) return kNo;
+  if (mem.stride(3) != 1 && mem.size(3) != 1) return kNo;
+  if (slots.scalar_type() != at::kLong || slots.dim() != 1 || !slots.is_contiguous() || slots.device() != mem.device())
+    return kNo;
+  PyObject* const groups = kvcaches.ptr();
+  if (!PyList_Check(groups) || PyList_GET_SIZE(groups) != 2) return kNo;
+  PyObject* const kl = PyList_GET_ITEM(groups, 0);
+  PyObject* const vl = PyList_GET_ITEM(groups, 1);
+  if (!PyList_Check(kl) || !PyList_Check(vl)) return kNo;
+  const Py_ssize_t nl = PyList_GET_SIZE(kl);
+  if (nl <= 0 || PyList_GET_SIZE(vl) != nl || mem.size(1) != nl) return kNo;
+  const int64_t t = slots.size(0);
+  const int64_t m = mem.size(2);
+  if (skip < 0 || (!scatter && skip != 0) || skip + t > m) return kNo;
+  if (nl > 64) return kNo;  // the plane tables below hold 2 x 64 planes
+  uint64_t caches[128], buffer[128];
+  int64_t nb = -1;
+  for (int axis = 0; axis < 2; ++axis) {
+    PyObject* const grp = axis == 0 ? kl : vl;
+    for (Py_ssize_t l = 0; l < nl; ++l) {
+      PyObject* const obj = PyList_GET_ITEM(grp, l);
+      if (!THPVariable_Check(obj)) return kNo;
+      const at::Tensor& c = THPVariable_Unpack(obj);
+      if (c.dim() != 4) return kNo;
+      if (nb < 0) nb = c.size(0);
+      if (nb <= 0 || c.size(0) != nb || c.size(1) != block_size || c.size(2) != num_heads || c.size(3) != head_size ||
+          c.scalar_type() != dt || c.device() != mem.device() || !c.is_contiguous())
+        return kNo;
+      caches[axis * nl + l] = reinterpret_cast<uint64_t>(c.data_ptr());
+    }
+  }
+  const int64_t elt = mem.element_size();
+  const int64_t row = num_heads * head_size * elt;
+  const uint64_t base = reinterpret_cast<uint64_t>(mem.data_ptr());
+  for (int axis = 0; axis < 2; ++axis)
+    for (Py_ssize_t l = 0; l < nl; ++l)
+      buffer[axis * nl + l] = base + static_cast<uint64_t>((axis * mem.stride(0) + l * mem.stride(1)) * elt);
+  const int64_t token_stride = (m > 1 ? mem.stride(2) : mem.size(3)) * elt;
+  if (t == 0 && scatter) return 0;
+  musa_aiter_hip_copy_rows_call call{};
+  call.num_planes = 2 * nl;
+  call.num_tokens = t;
+  call.row_bytes = row;
+  if (scatter) {
+    call.src_planes = buffer;
+    call.dst_planes = caches;
+    call.dst_idx = static_cast<const int64_t*>(slots.data_ptr());
+    call.num_rows_out = t;
+    call.src_offset = skip;
+    call.src_rows = m;
+    call.dst_rows = nb * block_size;
+    call.src_stride = token_stride;
+    call.dst_stride = row;
+    call.dedupe = 1;
+    call.claims = reinterpret_cast<const musa_aiter_hip_claims*>(claims);
+  } else {
+    call.src_planes = caches;
+    call.dst_planes = buffer;
+    call.src_idx = static_cast<const int64_t*>(slots.data_ptr());
+    call.num_rows_out = m;
+    call.src_rows = nb * block_size;
+    call.dst_rows = m;
+    call.src_stride = row;
+    call.dst_stride = token_stride;
+    call.zero_invalid = 1;
+  }
+  using Entry = int (*)(const musa_aiter_hip_copy_rows_call*, void*);
+  return reinterpret_cast<Entry>(entry)(&call, reinterpret_cast<void*>(stream));
+}
+
 }  // namespace
 
 PYBIND11_MODULE(_kv_host, m) {
@@ -133,6 +226,7 @@ PYBIND11_MODULE(_kv_host, m) {
   m.def("strided_table", &strided_table);
   m.def("int64_column", &int64_column, py::arg("items"));
   m.def("object_index", &object_index, py::arg("first"), py::arg("second"));
+  m.def("two_x_nl_rows", &two_x_nl_rows);
   m.attr("OK") = static_cast<int>(kOk);
   m.attr("SHAPE") = static_cast<int>(kShape);
   m.attr("DTYPE") = static_cast<int>(kDtype);

@@ -14,6 +14,20 @@ from dataclasses import dataclass
 from typing import Any
 
 _TRUTHY = {"1", "true", "TRUE", "yes", "YES"}
+_TRUTHY_BYTES = {v.encode() for v in _TRUTHY}
+
+# os.environ's backing dict (bytes keys and values on POSIX), read directly on hot paths: a lookup
+# costs about 50 ns against 0.4 us through os.environ.get, and changes made through os.environ
+# (os.environ[...] = ..., monkeypatch.setenv) are seen at once, as they are through os.environ.
+_ENV_BYTES = getattr(os.environ, "_data", None) if os.name == "posix" else None
+
+
+def env_bytes(key: bytes, default: bytes) -> bytes:
+    """The value of environment variable ``key`` (bytes), or ``default``."""
+    if _ENV_BYTES is None:
+        value = os.environ.get(key.decode())
+        return default if value is None else value.encode()
+    return _ENV_BYTES.get(key, default)
 
 
 @dataclass(frozen=True)
@@ -26,7 +40,7 @@ class DispatchRecord:
 
 
 def trace_enabled() -> bool:
-    return os.environ.get("MUSA_AITER_TRACE_DISPATCH", "0") in _TRUTHY
+    return env_bytes(b"MUSA_AITER_TRACE_DISPATCH", b"0") in _TRUTHY_BYTES
 
 
 def emit(record: DispatchRecord) -> None:
