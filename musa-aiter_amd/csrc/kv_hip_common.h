@@ -417,12 +417,19 @@ __device__ __forceinline__ uint32_t fp8_encode_fast(float w) {
 // gives 0x7F|sign, the reference's 480 clamp byte); E5M2 matches up to its
 // largest normal 57344, above which the reference keeps exponent-31 codes and
 // the callers must use fp8_encode_fast instead.
+//
+// The flush is w * step, step = clamp(|w| * 2^24 / m - (2^24 - 1), 0, 1) for the
+// smallest normal m = 2^E: one fma (exact up to its single rounding; the
+// product and the constant are exact) whose result is <= 0 exactly when
+// |w| <= pred(m) = m - m * 2^-24 and >= 1 when |w| >= m, clamped by the
+// instruction's clamp bit; w * +0 keeps w's sign.  Two VALU operations and no
+// lane mask, where a compare and a select need three and a wait state.
+// Checked against the compare-and-select form on every finite fp32 value.
 template <int CODEC>
 __device__ __forceinline__ float fp8_flush_small(float w) {
-  // |w| < minnorm as one float compare (abs is a free source modifier).
-  return (__builtin_fabsf(w) < __uint_as_float(Fp8Fmt<CODEC>::kMinNormBits))
-             ? __uint_as_float(__float_as_uint(w) & 0x80000000u)
-             : w;
+  constexpr float kBig = (CODEC == kE4M3) ? 0x1p30f : 0x1p38f;  // 2^24 / m
+  const float t = __builtin_fmaf(__builtin_fabsf(w), kBig, -16777215.0f);
+  return w * __builtin_amdgcn_fmed3f(t, 0.0f, 1.0f);
 }
 
 template <int CODEC>
