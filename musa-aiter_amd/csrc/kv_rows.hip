@@ -450,9 +450,12 @@ hipError_t launch_rows_vec(const RowArgs& a, int64_t planes, hipStream_t stream)
 // at least half of the destination rows, run destination-major: rows written
 // in address order, sources read wherever they are (random writes cost more
 // than random reads on this GPU; each destination row costs one tag read).
+// Paged destinations (page-first HiCache tensors, whose rows of one plane sit
+// a page stride apart) keep token order: the direct all-layer transfer ran
+// 1.42 ms token-major against 1.54 ms destination-major.
 bool dst_major(const RowCopyParams& p) {
   return p.owner != nullptr && p.owner_exclusive && p.dst_idx != nullptr && p.idx_stride <= 1 &&
-         p.num_tokens * 2 >= p.dst_rows && p.dst_rows <= (int64_t{1} << 32);
+         p.dst_page_rows == 0 && p.num_tokens * 2 >= p.dst_rows && p.dst_rows <= (int64_t{1} << 32);
 }
 
 hipError_t launch_row_copy(const RowCopyParams& p, hipStream_t stream) {
