@@ -129,26 +129,10 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_gather_kernel(const 
   const int64_t r0 = static_cast<int64_t>(blockIdx.z) * kChunkRows;  // this wave's cache rows
   const int64_t r_end = (r0 + kChunkRows < a.nrows) ? r0 + kChunkRows : a.nrows;
 
-  // Slot window: lane i holds token t0 - 1 + i (loaded before the table is
-  // built, so that the two loads overlap).
+  // Slot window: lane i holds token t0 - 1 + i, and the runs of the tile.
   const int64_t t = t0 - 1 + lane;
   int64_t s = -1;
   if (t >= 0 && t < a.num_tokens) s = slot_at(a, t);
-
-  // The workgroup's decode tables: its waves share the chunk (grid z), so the
-  // heads h_lo .. of rows [r0, r_end) (one table for a scalar scale).  The
-  // launcher routes chunks spanning more than kLutHeads heads elsewhere.
-  const int h_lo = (kLut && a.scale_mode != 0) ? head_of_row(a, static_cast<int>(r0)) : 0;
-  if constexpr (kLut) {
-    const int nh = a.scale_mode != 0 ? head_of_row(a, static_cast<int>(r_end - 1)) - h_lo + 1 : 1;
-    for (int e = static_cast<int>(threadIdx.x); e < nh * 256; e += kBlockThreads)
-      lut_all[e] = lut_value<CODEC, LDT, LutT>(static_cast<uint32_t>(e & 255), load_scale(a, kv, layer, h_lo + (e >> 8)));
-    __syncthreads();
-  }
-  if (t0 >= a.num_tokens) return;
-  uint8_t* const cache = a.cache[kv] + static_cast<int64_t>(layer) * a.cache_layer_stride;
-  uint8_t* const lin = a.lin[kv] + static_cast<int64_t>(layer) * a.lin_layer_stride;
-
   const bool valid = (s >= 0) && (s < a.num_slots);
   const uint64_t vmask = ballot(valid);
   const int64_t s_prev = from_prev_lane(s);
@@ -156,14 +140,68 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_gather_kernel(const 
   const bool cont = valid && prev_valid && (s == s_prev + 1) && ((s % BS) != 0);
   const uint64_t cmask = ballot(cont);
   const int64_t remaining = a.num_tokens - t0;
-  const int ntile = remaining < kTileTokens ? static_cast<int>(remaining) : kTileTokens;
+  const int ntile = remaining <= 0 ? 0 : (remaining < kTileTokens ? static_cast<int>(remaining) : kTileTokens);
   const uint64_t window = ((1ull << ntile) - 1ull) << 1;
   uint64_t heads = vmask & ~cmask & window;
 
+  uint8_t* const cache = a.cache[kv] + static_cast<int64_t>(layer) * a.cache_layer_stride;
+  uint8_t* const lin = a.lin[kv] + static_cast<int64_t>(layer) * a.lin_layer_stride;
   const int rg = lane / NCG;  // lane tile: rows r0 + rg*RPL .., column group ct
   const int ct = lane % NCG;
   const int64_t trow = r0 + rg * RPL;
   const bool tile_in = trow < r_end;
+  const uint32_t toff = static_cast<uint32_t>((rg * RPL * NCG + ct) * 16);
+
+  // One run starting at lane i of the window: its block, columns and first token.
+  struct Run {
+    int64_t blk, tf;
+    int c0, c1;
+  };
+  auto run_at = [&](int i) {
+    const int len = 1 + __builtin_ctzll(~(cmask >> (i + 1)));  // i <= kTileTokens < 63
+    const int64_t sh = readlane64(s, i);
+    const int64_t blk = sh / BS;
+    const int c0 = static_cast<int>(sh - blk * BS);
+    return Run{blk, t0 - 1 + i, c0, c0 + len};
+  };
+  auto whole_chunk = [&](const Run& r) { return r.c0 < CG && r.c1 > BS - CG; };
+  // FP8: each lane loads its own tile, RPL pieces 16 * NCG bytes apart.  A wave
+  // instruction touches 64 lines partially; the loads are cached so that the L2
+  // serves the rest of each line to the wave's next instructions.
+  auto load_tile = [&](const Run& r, u32x4 (&d)[RPL]) {
+    const buf_t cb = make_buf(cache + (r.blk * a.nrows + r0) * BS * ELT_C);
+#pragma unroll
+    for (int q = 0; q < RPL; ++q)
+      d[q] = buf_ld16_cached(cb, tile_in ? toff + static_cast<uint32_t>(q * NCG * 16) : kOffOob);
+  };
+
+  // FP8: the first run's tile is loaded before the workgroup builds its decode
+  // tables, so that the table work overlaps the loads' latency.
+  u32x4 d[RPL];
+  bool have_pre = false;
+  if constexpr (kLut) {
+    if (heads != 0) {
+      const Run r = run_at(__builtin_ctzll(heads));
+      if (whole_chunk(r)) {
+        load_tile(r, d);
+        have_pre = true;
+      }
+    }
+  }
+
+  // The workgroup's decode tables: its waves share the chunk (grid z), so the
+  // heads h_lo .. of rows [r0, r_end) (one table for a scalar scale).  The
+  // launcher routes chunks spanning more than kLutHeads heads elsewhere.
+  const int h_lo = (kLut && a.scale_mode != 0) ? head_of_row(a, static_cast<int>(r0)) : 0;
+  if constexpr (kLut) {
+    const int nh = a.scale_mode != 0 ? head_of_row(a, static_cast<int>(r_end - 1)) - h_lo + 1 : 1;
+#pragma unroll 1
+    for (int e = static_cast<int>(threadIdx.x); e < nh * 256; e += kBlockThreads)
+      lut_all[e] = lut_value<CODEC, LDT, LutT>(static_cast<uint32_t>(e & 255), load_scale(a, kv, layer, h_lo + (e >> 8)));
+    __syncthreads();
+  }
+  if (t0 >= a.num_tokens) return;
+
   // The lane's table: all RPL rows of its tile lie in one head (head_dim is a
   // multiple of RPL on this path).
   const LutT* lut = lut_all;
@@ -172,23 +210,19 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_gather_kernel(const 
   while (heads) {
     const int i = __builtin_ctzll(heads);
     heads &= heads - 1;
-    const uint64_t after = cmask >> (i + 1);  // i <= kTileTokens < 63
-    const int len = 1 + __builtin_ctzll(~after);
-    const int64_t sh = readlane64(s, i);
-    const int64_t blk = sh / BS;
-    const int c0 = static_cast<int>(sh - blk * BS);
-    const int c1 = c0 + len;
-    const int64_t tf = t0 - 1 + i;
-    uint8_t* const chunk = cache + (blk * a.nrows + r0) * BS * ELT_C;
-    if (c0 < CG && c1 > BS - CG) {
-      // The run touches every column group: stage the whole chunk.  Loads and
-      // stores go through wave-uniform buffer descriptors with per-lane 32-bit
-      // offsets (kOffOob for masked lanes): no per-lane branches and no shared
-      // 64-bit address registers, so the compiler issues all RPL loads back to
-      // back and never waits on one access before the next address.
-      const buf_t cb = make_buf(chunk);
-      u32x4 d[RPL];
+    const Run r = run_at(i);
+    const int64_t blk = r.blk;
+    const int c0 = r.c0;
+    const int c1 = r.c1;
+    const int64_t tf = r.tf;
+    if (whole_chunk(r)) {
+      // The run touches every column group: the whole chunk.  Loads and stores
+      // go through wave-uniform buffer descriptors with per-lane 32-bit offsets
+      // (kOffOob for masked lanes): no per-lane branches and no shared 64-bit
+      // address registers, so the compiler issues all RPL loads back to back
+      // and never waits on one access before the next address.
       if constexpr (kStage) {
+        const buf_t cb = make_buf(cache + (blk * a.nrows + r0) * BS * ELT_C);
         u32x4 v[RPL];
 #pragma unroll
         for (int k = 0; k < RPL; ++k) {
@@ -202,13 +236,8 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_gather_kernel(const 
         for (int q = 0; q < RPL; ++q) d[q] = lds[lds_slot<RPL, NCG>((rg * RPL + q) * NCG + ct)];
         wave_lds_sync();
       } else {
-        // Each lane loads its own tile: RPL pieces 16 * NCG bytes apart.  A wave
-        // instruction touches 64 lines partially; the loads are cached so that
-        // the L2 serves the rest of each line to the wave's next instructions.
-        const uint32_t toff = static_cast<uint32_t>((rg * RPL * NCG + ct) * 16);
-#pragma unroll
-        for (int q = 0; q < RPL; ++q)
-          d[q] = buf_ld16_cached(cb, tile_in ? toff + static_cast<uint32_t>(q * NCG * 16) : kOffOob);
+        if (!have_pre) load_tile(r, d);  // the first run's tile is already loaded
+        have_pre = false;
       }
       // The run's first token row at row r0; the lane's rows start rg * RPL
       // further.  Token offsets stay below 2 GiB (token stride <= 32 MiB).
