@@ -423,6 +423,31 @@ int lmcache_paged_to_kv_buffer_list2_u16(void* memory_tensor, const void* kvcach
                                          const int64_t* slot_mapping, int64_t memory_tokens, int64_t num_tokens,
                                          int64_t skip_prefix, int64_t num_blocks, int64_t block_size,
                                          int64_t num_heads, int64_t head_size, void* stream);
+/* The reference extension's kernel variants of the list2 transfer (lmcache_kv_transfer_ext.cpp:42-125:
+ * _coalesced, _contiguous, _contiguous_bulk, _torchmusa_style, _sorted), which it selects by environment
+ * variable and which all move the same bytes: here each is the list2 entry above, with the same
+ * arguments (the _sorted gather's sort order of the slots is accepted and not needed). */
+int lmcache_kv_buffer_to_paged_list2_u16_coalesced(const void* memory_tensor, void* kvcache0, void* kvcache1,
+                                                   const int64_t* slot_mapping, int64_t memory_tokens,
+                                                   int64_t num_tokens, int64_t skip_prefix, int64_t num_blocks,
+                                                   int64_t block_size, int64_t num_heads, int64_t head_size,
+                                                   void* stream);
+#define MUSA_AITER_KV_HIP_LIST2_GATHER_VARIANT(VARIANT)                                                           \
+  int lmcache_paged_to_kv_buffer_list2_u16_##VARIANT(void* memory_tensor, const void* kvcache0,                  \
+                                                     const void* kvcache1, const int64_t* slot_mapping,           \
+                                                     int64_t memory_tokens, int64_t num_tokens, int64_t skip_prefix, \
+                                                     int64_t num_blocks, int64_t block_size, int64_t num_heads,   \
+                                                     int64_t head_size, void* stream);
+MUSA_AITER_KV_HIP_LIST2_GATHER_VARIANT(coalesced)
+MUSA_AITER_KV_HIP_LIST2_GATHER_VARIANT(contiguous)
+MUSA_AITER_KV_HIP_LIST2_GATHER_VARIANT(contiguous_bulk)
+MUSA_AITER_KV_HIP_LIST2_GATHER_VARIANT(torchmusa_style)
+#undef MUSA_AITER_KV_HIP_LIST2_GATHER_VARIANT
+int lmcache_paged_to_kv_buffer_list2_u16_sorted(void* memory_tensor, const void* kvcache0, const void* kvcache1,
+                                                const int64_t* slot_mapping, const uint8_t* sorted_indices_bytes,
+                                                int64_t memory_tokens, int64_t num_tokens, int64_t skip_prefix,
+                                                int64_t num_blocks, int64_t block_size, int64_t num_heads,
+                                                int64_t head_size, void* stream);
 
 /* ---- LMCache MLA per-layer lists [NB,BS,HS] <-> [1,NL,M,HS] (binding lmcache_kv_transfer.py:920-950;
  * replaces lmcache_kv_transfer_extended.mu:541-575) ---- */

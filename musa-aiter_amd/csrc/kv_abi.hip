@@ -1144,6 +1144,41 @@ int lmcache_paged_to_kv_buffer_list2_u16(void* memory_tensor, const void* kvcach
                num_blocks, block_size, num_heads, head_size, stream);
 }
 
+// The reference extension's list2 kernel variants (lmcache_kv_transfer_ext.cpp:42-125) move the same
+// bytes; they all run the list2 transfer above.
+int lmcache_kv_buffer_to_paged_list2_u16_coalesced(const void* memory_tensor, void* kvcache0, void* kvcache1,
+                                                   const int64_t* slot_mapping, int64_t memory_tokens,
+                                                   int64_t num_tokens, int64_t skip_prefix, int64_t num_blocks,
+                                                   int64_t block_size, int64_t num_heads, int64_t head_size,
+                                                   void* stream) {
+  return list2(1, memory_tensor, kvcache0, kvcache1, slot_mapping, memory_tokens, num_tokens, skip_prefix,
+               num_blocks, block_size, num_heads, head_size, stream);
+}
+
+#define KVHIP_LIST2_GATHER_VARIANT(VARIANT)                                                                       \
+  int lmcache_paged_to_kv_buffer_list2_u16_##VARIANT(void* memory_tensor, const void* kvcache0,                  \
+                                                     const void* kvcache1, const int64_t* slot_mapping,           \
+                                                     int64_t memory_tokens, int64_t num_tokens, int64_t skip_prefix, \
+                                                     int64_t num_blocks, int64_t block_size, int64_t num_heads,   \
+                                                     int64_t head_size, void* stream) {                           \
+    return list2(0, memory_tensor, kvcache0, kvcache1, slot_mapping, memory_tokens, num_tokens, skip_prefix,      \
+                 num_blocks, block_size, num_heads, head_size, stream);                                           \
+  }
+KVHIP_LIST2_GATHER_VARIANT(coalesced)
+KVHIP_LIST2_GATHER_VARIANT(contiguous)
+KVHIP_LIST2_GATHER_VARIANT(contiguous_bulk)
+KVHIP_LIST2_GATHER_VARIANT(torchmusa_style)
+#undef KVHIP_LIST2_GATHER_VARIANT
+
+int lmcache_paged_to_kv_buffer_list2_u16_sorted(void* memory_tensor, const void* kvcache0, const void* kvcache1,
+                                                const int64_t* slot_mapping, const uint8_t* /*sorted_indices_bytes*/,
+                                                int64_t memory_tokens, int64_t num_tokens, int64_t skip_prefix,
+                                                int64_t num_blocks, int64_t block_size, int64_t num_heads,
+                                                int64_t head_size, void* stream) {
+  return list2(0, memory_tensor, kvcache0, kvcache1, slot_mapping, memory_tokens, num_tokens, skip_prefix,
+               num_blocks, block_size, num_heads, head_size, stream);
+}
+
 // ----- LMCache MLA list caches [NB, BS, HS] <-> [1, NL, M, HS] (lmcache_kv_transfer.py:920-950) -----
 
 #define KVHIP_MLA_LIST(SUFFIX, ELT)                                                                               \

@@ -37,7 +37,7 @@ def _declared_symbols() -> set[str]:
 
 def test_header_declares_expected_families():
     names = _declared_symbols()
-    assert len(names) == 120
+    assert len(names) == 126
     for required in ("musa_aiter_kv_load_and_reshape_flash_half", "musa_aiter_kv_triton_indexed_to_dense_bfloat16",
                      "musa_aiter_kv_reshape_and_cache_back_flash_float", "musa_aiter_kv_copy_paged_blocks_fp8_vec8",
                      "musa_aiter_hip_paged_dense_tiles","musa_aiter_kv_paged_to_linear_bfloat16", "musa_aiter_kv_linear_to_paged_multi_layer_half",

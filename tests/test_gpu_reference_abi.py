@@ -443,6 +443,46 @@ def test_list_and_list2_entries(suffix, dtype):
         assert np.array_equal(bits(kv[layer]).reshape(2, nb * bs, hidden), wkv[layer])
 
 
+@pytest.mark.parametrize("variant", ["coalesced", "contiguous", "contiguous_bulk", "torchmusa_style", "sorted"])
+def test_list2_kernel_variant_entries(variant):
+    # The reference extension's list2 kernel variants (lmcache_kv_transfer_ext.cpp:42-125), called with its
+    # argument orders; the sorted gather also receives the int32 sort order the extension computes.
+    nb, bs, nh, hs, t, skip = 11, 16, 4, 32, 90, 3
+    hidden, m = nh * hs, t + skip + 4
+    rng = np.random.default_rng(9)
+    gslots, dslots = _slots(rng, nb, bs, t, dup=False), _slots(rng, nb, bs, t, dup=True)
+    g_d, d_d = _dev(gslots), _dev(dslots)
+    gv, dv = _inside(gslots, nb, bs), _inside(dslots, nb, bs)
+    kv = [_payload((2, nb, bs, nh, hs), torch.bfloat16, 150 + layer) for layer in range(2)]
+    mem = _payload((2, 2, m, hidden), torch.bfloat16, 160)
+    want = bits(mem).copy()
+    name = f"lmcache_paged_to_kv_buffer_list2_u16_{variant}"
+    if variant == "sorted":
+        order = torch.sort(g_d, stable=False).indices.to(torch.int32)
+        fn = _bind(name, [P] * 5 + [I64] * 7 + [P])
+        rc = fn(mem.data_ptr(), kv[0].data_ptr(), kv[1].data_ptr(), g_d.data_ptr(), order.data_ptr(), m, t, skip, nb,
+                bs, nh, hs, _stream())
+    else:
+        fn = _bind(name, [P] * 4 + [I64] * 7 + [P])
+        rc = fn(mem.data_ptr(), kv[0].data_ptr(), kv[1].data_ptr(), g_d.data_ptr(), m, t, skip, nb, bs, nh, hs,
+                _stream())
+    assert rc == 0
+    for layer in range(2):
+        for a in range(2):
+            _gather_rows(bits(kv[layer])[a].reshape(nb * bs, hidden), gv, want[a, layer], skip)
+    assert np.array_equal(bits(mem), want)
+    if variant != "coalesced":
+        return
+    wkv = [bits(c).copy().reshape(2, nb * bs, hidden) for c in kv]
+    fn = _bind("lmcache_kv_buffer_to_paged_list2_u16_coalesced", [P] * 4 + [I64] * 7 + [P])
+    assert fn(mem.data_ptr(), kv[0].data_ptr(), kv[1].data_ptr(), d_d.data_ptr(), m, t, skip, nb, bs, nh, hs,
+              _stream()) == 0
+    for layer in range(2):
+        for a in range(2):
+            _scatter_rows(want[a, layer], dv, wkv[layer][a], skip)
+        assert np.array_equal(bits(kv[layer]).reshape(2, nb * bs, hidden), wkv[layer])
+
+
 @pytest.mark.parametrize("suffix,dtype", [("float", torch.float32), ("half", torch.float16),
                                           ("bfloat16", torch.bfloat16), ("u16", torch.bfloat16)])
 def test_mla_list_entries(suffix, dtype):
