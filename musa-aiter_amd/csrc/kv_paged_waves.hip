@@ -384,10 +384,12 @@ __device__ __forceinline__ float tile_elem(const u32x4& piece, int q) {
   else return __uint_as_float(piece[q]);
 }
 
-// BM (block-major): the waves visit cache blocks in block order instead of
-// token tiles (wave w of the grid owns block w), reading each block's claim
-// tags as the inverse map of the scatter (see paged_block_scatter_kernel):
-// the cache is then written in address order.
+// BM (block-major): the workgroups visit cache blocks in block order instead
+// of token tiles (workgroup x owns block x, its four waves four consecutive
+// row chunks of it), reading each block's claim tags as the inverse map of the
+// scatter (see paged_block_scatter_kernel): the cache is then written in
+// address order, and a workgroup reads its block's linear rows and writes its
+// cache bytes as one contiguous span each.
 template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS, bool BM>
 __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const TileArgs a) {
   static_assert(ELT_C == 1 && CODEC != kCopy, "the per-wave scatter quantises into one-byte caches");
@@ -399,19 +401,39 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const
   u32x4* const lds = lds_all + wave_in_block() * kPieces;
 
   const int lane = lane_id();
-  const int64_t unit = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();  // tile or block
+  // Token order: wave w of workgroup x owns tile 4x + w, grid z its chunk.
+  // Block order: workgroup x owns block x, its waves consecutive chunks.
+  const int64_t unit = BM ? static_cast<int64_t>(blockIdx.x)
+                          : static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();
+  const int chunk = BM ? static_cast<int>(blockIdx.z) * kWavesPerBlock + wave_in_block() : static_cast<int>(blockIdx.z);
   const int plane = static_cast<int>(blockIdx.y);
   const int layer = plane >> 1;
   const int kv = plane & 1;
   uint8_t* const cache = a.cache[kv] + static_cast<int64_t>(layer) * a.cache_layer_stride;
   const uint8_t* const lin = a.lin[kv] + static_cast<int64_t>(layer) * a.lin_layer_stride;
   // This wave's cache rows: up to W::kWaveChunks chunks of kChunkRows rows.
-  const int rw0 = static_cast<int>(blockIdx.z) * (kChunkRows * W::kWaveChunks);
+  const int rw0 = chunk * (kChunkRows * W::kWaveChunks);
+  if (rw0 >= a.nrows) return;
   const int rw_end = (rw0 + kChunkRows * W::kWaveChunks < a.nrows) ? rw0 + kChunkRows * W::kWaveChunks
                                                                     : static_cast<int>(a.nrows);
 
+  // Lane tile: rows trow .. trow + RPL - 1 of the chunk, block columns lo .. lo + COLS - 1.
+  const int half = lane & 1;
+  const int rg = (lane >> 1) / NCG;
+  const int ct = (lane >> 1) % NCG;
+  const int lo = ct * CG + half * COLS;
+  // The scale of the lane's rows in a chunk (1 for lanes past its end).  The
+  // first chunk's is loaded before the slots or tags, so that the two loads
+  // overlap instead of adding their latencies ahead of the linear loads.
+  auto chunk_scale = [&](int r0) {
+    const int r_end = (r0 + kChunkRows < rw_end) ? r0 + kChunkRows : rw_end;
+    const int trow = r0 + rg * RPL;
+    return trow < r_end ? load_scale(a, kv, layer, head_of_row(a, trow)) : 1.0f;
+  };
+  const float sc_first = chunk_scale(rw0);
+
   // Runs: `heads` marks the first lane of each, `cmask` the lanes continuing
-  // one, `first` gives a run's (block, first column, first token).
+  // one.
   uint64_t heads, cmask;
   int64_t s = -1, tok = -1;
   const int64_t t0 = unit * kTileTokens;
@@ -445,12 +467,6 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const
     heads = vmask & ~cmask;
   }
   if (heads == 0) return;
-
-  // Lane tile: rows trow .. trow + RPL - 1 of the chunk, block columns lo .. lo + COLS - 1.
-  const int half = lane & 1;
-  const int rg = (lane >> 1) / NCG;
-  const int ct = (lane >> 1) % NCG;
-  const int lo = ct * CG + half * COLS;
   u32x2* const lds_half = reinterpret_cast<u32x2*>(lds) + half;
 
 #pragma unroll 1
@@ -458,8 +474,7 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const
     const int r_end = (r0 + kChunkRows < rw_end) ? r0 + kChunkRows : rw_end;
     const int trow = r0 + rg * RPL;
     const bool tile_in = trow < r_end;
-    float sc = 1.0f;
-    if (tile_in) sc = load_scale(a, kv, layer, head_of_row(a, trow));
+    const float sc = r0 == rw0 ? sc_first : chunk_scale(r0);
     const bool scale_ok = fast_scale_ok(sc);
     const float r = scale_ok ? 1.0f / sc : 0.0f;
 
@@ -577,7 +592,11 @@ hipError_t launch_wave_gather(const TileArgs& a, int64_t planes, hipStream_t str
   if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
   const dim3 grid(static_cast<uint32_t>(blocks), static_cast<uint32_t>(planes), static_cast<uint32_t>(chunks));
   // Linear rows of whole lines are written through the L2 (cfg 3
-  // dequant-gather 5.39 -> 5.48 TB/s, caches read from HBM).
+  // dequant-gather 5.39 -> 5.48 TB/s, caches read from HBM).  The kernel
+  // runs 4 waves per SIMD (97 VGPRs): with 5 (95 VGPRs, scales loaded in one
+  // batch) it measured 2-5 % slower, with 3 (LDS-limited) within 1.5 %, and
+  // staging the tiles through LDS with whole-line loads gained 1.6 % on cfg 3
+  // but lost 6 % on the dense FP8 preload.
   if (whole_line_rows(a, ELT_L))
     hipLaunchKernelGGL((paged_wave_gather_kernel<ELT_C, ELT_L, CODEC, LDT, BS, kBufWT>), grid, dim3(kBlockThreads), 0,
                        stream, a);
@@ -595,12 +614,19 @@ hipError_t launch_wave_scatter(const TileArgs& a, int64_t planes, hipStream_t st
   // Block order when the claim tags are this call's inverse map and the tokens
   // cover a good share of the slots (as for the 16- and 32-bit scatter).
   const bool bm = a.owner != nullptr && a.owner_exclusive && a.num_tokens * 4 >= a.num_slots;
-  const int64_t units = bm ? a.num_slots / BS : (a.num_tokens + kTileTokens - 1) / kTileTokens;
-  const int64_t blocks = (units + kWavesPerBlock - 1) / kWavesPerBlock;
+  const int64_t blocks = bm ? a.num_slots / BS : ((a.num_tokens + kTileTokens - 1) / kTileTokens + kWavesPerBlock - 1) /
+                                                     kWavesPerBlock;
+  const int64_t zs = bm ? (chunks + kWavesPerBlock - 1) / kWavesPerBlock : chunks;
   if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
-  const dim3 grid(static_cast<uint32_t>(blocks), static_cast<uint32_t>(planes), static_cast<uint32_t>(chunks));
-  // (Grid z order: the chunks of a block folded next to each other in x, and
-  // write-through cache stores, measured no faster in block order.)
+  const dim3 grid(static_cast<uint32_t>(blocks), static_cast<uint32_t>(planes), static_cast<uint32_t>(zs));
+  // In block order one workgroup takes one block (grid z covers chunks past
+  // the fourth) and the lane's scale load is issued before the tag load: on
+  // configs[2]'s quant-store 5.04-5.16 -> 5.21-5.38 TB/s, where either change
+  // alone measured no faster.  Slower in the same runs: two or four blocks per
+  // wave under one tag load (-2 % / -7 %), four lanes per 16-byte group (69
+  // VGPRs, 7 waves per SIMD; -2 %), at most 4 or 3 workgroups per CU (-2 % /
+  // -9 %), cached or sc0 linear loads (-4 %), write-back cache stores (-8 %);
+  // write-through stores were level.
   if (bm)
     hipLaunchKernelGGL((paged_wave_scatter_kernel<ELT_C, ELT_L, CODEC, LDT, BS, true>), grid, dim3(kBlockThreads), 0,
                        stream, a);
