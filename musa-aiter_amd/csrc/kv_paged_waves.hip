@@ -624,7 +624,8 @@ hipError_t launch_wave_scatter(const TileArgs& a, int64_t planes, hipStream_t st
   // configs[2]'s quant-store 5.04-5.16 -> 5.21-5.38 TB/s, where either change
   // alone measured no faster.  Slower in the same runs: two or four blocks per
   // wave under one tag load (-2 % / -7 %), four lanes per 16-byte group (69
-  // VGPRs, 7 waves per SIMD; -2 %), at most 4 or 3 workgroups per CU (-2 % /
+  // VGPRs, 7 waves per SIMD; -2 %), one lane per group (whole 1 KiB loads,
+  // 142 VGPRs, 3 waves per SIMD; -6 %), at most 4 or 3 workgroups per CU (-2 % /
   // -9 %), cached or sc0 linear loads (-4 %), write-back cache stores (-8 %);
   // write-through stores were level.
   if (bm)
