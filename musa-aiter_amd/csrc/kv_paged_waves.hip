@@ -626,7 +626,8 @@ hipError_t launch_wave_scatter(const TileArgs& a, int64_t planes, hipStream_t st
   // wave under one tag load (-2 % / -7 %), four lanes per 16-byte group (69
   // VGPRs, 7 waves per SIMD; -2 %), one lane per group (whole 1 KiB loads,
   // 142 VGPRs, 3 waves per SIMD; -6 %), at most 4 or 3 workgroups per CU (-2 % /
-  // -9 %), cached or sc0 linear loads (-4 %), write-back cache stores (-8 %);
+  // -9 %), but 6 waves per SIMD (79 VGPRs: row groups padded in LDS so that
+  // the lanes' LDS and store addresses take immediate offsets) no faster, cached or sc0 linear loads (-4 %), write-back cache stores (-8 %);
   // write-through stores were level.
   if (bm)
     hipLaunchKernelGGL((paged_wave_scatter_kernel<ELT_C, ELT_L, CODEC, LDT, BS, true>), grid, dim3(kBlockThreads), 0,
