@@ -108,6 +108,36 @@ def test_fp8_quant_store_in_destination_order(fmt, lin, bs):
     assert np.array_equal(vc_d.cpu().numpy(), want_v)
 
 
+@pytest.mark.parametrize("nh, hd", [(2, 64), (5, 64), (10, 128), (9, 120)])
+@pytest.mark.parametrize("lin", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("bs", [16, 32])
+def test_fp8_quant_store_in_destination_order_row_counts(nh, hd, lin, bs):
+    # A workgroup takes one cache block, its waves consecutive row chunks (256 rows for bf16 at block
+    # size 16, 128 for fp32 or block size 32, 64 for both): row counts of 128 ... 1,280 give blocks of
+    # one partial chunk, of fewer chunks than waves (idle waves), and of more (a second grid z) with a
+    # partial last chunk.
+    nb = 14
+    rng = np.random.default_rng(nh * 1000 + hd + bs)
+    slots = tricky_slots(rng, nb, bs)
+    assert _covers(slots, nb * bs, 4)
+    t = len(slots)
+    gen = torch.Generator().manual_seed(nh + hd)
+    k = (torch.randn((t, nh, hd), generator=gen) * 3).to(lin)
+    v = (torch.randn((t, nh, hd), generator=gen) * 3).to(lin)
+    ks = (torch.rand(nh, generator=gen) * 0.02 + 0.001).to(torch.float32)
+    vs = (torch.rand(nh, generator=gen) * 0.02 + 0.001).to(torch.float32)
+    kc = torch.randint(0, 256, (nb, nh, hd, bs), dtype=torch.uint8, generator=gen)
+    vc = torch.randint(0, 256, (nb, nh, hd, bs), dtype=torch.uint8, generator=gen)
+    kc_d, vc_d = kc.to(DEV), vc.to(DEV)
+    s_d = torch.from_numpy(slots).to(DEV)
+    musa_aiter.kv_linear_to_paged_fp8(k.to(DEV), v.to(DEV), kc_d, vc_d, s_d, ks.to(DEV), vs.to(DEV), fp8_format="e4m3")
+    want_k, want_v = kc.numpy().copy(), vc.numpy().copy()
+    ko.linear_to_paged_fp8(k.to(torch.float32).numpy(), want_k, slots, ks.numpy(), "e4m3")
+    ko.linear_to_paged_fp8(v.to(torch.float32).numpy(), want_v, slots, vs.numpy(), "e4m3")
+    assert np.array_equal(kc_d.cpu().numpy(), want_k)
+    assert np.array_equal(vc_d.cpu().numpy(), want_v)
+
+
 @pytest.mark.parametrize("hidden", [576, 328])
 def test_mla_rows_scatter_in_destination_order(hidden):
     # 1,152-byte bf16 rows (whole lines) and 656-byte ones.
