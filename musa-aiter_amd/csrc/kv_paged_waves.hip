@@ -303,10 +303,11 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_gather_kernel(const 
 // one dword with the hardware converter, so its half of row q's 16-byte cache
 // piece leaves the converter already transposed.  The half pieces meet in
 // the wave's LDS region (the gather's swizzle) and leave as coalesced 16-byte
-// wave stores.  Runs that do not fill a whole block store the bytes of their
-// columns one by one.  The exactness conditions of the fast quotient and of
-// the converter are checked per lane on the loaded inputs and made wave
-// uniform.
+// wave stores; runs that do not fill a whole block take the same steps and
+// store only the bytes of their columns from those pieces.  The exactness
+// conditions of the fast quotient and of the converter are checked per lane
+// on the loaded inputs and made wave uniform; a wave that fails them encodes
+// its columns element by element.
 
 template <int ELT_L, int BS>
 struct ScatterShape {
@@ -417,11 +418,9 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const
   const int rw_end = (rw0 + kChunkRows * W::kWaveChunks < a.nrows) ? rw0 + kChunkRows * W::kWaveChunks
                                                                     : static_cast<int>(a.nrows);
 
-  // Lane tile: rows trow .. trow + RPL - 1 of the chunk, block columns lo .. lo + COLS - 1.
-  const int half = lane & 1;
+  // Lane tile: rows trow .. trow + RPL - 1 of the chunk, block columns lo .. lo + COLS - 1
+  // (rg here for the scales; each run derives the tile again).
   const int rg = (lane >> 1) / NCG;
-  const int ct = (lane >> 1) % NCG;
-  const int lo = ct * CG + half * COLS;
   // The scale of the lane's rows in a chunk (1 for lanes past its end).  The
   // first chunk's is loaded before the slots or tags, so that the two loads
   // overlap instead of adding their latencies ahead of the linear loads.
@@ -467,80 +466,112 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const
     heads = vmask & ~cmask;
   }
   if (heads == 0) return;
-  u32x2* const lds_half = reinterpret_cast<u32x2*>(lds) + half;
 
 #pragma unroll 1
   for (int r0 = rw0; r0 < rw_end; r0 += kChunkRows) {
     const int r_end = (r0 + kChunkRows < rw_end) ? r0 + kChunkRows : rw_end;
-    const int trow = r0 + rg * RPL;
-    const bool tile_in = trow < r_end;
     const float sc = r0 == rw0 ? sc_first : chunk_scale(r0);
     const bool scale_ok = fast_scale_ok(sc);
     const float r = scale_ok ? 1.0f / sc : 0.0f;
 
     // One run: block columns [c0, c1) of block blk from tokens tf, tf + 1, ...
     auto run = [&](int64_t blk, int c0, int c1, int64_t tf) {
+      // The lane's tile coordinates, derived again in every run from a lane id
+      // the compiler cannot see through: hoisted out of the run loop, the
+      // addresses built from them would stay live across every path and cost
+      // a wave per SIMD.
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int half = ln & 1;
+      const int rg = (ln >> 1) / NCG;
+      const int ct = (ln >> 1) % NCG;
+      const int lo = ct * CG + half * COLS;
+      const int trow = r0 + rg * RPL;
+      const bool tile_in = trow < r_end;
+      u32x2* const lds_half = reinterpret_cast<u32x2*>(lds) + half;
       uint8_t* const chunk = cache + (blk * a.nrows + r0) * BS;
-      const uint8_t* const lrow = lin + tf * a.lin_token_stride + static_cast<int64_t>(trow) * ELT_L;
-
-      if (c0 == 0 && c1 == BS) {
-        // Whole block: full cache pieces, unless some lane of the wave needs the
-        // integer encoders (then the byte path below takes the whole run).
-        // Linear pieces: a descriptor at the run's first token and row r0, a
-        // per-lane offset (row group, column) and a wave-uniform column step;
-        // lanes past the chunk read zeros.
-        const buf_t lbuf = make_buf(lin + tf * a.lin_token_stride + static_cast<int64_t>(r0) * ELT_L);
-        const uint32_t stride32 = static_cast<uint32_t>(a.lin_token_stride);
-        const uint32_t loff = tile_in ? static_cast<uint32_t>(rg * RPL * ELT_L) + static_cast<uint32_t>(lo) * stride32
-                                      : kOffOob;
-        u32x4 in[COLS];
+      const bool whole = c0 == 0 && c1 == BS;
+      // Linear pieces: a descriptor at the run's first token and row r0 and a
+      // per-lane offset (row group, column); lanes past the chunk, and columns
+      // outside a partial run, read zeros.  All of a lane's pieces are loaded
+      // at once, so a partial run costs one load latency like a whole block.
+      const buf_t lbuf = make_buf(lin + tf * a.lin_token_stride + static_cast<int64_t>(r0) * ELT_L);
+      const uint32_t stride32 = static_cast<uint32_t>(a.lin_token_stride);
+      const uint32_t prow = static_cast<uint32_t>(rg * RPL * ELT_L);
+      u32x4 in[COLS];
 #pragma unroll
-        for (int c = 0; c < COLS; ++c) in[c] = buf_ld16(lbuf, loff, static_cast<uint32_t>(c) * stride32);
-        TileBound<LDT> bound;
+      for (int j = 0; j < COLS; ++j) {
+        const int c = lo + j;
+        const bool mine = tile_in && c >= c0 && c < c1;
+        in[j] = buf_ld16(lbuf, mine ? prow + static_cast<uint32_t>(c - c0) * stride32 : kOffOob);
+      }
+      TileBound<LDT> bound;
 #pragma unroll
-        for (int c = 0; c < COLS; ++c) bound.add(in[c]);
-        bool soft = !bound.fast(sc);
-        if constexpr (CODEC == kE5M2) {
-          // The converter is exact up to 57344; |q| <= max|x| * r * (1 + 2^-22).
-          soft = soft || bound.max_abs() * r * (1.0f + 0x1p-20f) > __uint_as_float(kHwEncodeMaxBits<CODEC>);
+      for (int c = 0; c < COLS; ++c) bound.add(in[c]);
+      bool soft = !bound.fast(sc);
+      if constexpr (CODEC == kE5M2) {
+        // The converter is exact up to 57344; |q| <= max|x| * r * (1 + 2^-22).
+        soft = soft || bound.max_abs() * r * (1.0f + 0x1p-20f) > __uint_as_float(kHwEncodeMaxBits<CODEC>);
+      }
+      // Row q of the lane's tile as two dwords of four block columns each.
+      auto row_words = [&](int q, uint32_t (&word)[2]) {
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          float w[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            w[k] = quot_fast<LDT != kLinF32>(tile_elem<ELT_L, LDT, RPL>(in[4 * g + k], q), sc, r);
+          word[g] = fp8_pack4_hw<CODEC>(w[0], w[1], w[2], w[3]);
         }
-        if (ballot(tile_in && soft) == 0) {
+      };
+      if (ballot(tile_in && soft) == 0) {
+        // The lanes' half pieces meet in LDS; whole blocks leave as coalesced
+        // 16-byte stores, partial runs as the bytes of the run's columns of
+        // the same coalesced pieces.
 #pragma unroll
-          for (int q = 0; q < RPL; ++q) {
-            uint32_t word[2];
+        for (int q = 0; q < RPL; ++q) {
+          uint32_t word[2];
+          row_words(q, word);
+          lds_half[2 * lds_slot<RPL, NCG>((rg * RPL + q) * NCG + ct)] = u32x2{word[0], word[1]};
+        }
+        wave_lds_sync();
+        const buf_t cbuf = make_buf(chunk);
 #pragma unroll
-            for (int g = 0; g < 2; ++g) {
-              float w[4];
-#pragma unroll
-              for (int k = 0; k < 4; ++k)
-                w[k] = quot_fast<LDT != kLinF32>(tile_elem<ELT_L, LDT, RPL>(in[4 * g + k], q), sc, r);
-              word[g] = fp8_pack4_hw<CODEC>(w[0], w[1], w[2], w[3]);
+        for (int k = 0; k < kPieces / kWave; ++k) {
+          const int pc = k * kWave + lane;
+          const u32x4 v = lds[lds_slot<RPL, NCG>(pc)];
+          const bool row_in = r0 + pc / NCG < r_end;
+          if (whole) {
+            buf_st16(cbuf, row_in ? static_cast<uint32_t>(pc) * 16u : kOffOob, v);
+          } else if (row_in) {
+            // The piece's bytes inside the run: [b0, b1) of its 16 columns.
+            const int cg0 = (pc % NCG) * CG;
+            const int b0 = c0 > cg0 ? c0 - cg0 : 0;
+            const int b1 = c1 < cg0 + CG ? c1 - cg0 : CG;
+            uint8_t* const p = chunk + static_cast<int64_t>(pc) * 16;
+#pragma unroll 1
+            for (int b = b0; b < b1; ++b) {
+              const uint32_t d = (b >> 2) == 0 ? v[0] : (b >> 2) == 1 ? v[1] : (b >> 2) == 2 ? v[2] : v[3];
+              p[b] = static_cast<uint8_t>(d >> (8 * (b & 3)));
             }
-            lds_half[2 * lds_slot<RPL, NCG>((rg * RPL + q) * NCG + ct)] = u32x2{word[0], word[1]};
           }
-          wave_lds_sync();
-          const buf_t cbuf = make_buf(chunk);
-#pragma unroll
-          for (int k = 0; k < kPieces / kWave; ++k) {
-            const int pc = k * kWave + lane;
-            const u32x4 v = lds[lds_slot<RPL, NCG>(pc)];
-            buf_st16(cbuf, (r0 + pc / NCG < r_end) ? static_cast<uint32_t>(pc) * 16u : kOffOob, v);
-          }
-          wave_lds_sync();
-          return;
         }
+        wave_lds_sync();
+        return;
       }
 
-      // Partial block (or a block whose wave needs the integer encoders): the
-      // lane's columns inside the run, byte by byte.
+      // Some lane of the wave needs the integer encoders: the lane's columns
+      // inside the run, byte by byte.
       const int ca = c0 > lo ? c0 : lo;
       const int cb = c1 < lo + COLS ? c1 : lo + COLS;
       if (!tile_in) return;
+      const uint8_t* const lrow = lin + tf * a.lin_token_stride + static_cast<int64_t>(trow) * ELT_L;
       uint8_t* const crow = chunk + static_cast<int64_t>(rg * RPL) * BS;
 #pragma unroll 1
       for (int c = ca; c < cb; ++c) {
         const u32x4 piece = ld16(lrow + static_cast<int64_t>(c - c0) * a.lin_token_stride);
-#pragma unroll
+        // (Rows one at a time: this rare path keeps few registers live.)
+#pragma unroll 1
         for (int q = 0; q < RPL; ++q)
           crow[q * BS + c] =
               static_cast<uint8_t>(quant_one<CODEC, LDT>(tile_elem<ELT_L, LDT, RPL>(piece, q), sc, r, scale_ok));
@@ -622,13 +653,17 @@ hipError_t launch_wave_scatter(const TileArgs& a, int64_t planes, hipStream_t st
   // In block order one workgroup takes one block (grid z covers chunks past
   // the fourth) and the lane's scale load is issued before the tag load: on
   // configs[2]'s quant-store 5.04-5.16 -> 5.21-5.38 TB/s, where either change
-  // alone measured no faster.  Slower in the same runs: two or four blocks per
-  // wave under one tag load (-2 % / -7 %), four lanes per 16-byte group (69
-  // VGPRs, 7 waves per SIMD; -2 %), one lane per group (whole 1 KiB loads,
-  // 142 VGPRs, 3 waves per SIMD; -6 %), at most 4 or 3 workgroups per CU (-2 % /
-  // -9 %), but 6 waves per SIMD (79 VGPRs: row groups padded in LDS so that
-  // the lanes' LDS and store addresses take immediate offsets) no faster, cached or sc0 linear loads (-4 %), write-back cache stores (-8 %);
-  // write-through stores were level.
+  // alone measured no faster.  Partial runs (a sequence's last block) once
+  // loaded and encoded their columns one load at a time: those few waves ran
+  // several load latencies long and set the kernel's tail; sharing the
+  // whole-block path moved the quant-store on to 5.42-5.75 TB/s.  Slower in
+  // the same runs: two or four blocks per wave under one tag load (-2 % /
+  // -7 %), four lanes per 16-byte group (69 VGPRs, 7 waves per SIMD; -2 %),
+  // one lane per group (whole 1 KiB loads, 142 VGPRs, 3 waves per SIMD;
+  // -6 %), at most 4 or 3 workgroups per CU (-2 % / -9 %), cached or sc0
+  // linear loads (-4 %), write-back cache stores (-8 %); 6 waves per SIMD (79
+  // VGPRs: row groups padded in LDS so that the lanes' LDS and store addresses
+  // take immediate offsets) and write-through stores were level.
   if (bm)
     hipLaunchKernelGGL((paged_wave_scatter_kernel<ELT_C, ELT_L, CODEC, LDT, BS, true>), grid, dim3(kBlockThreads), 0,
                        stream, a);
