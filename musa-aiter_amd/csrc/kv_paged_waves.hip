@@ -561,19 +561,22 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const
       }
 
       // Some lane of the wave needs the integer encoders: the lane's columns
-      // inside the run, byte by byte.
-      const int ca = c0 > lo ? c0 : lo;
-      const int cb = c1 < lo + COLS ? c1 : lo + COLS;
+      // inside the run, element by element, from the pieces already loaded
+      // (no second round of loads: such waves would otherwise set the tail).
+      // Columns and rows one at a time, the column's piece picked by selects,
+      // so that this rare path keeps few registers live.
       if (!tile_in) return;
-      const uint8_t* const lrow = lin + tf * a.lin_token_stride + static_cast<int64_t>(trow) * ELT_L;
-      uint8_t* const crow = chunk + static_cast<int64_t>(rg * RPL) * BS;
+      const int ja = c0 > lo ? c0 - lo : 0;
+      const int jb = c1 < lo + COLS ? c1 - lo : COLS;
+      uint8_t* const crow = chunk + static_cast<int64_t>(rg * RPL) * BS + lo;
 #pragma unroll 1
-      for (int c = ca; c < cb; ++c) {
-        const u32x4 piece = ld16(lrow + static_cast<int64_t>(c - c0) * a.lin_token_stride);
-        // (Rows one at a time: this rare path keeps few registers live.)
+      for (int j = ja; j < jb; ++j) {
+        u32x4 piece = in[0];
+#pragma unroll
+        for (int k = 1; k < COLS; ++k) piece = (j == k) ? in[k] : piece;
 #pragma unroll 1
         for (int q = 0; q < RPL; ++q)
-          crow[q * BS + c] =
+          crow[q * BS + j] =
               static_cast<uint8_t>(quant_one<CODEC, LDT>(tile_elem<ELT_L, LDT, RPL>(piece, q), sc, r, scale_ok));
       }
     };
