@@ -91,4 +91,9 @@ hipError_t launch_wave_gather(const TileArgs& a, int64_t planes, hipStream_t str
 template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS>
 hipError_t launch_wave_scatter(const TileArgs& a, int64_t planes, hipStream_t stream);
 
+// Per-wave 16-bit linear -> paged scatter in destination order
+// (kv_paged_waves.hip): needs this call's claim tags as the inverse map.
+template <int BS>
+hipError_t launch_wave_copy_scatter(const TileArgs& a, int64_t planes, hipStream_t stream);
+
 }  // namespace kvhip

@@ -510,6 +510,14 @@ hipError_t launch_tile(const TileArgs& a0, int64_t planes, hipStream_t stream) {
       // next to each other in the grid (x = block * groups + group): on the
       // configs[1] scatter 5.60 TB/s, against 5.46-5.52 with four chunks (grid
       // z or folded), 5.33 with eight and 4.80 with one.
+      // 16-bit launches over fewer planes than the XCD order wants take the
+      // per-wave kernel (a workgroup per block, no workgroup barrier): the
+      // dense write-back (2 planes) 5.50-5.58 -> 5.60-5.74 TB/s; over
+      // configs[1]'s 64 planes the two kernels measured level, and the
+      // cooperative one below keeps them.
+      if constexpr (ELT == 2) {
+        if (planes < kXcdOrderPlanes) return launch_wave_copy_scatter<BS>(a0, planes, stream);
+      }
       using S = CoopShape<ELT, BS, kCoopThreads>;
       constexpr int64_t kGroupRows = S::kRows * kBlockScatterChunks;
       const int64_t groups = (a0.nrows + kGroupRows - 1) / kGroupRows;

@@ -1,5 +1,6 @@
-// Per-wave paged-A <-> linear FP8 kernels for MI355X (gfx950): the
-// dequant-gather and the quant-store.
+// Per-wave paged-A <-> linear kernels for MI355X (gfx950): the FP8
+// dequant-gather and quant-store, and the 16-bit scatter in destination order
+// for launches over few planes.
 //
 // Dequant-gather.  One wave owns the runs (consecutive tokens in consecutive
 // slots of one block) that start in its 16-token tile, for one chunk of cache
@@ -598,6 +599,114 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const
   }
 }
 
+
+// ----- per-wave 16-bit block-major scatter -----------------------------------------
+//
+// The bf16/fp16 scatter in destination order, shaped like the FP8 quant-store:
+// workgroup x owns cache block x, its waves consecutive chunks of kChunkRows
+// rows (grid z covers chunks past the fourth).  A lane loads 8 tokens' 16-byte
+// linear pieces (8 rows each) of one run, transposes the 8 x 8 tile in
+// registers into 8 cache pieces (8 tokens of one row each), and the pieces
+// meet in the wave's LDS region to leave as coalesced 16-byte stores (whole
+// blocks) or as the run's elements of those pieces (partial runs).  No
+// workgroup barrier: each wave's LDS region is its own.
+template <int BS>
+struct CopyScatterShape {
+  static constexpr int RPL = 8;                       // rows per linear piece (16-bit elements)
+  static constexpr int CG = 8;                        // tokens per cache piece
+  static constexpr int NCG = BS / CG;                 // cache pieces per cache row
+  static constexpr int RG = kWave / NCG;              // lane row groups per wave
+  static constexpr int kChunkRows = RG * RPL;         // cache rows per wave
+  static constexpr int kPieces = kChunkRows * NCG;    // 16-byte cache pieces per wave
+  static_assert(BS % CG == 0 && kWave % NCG == 0 && kPieces % kWave == 0, "block row of whole pieces");
+};
+
+template <int BS, int CSTP>
+__global__ __launch_bounds__(kBlockThreads) void paged_wave_copy_scatter_kernel(const TileArgs a) {
+  using W = CopyScatterShape<BS>;
+  constexpr int ELT = 2, RPL = W::RPL, CG = W::CG, NCG = W::NCG, kChunkRows = W::kChunkRows;
+  constexpr int kPieces = W::kPieces;
+  __shared__ u32x4 lds_all[kWavesPerBlock * kPieces];
+  u32x4* const lds = lds_all + wave_in_block() * kPieces;
+
+  const int lane = lane_id();
+  const int64_t blk = blockIdx.x;
+  const int plane = static_cast<int>(blockIdx.y);
+  const int layer = plane >> 1;
+  const int kv = plane & 1;
+  const int r0 = static_cast<int>(blockIdx.z) * (kWavesPerBlock * kChunkRows) + wave_in_block() * kChunkRows;
+  if (r0 >= a.nrows || blk * BS >= a.num_slots) return;
+  const int r_end = (r0 + kChunkRows < a.nrows) ? r0 + kChunkRows : static_cast<int>(a.nrows);
+
+  // Lane p < BS holds the tag of slot blk * BS + p: runs of consecutive tokens.
+  uint64_t tag = 0;
+  if (lane < BS) tag = a.owner[blk * BS + lane];
+  const bool valid = lane < BS && static_cast<uint32_t>(tag >> 32) == a.epoch && static_cast<uint32_t>(tag) != 0u;
+  const int64_t tok = static_cast<int64_t>(static_cast<uint32_t>(tag)) - 1;
+  const uint64_t vmask = ballot(valid);
+  const int64_t tok_prev = from_prev_lane(tok);
+  const bool prev_valid = lane > 0 && ((vmask >> (lane - 1)) & 1ull);
+  const uint64_t cmask = ballot(valid && prev_valid && tok == tok_prev + 1);
+  uint64_t heads = vmask & ~cmask;
+  if (heads == 0) return;
+
+  uint8_t* const cache = a.cache[kv] + static_cast<int64_t>(layer) * a.cache_layer_stride;
+  const uint8_t* const lin = a.lin[kv] + static_cast<int64_t>(layer) * a.lin_layer_stride;
+  uint8_t* const chunk = cache + (blk * a.nrows + r0) * (BS * ELT);
+  const uint32_t stride32 = static_cast<uint32_t>(a.lin_token_stride);
+  while (heads) {
+    const int c0 = __builtin_ctzll(heads);
+    heads &= heads - 1;
+    const int c1 = c0 + 1 + __builtin_ctzll(~(cmask >> (c0 + 1)));  // c0 < BS <= 32
+    const int64_t tf = readlane64(tok, c0);
+    const bool whole = c0 == 0 && c1 == BS;
+    // The lane's tile (rows rg*RPL .. of the chunk, tokens ct*CG ..), derived
+    // in each run so that its addresses are not kept live across runs.
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int rg = ln / NCG;
+    const int ct = ln % NCG;
+    const bool tile_in = r0 + rg * RPL < r_end;
+    const buf_t lbuf = make_buf(lin + tf * a.lin_token_stride + static_cast<int64_t>(r0) * ELT);
+    const uint32_t prow = static_cast<uint32_t>(rg * RPL * ELT);
+    u32x4 in[CG];
+#pragma unroll
+    for (int j = 0; j < CG; ++j) {
+      const int c = ct * CG + j;
+      const bool mine = tile_in && c >= c0 && c < c1;
+      in[j] = buf_ld16(lbuf, mine ? prow + static_cast<uint32_t>(c - c0) * stride32 : kOffOob);
+    }
+#pragma unroll
+    for (int q = 0; q < RPL; ++q) {
+      u32x4 o;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) o[k] = pack16(elem16(in[2 * k], q), elem16(in[2 * k + 1], q));
+      lds[lds_slot<RPL, NCG>((rg * RPL + q) * NCG + ct)] = o;
+    }
+    wave_lds_sync();
+    const buf_t cbuf = make_buf(chunk);
+#pragma unroll
+    for (int k = 0; k < kPieces / kWave; ++k) {
+      const int pc = k * kWave + ln;
+      const u32x4 v = lds[lds_slot<RPL, NCG>(pc)];
+      const bool row_in = r0 + pc / NCG < r_end;
+      if (whole) {
+        buf_st16_p<CSTP>(cbuf, row_in ? static_cast<uint32_t>(pc) * 16u : kOffOob, v);
+      } else if (row_in) {
+        // The piece's elements inside the run: [e0, e1) of its 8 tokens.
+        const int cg0 = (pc % NCG) * CG;
+        const int e0 = c0 > cg0 ? c0 - cg0 : 0;
+        const int e1 = c1 < cg0 + CG ? c1 - cg0 : CG;
+#pragma unroll 1
+        for (int e = e0; e < e1; ++e) {
+          const uint32_t d = (e >> 1) == 0 ? v[0] : (e >> 1) == 1 ? v[1] : (e >> 1) == 2 ? v[2] : v[3];
+          buf_st_elem<ELT>(cbuf, static_cast<uint32_t>(pc * 16 + e * ELT), half_of(d, e & 1));
+        }
+      }
+    }
+    wave_lds_sync();
+  }
+}
 }  // namespace
 
 // True when every linear token row covers whole 128-byte lines (row size,
@@ -675,6 +784,22 @@ hipError_t launch_wave_scatter(const TileArgs& a, int64_t planes, hipStream_t st
                        stream, a);
   return hipGetLastError();
 }
+
+template <int BS>
+hipError_t launch_wave_copy_scatter(const TileArgs& a, int64_t planes, hipStream_t stream) {
+  using W = CopyScatterShape<BS>;
+  const int64_t chunks = (a.nrows + W::kChunkRows - 1) / W::kChunkRows;
+  const int64_t zs = (chunks + kWavesPerBlock - 1) / kWavesPerBlock;
+  const int64_t nblk = a.num_slots / BS;
+  if (zs > 65535 || nblk > 0x7FFFFFFF) return hipErrorInvalidValue;
+  // Whole blocks are written through the L2, as in the cooperative kernel.
+  const dim3 grid(static_cast<uint32_t>(nblk), static_cast<uint32_t>(planes), static_cast<uint32_t>(zs));
+  hipLaunchKernelGGL((paged_wave_copy_scatter_kernel<BS, kBufWT>), grid, dim3(kBlockThreads), 0, stream, a);
+  return hipGetLastError();
+}
+template hipError_t launch_wave_copy_scatter<8>(const TileArgs&, int64_t, hipStream_t);
+template hipError_t launch_wave_copy_scatter<16>(const TileArgs&, int64_t, hipStream_t);
+template hipError_t launch_wave_copy_scatter<32>(const TileArgs&, int64_t, hipStream_t);
 
 #define KVHIP_WAVE_GATHER(CODEC, ELT_L, LDT)                                                             \
   template hipError_t launch_wave_gather<1, ELT_L, CODEC, LDT, 16>(const TileArgs&, int64_t, hipStream_t);  \
