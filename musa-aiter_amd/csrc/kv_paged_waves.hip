@@ -196,9 +196,23 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_gather_kernel(const 
   const int h_lo = (kLut && a.scale_mode != 0) ? head_of_row(a, static_cast<int>(r0)) : 0;
   if constexpr (kLut) {
     const int nh = a.scale_mode != 0 ? head_of_row(a, static_cast<int>(r_end - 1)) - h_lo + 1 : 1;
-#pragma unroll 1
-    for (int e = static_cast<int>(threadIdx.x); e < nh * 256; e += kBlockThreads)
-      lut_all[e] = lut_value<CODEC, LDT, LutT>(static_cast<uint32_t>(e & 255), load_scale(a, kv, layer, h_lo + (e >> 8)));
+    // Thread x writes code x of each table.  The heads' scales (load_scale's
+    // indexing; indices past the last head repeat it, so every load stays in
+    // the scale array) are all loaded before the first entry: the empty asm
+    // statements keep the compiler from sinking each load, and its wait, into
+    // its table's branch.
+    static_assert(kBlockThreads == 256, "one code per thread and table");
+    const float* const sp = a.scale[kv] + (a.scale_mode == 0   ? 0
+                                           : a.scale_mode == 1 ? h_lo
+                                                               : static_cast<int64_t>(layer) * a.num_heads + h_lo);
+    float scs[kLutHeads];
+#pragma unroll
+    for (int k = 0; k < kLutHeads; ++k) scs[k] = sp[k < nh ? k : nh - 1];
+#pragma unroll
+    for (int k = 0; k < kLutHeads; ++k) asm volatile("" : "+v"(scs[k]));
+#pragma unroll
+    for (int k = 0; k < kLutHeads; ++k)
+      if (k < nh) lut_all[k * 256 + threadIdx.x] = lut_value<CODEC, LDT, LutT>(threadIdx.x, scs[k]);
     __syncthreads();
   }
   if (t0 >= a.num_tokens) return;
@@ -717,6 +731,14 @@ bool whole_line_rows(const TileArgs& a, int elt) {
          reinterpret_cast<uintptr_t>(a.lin[0]) % kLine == 0 && reinterpret_cast<uintptr_t>(a.lin[1]) % kLine == 0;
 }
 
+// Dynamic LDS of the FP8 dequant-gather's workgroups, unused by the kernel:
+// with its 4-8 KiB of decode tables, 3 workgroups fit in a CU's 160 KiB and 4
+// do not.
+constexpr unsigned kGatherLdsPad = 38000;
+static_assert(4 * (kGatherLdsPad + kLutHeads * 256 * 2) > 160 * 1024 &&
+                  3 * (kGatherLdsPad + kLutHeads * 256 * 4 + 16) <= 160 * 1024,
+              "3 workgroups per CU, not 4");
+
 template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS>
 hipError_t launch_wave_gather(const TileArgs& a, int64_t planes, hipStream_t stream) {
   using W = WaveShape<ELT_C, ELT_L, BS>;
@@ -735,17 +757,21 @@ hipError_t launch_wave_gather(const TileArgs& a, int64_t planes, hipStream_t str
   if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
   const dim3 grid(static_cast<uint32_t>(blocks), static_cast<uint32_t>(planes), static_cast<uint32_t>(chunks));
   // Linear rows of whole lines are written through the L2 (cfg 3
-  // dequant-gather 5.39 -> 5.48 TB/s, caches read from HBM).  The kernel
-  // runs 4 waves per SIMD (97 VGPRs): with 5 (95 VGPRs, scales loaded in one
-  // batch) it measured 2-5 % slower, with 3 (LDS-limited) within 1.5 %, and
-  // staging the tiles through LDS with whole-line loads gained 1.6 % on cfg 3
-  // but lost 6 % on the dense FP8 preload.
+  // dequant-gather 5.39 -> 5.48 TB/s, caches read from HBM).  Each wave
+  // instruction touches 64 cache lines partially and the wave's next ones
+  // read the rest, so fewer waves per CU keep more of those lines in the L1:
+  // the launch adds dynamic LDS (kGatherLdsPad, unused) so that 3 workgroups
+  // fit per CU.  Measured on cfg 3 against 4 per CU (two runs): per-head
+  // scales +0.8-1.3 % (E4M3) and +1.5 % (E5M2), scalar scale and the dense
+  // FP8 preload -0.3-0.5 %;
+  // 5 per CU was 2-5 % slower, and staging the tiles through LDS with
+  // whole-line loads gained 1.6 % on cfg 3 but lost 6 % on the dense preload.
   if (whole_line_rows(a, ELT_L))
-    hipLaunchKernelGGL((paged_wave_gather_kernel<ELT_C, ELT_L, CODEC, LDT, BS, kBufWT>), grid, dim3(kBlockThreads), 0,
-                       stream, a);
+    hipLaunchKernelGGL((paged_wave_gather_kernel<ELT_C, ELT_L, CODEC, LDT, BS, kBufWT>), grid, dim3(kBlockThreads),
+                       kGatherLdsPad, stream, a);
   else
-    hipLaunchKernelGGL((paged_wave_gather_kernel<ELT_C, ELT_L, CODEC, LDT, BS, kBufNT>), grid, dim3(kBlockThreads), 0,
-                       stream, a);
+    hipLaunchKernelGGL((paged_wave_gather_kernel<ELT_C, ELT_L, CODEC, LDT, BS, kBufNT>), grid, dim3(kBlockThreads),
+                       kGatherLdsPad, stream, a);
   return hipGetLastError();
 }
 
