@@ -82,6 +82,29 @@ def test_paged_multi_layer_scatter_in_destination_order(dtype, bs):
     assert np.array_equal(bits(vc_d), want_v)
 
 
+@pytest.mark.parametrize("nh, hd", [(2, 64), (5, 64), (10, 128), (9, 120)])
+@pytest.mark.parametrize("bs", [8, 16, 32])
+def test_paged_scatter_in_destination_order_row_counts(nh, hd, bs):
+    # 16-bit scatters over few planes run one workgroup per cache block, its waves consecutive chunks of
+    # 512, 256 or 128 rows (block size 8, 16, 32): row counts of 128 ... 1,280 give blocks of one
+    # partial chunk, of fewer chunks than waves, and of more (a second grid z) with a partial last chunk.
+    nl, nb = 2, 14
+    rng = np.random.default_rng(nh * 100 + hd + bs)
+    gen = torch.Generator().manual_seed(nh + hd + bs)
+    slots = tricky_slots(rng, nb, bs)
+    assert _covers(slots, nb * bs, 4)
+    t = len(slots)
+    kl, vl = (random_payload((nl, t, nh, hd), torch.bfloat16, gen) for _ in range(2))
+    kc, vc = (random_payload((nl, nb, nh, hd, bs), torch.bfloat16, gen) for _ in range(2))
+    kc_d, vc_d = kc.to(DEV), vc.to(DEV)
+    musa_aiter.kv_linear_to_paged_multi_layer(kl.to(DEV), vl.to(DEV), kc_d, vc_d, torch.from_numpy(slots).to(DEV))
+    want_k, want_v = bits(kc).copy(), bits(vc).copy()
+    ko.linear_to_paged_multi_layer(bits(kl), want_k, slots)
+    ko.linear_to_paged_multi_layer(bits(vl), want_v, slots)
+    assert np.array_equal(bits(kc_d), want_k)
+    assert np.array_equal(bits(vc_d), want_v)
+
+
 @pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
 @pytest.mark.parametrize("lin", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("bs", [16, 32])
