@@ -148,13 +148,101 @@ __device__ __forceinline__ void scatter_run_chunks(uint8_t* tile, buf_t cbuf, bu
   }
 }
 
+// Scatter tiles of short runs (one or a few tokens per block, as a decode
+// step's one new token per sequence) skip the LDS transpose, which costs one
+// load round trip and 2 x C workgroup barriers per run.  Wave w takes tokens
+// w, w + W, ... of the tile (W waves) and, per 64-row block of the group [rb,
+// re), moves row (block * 64 + lane) of the token: one instruction covers 64
+// consecutive rows, one 128-byte line of the linear row (16-bit elements) and
+// 16 lines of the block column.  The token is wave-uniform, so its linear row
+// and block column are scalar buffer descriptors.  Lane i + 1 of `s` holds the
+// slot of token t0 + i; bit i + 1 of `vw` (bits 1..kTileTokens) says that the
+// token moves.  Every load of a batch (up to 32 rows per lane) is issued
+// before its stores.
+template <int ELT, int BS, int NT>
+__device__ __forceinline__ void scatter_token_rows(const TileArgs& a, uint8_t* cache, uint8_t* lin, int64_t s,
+                                                   uint64_t vw, int64_t t0, int64_t rb, int64_t re) {
+  constexpr int ROWB = BS * ELT;
+  constexpr int kGroupRows = CoopShape<ELT, BS, NT>::kRows * kChunksPerGroup<true>;
+  static_assert(kGroupRows % kWave == 0, "row blocks of one wave");
+  constexpr int NRB = kGroupRows / kWave;   // 64-row blocks per token
+  constexpr int kWaves = NT / kWave;
+  constexpr int TPW = kTileTokens / kWaves;  // tokens per wave
+  constexpr int TB = TPW * NRB <= 32 ? TPW : 32 / NRB;  // tokens per batch (at most 32 rows in flight per lane)
+  static_assert(TB >= 1 && TPW % TB == 0, "whole batches");
+  if (vw == 0) return;
+  const int lane = lane_id();
+  const int wave = wave_in_block();
+  const int64_t blk = s / BS;
+  const int64_t cbase = (blk * a.nrows + rb) * ROWB + (s - blk * BS) * ELT;
+  const int rows = static_cast<int>(re - rb);
+  uint8_t* const lin0 = lin + t0 * a.lin_token_stride + rb * ELT;
+  // Descriptors of token k of this wave: a token that does not move gets no
+  // records, so its accesses are dropped without a lane mask.
+  auto token = [&](int k) { return wave + kWaves * k; };
+  auto records = [&](int k) -> int { return ((vw >> (token(k) + 1)) & 1ull) ? 0x7FFFFFFF : 0; };
+  auto cdesc = [&](int k) {
+    return __builtin_amdgcn_make_buffer_rsrc(cache + readlane64(cbase, token(k) + 1), 0, records(k), 0x00020000);
+  };
+  auto ldesc = [&](int k) {
+    return __builtin_amdgcn_make_buffer_rsrc(lin0 + static_cast<int64_t>(token(k)) * a.lin_token_stride, 0,
+                                             records(k), 0x00020000);
+  };
+  // Row r = block * 64 + lane of the group; rows past its end are dropped.
+  auto off = [&](int rbk, int bytes) -> uint32_t {
+    const int r = rbk * kWave + lane;
+    return r < rows ? static_cast<uint32_t>(r * bytes) : kOffOob;
+  };
+#pragma unroll
+  for (int k0 = 0; k0 < TPW; k0 += TB) {
+    uint32_t v[TB][NRB];
+#pragma unroll
+    for (int k = 0; k < TB; ++k) {
+      const buf_t src = ldesc(k0 + k);
+#pragma unroll
+      for (int q = 0; q < NRB; ++q) {
+        if constexpr (ELT == 2) v[k][q] = __builtin_amdgcn_raw_buffer_load_b16(src, off(q, ELT), 0, kBufNT);
+        else v[k][q] = __builtin_amdgcn_raw_buffer_load_b32(src, off(q, ELT), 0, kBufNT);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < TB; ++k) {
+      const buf_t dst = cdesc(k0 + k);
+#pragma unroll
+      for (int q = 0; q < NRB; ++q) {
+        if constexpr (ELT == 2)
+          __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(v[k][q]), dst, off(q, ROWB), 0, 0);
+        else
+          __builtin_amdgcn_raw_buffer_store_b32(v[k][q], dst, off(q, ROWB), 0, 0);
+      }
+    }
+  }
+}
+
+// Scatter runs of a tile that average fewer than this many tokens take
+// scatter_token_rows.  Measured against one 16-bit layer ([8192, 8, 128, 16]
+// cache, 16-4,096 tokens in runs of k): k = 1-4 faster (4,096 tokens of
+// runs of 3: 45.2 -> 41.0 us; 256 tokens of single tokens 37.2 -> 11.6 us),
+// k = 6 level (31.9 against 32.5 us).  Gathers keep the run form: the same
+// form on gathers cost configs[0]'s gather 4 % (5,030 -> 4,860 GB/s) though
+// none of its tiles took it.
+constexpr int kShortRunTokens = 6;
+
+// Waves per SIMD the tile kernel's register budget must allow: all eight
+// (64 VGPRs), which the short-launch scatters over 16- and 32-column blocks
+// otherwise miss by 7 registers; 8-column scatters would spill, and keep the
+// compiler's choice (at least one wave).
+template <int BS, bool SCATTER>
+constexpr int kTileMinWaves = (SCATTER && BS == 8) ? 1 : 8;
+
 // FEW selects the form for launches bound by per-workgroup latency rather than
 // by HBM: for a scatter the loads-first chunk loop, for a gather the natural
 // workgroup order (FEW false: the XCD-contiguous order).  NT is the workgroup
 // size; a chunk is NT 16-byte pieces.  LSTP: cache-policy bits of a gather's
 // linear-side stores.
 template <int ELT, int BS, bool SCATTER, bool FEW, int NT = kCoopThreads, int LSTP = kBufNT>
-__global__ __launch_bounds__(NT) void paged_tile_kernel(const TileArgs a) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(kTileMinWaves<BS, SCATTER>)))
+void paged_tile_kernel(const TileArgs a) {
   using S = CoopShape<ELT, BS, NT>;
   constexpr int CG = S::CG, NCG = S::NCG, ROWB = S::ROWB, kRows = S::kRows;
   constexpr int RPL = S::RPL, PITCH = S::PITCH;
@@ -219,6 +307,26 @@ __global__ __launch_bounds__(NT) void paged_tile_kernel(const TileArgs a) {
   constexpr uint32_t kLinStep = kRows * ELT;        // bytes between chunks, linear side
   const uint32_t cpiece = static_cast<uint32_t>(tid) * 16u;
   const uint32_t stride32 = static_cast<uint32_t>(a.lin_token_stride);
+
+  if constexpr (SCATTER) {
+    // Lanes of the runs that start in this tile (lanes at its start that
+    // continue an earlier tile's run belong to that tile): adding a head's
+    // next bit to cmask carries through exactly the continuation bits of its
+    // run.  The tile's last run may go on past the tile's end and keeps the
+    // run form; short runs before it move with scatter_token_rows.
+    uint64_t tok_heads = heads;
+    uint64_t tok_lanes = heads | (((cmask + (heads << 1)) ^ cmask) & cmask);
+    if (tok_lanes & ~window) {
+      const uint64_t below_last = (1ull << (63 - __builtin_clzll(heads))) - 1ull;
+      tok_heads &= below_last;
+      tok_lanes &= below_last;
+    }
+    const int truns = __builtin_popcountll(tok_heads);
+    if (truns > 0 && __builtin_popcountll(tok_lanes) < truns * kShortRunTokens) {
+      scatter_token_rows<ELT, BS, NT>(a, cache, lin, s, tok_lanes, t0, rb, re);
+      heads &= ~tok_heads;
+    }
+  }
 
   [[maybe_unused]] bool tile_used = false;  // wave-uniform: some chunk of this workgroup has filled the LDS tile
   while (heads) {

@@ -64,6 +64,25 @@ def make_slots(kind: str, rng: np.random.Generator, *, block_size: int, tokens: 
     elif kind == "duplicates":
         nb = (tokens + bs - 1) // bs + spare_blocks
         slots = rng.integers(-1, max(2, (nb * bs) // 4), size=tokens).astype(np.int64)
+    elif kind == "decode":
+        # Decode steps: each sequence appends 1-6 tokens at a random offset of
+        # its own blocks (a run may cross into the next block); every eighth
+        # appends a longer chunk.  Tiles mix runs of one token with whole blocks.
+        lengths, remaining = [], tokens
+        while remaining > 0:
+            length = int(rng.integers(2 * bs, 3 * bs + 2)) if rng.random() < 0.125 else int(rng.integers(1, 7))
+            lengths.append(min(remaining, length))
+            remaining -= lengths[-1]
+        offsets = rng.integers(0, bs, size=len(lengths))
+        need = [(int(o) + n + bs - 1) // bs for o, n in zip(offsets, lengths)]
+        nb = sum(need) + spare_blocks
+        perm, pos, out = rng.permutation(nb), 0, []
+        for o, n, k in zip(offsets, lengths, need):
+            table = perm[pos:pos + k]
+            pos += k
+            j = int(o) + np.arange(n)
+            out.append(table[j // bs] * bs + j % bs)
+        slots = np.concatenate(out).astype(np.int64)
     elif kind == "identity":
         nb = (tokens + bs - 1) // bs + spare_blocks
         slots = np.arange(tokens, dtype=np.int64)

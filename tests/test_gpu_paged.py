@@ -238,6 +238,40 @@ def test_kernel_forms_either_side_of_the_launch_thresholds(layers, tokens, kind)
     assert np.array_equal(bits(vc_d), want_v)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("bs", [8, 16, 32])
+@pytest.mark.parametrize("layers,tokens,kind", [
+    (1, 301, "decode"),          # short launches: loads-first scatter, 128-thread gather
+    (3, 301, "decode"),
+    (2, 40000, "decode"),        # scatter above 8,192 workgroups: chunk-by-chunk form
+    (16, 5000, "decode"),        # gather over 32 planes above 8,192 workgroups: XCD-contiguous order
+    (2, 3000, "duplicates"),     # claimed slots in per-token tiles
+])
+def test_short_run_tiles_match_oracle(dtype, bs, layers, tokens, kind):
+    # Tiles whose runs average fewer than 8 tokens move each token's rows
+    # directly instead of through the LDS transpose; the decode pattern puts
+    # such tiles next to tiles of whole blocks in one launch.
+    shape = (4, 64, bs)
+    nh, hd, _ = shape
+    slots, kc, vc = _case(dtype, shape, kind, tokens=tokens, seed=51 + bs + layers, layers=layers)
+    if kind == "decode":
+        slots[np.random.default_rng(bs).random(len(slots)) < 0.05] = -1
+    s_d = torch.from_numpy(slots).to(DEV)
+    ok, ov = musa_aiter.kv_paged_to_linear_multi_layer(kc.to(DEV), vc.to(DEV), s_d)
+    assert np.array_equal(bits(ok), ko.paged_to_linear_multi_layer(bits(kc), slots))
+    assert np.array_equal(bits(ov), ko.paged_to_linear_multi_layer(bits(vc), slots))
+    gen = torch.Generator().manual_seed(9)
+    kl = random_payload((layers, len(slots), nh, hd), dtype, gen)
+    vl = random_payload((layers, len(slots), nh, hd), dtype, gen)
+    kc_d, vc_d = kc.to(DEV), vc.to(DEV)
+    musa_aiter.kv_linear_to_paged_multi_layer(kl.to(DEV), vl.to(DEV), kc_d, vc_d, s_d)
+    want_k, want_v = bits(kc).copy(), bits(vc).copy()
+    ko.linear_to_paged_multi_layer(bits(kl), want_k, slots)
+    ko.linear_to_paged_multi_layer(bits(vl), want_v, slots)
+    assert np.array_equal(bits(kc_d), want_k)
+    assert np.array_equal(bits(vc_d), want_v)
+
+
 @pytest.mark.parametrize("dtype,shape,tokens", [
     (torch.float32, (4, 32, 32), 3000),   # 32 planes x 188 tiles x 2 row groups (12,032 workgroups): XCD order
     (torch.float16, (2, 64, 8), 5000),    # 32 planes x 313 tiles x 1 row group (10,016 workgroups): XCD order
