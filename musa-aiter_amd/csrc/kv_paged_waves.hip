@@ -400,6 +400,118 @@ __device__ __forceinline__ float tile_elem(const u32x4& piece, int q) {
   else return __uint_as_float(piece[q]);
 }
 
+// Quant-store tiles of short runs (a decode step's one to a few new tokens
+// per sequence): instead of walking the runs one by one (a load round trip,
+// the LDS exchange and the stores per run), the wave moves its chunk's rows of
+// every such token at once, one row per lane: row r0 + m * 64 + lane of the
+// token, M = kChunkRows / 64 rows per token.  The token is wave-uniform, so
+// its linear row and its block column are scalar buffer descriptors (no
+// records for a token that does not move) and a wave instruction covers 64
+// consecutive rows: 64 elements of the linear row, 64 bytes of the block
+// column at a row stride.  Every element is encoded on its own, as the
+// element path of the run form does.  Lane i + 1 of `s` holds the slot of
+// token t0 + i; bit i + 1 of `vw` says that the token moves.
+template <int CODEC, int LDT, int ELT_L, int BS, int M>
+__device__ __forceinline__ void quant_token_rows(const TileArgs& a, uint8_t* cache, const uint8_t* lin, int kv,
+                                                 int layer, int64_t s, uint64_t vw, int64_t t0, int r0, int r_end) {
+  constexpr int TB = 16 / M < kTileTokens ? 16 / M : kTileTokens;  // tokens per batch: 16 elements in flight per lane
+  static_assert(kTileTokens % TB == 0, "whole batches");
+  // The lane id and slot pass through an opaque copy, so that nothing derived
+  // from them is hoisted out of the caller's chunk loop (it would stay live
+  // across the run form and cost it a wave per SIMD).
+  int lane = lane_id();
+  asm volatile("" : "+v"(lane));
+  asm volatile("" : "+v"(s));
+  float sc[M], rc[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const int row = r0 + m * kWave + lane;
+    sc[m] = row < r_end ? load_scale(a, kv, layer, head_of_row(a, row)) : 1.0f;
+    rc[m] = fast_scale_ok(sc[m]) ? 1.0f / sc[m] : 0.0f;
+  }
+  auto off = [&](int m, int bytes) -> uint32_t {
+    return r0 + m * kWave + lane < r_end ? static_cast<uint32_t>((m * kWave + lane) * bytes) : kOffOob;
+  };
+  const int64_t blk = s / BS;
+  const int64_t cbase = (blk * a.nrows + r0) * BS + (s - blk * BS);
+  const uint8_t* const lin0 = lin + t0 * a.lin_token_stride + static_cast<int64_t>(r0) * ELT_L;
+  auto records = [&](int i) -> int { return ((vw >> (i + 1)) & 1ull) ? 0x7FFFFFFF : 0; };
+#pragma unroll 1
+  for (int i0 = 0; i0 < kTileTokens; i0 += TB) {
+    if (((vw >> (i0 + 1)) & ((1ull << TB) - 1ull)) == 0) continue;
+    uint32_t v[TB][M];
+#pragma unroll
+    for (int k = 0; k < TB; ++k) {
+      const buf_t src = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint8_t*>(lin0) + static_cast<int64_t>(i0 + k) * a.lin_token_stride, 0, records(i0 + k),
+          0x00020000);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        if constexpr (ELT_L == 2) v[k][m] = __builtin_amdgcn_raw_buffer_load_b16(src, off(m, ELT_L), 0, kBufNT);
+        else v[k][m] = __builtin_amdgcn_raw_buffer_load_b32(src, off(m, ELT_L), 0, kBufNT);
+      }
+    }
+    auto elem = [&](uint32_t bits) { return ELT_L == 2 ? lin_to_f32<LDT>(bits) : __uint_as_float(bits); };
+    auto cdesc = [&](int k) {
+      return __builtin_amdgcn_make_buffer_rsrc(cache + readlane64(cbase, i0 + k + 1), 0, records(i0 + k),
+                                               0x00020000);
+    };
+    // The fast quotient's range (quant_one's test), for the whole batch at once.
+    bool fast = true;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      fast = fast && fast_scale_ok(sc[m]);
+#pragma unroll
+      for (int k = 0; k < TB; ++k) {
+        const uint32_t ax = __float_as_uint(elem(v[k][m])) & 0x7FFFFFFFu;
+        fast = fast && (ax == 0u || (ax >= kFastLoBits && ax < kFastHiBits));
+      }
+    }
+    if (ballot(!fast) == 0) {
+#pragma unroll
+      for (int k = 0; k < TB; ++k) {
+        const buf_t dst = cdesc(k);
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          const uint32_t code = fp8_encode_fast<CODEC>(quot_fast<LDT != kLinF32>(elem(v[k][m]), sc[m], rc[m]));
+          __builtin_amdgcn_raw_buffer_store_b8(static_cast<uint8_t>(code), dst, off(m, BS), 0, 0);
+        }
+      }
+    } else {
+      // Some element needs the exact quotient: one element at a time, read
+      // again, so that this rare path keeps few registers live.
+#pragma unroll 1
+      for (int k = 0; k < TB; ++k) {
+        const buf_t src = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(lin0) + static_cast<int64_t>(i0 + k) * a.lin_token_stride, 0, records(i0 + k),
+            0x00020000);
+        const buf_t dst = cdesc(k);
+#pragma unroll 1
+        for (int m = 0; m < M; ++m) {
+          const uint32_t x = ELT_L == 2 ? __builtin_amdgcn_raw_buffer_load_b16(src, off(m, ELT_L), 0, kBufNT)
+                                        : __builtin_amdgcn_raw_buffer_load_b32(src, off(m, ELT_L), 0, kBufNT);
+          float scm = sc[0], rcm = rc[0];
+#pragma unroll
+          for (int j = 1; j < M; ++j) {
+            scm = m == j ? sc[j] : scm;
+            rcm = m == j ? rc[j] : rcm;
+          }
+          const uint32_t code = quant_one<CODEC, LDT>(elem(x), scm, rcm, fast_scale_ok(scm));
+          __builtin_amdgcn_raw_buffer_store_b8(static_cast<uint8_t>(code), dst, off(m, BS), 0, 0);
+        }
+      }
+    }
+  }
+}
+
+// Quant-store runs of a tile that average fewer than this many tokens take
+// quant_token_rows.  Measured on one E4M3 layer ([8192, 8, 128, 16] cache,
+// bf16 rows, per-head scales), per call: runs of 1-4 tokens faster at 16 to
+// 4,096 tokens (single tokens 34.6 -> 11.0 us at 16, 61.4 -> 39.0 us at
+// 4,096; runs of 4 24.7 -> 22.8 us at 4,096), runs of 6 level with 6 and 7 %
+// slower with 8.
+constexpr int kQuantShortRunTokens = 6;
+
 // BM (block-major): the workgroups visit cache blocks in block order instead
 // of token tiles (workgroup x owns block x, its four waves four consecutive
 // row chunks of it), reading each block's claim tags as the inverse map of the
@@ -449,6 +561,7 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const
   // Runs: `heads` marks the first lane of each, `cmask` the lanes continuing
   // one.
   uint64_t heads, cmask;
+  uint64_t tok_lanes = 0;  // token order: lanes whose tokens take quant_token_rows
   int64_t s = -1, tok = -1;
   const int64_t t0 = unit * kTileTokens;
   if constexpr (!BM) {
@@ -467,6 +580,20 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const
     const int ntile = remaining < kTileTokens ? static_cast<int>(remaining) : kTileTokens;
     const uint64_t window = ((1ull << ntile) - 1ull) << 1;
     heads = vmask & ~cmask & window;
+    // Lanes of the runs that start in this tile: adding a head's next bit to
+    // cmask carries through exactly the continuation bits of its run.  A last
+    // run that goes on past the tile's end keeps the run form; short runs
+    // before it move with quant_token_rows.
+    uint64_t tok_heads = heads;
+    tok_lanes = heads | (((cmask + (heads << 1)) ^ cmask) & cmask);
+    if (tok_lanes & ~window) {
+      const uint64_t below_last = (1ull << (63 - __builtin_clzll(heads))) - 1ull;
+      tok_heads &= below_last;
+      tok_lanes &= below_last;
+    }
+    const int truns = __builtin_popcountll(tok_heads);
+    if (truns > 0 && __builtin_popcountll(tok_lanes) < truns * kQuantShortRunTokens) heads &= ~tok_heads;
+    else tok_lanes = 0;
   } else {
     // Lane p < BS holds the tag of slot unit * BS + p.
     if (unit * BS >= a.num_slots) return;
@@ -480,11 +607,17 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const
     cmask = ballot(valid && prev_valid && tok == tok_prev + 1);
     heads = vmask & ~cmask;
   }
-  if (heads == 0) return;
+  if (heads == 0 && tok_lanes == 0) return;
 
 #pragma unroll 1
   for (int r0 = rw0; r0 < rw_end; r0 += kChunkRows) {
     const int r_end = (r0 + kChunkRows < rw_end) ? r0 + kChunkRows : rw_end;
+    if constexpr (!BM) {
+      static_assert(kChunkRows % kWave == 0, "whole rows per lane");
+      if (tok_lanes != 0)
+        quant_token_rows<CODEC, LDT, ELT_L, BS, kChunkRows / kWave>(a, cache, lin, kv, layer, s, tok_lanes, t0, r0,
+                                                                    r_end);
+    }
     const float sc = r0 == rw0 ? sc_first : chunk_scale(r0);
     const bool scale_ok = fast_scale_ok(sc);
     const float r = scale_ok ? 1.0f / sc : 0.0f;

@@ -267,3 +267,54 @@ def test_quant_store_matches_reference_golden_codes(fmt, lin):
         musa_aiter.kv_linear_to_paged_fp8(x, x, kc, vc, slots, scale, scale, fp8_format=fmt)
         got = kc.permute(0, 3, 1, 2).reshape(-1).cpu().numpy()   # slot-major = token-major rows
         assert np.array_equal(got, table[i][flat ^ 0x8000]), float(s)
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("lin", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("bs", [16, 32])
+@pytest.mark.parametrize("inputs", ["all_patterns", "fast_range"])
+def test_quant_store_decode_shaped_tiles(fmt, lin, bs, inputs):
+    """Decode-shaped slots (one to six tokens per sequence at random block offsets, every eighth
+    sequence longer), token order (the cache is mostly unused): tiles of short runs quantise
+    each token's rows element by element; every bit pattern reaches the exact path, the
+    fast-range inputs the fast one."""
+    dtype = LIN_DTYPES[lin]
+    rng = np.random.default_rng(61 + bs)
+    x = _all_patterns(dtype) if inputs == "all_patterns" else _fast_range_inputs(lin, rng)
+    tokens = x.shape[0]
+    slots, nb = make_slots("decode", rng, block_size=bs, tokens=tokens, spare_blocks=300)
+    slots[rng.random(tokens) < 0.05] = -1
+    assert 4 * tokens < nb * bs  # below the destination-order coverage
+    xv = x.flip(0).contiguous()
+    for scale_kind in ("scalar", "per_head"):
+        ks, vs = _scales(scale_kind, rng), _scales(scale_kind, rng).flip(0).contiguous()
+        kc_d = torch.zeros(nb, NH, HD, bs, dtype=torch.uint8, device=DEV)
+        vc_d = torch.zeros_like(kc_d)
+        s_d = torch.from_numpy(slots).to(DEV)
+        musa_aiter.kv_linear_to_paged_fp8(x.to(DEV), xv.to(DEV), kc_d, vc_d, s_d, ks.to(DEV), vs.to(DEV),
+                                          fp8_format=fmt)
+        want_k = np.zeros((nb, NH, HD, bs), np.uint8)
+        want_v = np.zeros_like(want_k)
+        ko.linear_to_paged_fp8(_lin_f32(x), want_k, slots, ks.numpy(), fmt)
+        ko.linear_to_paged_fp8(_lin_f32(xv), want_v, slots, vs.numpy(), fmt)
+        got_k, got_v = kc_d.cpu().numpy(), vc_d.cpu().numpy()
+        assert np.array_equal(got_k, want_k), (scale_kind, np.argwhere(got_k != want_k)[:5])
+        assert np.array_equal(got_v, want_v), (scale_kind, np.argwhere(got_v != want_v)[:5])
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_quant_store_decode_shaped_duplicates(fmt):
+    """Repeated slots in token order: the claim tags keep the last writer in per-token tiles."""
+    rng = np.random.default_rng(71)
+    x = _all_patterns(torch.bfloat16)
+    tokens = x.shape[0]
+    slots, nb = make_slots("duplicates", rng, block_size=BS, tokens=tokens, spare_blocks=300)
+    ks = _scales("per_head", rng)
+    kc_d = torch.zeros(nb, NH, HD, BS, dtype=torch.uint8, device=DEV)
+    vc_d = torch.zeros_like(kc_d)
+    s_d = torch.from_numpy(slots).to(DEV)
+    musa_aiter.kv_linear_to_paged_fp8(x.to(DEV), x.to(DEV), kc_d, vc_d, s_d, ks.to(DEV), ks.to(DEV), fp8_format=fmt)
+    want = np.zeros((nb, NH, HD, BS), np.uint8)
+    ko.linear_to_paged_fp8(_lin_f32(x), want, slots, ks.numpy(), fmt)
+    assert np.array_equal(kc_d.cpu().numpy(), want)
+    assert np.array_equal(vc_d.cpu().numpy(), want)
