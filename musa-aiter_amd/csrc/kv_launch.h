@@ -11,6 +11,10 @@ namespace kvhip {
 
 constexpr int kMaxPlanes = 128;
 
+// Paged scatters of at most this many tokens resolve repeated slots inside
+// their kernel (PagedTileParams::scan_dupes) instead of a claim pass.
+constexpr int kScanTokens = 256;
+
 // Paged-A layout [NL, NB, NH, HD, BS] (block_size innermost) <-> token-major
 // linear rows.  K and V are the two planes of every layer.
 struct PagedTileParams {
@@ -41,6 +45,10 @@ struct PagedTileParams {
   // epoch on slots this call does not write.
   int owner_exclusive;
   BlockTableSlots bt;        // block_tables set: slots derived per dense token, `slots` unused
+  // Scatter of at most kScanTokens tokens without claim tags: the kernels find
+  // each slot's last token themselves (ScanTable).  launch_paged_tiles returns
+  // hipErrorNotSupported, launching nothing, when the call's kernel cannot.
+  int scan_dupes;
 };
 
 hipError_t launch_paged_tiles(const PagedTileParams& p, hipStream_t stream);

@@ -4,6 +4,7 @@
 #pragma once
 
 #include "kv_hip_common.h"
+#include "kv_launch.h"
 
 namespace kvhip {
 
@@ -29,6 +30,7 @@ struct TileArgs {
   float inv_head_dim;          // 1 / head_dim, for small-integer division by head_dim
   BlockTableSlots bt;          // block_tables set: slots derived per dense token
   int32_t row_groups;          // tile kernel: row groups per block (grid x of a gather = tile * row_groups + group)
+  int32_t scan_dupes;          // scatter: resolve repeated slots with a ScanTable instead of claim tags
 };
 
 // Slot of token t: the slot vector's entry, or the block-table slot of the
@@ -39,6 +41,70 @@ __device__ __forceinline__ int64_t slot_at(const TileArgs& a, int64_t t) {
 }
 
 constexpr int kTileTokens = 16;
+
+// Small scatters resolve repeated destinations without the claim pass (one
+// launch and one dependent load fewer): every workgroup maps each slot of the
+// call to the last token that writes it, in LDS -- open addressing over
+// 2 x kScanTokens entries, a 64-bit compare-and-swap claiming an entry for the
+// slot and an atomic max keeping the token -- and a token writes only if it is
+// its slot's last token, the claim pass's rule (last writer wins).  The host
+// keeps such calls at or below kScanTokens tokens, so at most half the
+// entries are taken and every probe sequence ends.
+constexpr int kScanEntries = 2 * kScanTokens;
+constexpr unsigned long long kScanEmpty = ~0ull;
+
+struct ScanTable {
+  unsigned long long key[kScanEntries];
+  int last[kScanEntries];
+};
+
+// The workgroup's table (static LDS of the kernels that call it).
+__device__ __forceinline__ ScanTable& scan_table() {
+  __shared__ ScanTable tb;
+  return tb;
+}
+
+__device__ __forceinline__ uint32_t scan_hash(int64_t s) {
+  return static_cast<uint32_t>((static_cast<uint64_t>(s) * 0x9E3779B97F4A7C15ull) >> 40) & (kScanEntries - 1);
+}
+
+// Fills the table from the call's slots; every thread of the workgroup calls
+// it (it holds two workgroup barriers).
+template <int NT>
+__device__ void scan_build(ScanTable& tb, const TileArgs& a) {
+  const int tid = static_cast<int>(threadIdx.x);
+  for (int e = tid; e < kScanEntries; e += NT) {
+    tb.key[e] = kScanEmpty;
+    tb.last[e] = -1;
+  }
+  __syncthreads();
+  for (int64_t j = tid; j < a.num_tokens; j += NT) {
+    const int64_t s = slot_at(a, j);
+    if (s < 0 || s >= a.num_slots) continue;
+    uint32_t h = scan_hash(s);
+    for (int probe = 0; probe < kScanEntries; ++probe) {
+      const unsigned long long prev = atomicCAS(&tb.key[h], kScanEmpty, static_cast<unsigned long long>(s));
+      if (prev == kScanEmpty || prev == static_cast<unsigned long long>(s)) {
+        atomicMax(&tb.last[h], static_cast<int>(j));
+        break;
+      }
+      h = (h + 1) & (kScanEntries - 1);
+    }
+  }
+  __syncthreads();
+}
+
+// True when token t is the last token of the call writing slot s (s valid).
+__device__ __forceinline__ bool scan_is_last(const ScanTable& tb, int64_t s, int64_t t) {
+  uint32_t h = scan_hash(s);
+  for (int probe = 0; probe < kScanEntries; ++probe) {
+    const unsigned long long k = tb.key[h];
+    if (k == static_cast<unsigned long long>(s)) return tb.last[h] == static_cast<int>(t);
+    if (k == kScanEmpty) return false;
+    h = (h + 1) & (kScanEntries - 1);
+  }
+  return false;
+}
 
 // head = row / head_dim for rows below 2^24: a float reciprocal and one
 // exact correction step.

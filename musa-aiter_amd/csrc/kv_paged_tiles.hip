@@ -280,7 +280,13 @@ void paged_tile_kernel(const TileArgs a) {
   if (t >= 0 && t < a.num_tokens) s = slot_at(a, t);
   bool valid = (s >= 0) && (s < a.num_slots);
   if constexpr (SCATTER) {
-    if (valid && a.owner != nullptr) valid = (a.owner[s] == claim_tag(a.epoch, t));
+    if (a.scan_dupes) {
+      ScanTable& scan = scan_table();
+      scan_build<NT>(scan, a);
+      if (valid) valid = scan_is_last(scan, s, t);
+    } else if (valid && a.owner != nullptr) {
+      valid = (a.owner[s] == claim_tag(a.epoch, t));
+    }
   }
   const uint64_t vmask = ballot(valid);
   const int64_t s_prev = from_prev_lane(s);
@@ -710,6 +716,9 @@ hipError_t dispatch_bs(const TileArgs& a, int64_t bs, bool fast, int64_t planes,
       if (bs == 32) return launch_wave_scatter<ELT_C, ELT_L, CODEC, LDT, 32>(a, planes, stream);
     }
   }
+  // The element kernel checks claim tags only: a call without them takes the
+  // claim pass first.
+  if (SCATTER && a.scan_dupes) return hipErrorNotSupported;
   return launch_elem<ELT_C, ELT_L, CODEC, LDT, SCATTER>(a, planes, stream);
 }
 
@@ -763,6 +772,8 @@ hipError_t launch_paged_tiles(const PagedTileParams& p, hipStream_t stream) {
   a.fill_zeros = p.fill_zeros;
   a.epoch = p.epoch;
   a.owner_exclusive = p.owner_exclusive;
+  a.scan_dupes = p.scan_dupes;
+  if (a.scan_dupes && (!p.scatter || p.num_tokens > kScanTokens)) return hipErrorInvalidValue;
   a.block_size = static_cast<int32_t>(p.block_size);
   a.inv_head_dim = 1.0f / static_cast<float>(p.head_dim);
   a.bt = p.bt;

@@ -566,12 +566,18 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_scatter_kernel(const
   const int64_t t0 = unit * kTileTokens;
   if constexpr (!BM) {
     // Slot window: lane i holds token t0 - 1 + i; a token whose claim lost to a
-    // later duplicate writes nothing.
+    // later duplicate writes nothing.  The duplicate table is built by every
+    // wave of the workgroup, before any of them leaves.
+    if (a.scan_dupes) scan_build<kBlockThreads>(scan_table(), a);
     if (t0 >= a.num_tokens) return;
     const int64_t t = t0 - 1 + lane;
     if (t >= 0 && t < a.num_tokens) s = slot_at(a, t);
     bool valid = (s >= 0) && (s < a.num_slots);
-    if (valid && a.owner != nullptr) valid = (a.owner[s] == claim_tag(a.epoch, t));
+    if (a.scan_dupes) {
+      if (valid) valid = scan_is_last(scan_table(), s, t);
+    } else if (valid && a.owner != nullptr) {
+      valid = (a.owner[s] == claim_tag(a.epoch, t));
+    }
     const uint64_t vmask = ballot(valid);
     const int64_t s_prev = from_prev_lane(s);
     const bool prev_valid = lane > 0 && ((vmask >> (lane - 1)) & 1ull);

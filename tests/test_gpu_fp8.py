@@ -303,11 +303,12 @@ def test_quant_store_decode_shaped_tiles(fmt, lin, bs, inputs):
 
 
 @pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
-def test_quant_store_decode_shaped_duplicates(fmt):
-    """Repeated slots in token order: the claim tags keep the last writer in per-token tiles."""
+@pytest.mark.parametrize("tokens", [200, 512])
+def test_quant_store_decode_shaped_duplicates(fmt, tokens):
+    """Repeated slots in token order keep the last writer in per-token tiles: found in the
+    kernel's LDS table for calls of at most 256 tokens, by the claim pass above."""
     rng = np.random.default_rng(71)
-    x = _all_patterns(torch.bfloat16)
-    tokens = x.shape[0]
+    x = _all_patterns(torch.bfloat16).repeat(8, 1, 1)[:tokens].contiguous()  # 64 tokens of patterns, repeated
     slots, nb = make_slots("duplicates", rng, block_size=BS, tokens=tokens, spare_blocks=300)
     ks = _scales("per_head", rng)
     kc_d = torch.zeros(nb, NH, HD, BS, dtype=torch.uint8, device=DEV)
