@@ -1082,6 +1082,57 @@ def bench_batch_copy() -> dict:
     return out
 
 
+def bench_decode() -> dict:
+    """Decode-step scatters: T new tokens, one per sequence at a random offset of its own block, into one
+    layer's [NB, NH, HD, BS] caches, through the reference-named C entries (the per-layer call of a decode
+    step).  Per-call latency (100 back-to-back calls per timing); the bf16 copy and the FP8 E4M3 quant-store
+    with per-head scales.  Calls of at most 256 tokens resolve repeated slots inside the kernel."""
+    from musa_aiter.ops import _hip
+    from tests import torch_ref
+
+    dev = torch.device("cuda", 0)
+    lib = _hip.library()
+    gen = torch.Generator(device=dev).manual_seed(10)
+    kc = torch.zeros((NB, NH, HD, BS), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    qk = torch.zeros((NB, NH, HD, BS), dtype=torch.uint8, device=dev)
+    qv = torch.zeros_like(qk)
+    sc = _bind(lib, "musa_aiter_kv_linear_to_paged_bfloat16", 5, 5)
+    q = _bind(lib, "musa_aiter_kv_linear_to_paged_fp8_vec4_e4m3", 7, 5)
+    q.argtypes = q.argtypes[:-1] + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int]
+    rng = np.random.default_rng(10)
+    out = {"cache": [NB, NH, HD, BS], "pattern": "one token per sequence, random block and offset"}
+    parity = True
+    for t in (16, 64, 256):
+        blocks = rng.choice(NB, size=t, replace=False)
+        slots_np = (blocks * BS + rng.integers(0, BS, size=t)).astype(np.int64)
+        slots = torch.from_numpy(slots_np).to(dev)
+        kl = torch.randn((t, NH, HD), generator=gen, device=dev).to(torch.bfloat16)
+        vl = torch.randn((t, NH, HD), generator=gen, device=dev).to(torch.bfloat16)
+        ks = (kl.float().abs().amax(dim=(0, 2)) / 448.0).contiguous()
+        vs = (vl.float().abs().amax(dim=(0, 2)) / 448.0).contiguous()
+        sa = (kl.data_ptr(), vl.data_ptr(), slots.data_ptr(), kc.data_ptr(), vc.data_ptr(), t, NB, NH, HD, BS)
+        qa = (kl.data_ptr(), vl.data_ptr(), slots.data_ptr(), qk.data_ptr(), qv.data_ptr(), ks.data_ptr(),
+              vs.data_ptr(), t, NB, NH, HD, BS, 2)
+        _check(sc(*sa, _stream()), "decode scatter")
+        _check(q(*qa, _stream(), 1), "decode quant-store")
+        torch.cuda.synchronize()
+        # Parity outside the timed region: the written rows against the inputs (bf16) and against the
+        # reference encoder's steps (FP8, tests/torch_ref.py), on the CPU.
+        parity &= bool(torch.equal(torch_ref.paged_rows(kc)[slots], kl) and
+                       torch.equal(torch_ref.paged_rows(vc)[slots], vl))
+        want = torch_ref.fp8_quantize(kl.cpu(), ks.cpu().reshape(-1, 1), "e4m3")
+        parity &= bool(torch.equal(torch_ref.paged_rows(qk)[slots].cpu(), want))
+        ms_s = batched_ms(lambda: _check(sc(*sa, _stream()), "decode scatter"), launches=100)
+        ms_q = batched_ms(lambda: _check(q(*qa, _stream(), 1), "decode quant-store"), launches=100)
+        out[f"tokens_{t}"] = {"bf16_scatter_us": float(np.median(ms_s)) * 1e3,
+                              "fp8_e4m3_quant_store_us": float(np.median(ms_q)) * 1e3}
+    out["parity"] = parity
+    log("decode: " + ", ".join(f"{k} {v['bf16_scatter_us']:.1f}/{v['fp8_e4m3_quant_store_us']:.1f} us"
+                               for k, v in out.items() if k.startswith("tokens_")))
+    return out
+
+
 def bench_cachegen() -> dict:
     """CacheGen-style codec (kv_cachegen_encode / kv_cachegen_decode, 256 bins) on a 32-layer K/V tensor of
     4096 tokens x 8 heads x 128 ([32, 2, 4096, 8, 128], 268,435,456 elements), in bf16 and float32.
@@ -1313,6 +1364,12 @@ def summary_lines(line: dict) -> list[str]:
                    f"{_of(b['gather']['gbs'], b['ceilings']['gather_pattern']['gbs'])} | scatter "
                    f"{_pct(b['scatter']['gbs'])} {_of(b['scatter']['gbs'], b['ceilings']['scatter_pattern']['gbs'])}"
                    f" | fp8 656B rows {_pct(c5['fp8_656_rows']['gather']['gbs'])}")
+    dec = x.get("decode_step_scatters")
+    if dec:
+        ts = [k for k in dec if k.startswith("tokens_")]
+        out.append("decode scatter us/call T=" + "/".join(k[7:] for k in ts) + ": bf16 "
+                   + "/".join(f"{dec[k]['bf16_scatter_us']:.1f}" for k in ts) + ", fp8 e4m3 "
+                   + "/".join(f"{dec[k]['fp8_e4m3_quant_store_us']:.1f}" for k in ts))
     nxt = []
     for key, names in (("dense_preload_and_block_copies",
                         (("load_and_reshape_flash", "dense load"), ("reshape_and_cache_back_flash", "write-back"),
@@ -1344,10 +1401,10 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--configs", default="1,2,3,4,5,6,7,8,9",
+    parser.add_argument("--configs", default="1,2,3,4,5,6,7,8,9,10",
                         help="comma list of BASELINE configs to run (2, the headline, always runs; 6 = dense "
                              "preload and block copies; 7 = SGLang HiCache transfers; 8 = LMCache host <-> "
-                             "device copy batches; 9 = CacheGen codec)")
+                             "device copy batches; 9 = CacheGen codec; 10 = decode-step scatter latency)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--placements", type=int, default=5,
                         help="re-allocate the configs[1] caches this many times and time the step on each "
@@ -1386,7 +1443,8 @@ def main() -> int:
     runners = {1: ("config1_fp16_single_layer_gather", bench_config1), 3: ("config3_fp8", bench_config3),
                4: ("config4_lmcache_two_x_nl", bench_config4), 5: ("config5_mla_rows", bench_config5),
                6: ("dense_preload_and_block_copies", bench_dense), 7: ("sglang_hicache_transfers", bench_hicache),
-               8: ("lmcache_host_device_batches", bench_batch_copy), 9: ("cachegen_codec", bench_cachegen)}
+               8: ("lmcache_host_device_batches", bench_batch_copy), 9: ("cachegen_codec", bench_cachegen),
+               10: ("decode_step_scatters", bench_decode)}
     for cfg in sorted(configs - {2}):
         if cfg not in runners:
             continue
