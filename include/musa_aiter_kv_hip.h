@@ -51,6 +51,15 @@ int64_t musa_aiter_hip_graph_claim_arrays(void);
  * descriptor rings of large host batches; the static array of musa_aiter_hip_paged_tiles_noalloc
  * is not counted).  The generic entries below allocate nothing when given caller-owned claims. */
 int64_t musa_aiter_hip_allocated_bytes(void);
+/* No reference counterpart: the largest entry of an int64 index vector, for the Python layer's
+ * host-side bounds checks (the reference reads slot_mapping.max() with torch, kv_transfer.py:3024).
+ * Launches `parts` (1-4096) workgroups on `stream`; workgroup w writes the maximum of the entries it
+ * visits to partial[w] (INT64_MIN if none) and then `stamp` (nonzero, a value the caller changes per
+ * call) to partial[parts + w].  `partial` (2 * parts entries) is pinned host memory the caller owns;
+ * the call returns once every stamp is there (after at most 0.2 s of polling it synchronises the
+ * stream instead), so the maxima can be read right after it; n >= 1. */
+int musa_aiter_hip_index_max(const int64_t* idx, int64_t n, int64_t* partial, int64_t parts, int64_t stamp,
+                             void* stream);
 /* No reference counterpart: the access-pattern ceiling of a paged copy, timed by bench.py.  Copies
  * num_blocks whole blocks of every plane: block i reads block src_blocks[i] (NULL: i) of the source
  * region and writes block dst_blocks[i] (NULL: i) of the destination; block sizes are multiples of

@@ -13,6 +13,7 @@
 // LMCache buffers, skip prefixes); the reference-named symbols are thin
 // wrappers over the same launchers.
 #include <atomic>
+#include <chrono>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -645,6 +646,27 @@ int64_t musa_aiter_hip_graph_claim_arrays() {
 }
 
 int64_t musa_aiter_hip_allocated_bytes() { return g_allocated_bytes.load(); }
+
+int musa_aiter_hip_index_max(const int64_t* idx, int64_t n, int64_t* partial, int64_t parts, int64_t stamp,
+                             void* stream) {
+  if (stamp == 0) return hipErrorInvalidValue;
+  hipError_t err = kvhip::launch_index_max(idx, n, partial, parts, stamp, as_stream(stream));
+  if (err != hipSuccess) return err;
+  // The stamps arrive as the kernel ends; polling them returns sooner than a
+  // stream synchronisation.  A kernel that has not run after 0.2 s (the
+  // stream busy with earlier work) is waited for by the synchronisation.
+  const auto deadline = std::chrono::steady_clock::now() + std::chrono::milliseconds(200);
+  for (int64_t w = 0; w < parts;) {
+    if (__atomic_load_n(&partial[parts + w], __ATOMIC_ACQUIRE) == stamp) {
+      ++w;
+    } else if (std::chrono::steady_clock::now() > deadline) {
+      return hipStreamSynchronize(as_stream(stream));
+    } else {
+      __builtin_ia32_pause();
+    }
+  }
+  return hipSuccess;
+}
 
 // ----- generic entries used by the Python host layer ----------------------------------------
 

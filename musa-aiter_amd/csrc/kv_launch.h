@@ -113,6 +113,11 @@ hipError_t launch_claim(const ClaimSource& src, int64_t n, int64_t rows, uint64_
                         hipStream_t stream, bool reset = false);
 hipError_t launch_fill_u64(uint64_t* p, int64_t n, uint64_t value, hipStream_t stream);
 
+// Maxima of idx[0, n) per workgroup into partial[0, parts), then `stamp`
+// into partial[parts, 2 * parts) (kv_rows.hip).
+hipError_t launch_index_max(const int64_t* idx, int64_t n, int64_t* partial, int64_t parts, int64_t stamp,
+                            hipStream_t stream);
+
 // Block-granular byte copies between an LMCache staging object and padded pages.
 struct StridedBlockParams {
   uint8_t* staging;

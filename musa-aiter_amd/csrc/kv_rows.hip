@@ -330,6 +330,32 @@ __global__ __launch_bounds__(kBlockThreads) void fill_u64_kernel(uint64_t* p, in
     p[i] = value;
 }
 
+// Largest entry of an int64 vector: workgroup w writes the maximum of the
+// entries it visits (grid stride) to partial[w], INT64_MIN if none, and then,
+// with a system-scope release, `stamp` to partial[parts + w], so that a host
+// thread polling pinned host memory sees the maximum once it sees the stamp.
+__global__ __launch_bounds__(kBlockThreads) void index_max_kernel(const int64_t* idx, int64_t n, int64_t* partial,
+                                                                  int64_t stamp) {
+  int64_t m = INT64_MIN;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    m = idx[i] > m ? idx[i] : m;
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const int64_t o = __shfl_xor(static_cast<long long>(m), off);
+    m = o > m ? o : m;
+  }
+  __shared__ int64_t wave_max[kWavesPerBlock];
+  if (lane_id() == 0) wave_max[threadIdx.x / kWave] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 1; w < kWavesPerBlock; ++w) m = wave_max[w] > m ? wave_max[w] : m;
+    partial[blockIdx.x] = m;
+    __hip_atomic_store(&partial[gridDim.x + blockIdx.x], stamp, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+}
+
 // ----- strided block transfer ------------------------------------------------------
 // Staging [NL, staging_tokens, row_bytes] <-> per-layer pages addressed by block
 // id.  Mode 0 pages hold plain rows at block*stride + t*row_bytes; mode 1 pages
@@ -605,6 +631,14 @@ hipError_t launch_claim(const ClaimSource& src, int64_t n, int64_t rows, uint64_
   const int64_t blocks = (n + kBlockThreads - 1) / kBlockThreads;
   hipLaunchKernelGGL(claim_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kBlockThreads), 0, stream, src.idx,
                      src.idx_stride, src.bt, src.src_idx, src.src_rows, n, rows, owner, epoch, reset ? 1 : 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_index_max(const int64_t* idx, int64_t n, int64_t* partial, int64_t parts, int64_t stamp,
+                            hipStream_t stream) {
+  if (idx == nullptr || partial == nullptr || n <= 0 || parts < 1 || parts > 4096) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(index_max_kernel, dim3(static_cast<uint32_t>(parts)), dim3(kBlockThreads), 0, stream, idx, n,
+                     partial, stamp);
   return hipGetLastError();
 }
 

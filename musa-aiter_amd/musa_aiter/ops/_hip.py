@@ -94,6 +94,7 @@ _SIGNATURES: dict[str, list] = {
     "musa_aiter_hip_backend_name": [],
     "musa_aiter_hip_graph_claim_arrays": [],
     "musa_aiter_hip_allocated_bytes": [],
+    "musa_aiter_hip_index_max": [_c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p],  # idx, n, partial, parts, stamp, stream
     "musa_aiter_kv_transfer_abi_version": [],
     "native_lmcache_kv_transfer_abi_version": [],
     "musa_aiter_fp8_kv_cache_abi_version": [],
@@ -276,6 +277,33 @@ def claims_for(device: torch.device, stream: ctypes.c_void_p, rows: int):
         c.epoch = 0
     c.epoch += 1
     return ctypes.addressof(c), entry
+
+
+_INDEX_MAX_PARTS = 64
+_index_max_lock = threading.Lock()
+_index_max_bufs: dict[int, list] = {}
+
+
+def index_max(idx: torch.Tensor) -> int:
+    """Largest entry of a non-empty contiguous int64 device vector, read on the host.
+
+    One small reduction kernel writes per-workgroup maxima, each followed by a stamp, into a pinned host
+    tensor of this module (from torch's host allocator, one per device); the C entry returns when the
+    stamps have arrived.  The same value as ``int(idx.max().item())``, the reference's read."""
+    n = idx.numel()
+    device = idx.device
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    parts = max(1, min(_INDEX_MAX_PARTS, (n + 4095) // 4096))
+    with on_device(device), _index_max_lock:
+        entry = _index_max_bufs.get(index)
+        if entry is None:
+            entry = [torch.zeros(2 * _INDEX_MAX_PARTS, dtype=torch.int64, pin_memory=True), 0]
+            _index_max_bufs[index] = entry
+        buf = entry[0]
+        entry[1] += 1  # the stamp of this call (nonzero, never repeated)
+        check(fn("musa_aiter_hip_index_max")(ptr(idx), n, ptr(buf), parts, entry[1], stream_ptr(device)),
+              "index_max")
+        return int(buf.numpy()[:parts].max())
 
 
 def allocated_bytes() -> int:

@@ -144,7 +144,10 @@ def _check_slots_in_bounds(slots_long: torch.Tensor, nb: int, bs: int, name: str
     """Raise if a non-negative slot is >= nb*bs; one device->host sync per call."""
     if slots_long.numel() == 0:
         return
-    max_slot = int(slots_long.max().item())
+    if slots_long.is_cuda and slots_long.dtype == torch.int64 and slots_long.is_contiguous() and _hip.is_available():
+        max_slot = _hip.index_max(slots_long)
+    else:
+        max_slot = int(slots_long.max().item())
     if max_slot >= nb * bs:
         raise ValueError(f"{name}: slot index {max_slot} out of bounds for caches (max {nb * bs - 1})")
 

@@ -37,7 +37,7 @@ def _declared_symbols() -> set[str]:
 
 def test_header_declares_expected_families():
     names = _declared_symbols()
-    assert len(names) == 126
+    assert len(names) == 127
     for required in ("musa_aiter_kv_load_and_reshape_flash_half", "musa_aiter_kv_triton_indexed_to_dense_bfloat16",
                      "musa_aiter_kv_reshape_and_cache_back_flash_float", "musa_aiter_kv_copy_paged_blocks_fp8_vec8",
                      "musa_aiter_hip_paged_dense_tiles","musa_aiter_kv_paged_to_linear_bfloat16", "musa_aiter_kv_linear_to_paged_multi_layer_half",
@@ -46,7 +46,7 @@ def test_header_declares_expected_families():
                      "lmcache_kv_strided_block_transfer", "musa_aiter_hip_paged_tiles",
                      "musa_aiter_hicache_transfer_bytes", "musa_aiter_hicache_transfer_abi_version",
                      "musa_aiter_hip_copy_rows_paged", "musa_aiter_hip_copy_rows_packed", "musa_aiter_hip_copy_blocks",
-                     "musa_aiter_hip_allocated_bytes"):
+                     "musa_aiter_hip_allocated_bytes", "musa_aiter_hip_index_max"):
         assert required in names
 
 

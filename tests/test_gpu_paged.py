@@ -285,3 +285,20 @@ def test_xcd_order_gathers_other_shapes(dtype, shape, tokens):
     ok, ov = musa_aiter.kv_paged_to_linear_multi_layer(kc.to(DEV), vc.to(DEV), s_d)
     assert np.array_equal(bits(ok), ko.paged_to_linear_multi_layer(bits(kc), slots))
     assert np.array_equal(bits(ov), ko.paged_to_linear_multi_layer(bits(vc), slots))
+
+
+@pytest.mark.parametrize("n", [1, 100, 4097, 300_001])
+def test_index_max_matches_torch(n):
+    # The host-side bounds checks read the largest slot through musa_aiter_hip_index_max: one to 64
+    # workgroups writing their maxima to pinned host memory.  Negative (skipped) slots included.
+    from musa_aiter.ops import _hip
+
+    rng = np.random.default_rng(n)
+    vals = rng.integers(-(2 ** 40), 2 ** 40, size=n).astype(np.int64)
+    for case in range(3):
+        if case == 1:
+            vals = -np.abs(vals) - 1  # all skipped
+        if case == 2:
+            vals[rng.integers(0, n)] = 2 ** 62  # one large entry anywhere
+        t = torch.from_numpy(vals.copy()).to(DEV)
+        assert _hip.index_max(t) == int(t.max().item())
