@@ -344,11 +344,12 @@ int paged_tiles(int scatter, int codec, int cache_elt, int lin_elt, int lin_dtyp
   p.scale_mode = scale_mode;
   p.fill_zeros = fill_zeros;
   if (bt != nullptr) p.bt = *bt;
-  if (scatter && dedupe && t > 1 && t <= kvhip::kScanTokens && fixed_owner == nullptr) {
+  if (scatter && dedupe && t > 1 && t <= kvhip::kScanTokens) {
     // Small scatters find repeated slots inside the kernel (one launch, no
-    // tags written; caller-owned tags stay untouched, which no later call
-    // reads since every call claims under an epoch of its own); the element
-    // kernel cannot, and then the claim pass runs.
+    // tags written; caller-owned tags and the allocation-free entry's array
+    // stay untouched, which no later call reads since every call claims under
+    // an epoch of its own or clears first); the element kernel cannot, and
+    // then the claim pass runs.
     p.scan_dupes = 1;
     const hipError_t err = kvhip::launch_paged_tiles(p, stream);
     if (err != hipErrorNotSupported) return err;
