@@ -148,9 +148,9 @@ __device__ __forceinline__ void scatter_run_chunks(uint8_t* tile, buf_t cbuf, bu
   }
 }
 
-// Scatter tiles of short runs (one or a few tokens per block, as a decode
-// step's one new token per sequence) skip the LDS transpose, which costs one
-// load round trip and 2 x C workgroup barriers per run.  Wave w takes tokens
+// Tiles of short runs (one or a few tokens per block, as a decode step's one
+// new token per sequence) skip the LDS transpose, which costs one load round
+// trip and 2 x C workgroup barriers per run.  Wave w takes tokens
 // w, w + W, ... of the tile (W waves) and, per 64-row block of the group [rb,
 // re), moves row (block * 64 + lane) of the token: one instruction covers 64
 // consecutive rows, one 128-byte line of the linear row (16-bit elements) and
@@ -159,11 +159,11 @@ __device__ __forceinline__ void scatter_run_chunks(uint8_t* tile, buf_t cbuf, bu
 // slot of token t0 + i; bit i + 1 of `vw` (bits 1..kTileTokens) says that the
 // token moves.  Every load of a batch (up to 32 rows per lane) is issued
 // before its stores.
-template <int ELT, int BS, int NT>
-__device__ __forceinline__ void scatter_token_rows(const TileArgs& a, uint8_t* cache, uint8_t* lin, int64_t s,
-                                                   uint64_t vw, int64_t t0, int64_t rb, int64_t re) {
+template <int ELT, int BS, int NT, bool SCATTER>
+__device__ __forceinline__ void token_rows(const TileArgs& a, uint8_t* cache, uint8_t* lin, int64_t s, uint64_t vw,
+                                           int64_t t0, int64_t rb, int64_t re) {
   constexpr int ROWB = BS * ELT;
-  constexpr int kGroupRows = CoopShape<ELT, BS, NT>::kRows * kChunksPerGroup<true>;
+  constexpr int kGroupRows = CoopShape<ELT, BS, NT>::kRows * kChunksPerGroup<SCATTER>;
   static_assert(kGroupRows % kWave == 0, "row blocks of one wave");
   constexpr int NRB = kGroupRows / kWave;   // 64-row blocks per token
   constexpr int kWaves = NT / kWave;
@@ -196,37 +196,47 @@ __device__ __forceinline__ void scatter_token_rows(const TileArgs& a, uint8_t* c
 #pragma unroll
   for (int k0 = 0; k0 < TPW; k0 += TB) {
     uint32_t v[TB][NRB];
+    // Linear rows: non-temporal (whole lines per instruction); cache columns:
+    // default policy (the L2 merges a line's columns).
+    constexpr int kSrcBytes = SCATTER ? ELT : ROWB, kSrcPol = SCATTER ? kBufNT : 0;
+    constexpr int kDstBytes = SCATTER ? ROWB : ELT, kDstPol = SCATTER ? 0 : kBufNT;
 #pragma unroll
     for (int k = 0; k < TB; ++k) {
-      const buf_t src = ldesc(k0 + k);
+      const buf_t src = SCATTER ? ldesc(k0 + k) : cdesc(k0 + k);
 #pragma unroll
       for (int q = 0; q < NRB; ++q) {
-        if constexpr (ELT == 2) v[k][q] = __builtin_amdgcn_raw_buffer_load_b16(src, off(q, ELT), 0, kBufNT);
-        else v[k][q] = __builtin_amdgcn_raw_buffer_load_b32(src, off(q, ELT), 0, kBufNT);
+        if constexpr (ELT == 2) v[k][q] = __builtin_amdgcn_raw_buffer_load_b16(src, off(q, kSrcBytes), 0, kSrcPol);
+        else v[k][q] = __builtin_amdgcn_raw_buffer_load_b32(src, off(q, kSrcBytes), 0, kSrcPol);
       }
     }
 #pragma unroll
     for (int k = 0; k < TB; ++k) {
-      const buf_t dst = cdesc(k0 + k);
+      const buf_t dst = SCATTER ? cdesc(k0 + k) : ldesc(k0 + k);
 #pragma unroll
       for (int q = 0; q < NRB; ++q) {
         if constexpr (ELT == 2)
-          __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(v[k][q]), dst, off(q, ROWB), 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(v[k][q]), dst, off(q, kDstBytes), 0, kDstPol);
         else
-          __builtin_amdgcn_raw_buffer_store_b32(v[k][q], dst, off(q, ROWB), 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b32(v[k][q], dst, off(q, kDstBytes), 0, kDstPol);
       }
     }
   }
 }
 
 // Scatter runs of a tile that average fewer than this many tokens take
-// scatter_token_rows.  Measured against one 16-bit layer ([8192, 8, 128, 16]
-// cache, 16-4,096 tokens in runs of k): k = 1-4 faster (4,096 tokens of
-// runs of 3: 45.2 -> 41.0 us; 256 tokens of single tokens 37.2 -> 11.6 us),
-// k = 6 level (31.9 against 32.5 us).  Gathers keep the run form: the same
-// form on gathers cost configs[0]'s gather 4 % (5,030 -> 4,860 GB/s) though
-// none of its tiles took it.
+// token_rows.  Measured against one 16-bit layer ([8192, 8, 128, 16] cache,
+// 16-4,096 tokens in runs of k): k = 1-4 faster (4,096 tokens of runs of 3:
+// 45.2 -> 41.0 us; 256 tokens of single tokens 37.2 -> 11.6 us), k = 6 level
+// (31.9 against 32.5 us).
 constexpr int kShortRunTokens = 6;
+
+// Gathers take token_rows only in launches of at most kTokenGatherTokens
+// tokens (a kernel instantiation of their own, TOKG): compiled into every
+// gather, the form cost configs[0]'s gather 4 % (5,030 -> 4,860 GB/s) though
+// none of its tiles took it.  There a tile takes it when its runs average
+// fewer than kShortGatherRunTokens tokens and none goes on past the tile.
+constexpr int64_t kTokenGatherTokens = 256;
+constexpr int kShortGatherRunTokens = 3;
 
 // Waves per SIMD the tile kernel's register budget must allow: all eight
 // (64 VGPRs), which the short-launch scatters over 16- and 32-column blocks
@@ -240,7 +250,7 @@ constexpr int kTileMinWaves = (SCATTER && BS == 8) ? 1 : 8;
 // workgroup order (FEW false: the XCD-contiguous order).  NT is the workgroup
 // size; a chunk is NT 16-byte pieces.  LSTP: cache-policy bits of a gather's
 // linear-side stores.
-template <int ELT, int BS, bool SCATTER, bool FEW, int NT = kCoopThreads, int LSTP = kBufNT>
+template <int ELT, int BS, bool SCATTER, bool FEW, int NT = kCoopThreads, int LSTP = kBufNT, bool TOKG = false>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(kTileMinWaves<BS, SCATTER>)))
 void paged_tile_kernel(const TileArgs a) {
   using S = CoopShape<ELT, BS, NT>;
@@ -319,7 +329,7 @@ void paged_tile_kernel(const TileArgs a) {
     // continue an earlier tile's run belong to that tile): adding a head's
     // next bit to cmask carries through exactly the continuation bits of its
     // run.  The tile's last run may go on past the tile's end and keeps the
-    // run form; short runs before it move with scatter_token_rows.
+    // run form; short runs before it move with token_rows.
     uint64_t tok_heads = heads;
     uint64_t tok_lanes = heads | (((cmask + (heads << 1)) ^ cmask) & cmask);
     if (tok_lanes & ~window) {
@@ -329,8 +339,18 @@ void paged_tile_kernel(const TileArgs a) {
     }
     const int truns = __builtin_popcountll(tok_heads);
     if (truns > 0 && __builtin_popcountll(tok_lanes) < truns * kShortRunTokens) {
-      scatter_token_rows<ELT, BS, NT>(a, cache, lin, s, tok_lanes, t0, rb, re);
+      token_rows<ELT, BS, NT, true>(a, cache, lin, s, tok_lanes, t0, rb, re);
       heads &= ~tok_heads;
+    }
+  }
+  if constexpr (!SCATTER && TOKG) {
+    // The same lanes for a gather, which takes token_rows only for a whole
+    // tile (all its runs, none of them going on past the tile).
+    const uint64_t owned = heads | (((cmask + (heads << 1)) ^ cmask) & cmask);
+    const int nr = __builtin_popcountll(heads);
+    if (nr > 0 && (owned & ~window) == 0 && __builtin_popcountll(owned) < nr * kShortGatherRunTokens) {
+      token_rows<ELT, BS, NT, false>(a, cache, lin, s, owned, t0, rb, re);
+      heads = 0;
     }
   }
 
@@ -668,8 +688,15 @@ hipError_t launch_tile(const TileArgs& a0, int64_t planes, hipStream_t stream) {
       // 64 planes this form is 1 % slower than 256 threads).
       err = tile_grid<ELT, BS, SCATTER, kShortGatherThreads>(a0, planes, &a, &grid, &workgroups);
       if (err != hipSuccess) return err;
-      if (lines)
+      const bool tok = a0.num_tokens <= kTokenGatherTokens;
+      if (lines && tok)
+        hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, SCATTER, true, kShortGatherThreads, kBufWT, true>), grid,
+                           dim3(kShortGatherThreads), 0, stream, a);
+      else if (lines)
         hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, SCATTER, true, kShortGatherThreads, kBufWT>), grid,
+                           dim3(kShortGatherThreads), 0, stream, a);
+      else if (tok)
+        hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, SCATTER, true, kShortGatherThreads, kBufNT, true>), grid,
                            dim3(kShortGatherThreads), 0, stream, a);
       else
         hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, SCATTER, true, kShortGatherThreads>), grid,
@@ -684,7 +711,10 @@ hipError_t launch_tile(const TileArgs& a0, int64_t planes, hipStream_t stream) {
   const bool few = SCATTER ? workgroups <= kFewGroups
                            : !(planes >= kXcdOrderPlanes && workgroups > kFewGroups &&
                                workgroups <= int64_t{0xFFFFFFFF});
-  if (few)
+  if (few && !SCATTER && a0.num_tokens <= kTokenGatherTokens)
+    hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, SCATTER, true, kCoopThreads, kBufNT, !SCATTER>), grid,
+                       dim3(kCoopThreads), 0, stream, a);
+  else if (few)
     hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, SCATTER, true>), grid, dim3(kCoopThreads), 0, stream, a);
   else if (lines)
     hipLaunchKernelGGL((paged_tile_kernel<ELT, BS, SCATTER, false, kCoopThreads, kBufWT>), grid, dim3(kCoopThreads),

@@ -241,6 +241,8 @@ def test_kernel_forms_either_side_of_the_launch_thresholds(layers, tokens, kind)
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("bs", [8, 16, 32])
 @pytest.mark.parametrize("layers,tokens,kind", [
+    (1, 200, "decode"),          # at most 256 tokens: gathers may take the per-token form too,
+    (4, 256, "random"),          # scatters resolve repeated slots in LDS
     (1, 301, "decode"),          # short launches: loads-first scatter, 128-thread gather
     (3, 301, "decode"),
     (2, 40000, "decode"),        # scatter above 8,192 workgroups: chunk-by-chunk form
