@@ -12,8 +12,8 @@
 // decoded by one LDS read from the workgroup's decode tables (value x scale
 // already rounded to the linear type), about 2.5 VALU instructions per
 // element against 16.8 for decoding, scaling and rounding in registers.  The
-// LDS holds only those tables (4 KiB), so the kernel's 66 VGPRs set its
-// occupancy.  Copies (no decode) stage the chunk through the wave's LDS
+// LDS holds only those tables (4 KiB); the launch pads it so that 3
+// workgroups share a CU (launch_wave_gather).  Copies (no decode) stage the chunk through the wave's LDS
 // region instead: coalesced loads, exchanged so that each lane holds its tile.
 // Runs that do not cover every column group of the block row load only the
 // column groups they cover.
@@ -107,7 +107,64 @@ struct WaveShape {
 
 // STP: cache-policy bits of the full runs' linear stores (kBufWT when every
 // linear row is whole 128-byte lines).
-template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS, int STP>
+// Dequant-gather tiles of short runs in small launches (TOKG: a kernel
+// instantiation of its own, for calls of at most kTokenGatherTokens tokens):
+// instead of walking the runs one by one, the wave moves its chunk's rows of
+// every such token at once, one row per lane (row r0 + m * 64 + lane, M =
+// kChunkRows / 64 rows per token): the token's code byte through a scalar
+// buffer descriptor of its block column (no records for a token that does
+// not move), its value from the head's decode table, and the element to the
+// token's linear row.  `lut_off[m]` is the offset of row m's table.  Lane
+// i + 1 of `s` holds the slot of token t0 + i; bit i + 1 of `vw` says that the
+// token moves.
+template <int ELT_L, int BS, int M, typename LutT>
+__device__ __forceinline__ void dequant_token_rows(const TileArgs& a, const uint8_t* cache, uint8_t* lin,
+                                                   const LutT* lut_all, const int (&lut_off)[M], int64_t s,
+                                                   uint64_t vw, int64_t t0, int64_t r0, int64_t r_end) {
+  constexpr int TB = 32 / M < kTileTokens ? 32 / M : kTileTokens;  // tokens per batch: 32 codes in flight per lane
+  static_assert(kTileTokens % TB == 0, "whole batches");
+  int lane = lane_id();
+  asm volatile("" : "+v"(lane));
+  const int64_t blk = s / BS;
+  const int64_t cbase = (blk * a.nrows + r0) * BS + (s - blk * BS);
+  uint8_t* const lin0 = lin + t0 * a.lin_token_stride + r0 * ELT_L;
+  const int rows = static_cast<int>(r_end - r0);
+  auto off = [&](int m, int bytes) -> uint32_t {
+    return m * kWave + lane < rows ? static_cast<uint32_t>((m * kWave + lane) * bytes) : kOffOob;
+  };
+  auto records = [&](int i) -> int { return ((vw >> (i + 1)) & 1ull) ? 0x7FFFFFFF : 0; };
+#pragma unroll 1
+  for (int i0 = 0; i0 < kTileTokens; i0 += TB) {
+    if (((vw >> (i0 + 1)) & ((1ull << TB) - 1ull)) == 0) continue;
+    uint32_t code[TB][M];
+#pragma unroll
+    for (int k = 0; k < TB; ++k) {
+      const buf_t src = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(cache) + readlane64(cbase, i0 + k + 1), 0,
+                                                          records(i0 + k), 0x00020000);
+#pragma unroll
+      for (int m = 0; m < M; ++m) code[k][m] = __builtin_amdgcn_raw_buffer_load_b8(src, off(m, BS), 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < TB; ++k) {
+      const buf_t dst = __builtin_amdgcn_make_buffer_rsrc(lin0 + static_cast<int64_t>(i0 + k) * a.lin_token_stride, 0,
+                                                          records(i0 + k), 0x00020000);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const LutT v = lut_all[lut_off[m] + code[k][m]];
+        if constexpr (ELT_L == 2) __builtin_amdgcn_raw_buffer_store_b16(v, dst, off(m, ELT_L), 0, kBufNT);
+        else __builtin_amdgcn_raw_buffer_store_b32(v, dst, off(m, ELT_L), 0, kBufNT);
+      }
+    }
+  }
+}
+
+// Launches of at most this many tokens take the TOKG instantiation; there a
+// tile takes dequant_token_rows when its runs average fewer than
+// kShortDequantRunTokens tokens and none goes on past the tile.
+constexpr int64_t kTokenDequantTokens = 256;
+constexpr int kShortDequantRunTokens = 3;
+
+template <int ELT_C, int ELT_L, int CODEC, int LDT, int BS, int STP, bool TOKG = false>
 __global__ __launch_bounds__(kBlockThreads) void paged_wave_gather_kernel(const TileArgs a) {
   using W = WaveShape<ELT_C, ELT_L, BS>;
   constexpr int RPL = W::RPL, CG = W::CG, NCG = W::NCG, kChunkRows = W::kChunkRows;
@@ -221,6 +278,26 @@ __global__ __launch_bounds__(kBlockThreads) void paged_wave_gather_kernel(const 
   // multiple of RPL on this path).
   const LutT* lut = lut_all;
   if (kLut && a.scale_mode != 0 && tile_in) lut += (head_of_row(a, static_cast<int>(trow)) - h_lo) * 256;
+
+  if constexpr (TOKG && kLut) {
+    // A whole tile of short runs (none going on past the tile) moves token by
+    // token; the lanes of the runs that start in the tile are those a head's
+    // next bit carries through in cmask.
+    const uint64_t owned = heads | (((cmask + (heads << 1)) ^ cmask) & cmask);
+    const int nr = __builtin_popcountll(heads);
+    if (nr > 0 && (owned & ~window) == 0 && __builtin_popcountll(owned) < nr * kShortDequantRunTokens) {
+      constexpr int M = kChunkRows / kWave;
+      static_assert(kChunkRows % kWave == 0, "whole rows per lane");
+      int lut_off[M];
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const int64_t row = r0 + m * kWave + lane;
+        lut_off[m] = (a.scale_mode != 0 && row < r_end) ? (head_of_row(a, static_cast<int>(row)) - h_lo) * 256 : 0;
+      }
+      dequant_token_rows<ELT_L, BS, M, LutT>(a, cache, lin, lut_all, lut_off, s, owned, t0, r0, r_end);
+      heads = 0;
+    }
+  }
 
   while (heads) {
     const int i = __builtin_ctzll(heads);
@@ -905,9 +982,16 @@ hipError_t launch_wave_gather(const TileArgs& a, int64_t planes, hipStream_t str
   // FP8 preload -0.3-0.5 %;
   // 5 per CU was 2-5 % slower, and staging the tiles through LDS with
   // whole-line loads gained 1.6 % on cfg 3 but lost 6 % on the dense preload.
-  if (whole_line_rows(a, ELT_L))
+  const bool tok = a.num_tokens <= kTokenDequantTokens;
+  if (whole_line_rows(a, ELT_L) && tok)
+    hipLaunchKernelGGL((paged_wave_gather_kernel<ELT_C, ELT_L, CODEC, LDT, BS, kBufWT, true>), grid,
+                       dim3(kBlockThreads), kGatherLdsPad, stream, a);
+  else if (whole_line_rows(a, ELT_L))
     hipLaunchKernelGGL((paged_wave_gather_kernel<ELT_C, ELT_L, CODEC, LDT, BS, kBufWT>), grid, dim3(kBlockThreads),
                        kGatherLdsPad, stream, a);
+  else if (tok)
+    hipLaunchKernelGGL((paged_wave_gather_kernel<ELT_C, ELT_L, CODEC, LDT, BS, kBufNT, true>), grid,
+                       dim3(kBlockThreads), kGatherLdsPad, stream, a);
   else
     hipLaunchKernelGGL((paged_wave_gather_kernel<ELT_C, ELT_L, CODEC, LDT, BS, kBufNT>), grid, dim3(kBlockThreads),
                        kGatherLdsPad, stream, a);

@@ -300,6 +300,12 @@ def test_quant_store_decode_shaped_tiles(fmt, lin, bs, inputs):
         got_k, got_v = kc_d.cpu().numpy(), vc_d.cpu().numpy()
         assert np.array_equal(got_k, want_k), (scale_kind, np.argwhere(got_k != want_k)[:5])
         assert np.array_equal(got_v, want_v), (scale_kind, np.argwhere(got_v != want_v)[:5])
+        # The same slots back (at most 256 tokens: the dequant-gather's per-token tiles).
+        for out_name, out_dtype in LIN_DTYPES.items():
+            rk, rv = musa_aiter.kv_paged_fp8_to_linear(kc_d, vc_d, s_d, ks.to(DEV), vs.to(DEV), out_dtype=out_dtype,
+                                                       fp8_format=fmt)
+            assert np.array_equal(bits(rk), ko.paged_fp8_to_linear(want_k, slots, ks.numpy(), fmt, out_name))
+            assert np.array_equal(bits(rv), ko.paged_fp8_to_linear(want_v, slots, vs.numpy(), fmt, out_name))
 
 
 @pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
