@@ -1085,8 +1085,9 @@ def bench_batch_copy() -> dict:
 def bench_decode() -> dict:
     """Decode-step scatters: T new tokens, one per sequence at a random offset of its own block, into one
     layer's [NB, NH, HD, BS] caches, through the reference-named C entries (the per-layer call of a decode
-    step).  Per-call latency (100 back-to-back calls per timing); the bf16 copy and the FP8 E4M3 quant-store
-    with per-head scales.  Calls of at most 256 tokens resolve repeated slots inside the kernel."""
+    step), and the gathers of the same slots back.  Per-call latency (100 back-to-back calls per timing);
+    the bf16 copy and the FP8 E4M3 quant-store / dequant-gather with per-head scales.  Calls of at most 256
+    tokens resolve repeated slots inside the kernel and gather short runs token by token."""
     from musa_aiter.ops import _hip
     from tests import torch_ref
 
@@ -1098,8 +1099,11 @@ def bench_decode() -> dict:
     qk = torch.zeros((NB, NH, HD, BS), dtype=torch.uint8, device=dev)
     qv = torch.zeros_like(qk)
     sc = _bind(lib, "musa_aiter_kv_linear_to_paged_bfloat16", 5, 5)
+    ga = _bind(lib, "musa_aiter_kv_paged_to_linear_bfloat16", 5, 5)
     q = _bind(lib, "musa_aiter_kv_linear_to_paged_fp8_vec4_e4m3", 7, 5)
-    q.argtypes = q.argtypes[:-1] + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int]
+    dq = _bind(lib, "musa_aiter_kv_paged_fp8_to_linear_vec4_e4m3", 7, 5)
+    for f in (q, dq):
+        f.argtypes = f.argtypes[:-1] + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int]
     rng = np.random.default_rng(10)
     out = {"cache": [NB, NH, HD, BS], "pattern": "one token per sequence, random block and offset"}
     parity = True
@@ -1111,25 +1115,40 @@ def bench_decode() -> dict:
         vl = torch.randn((t, NH, HD), generator=gen, device=dev).to(torch.bfloat16)
         ks = (kl.float().abs().amax(dim=(0, 2)) / 448.0).contiguous()
         vs = (vl.float().abs().amax(dim=(0, 2)) / 448.0).contiguous()
+        ok, ov = torch.empty_like(kl), torch.empty_like(vl)
         sa = (kl.data_ptr(), vl.data_ptr(), slots.data_ptr(), kc.data_ptr(), vc.data_ptr(), t, NB, NH, HD, BS)
+        gargs = (kc.data_ptr(), vc.data_ptr(), slots.data_ptr(), ok.data_ptr(), ov.data_ptr(), t, NB, NH, HD, BS)
         qa = (kl.data_ptr(), vl.data_ptr(), slots.data_ptr(), qk.data_ptr(), qv.data_ptr(), ks.data_ptr(),
               vs.data_ptr(), t, NB, NH, HD, BS, 2)
+        da = (qk.data_ptr(), qv.data_ptr(), slots.data_ptr(), ks.data_ptr(), vs.data_ptr(), ok.data_ptr(),
+              ov.data_ptr(), t, NB, NH, HD, BS, 2)
         _check(sc(*sa, _stream()), "decode scatter")
         _check(q(*qa, _stream(), 1), "decode quant-store")
+        _check(ga(*gargs, _stream()), "decode gather")
         torch.cuda.synchronize()
+        parity &= bool(torch.equal(ok, kl) and torch.equal(ov, vl))
         # Parity outside the timed region: the written rows against the inputs (bf16) and against the
         # reference encoder's steps (FP8, tests/torch_ref.py), on the CPU.
         parity &= bool(torch.equal(torch_ref.paged_rows(kc)[slots], kl) and
                        torch.equal(torch_ref.paged_rows(vc)[slots], vl))
         want = torch_ref.fp8_quantize(kl.cpu(), ks.cpu().reshape(-1, 1), "e4m3")
         parity &= bool(torch.equal(torch_ref.paged_rows(qk)[slots].cpu(), want))
+        _check(dq(*da, _stream(), 1), "decode dequant-gather")
+        torch.cuda.synchronize()
+        want_deq = torch_ref.fp8_dequantize(want, ks.cpu().reshape(-1, 1), "e4m3", torch.bfloat16)
+        parity &= bool(torch.equal(ok.cpu(), want_deq))
         ms_s = batched_ms(lambda: _check(sc(*sa, _stream()), "decode scatter"), launches=100)
         ms_q = batched_ms(lambda: _check(q(*qa, _stream(), 1), "decode quant-store"), launches=100)
+        ms_g = batched_ms(lambda: _check(ga(*gargs, _stream()), "decode gather"), launches=100)
+        ms_d = batched_ms(lambda: _check(dq(*da, _stream(), 1), "decode dequant-gather"), launches=100)
         out[f"tokens_{t}"] = {"bf16_scatter_us": float(np.median(ms_s)) * 1e3,
-                              "fp8_e4m3_quant_store_us": float(np.median(ms_q)) * 1e3}
+                              "fp8_e4m3_quant_store_us": float(np.median(ms_q)) * 1e3,
+                              "bf16_gather_us": float(np.median(ms_g)) * 1e3,
+                              "fp8_e4m3_dequant_gather_us": float(np.median(ms_d)) * 1e3}
     out["parity"] = parity
-    log("decode: " + ", ".join(f"{k} {v['bf16_scatter_us']:.1f}/{v['fp8_e4m3_quant_store_us']:.1f} us"
-                               for k, v in out.items() if k.startswith("tokens_")))
+    log("decode (scatter bf16/fp8, gather bf16/fp8): " + ", ".join(
+        f"{k} {v['bf16_scatter_us']:.1f}/{v['fp8_e4m3_quant_store_us']:.1f}/{v['bf16_gather_us']:.1f}/"
+        f"{v['fp8_e4m3_dequant_gather_us']:.1f} us" for k, v in out.items() if k.startswith("tokens_")))
     return out
 
 
@@ -1367,9 +1386,11 @@ def summary_lines(line: dict) -> list[str]:
     dec = x.get("decode_step_scatters")
     if dec:
         ts = [k for k in dec if k.startswith("tokens_")]
-        out.append("decode scatter us/call T=" + "/".join(k[7:] for k in ts) + ": bf16 "
-                   + "/".join(f"{dec[k]['bf16_scatter_us']:.1f}" for k in ts) + ", fp8 e4m3 "
-                   + "/".join(f"{dec[k]['fp8_e4m3_quant_store_us']:.1f}" for k in ts))
+        def us(key):
+            return "/".join(f"{dec[k][key]:.1f}" for k in ts if key in dec[k])
+        out.append("decode us/call T=" + "/".join(k[7:] for k in ts) + ": scatter bf16 " + us("bf16_scatter_us")
+                   + ", fp8 e4m3 " + us("fp8_e4m3_quant_store_us") + " | gather bf16 " + us("bf16_gather_us")
+                   + ", fp8 e4m3 " + us("fp8_e4m3_dequant_gather_us"))
     nxt = []
     for key, names in (("dense_preload_and_block_copies",
                         (("load_and_reshape_flash", "dense load"), ("reshape_and_cache_back_flash", "write-back"),
